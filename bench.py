@@ -1,0 +1,276 @@
+#!/usr/bin/env python3
+"""Benchmark of the block-quantized linear-layer path on one MI355X.
+
+Workload: the seven linear layers of one
+Llama-3-8B-shaped decoder layer at batch M = 1, Q4_K_M mixture
+  q 4096->4096 Q4_K, k 4096->1024 Q4_K, v 4096->1024 Q6_K, o 4096->4096 Q4_K,
+  gate/up 4096->14336 Q4_K, down 14336->4096 Q6_K,
+run as dequant_matmul_a8.v2 with activation blocks of 256 (the path
+mim-import writes for K-quant weights): each step quantizes the layer's four
+input vectors (attention input, attention output, FFN input, FFN hidden) and
+runs the seven products. Weights W ~ N(0, 0.02^2) (numpy PCG64, seeds 0..6 in
+the order above), encoded on the GPU by libmimg's encoder; activations
+x ~ N(0, 1) (seeds 100..103). Synthetic data; no checkpoint.
+
+To measure HBM rather than the 256 MB MALL, the weights are copied into
+--rotate (default 32) distinct layers (4.4 GB, a whole 8B model's linears)
+and step s uses layer s mod rotate. Each layer's step is captured in a HIP
+graph. Timed region: exactly --steps steps between two synchronisations.
+
+value = bytes per step / time per step, bytes by BASELINE.md's formula
+(sum of N*(K/QK)*block_bytes + K*4 + N*4 over the seven matrices).
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mimir-model_amd"))
+
+import hiprt  # noqa: E402
+import mimg  # noqa: E402
+
+METRIC = "Q4_K GEMV GB/s (% of HBM peak); decode tok/s at 8B Q4_K_M; prefill TFLOP/s"
+HBM_PEAK_GBS = 8000.0
+Q4_K, Q6_K = mimg.Q4_K, mimg.Q6_K
+
+# (name, N, K, dtype, weight seed, input index)
+CFG1 = [
+    ("q", 4096, 4096, Q4_K, 0, 0),
+    ("k", 1024, 4096, Q4_K, 1, 0),
+    ("v", 1024, 4096, Q6_K, 2, 0),
+    ("o", 4096, 4096, Q4_K, 3, 1),
+    ("gate", 14336, 4096, Q4_K, 4, 2),
+    ("up", 14336, 4096, Q4_K, 5, 2),
+    ("down", 4096, 14336, Q6_K, 6, 3),
+]
+INPUT_K = [4096, 4096, 4096, 14336]
+
+
+def weight_bytes(n, k, dt):
+    return n * (k // 256) * (144 if dt == Q4_K else 210)
+
+
+def step_bytes():
+    return sum(weight_bytes(n, k, dt) + k * 4 + n * 4 for _, n, k, dt, _, _ in CFG1)
+
+
+def launch_bytes(n, k, dt):
+    """Algorithmic bytes of one GEMV launch at M = 1: the weight blocks, the
+    int8 quants, one f32 scale per 256, the per-32 (Q4_K) or per-16 (Q6_K)
+    int16 sums, and the f32 outputs."""
+    sums = (k // 32) * 2 if dt == Q4_K else (k // 16) * 2
+    return weight_bytes(n, k, dt) + k + (k // 256) * 4 + sums + n * 4
+
+
+def make_weights(stream, rotate, log):
+    """Encodes the seven matrices on the GPU and registers `rotate` device
+    copies of each. Returns ([per layer: {name: Weight}], {name: host bytes})."""
+    layers = [dict() for _ in range(rotate)]
+    host_bytes = {}
+    for name, n, k, dt, seed, _ in CFG1:
+        t0 = time.time()
+        w32 = np.random.default_rng(seed).standard_normal((n, k), dtype=np.float32)
+        w32 *= np.float32(0.02)
+        xd = hiprt.DeviceBuffer.from_array(w32)
+        del w32
+        nb = weight_bytes(n, k, dt)
+        enc = hiprt.DeviceBuffer(nb)
+        mimg.quantize_dev(dt, xd.ptr, n * k, enc.ptr, nb, stream.handle)
+        stream.sync()
+        xd.free()
+        host_bytes[name] = enc.download(np.uint8)
+        for l in range(rotate):
+            layers[l][name] = mimg.Weight((enc.ptr, nb), dt, n, k, device=True)
+        enc.free()
+        log(f"  {name}: {n}x{k} {'Q4_K' if dt == Q4_K else 'Q6_K'} {nb / 1e6:.1f} MB x {rotate} ({time.time() - t0:.1f} s)")
+    return layers, host_bytes
+
+
+def cpu_baseline(host_bytes, xs, seconds, log):
+    """The oracle's linear_a8 (C restatement of the reference numerics) over
+    the seven matrices of one layer, on this host's cores."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import mimref
+
+    threads = min(16, os.cpu_count() or 1)
+    nbytes = step_bytes()
+
+    def one_layer(t):
+        for name, n, k, dt, _, inp in CFG1:
+            mimref.linear_a8(xs[inp], host_bytes[name], dt, n, k, block=256, threads=t)
+
+    one_layer(threads)  # warm the page cache
+    reps, t0 = 0, time.time()
+    while time.time() - t0 < seconds or reps == 0:
+        one_layer(threads)
+        reps += 1
+    all_s = (time.time() - t0) / reps
+    t0 = time.time()
+    one_layer(1)
+    one_s = time.time() - t0
+    cpu_model = platform.processor() or ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    log(f"  cpu: {threads} threads {nbytes / all_s / 1e9:.2f} GB/s, 1 thread {nbytes / one_s / 1e9:.2f} GB/s")
+    return {
+        "value": round(nbytes / all_s / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"one cfg1 layer set (7 matrices, {nbytes / 1e6:.1f} MB) at M=1 through oracle/ linear_a8 "
+                  f"(C restatement of dotQ4KQ8KAVX2/dotQ6KQ8KAVX2 numerics), {reps} passes in {reps * all_s:.1f} s",
+        "value_1thread": round(nbytes / one_s / 1e9, 3),
+        "cpu_model": cpu_model,
+        "nproc": os.cpu_count(),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=320)
+    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--rotate", type=int, default=32)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
+    ap.add_argument("--roofline-launches", type=int, default=128)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (row sharding is a design note). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    def log(msg):
+        print(msg, file=sys.stderr, flush=True)
+
+    mimg.init(0)
+    stream = hiprt.Stream()
+    log(f"bench: cfg1 layer set, M=1, rotate {args.rotate}")
+    layers, host_bytes = make_weights(stream, args.rotate, log)
+
+    xs = [np.random.default_rng(100 + i).standard_normal((1, k), dtype=np.float32) for i, k in enumerate(INPUT_K)]
+    xd = [hiprt.DeviceBuffer.from_array(x) for x in xs]
+    ws_bytes = [mimg.a8_workspace_bytes(1, k) for k in INPUT_K]
+    ws = [hiprt.DeviceBuffer(b) for b in ws_bytes]
+    yd = {name: hiprt.DeviceBuffer(n * 4) for name, n, _, _, _, _ in CFG1}
+
+    def enqueue_step(l):
+        for i, k in enumerate(INPUT_K):
+            mimg.quantize_act_dev(xd[i].ptr, 1, k, 256, ws[i].ptr, ws_bytes[i], stream.handle)
+        for name, n, k, dt, _, inp in CFG1:
+            mimg.matmul_a8_quantized_dev(layers[l][name], xd[inp].ptr, 1, None, 256, yd[name].ptr,
+                                         ws[inp].ptr, ws_bytes[inp], stream.handle)
+
+    if args.eager:
+        run_step = enqueue_step
+    else:
+        graphs = [hiprt.Graph(stream, lambda l=l: enqueue_step(l)) for l in range(args.rotate)]
+
+        def run_step(l):
+            graphs[l].launch(stream)
+
+    for s in range(args.warmup):
+        run_step(s % args.rotate)
+    stream.sync()
+    log("  warmup done")
+
+    e0, e1 = hiprt.Event(), hiprt.Event()
+    hiprt.device_sync()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for s in range(args.steps):
+        run_step(s % args.rotate)
+    e1.record(stream)
+    e1.sync()
+    hiprt.device_sync()
+    wall = time.perf_counter() - t0
+    ms_gpu = e0.elapsed_ms(e1)
+    ms_per_step = ms_gpu / args.steps
+    value = step_bytes() / (ms_per_step * 1e-3) / 1e9
+    log(f"  timed: {args.steps} steps, {ms_per_step * 1e3:.2f} us/step (events), wall {wall * 1e3 / args.steps:.2f} us/step, {value:.1f} GB/s")
+
+    # Roofline of the dominant kernel: the Q4_K GEMV at the gate/up shape
+    # (14336 x 4096, 33 MB), per-launch HIP events on the launch stream,
+    # over distinct rotation copies so every launch reads from HBM.
+    def per_launch(name):
+        _, n, k, dt, _, inp = next(c for c in CFG1 if c[0] == name)
+        evs = [(hiprt.Event(), hiprt.Event()) for _ in range(args.roofline_launches)]
+        mimg.quantize_act_dev(xd[inp].ptr, 1, k, 256, ws[inp].ptr, ws_bytes[inp], stream.handle)
+        for i, (a, b) in enumerate(evs):
+            a.record(stream)
+            mimg.matmul_a8_quantized_dev(layers[i % args.rotate][name], xd[inp].ptr, 1, None, 256, yd[name].ptr,
+                                         ws[inp].ptr, ws_bytes[inp], stream.handle)
+            b.record(stream)
+        stream.sync()
+        ts = np.array([a.elapsed_ms(b) for a, b in evs[4:]])
+        us = float(np.mean(ts)) * 1e3
+        nbytes = launch_bytes(n, k, dt)
+        return us, nbytes, nbytes / (us * 1e-6) / 1e9
+
+    g_us, g_bytes, g_gbs = per_launch("gate")
+    d_us, d_bytes, d_gbs = per_launch("down")
+    log(f"  gate GEMV (Q4_K 14336x4096): {g_us:.2f} us/launch, {g_gbs:.0f} GB/s; "
+        f"down GEMV (Q6_K 4096x14336): {d_us:.2f} us/launch, {d_gbs:.0f} GB/s")
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "gemv_q4k_gate_traffic.json")
+    if os.path.exists(tpath):
+        try:
+            traffic = json.load(open(tpath)).get("bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 x q4_k/q6_k, i32 block sums, f32 epilogue",
+        "data": "synthetic (W ~ N(0,0.02^2) seeds 0..6 encoded Q4_K/Q6_K; x ~ N(0,1) seeds 100..103)",
+        "config": {
+            "workload": "cfg1: Llama-3-8B decoder-layer linear set, M=1, Q4_K_M (q,k,o,gate,up Q4_K; v,down Q6_K), "
+                        "dequant_matmul_a8.v2 block=256",
+            "bytes_per_step": step_bytes(),
+            "rotation_layers": args.rotate,
+            "graphs": not args.eager,
+            "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(g_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(g_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "gemv_a8k_kernel<Q4_K,1> at 14336x4096 (gate/up)",
+            "launch_bytes": g_bytes,
+            "avg_launch_us": round(g_us, 3),
+            "q6k_down": {"avg_launch_us": round(d_us, 3), "launch_bytes": d_bytes, "achieved": round(d_gbs, 1)},
+        },
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(host_bytes, xs, args.cpu_seconds, log)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

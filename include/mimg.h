@@ -1,0 +1,161 @@
+/*
+ * mimg.h — C ABI of libmimg, the MI355X (gfx950) block-quantized
+ * linear-layer path of mimir-model.
+ *
+ * The reference runs these products on the CPU inside the interp executor's
+ * fast paths:
+ *
+ *   type fastFunc func(attrs []mim.Attr, in []*ref.Tensor, dts []mim.DType,
+ *                      shapes [][]int) (out []*ref.Tensor, handled bool, err error)
+ *   fastPaths["dequant_matmul_a8.v2" | "dequant_matmul_a8.v1" | "dequant_matmul.v1"]
+ *                                                  (reference interp/fast.go:40-59)
+ *
+ * A Go cgo shim (mimir-model_amd/go/mimg_fast.go) registers replacements for
+ * those keys that call the functions below; the signature of fastFunc and
+ * its callers (interp/interp.go:853-877, interp/plan.go:834-896) are
+ * unchanged. Plain pointers and sizes only.
+ *
+ * Status codes: 0 = done; > 0 = not handled, the caller runs its own path
+ * (the reference's handled = false); < 0 = error, text in mimg_last_error().
+ * No function aborts the process.
+ *
+ * Dtype ids are mim's (reference dtype.go:22-46): F32 = 1, Q8_0 = 64,
+ * Q4_K = 66, Q6_K = 67. Weights are [N, K] row-major in their on-disk block
+ * layout (spec/dtypes.md), uploaded once and never repacked.
+ *
+ * Thread safety: every function may be called from any thread. Host-memory
+ * entry points run on a stream owned by the calling thread and return when
+ * the result is in host memory. Device-memory entry points (suffix _dev)
+ * enqueue on the caller's stream and return at once; device pointers must
+ * stay valid until that stream reaches the work.
+ */
+#ifndef MIMG_H
+#define MIMG_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MIMG_OK 0
+#define MIMG_NOT_HANDLED 1
+#define MIMG_ERR_ARG (-1)
+#define MIMG_ERR_HIP (-2)
+#define MIMG_ERR_NOT_INIT (-3)
+#define MIMG_ERR_HANDLE (-4)
+#define MIMG_ERR_DEVICE (-5)
+#define MIMG_ERR_WORKSPACE (-6)
+
+#define MIMG_DT_F32 1u
+#define MIMG_DT_Q8_0 64u
+#define MIMG_DT_Q4_K 66u
+#define MIMG_DT_Q6_K 67u
+
+/* Selects the GPU and checks that it is gfx950. Idempotent for one device.
+ * No reference counterpart: the reference runs on the CPU; a Program's
+ * lifetime (interp.Load, interp/interp.go:101-122) brackets init/shutdown. */
+int mimg_init(int device);
+
+/* Frees every registered weight and the per-thread buffers. */
+void mimg_shutdown(void);
+
+/* Text of the last error of the calling thread ("" if none). */
+const char *mimg_last_error(void);
+
+/* Library version, (major << 16) | minor. */
+int mimg_version(void);
+
+/* Uploads a weight matrix once, byte for byte, and returns its handle.
+ * Replaces the zero-copy ref.Tensor{Data: f.TensorData(t)} the fast paths
+ * read (interp/interp.go:101-122 -> file.go:394-398): the same (host, len,
+ * dtype, n, k) returns the same handle without a second upload, so a Go
+ * caller may pass W.Data of every call (its mmap slice is stable for the
+ * Program's life). len must equal n * (k / block_elems) * block_bytes. */
+int mimg_register_weight(const void *host, uint64_t len, uint32_t dtype, int64_t n, int64_t k,
+                         uint64_t *handle);
+
+/* As mimg_register_weight for bytes already in device memory (copied into a
+ * buffer of the library; no host key). No reference counterpart: for callers
+ * that keep the file's weights resident on the GPU. */
+int mimg_register_weight_device(const void *dev, uint64_t len, uint32_t dtype, int64_t n, int64_t k,
+                                uint64_t *handle);
+
+/* Frees a weight's device buffer. */
+int mimg_release_weight(uint64_t handle);
+
+/* Device address of a weight's bytes and the number of its rows that the
+ * 8-bit kernels refuse (a block scale that is not finite). */
+int mimg_weight_info(uint64_t handle, const void **dev_ptr, int64_t *n_refused);
+
+/* ---- host-memory entry points: one fast-path call each ------------------ */
+
+/* dequant_matmul_a8.v1 (block = 32) and dequant_matmul_a8.v2 (block = 32 or
+ * 256): y[rows, N] = x[rows, K] . W^T + bias with x quantized to 8-bit
+ * blocks (reference fastDequantMatmulA8/fastDequantMatmulA8V2 ->
+ * dequantMatmulA8 -> linearA8, interp/fast.go:226-379; attribute check
+ * a8Block, interp/transformer.go:201-214). A dtype without an 8-bit kernel
+ * for `block` runs the float32 path, as the reference does (fast.go:256-259).
+ * Rows of x with a NaN or |x| > 2^60, and rows of W with a non-finite block
+ * scale, use the float32 path (fast.go:323-377). bias may be NULL. Returns
+ * MIMG_ERR_ARG for block not in {32, 256} (the reference's error). */
+int mimg_dequant_matmul_a8(uint64_t w, const float *x, int64_t rows, const float *bias, int block,
+                           float *y);
+
+/* dequant_matmul.v1: float32 activations (reference fastDequantMatmul ->
+ * linearFast -> linearF32, interp/fast.go:161-224). */
+int mimg_dequant_matmul(uint64_t w, const float *x, int64_t rows, const float *bias, float *y);
+
+/* mim.Dequantize for Q8_0, Q4_K and Q6_K, bit for bit (reference
+ * quant.go:37-73): src holds len bytes, dst n floats. Errors as the
+ * reference: size mismatch -> MIMG_ERR_ARG, other dtypes -> MIMG_NOT_HANDLED. */
+int mimg_dequantize(uint32_t dtype, const void *src, uint64_t len, float *dst, int64_t n);
+
+/* ---- device-memory entry points (async on `stream`, a hipStream_t) ------ */
+
+/* Bytes of the workspace the 8-bit entry points need for rows x K. */
+uint64_t mimg_a8_workspace_bytes(int64_t rows, int64_t k);
+
+/* Byte offsets, inside that workspace, of the quantized activations:
+ * off[0] q int8[rows][K], off[1] d float[rows][K/32], off[2] xs
+ * int16[rows][K/32], off[3] ys16 int16[rows][K/16], off[4] dbs
+ * float[rows][K/32], off[5] ok int32[rows]. (Reference Q8Batch layout,
+ * internal/kernels/q8.go:154-193, with per-16 sums added.) */
+int mimg_a8_workspace_offsets(int64_t rows, int64_t k, uint64_t off[6]);
+
+/* Q8.QuantizeBlocks for each row of x (reference internal/kernels/q8.go:50-97)
+ * into the workspace. x must be 16-byte aligned. */
+int mimg_quantize_act_dev(const float *x, int64_t rows, int64_t k, int block, void *ws,
+                          uint64_t ws_bytes, void *stream);
+
+/* mimg_dequant_matmul_a8 on device buffers: quantizes x into ws, then runs
+ * the product. y is [rows, N] row-major. */
+int mimg_linear_a8_dev(uint64_t w, const float *x, int64_t rows, const float *bias, int block, float *y,
+                       void *ws, uint64_t ws_bytes, void *stream);
+
+/* The product alone, for activations already quantized into ws by
+ * mimg_quantize_act_dev with the same rows, K and block. */
+int mimg_matmul_a8_quantized_dev(uint64_t w, const float *x, int64_t rows, const float *bias, int block,
+                                 float *y, const void *ws, uint64_t ws_bytes, void *stream);
+
+/* mimg_dequant_matmul on device buffers. */
+int mimg_linear_f32_dev(uint64_t w, const float *x, int64_t rows, const float *bias, float *y,
+                        void *stream);
+
+/* mimg_dequantize on device buffers. */
+int mimg_dequantize_dev(uint32_t dtype, const void *src, uint64_t len, float *dst, int64_t n,
+                        void *stream);
+
+/* Encodes n float32 values into blocks of dtype on the GPU (dst_len bytes).
+ * Q8_0 is the reference's encoder (mim.Quantize, quant.go:165-228). The
+ * reference has no Q4_K/Q6_K encoder (quant.go:165-194 returns
+ * CodeUnsupportedDType); encoders are not normative (spec/dtypes.md:44-45),
+ * and these two are this library's own, for synthetic weights. */
+int mimg_quantize_dev(uint32_t dtype, const float *src, int64_t n, void *dst, uint64_t dst_len,
+                      void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

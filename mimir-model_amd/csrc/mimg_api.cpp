@@ -1,0 +1,518 @@
+// C ABI of libmimg (include/mimg.h): weight registry, per-thread streams and
+// buffers, argument checks in the reference's terms, and dispatch to the
+// gfx950 kernels. No CPU compute path: every product runs on the GPU.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/mimg.h"
+#include "mimg_device.hpp"
+#include "mimg_kernels.hpp"
+
+using namespace mimg;
+
+namespace {
+
+thread_local std::string t_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_err = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                    \
+    do {                                                                                 \
+        hipError_t e_ = (expr);                                                          \
+        if (e_ != hipSuccess)                                                            \
+            return fail(MIMG_ERR_HIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_),     \
+                        __FILE__, __LINE__);                                             \
+    } while (0)
+
+struct Weight {
+    DevWeight dw;
+    uint8_t* data = nullptr;
+    uint8_t* wref = nullptr;
+    uint64_t len = 0;
+    bool has_key = false;
+    std::tuple<uintptr_t, uint64_t, uint32_t, int64_t, int64_t> key;
+};
+
+std::mutex g_mu;
+int g_device = -1;
+uint64_t g_next = 1;
+std::unordered_map<uint64_t, Weight*> g_weights;
+std::map<std::tuple<uintptr_t, uint64_t, uint32_t, int64_t, int64_t>, uint64_t> g_keys;
+
+// Per-thread stream and grow-only device buffers of the host-memory entry
+// points.
+struct ThreadCtx {
+    hipStream_t stream = nullptr;
+    void* buf[4] = {nullptr, nullptr, nullptr, nullptr};
+    size_t cap[4] = {0, 0, 0, 0};
+    ~ThreadCtx() {
+        for (int i = 0; i < 4; i++)
+            if (buf[i]) (void)hipFree(buf[i]);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+thread_local ThreadCtx t_ctx;
+
+int64_t block_elems(uint32_t dt) {
+    switch (dt) {
+    case DT_Q8_0: return 32;
+    case DT_Q4_K:
+    case DT_Q6_K: return 256;
+    }
+    return -1;
+}
+int64_t block_bytes(uint32_t dt) {
+    switch (dt) {
+    case DT_Q8_0: return Q80_BYTES;
+    case DT_Q4_K: return Q4K_BYTES;
+    case DT_Q6_K: return Q6K_BYTES;
+    }
+    return -1;
+}
+
+const char* dt_name(uint32_t dt) {
+    switch (dt) {
+    case DT_Q8_0: return "q8_0";
+    case DT_Q4_K: return "q4_k";
+    case DT_Q6_K: return "q6_k";
+    case DT_F32: return "f32";
+    }
+    return "?";
+}
+
+int ensure_device() {
+    if (g_device < 0) return fail(MIMG_ERR_NOT_INIT, "mimg_init has not been called");
+    HIP_TRY(hipSetDevice(g_device));
+    return MIMG_OK;
+}
+
+int ensure_thread_stream() {
+    if (!t_ctx.stream) HIP_TRY(hipStreamCreateWithFlags(&t_ctx.stream, hipStreamNonBlocking));
+    return MIMG_OK;
+}
+
+int thread_buf(int i, size_t bytes, void** out) {
+    if (bytes == 0) bytes = 256;
+    if (t_ctx.cap[i] < bytes) {
+        if (t_ctx.buf[i]) HIP_TRY(hipFree(t_ctx.buf[i]));
+        t_ctx.buf[i] = nullptr;
+        t_ctx.cap[i] = 0;
+        HIP_TRY(hipMalloc(&t_ctx.buf[i], bytes));
+        t_ctx.cap[i] = bytes;
+    }
+    *out = t_ctx.buf[i];
+    return MIMG_OK;
+}
+
+int lookup(uint64_t h, Weight** out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_weights.find(h);
+    if (it == g_weights.end()) return fail(MIMG_ERR_HANDLE, "unknown weight handle %llu", (unsigned long long)h);
+    *out = it->second;
+    return MIMG_OK;
+}
+
+int check_shape(uint32_t dtype, uint64_t len, int64_t n, int64_t k) {
+    int64_t be = block_elems(dtype);
+    if (be < 0) return fail(MIMG_NOT_HANDLED, "dtype %u has no kernel", dtype);
+    if (n <= 0 || k <= 0) return fail(MIMG_ERR_ARG, "weight shape [%lld, %lld]", (long long)n, (long long)k);
+    if (k % be)
+        return fail(MIMG_ERR_ARG, "%s: K = %lld is not a multiple of the block size %lld", dt_name(dtype),
+                    (long long)k, (long long)be);
+    uint64_t want = (uint64_t)n * (uint64_t)(k / be) * (uint64_t)block_bytes(dtype);
+    if (len != want)
+        return fail(MIMG_ERR_ARG, "%s [%lld, %lld] needs %llu bytes, got %llu", dt_name(dtype), (long long)n,
+                    (long long)k, (unsigned long long)want, (unsigned long long)len);
+    return MIMG_OK;
+}
+
+int register_impl(const void* src, uint64_t len, uint32_t dtype, int64_t n, int64_t k, bool from_host,
+                  uint64_t* handle) {
+    if (!handle || !src) return fail(MIMG_ERR_ARG, "null pointer");
+    int rc = check_shape(dtype, len, n, k);
+    if (rc) return rc;
+    if ((rc = ensure_device())) return rc;
+    auto key = std::make_tuple((uintptr_t)src, len, dtype, n, k);
+    if (from_host) {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_keys.find(key);
+        if (it != g_keys.end()) {
+            *handle = it->second;
+            return MIMG_OK;
+        }
+    }
+    Weight* w = new Weight();
+    hipError_t e = hipMalloc((void**)&w->data, len + WEIGHT_PAD);
+    if (e == hipSuccess) e = hipMalloc((void**)&w->wref, (size_t)n);
+    if (e == hipSuccess) e = hipMemset(w->data + len, 0, WEIGHT_PAD);
+    if (e == hipSuccess)
+        e = hipMemcpy(w->data, src, len, from_host ? hipMemcpyHostToDevice : hipMemcpyDeviceToDevice);
+    if (e == hipSuccess) e = launch_weight_refusals(dtype, w->data, n, k, w->wref, nullptr);
+    std::vector<uint8_t> flags;
+    if (e == hipSuccess) {
+        flags.resize((size_t)n);
+        e = hipMemcpy(flags.data(), w->wref, (size_t)n, hipMemcpyDeviceToHost);
+    }
+    if (e != hipSuccess) {
+        if (w->data) (void)hipFree(w->data);
+        if (w->wref) (void)hipFree(w->wref);
+        delete w;
+        return fail(MIMG_ERR_HIP, "weight upload: %s", hipGetErrorString(e));
+    }
+    int64_t refused = 0;
+    for (uint8_t f : flags) refused += f;
+    w->len = len;
+    w->dw.dt = dtype;
+    w->dw.n = n;
+    w->dw.k = k;
+    w->dw.row_bytes = k / block_elems(dtype) * block_bytes(dtype);
+    w->dw.data = w->data;
+    w->dw.wref = w->wref;
+    w->dw.n_refused = refused;
+    w->has_key = from_host;
+    w->key = key;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (from_host) {
+        auto it = g_keys.find(key);
+        if (it != g_keys.end()) {  // another thread registered it meanwhile
+            (void)hipFree(w->data);
+            (void)hipFree(w->wref);
+            delete w;
+            *handle = it->second;
+            return MIMG_OK;
+        }
+        g_keys[key] = g_next;
+    }
+    g_weights[g_next] = w;
+    *handle = g_next++;
+    return MIMG_OK;
+}
+
+bool fused_q8_blocks(uint32_t dt, int block) {
+    // FusedQ8Blocks (reference internal/kernels/q8.go:105-117) on a machine
+    // with every kernel: blocks of 32 for Q4_K/Q6_K/Q8_0, 256 for Q4_K/Q6_K.
+    if (block == 32) return dt == DT_Q4_K || dt == DT_Q6_K || dt == DT_Q8_0;
+    if (block == 256) return dt == DT_Q4_K || dt == DT_Q6_K;
+    return false;
+}
+
+// Everything after quantization: the product of the quantized rows.
+int matmul_quantized(const Weight* w, const float* x, int64_t rows, const float* bias, int block, float* y,
+                     const ActPtrs& a, hipStream_t s) {
+    const int64_t K = w->dw.k, N = w->dw.n, R32 = K / 32, R16 = K / 16;
+    for (int64_t r0 = 0; r0 < rows; r0 += 8) {
+        const int64_t mr = rows - r0 < 8 ? rows - r0 : 8;
+        ActPtrs c;
+        c.q = a.q + r0 * K;
+        c.d32 = a.d32 + r0 * R32;
+        c.xs = a.xs + r0 * R32;
+        c.ys16 = a.ys16 + r0 * R16;
+        c.dbs = a.dbs + r0 * R32;
+        c.ok = a.ok + r0;
+        hipError_t e;
+        if (block == 256)
+            e = launch_gemv_a8k(w->dw, c, mr, rows, x + r0 * K, bias, y + r0 * N, N, s);
+        else
+            e = launch_gemv_q8_0_a8(w->dw, c, mr, rows, x + r0 * K, bias, y + r0 * N, N, s);
+        if (e != hipSuccess) return fail(MIMG_ERR_HIP, "product launch: %s", hipGetErrorString(e));
+    }
+    return MIMG_OK;
+}
+
+// Argument checks shared by the 8-bit entry points. Returns > 0 with
+// *use_f32 set when the dtype has no 8-bit kernel for `block`.
+int a8_checks(const Weight* w, int64_t rows, int block, bool* use_f32) {
+    *use_f32 = false;
+    if (block != 32 && block != 256)
+        return fail(MIMG_ERR_ARG, "dequant_matmul_a8: block must be 32 or 256, got %d", block);
+    if (rows < 0) return fail(MIMG_ERR_ARG, "rows = %lld", (long long)rows);
+    if (!fused_q8_blocks(w->dw.dt, block)) {
+        *use_f32 = true;
+        return MIMG_OK;
+    }
+    if (block == 32 && w->dw.dt != DT_Q8_0)
+        return fail(MIMG_NOT_HANDLED, "%s with activation blocks of 32 has no GPU kernel yet", dt_name(w->dw.dt));
+    return MIMG_OK;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int mimg_version(void) { return (0 << 16) | 1; }
+
+const char* mimg_last_error(void) { return t_err.c_str(); }
+
+int mimg_init(int device) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int count = 0;
+    HIP_TRY(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count) return fail(MIMG_ERR_DEVICE, "device %d of %d", device, count);
+    if (g_device >= 0 && g_device != device)
+        return fail(MIMG_ERR_DEVICE, "already initialised on device %d", g_device);
+    hipDeviceProp_t prop;
+    HIP_TRY(hipGetDeviceProperties(&prop, device));
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(MIMG_ERR_DEVICE, "device %d is %s; libmimg is built for gfx950", device, prop.gcnArchName);
+    HIP_TRY(hipSetDevice(device));
+    g_device = device;
+    return MIMG_OK;
+}
+
+void mimg_shutdown(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_device >= 0) (void)hipSetDevice(g_device);
+    for (auto& kv : g_weights) {
+        (void)hipFree(kv.second->data);
+        (void)hipFree(kv.second->wref);
+        delete kv.second;
+    }
+    g_weights.clear();
+    g_keys.clear();
+}
+
+int mimg_register_weight(const void* host, uint64_t len, uint32_t dtype, int64_t n, int64_t k, uint64_t* handle) {
+    return register_impl(host, len, dtype, n, k, true, handle);
+}
+
+int mimg_register_weight_device(const void* dev, uint64_t len, uint32_t dtype, int64_t n, int64_t k,
+                                uint64_t* handle) {
+    return register_impl(dev, len, dtype, n, k, false, handle);
+}
+
+int mimg_release_weight(uint64_t handle) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_weights.find(handle);
+    if (it == g_weights.end()) return fail(MIMG_ERR_HANDLE, "unknown weight handle %llu", (unsigned long long)handle);
+    Weight* w = it->second;
+    if (w->has_key) g_keys.erase(w->key);
+    g_weights.erase(it);
+    HIP_TRY(hipDeviceSynchronize());
+    (void)hipFree(w->data);
+    (void)hipFree(w->wref);
+    delete w;
+    return MIMG_OK;
+}
+
+int mimg_weight_info(uint64_t handle, const void** dev_ptr, int64_t* n_refused) {
+    Weight* w;
+    int rc = lookup(handle, &w);
+    if (rc) return rc;
+    if (dev_ptr) *dev_ptr = w->data;
+    if (n_refused) *n_refused = w->dw.n_refused;
+    return MIMG_OK;
+}
+
+uint64_t mimg_a8_workspace_bytes(int64_t rows, int64_t k) {
+    if (rows < 0 || k <= 0) return 0;
+    return act_layout(rows, k).total;
+}
+
+int mimg_a8_workspace_offsets(int64_t rows, int64_t k, uint64_t off[6]) {
+    if (rows < 0 || k <= 0 || !off) return fail(MIMG_ERR_ARG, "bad workspace shape");
+    ActLayout l = act_layout(rows, k);
+    off[0] = l.q;
+    off[1] = l.d32;
+    off[2] = l.xs;
+    off[3] = l.ys16;
+    off[4] = l.dbs;
+    off[5] = l.ok;
+    return MIMG_OK;
+}
+
+int mimg_quantize_act_dev(const float* x, int64_t rows, int64_t k, int block, void* ws, uint64_t ws_bytes,
+                          void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (block != 32 && block != 256) return fail(MIMG_ERR_ARG, "block must be 32 or 256, got %d", block);
+    if (rows < 0 || k <= 0 || k % block) return fail(MIMG_ERR_ARG, "K = %lld with blocks of %d", (long long)k, block);
+    if (rows == 0) return MIMG_OK;
+    if (!x || !ws || !aligned(x, 16) || !aligned(ws, 256)) return fail(MIMG_ERR_ARG, "x must be 16-byte and ws 256-byte aligned");
+    ActLayout l = act_layout(rows, k);
+    if (ws_bytes < l.total) return fail(MIMG_ERR_WORKSPACE, "workspace %llu < %llu bytes", (unsigned long long)ws_bytes, (unsigned long long)l.total);
+    HIP_TRY(launch_quantize_act(x, rows, k, block, act_ptrs(ws, l), (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_linear_f32_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, float* y, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    Weight* w;
+    if ((rc = lookup(wh, &w))) return rc;
+    if (rows < 0) return fail(MIMG_ERR_ARG, "rows = %lld", (long long)rows);
+    if (rows == 0) return MIMG_OK;
+    if (!x || !y) return fail(MIMG_ERR_ARG, "null pointer");
+    HIP_TRY(launch_linear_f32(w->dw, x, rows, bias, y, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_matmul_a8_quantized_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, int block, float* y,
+                                 const void* ws, uint64_t ws_bytes, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    Weight* w;
+    if ((rc = lookup(wh, &w))) return rc;
+    bool use_f32;
+    if ((rc = a8_checks(w, rows, block, &use_f32))) return rc;
+    if (use_f32) return fail(MIMG_ERR_ARG, "%s has no 8-bit kernel for blocks of %d", dt_name(w->dw.dt), block);
+    if (rows == 0) return MIMG_OK;
+    if (!x || !y || !ws || !aligned(ws, 256)) return fail(MIMG_ERR_ARG, "null or misaligned pointer");
+    ActLayout l = act_layout(rows, w->dw.k);
+    if (ws_bytes < l.total) return fail(MIMG_ERR_WORKSPACE, "workspace %llu < %llu bytes", (unsigned long long)ws_bytes, (unsigned long long)l.total);
+    return matmul_quantized(w, x, rows, bias, block, y, act_ptrs((void*)ws, l), (hipStream_t)stream);
+}
+
+int mimg_linear_a8_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, int block, float* y, void* ws,
+                       uint64_t ws_bytes, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    Weight* w;
+    if ((rc = lookup(wh, &w))) return rc;
+    bool use_f32;
+    if ((rc = a8_checks(w, rows, block, &use_f32))) return rc;
+    if (use_f32) return mimg_linear_f32_dev(wh, x, rows, bias, y, stream);
+    if (rows == 0) return MIMG_OK;
+    if ((rc = mimg_quantize_act_dev(x, rows, w->dw.k, block, ws, ws_bytes, stream))) return rc;
+    return mimg_matmul_a8_quantized_dev(wh, x, rows, bias, block, y, ws, ws_bytes, stream);
+}
+
+int mimg_dequantize_dev(uint32_t dtype, const void* src, uint64_t len, float* dst, int64_t n, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    int64_t be = block_elems(dtype);
+    if (be < 0) return fail(MIMG_NOT_HANDLED, "cannot decode dtype %u on the GPU", dtype);
+    if (n < 0 || n % be) return fail(MIMG_ERR_ARG, "%s: %lld elements is not a multiple of the block size %lld", dt_name(dtype), (long long)n, (long long)be);
+    if ((uint64_t)(n / be * block_bytes(dtype)) != len)
+        return fail(MIMG_ERR_ARG, "%s: %lld elements need %lld bytes, got %llu", dt_name(dtype), (long long)n,
+                    (long long)(n / be * block_bytes(dtype)), (unsigned long long)len);
+    if (n == 0) return MIMG_OK;
+    HIP_TRY(launch_dequantize(dtype, (const uint8_t*)src, n, dst, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_quantize_dev(uint32_t dtype, const float* src, int64_t n, void* dst, uint64_t dst_len, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    int64_t be = block_elems(dtype);
+    if (be < 0) return fail(MIMG_NOT_HANDLED, "cannot encode dtype %u", dtype);
+    if (n < 0 || n % be) return fail(MIMG_ERR_ARG, "%s: %lld elements is not a multiple of the block size %lld", dt_name(dtype), (long long)n, (long long)be);
+    if ((uint64_t)(n / be * block_bytes(dtype)) != dst_len)
+        return fail(MIMG_ERR_ARG, "%s: %lld elements need %lld bytes, got %llu", dt_name(dtype), (long long)n,
+                    (long long)(n / be * block_bytes(dtype)), (unsigned long long)dst_len);
+    if (n == 0) return MIMG_OK;
+    HIP_TRY(launch_encode(dtype, src, n, (uint8_t*)dst, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_dequantize(uint32_t dtype, const void* src, uint64_t len, float* dst, int64_t n) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    int64_t be = block_elems(dtype);
+    if (be < 0) return fail(MIMG_NOT_HANDLED, "cannot decode dtype %u on the GPU", dtype);
+    if (n < 0 || n % be || (uint64_t)(n / be * block_bytes(dtype)) != len)
+        return fail(MIMG_ERR_ARG, "%s: %lld elements and %llu bytes do not match", dt_name(dtype), (long long)n, (unsigned long long)len);
+    if (n == 0) return MIMG_OK;
+    if ((rc = ensure_thread_stream())) return rc;
+    void *s_d, *d_d;
+    if ((rc = thread_buf(0, len + WEIGHT_PAD, &s_d))) return rc;
+    if ((rc = thread_buf(1, (size_t)n * 4, &d_d))) return rc;
+    hipStream_t s = t_ctx.stream;
+    HIP_TRY(hipMemcpyAsync(s_d, src, len, hipMemcpyHostToDevice, s));
+    HIP_TRY(launch_dequantize(dtype, (const uint8_t*)s_d, n, (float*)d_d, s));
+    HIP_TRY(hipMemcpyAsync(dst, d_d, (size_t)n * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return MIMG_OK;
+}
+
+static int host_call(uint64_t wh, const float* x, int64_t rows, const float* bias, int block, float* y, bool a8) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    Weight* w;
+    if ((rc = lookup(wh, &w))) return rc;
+    if (rows < 0) return fail(MIMG_ERR_ARG, "rows = %lld", (long long)rows);
+    bool use_f32 = !a8;
+    if (a8 && (rc = a8_checks(w, rows, block, &use_f32))) return rc;
+    if (rows == 0) return MIMG_OK;
+    if (!x || !y) return fail(MIMG_ERR_ARG, "null pointer");
+    if ((rc = ensure_thread_stream())) return rc;
+    const int64_t K = w->dw.k, N = w->dw.n;
+    void *x_d, *y_d, *b_d = nullptr, *ws = nullptr;
+    if ((rc = thread_buf(0, (size_t)(rows * K * 4), &x_d))) return rc;
+    if ((rc = thread_buf(1, (size_t)(rows * N * 4), &y_d))) return rc;
+    if (bias && (rc = thread_buf(2, (size_t)N * 4, &b_d))) return rc;
+    uint64_t wsb = act_layout(rows, K).total;
+    if (!use_f32 && (rc = thread_buf(3, wsb, &ws))) return rc;
+    hipStream_t s = t_ctx.stream;
+    HIP_TRY(hipMemcpyAsync(x_d, x, (size_t)(rows * K * 4), hipMemcpyHostToDevice, s));
+    if (bias) HIP_TRY(hipMemcpyAsync(b_d, bias, (size_t)N * 4, hipMemcpyHostToDevice, s));
+    if (use_f32)
+        rc = mimg_linear_f32_dev(wh, (const float*)x_d, rows, (const float*)b_d, (float*)y_d, s);
+    else
+        rc = mimg_linear_a8_dev(wh, (const float*)x_d, rows, (const float*)b_d, block, (float*)y_d, ws, wsb, s);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(y, y_d, (size_t)(rows * N * 4), hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return MIMG_OK;
+}
+
+int mimg_dequant_matmul_a8(uint64_t w, const float* x, int64_t rows, const float* bias, int block, float* y) {
+    return host_call(w, x, rows, bias, block, y, true);
+}
+
+int mimg_dequant_matmul(uint64_t w, const float* x, int64_t rows, const float* bias, float* y) {
+    return host_call(w, x, rows, bias, 0, y, false);
+}
+
+}  // extern "C"
+
+namespace mimg {
+
+static size_t up256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+ActLayout act_layout(int64_t rows, int64_t K) {
+    ActLayout l;
+    size_t r = (size_t)rows, k = (size_t)K;
+    l.q = 0;
+    l.d32 = up256(l.q + r * k);
+    l.xs = up256(l.d32 + r * (k / 32) * 4);
+    l.ys16 = up256(l.xs + r * (k / 32) * 2);
+    l.dbs = up256(l.ys16 + r * (k / 16) * 2);
+    l.ok = up256(l.dbs + r * (k / 32) * 4);
+    l.total = up256(l.ok + r * 4);
+    return l;
+}
+
+ActPtrs act_ptrs(void* base, const ActLayout& l) {
+    uint8_t* b = (uint8_t*)base;
+    ActPtrs a;
+    a.q = (int8_t*)(b + l.q);
+    a.d32 = (float*)(b + l.d32);
+    a.xs = (int16_t*)(b + l.xs);
+    a.ys16 = (int16_t*)(b + l.ys16);
+    a.dbs = (float*)(b + l.dbs);
+    a.ok = (int32_t*)(b + l.ok);
+    return a;
+}
+
+}  // namespace mimg

@@ -1,0 +1,64 @@
+// Kernel launchers of libmimg (host-side declarations shared by the .hip
+// files and the C-ABI in mimg_api.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace mimg {
+
+// Quantized activations of `rows` rows of K elements, in device memory
+// (reference Q8Batch, internal/kernels/q8.go:154-193, with the per-16 sums
+// added): q int8 [rows][K]; d32, dbs float [rows][K/32]; xs int16
+// [rows][K/32]; ys16 int16 [rows][K/16]; ok int32 [rows].
+struct ActPtrs {
+    int8_t* q;
+    float* d32;
+    int16_t* xs;
+    int16_t* ys16;
+    float* dbs;
+    int32_t* ok;
+};
+
+// Byte offsets of the ActPtrs arrays in one workspace, each 256-aligned.
+struct ActLayout {
+    size_t q, d32, xs, ys16, dbs, ok, total;
+};
+ActLayout act_layout(int64_t rows, int64_t K);
+ActPtrs act_ptrs(void* base, const ActLayout& l);
+
+// A registered weight matrix on the device (bytes exactly as in the file).
+struct DevWeight {
+    uint32_t dt;
+    int64_t n, k, row_bytes;
+    const uint8_t* data;   // n*row_bytes bytes + WEIGHT_PAD
+    const uint8_t* wref;   // n flags: 1 if a block scale of the row is not finite
+    int64_t n_refused;
+};
+
+hipError_t launch_quantize_act(const float* x, int64_t rows, int64_t K, int block, const ActPtrs& a,
+                               hipStream_t stream);
+
+hipError_t launch_weight_refusals(uint32_t dt, const uint8_t* w, int64_t n, int64_t k, uint8_t* wref,
+                                  hipStream_t stream);
+
+// y[i*N+j] for act rows [0, rows) (rows <= 8 per launch, `total_rows` is the
+// row count of the whole call, which selects the float32 fallback's order).
+hipError_t launch_gemv_a8k(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows,
+                           const float* x, const float* bias, float* y, int64_t y_stride,
+                           hipStream_t stream);
+
+hipError_t launch_gemv_q8_0_a8(const DevWeight& w, const ActPtrs& a, int64_t rows,
+                               int64_t total_rows, const float* x, const float* bias, float* y,
+                               int64_t y_stride, hipStream_t stream);
+
+hipError_t launch_linear_f32(const DevWeight& w, const float* x, int64_t rows, const float* bias,
+                             float* y, hipStream_t stream);
+
+hipError_t launch_dequantize(uint32_t dt, const uint8_t* src, int64_t n_elems, float* dst,
+                             hipStream_t stream);
+
+hipError_t launch_encode(uint32_t dt, const float* x, int64_t n, uint8_t* dst, hipStream_t stream);
+
+}  // namespace mimg

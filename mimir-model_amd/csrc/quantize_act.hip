@@ -1,0 +1,95 @@
+// Activation quantizer: rows of f32 activations to 8-bit blocks of 32 or 256
+// (reference Q8.QuantizeBlocks, internal/kernels/q8.go:50-97, with
+// amaxQ8Go/quantQ8Go/sumsQ8Go at q8.go:237-273).
+//
+// Per block: amax = max|x|; the row is refused (ok = 0) if any |x| is NaN or
+// above 2^60; q = RoundToEven(127*f64(x)/f64(amax)) (0 when amax == 0), in
+// float64 with a correctly rounded division, so q is the exact quotient
+// rounded to nearest even; d = f32(amax)/127 (correctly rounded f32
+// division), stored for each run of 32; xs = sum of each run of 32;
+// ys16 = sum of each run of 16 (used by the Q6_K kernels for the bias of
+// 32); dbs = d*f32(xs).
+//
+// One workgroup per row; each wave takes one block of 256 elements at a time
+// (or eight blocks of 32), four elements per lane, float4 loads.
+#include "mimg_device.hpp"
+#include "mimg_kernels.hpp"
+
+namespace mimg {
+
+template <int BLOCK>
+__global__ __launch_bounds__(256) void quantize_act_kernel(const float* __restrict__ x, int64_t K,
+                                                           ActPtrs a) {
+    const int row = blockIdx.x;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const float* xr = x + (int64_t)row * K;
+    const int64_t R32 = K / 32;
+    bool bad = false;
+    for (int64_t c = wave; c * 256 < K; c += 4) {
+        const int64_t e0 = c * 256 + 4 * lane;
+        // blocks of 32: K is a multiple of 32, so each group of eight lanes
+        // is wholly inside or outside the row (the DPP steps stay in-group)
+        if (BLOCK == 32 && e0 >= K) continue;
+        float4 v = *(const float4*)(xr + e0);
+        float av[4] = {fabsf(v.x), fabsf(v.y), fabsf(v.z), fabsf(v.w)};
+        bool lbad = false;
+        float m = 0.f;
+        for (int i = 0; i < 4; i++) {
+            lbad |= !(av[i] <= 0x1p60f);
+            m = fmaxf(m, av[i]);
+        }
+        float amax;
+        bool bbad;
+        if (BLOCK == 256) {
+            // max over the wave; fmaxf of non-negative finite values is exact
+            for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+            amax = m;
+            bbad = __any(lbad);
+        } else {
+            amax = group8_max(m);  // eight lanes hold one block of 32
+            bbad = lbad;
+        }
+        bad |= bbad;
+        const float xv[4] = {v.x, v.y, v.z, v.w};
+        int qv[4];
+        for (int i = 0; i < 4; i++) {
+            if (lbad || amax == 0.f) {
+                qv[i] = 0;
+            } else {
+                double t = (127.0 * (double)xv[i]) / (double)amax;
+                qv[i] = (int)__builtin_rint(t);
+            }
+        }
+        uint32_t packed = (uint32_t)(qv[0] & 0xFF) | ((uint32_t)(qv[1] & 0xFF) << 8) |
+                          ((uint32_t)(qv[2] & 0xFF) << 16) | ((uint32_t)(qv[3] & 0xFF) << 24);
+        *(uint32_t*)(a.q + (int64_t)row * K + e0) = packed;
+        int s4 = qv[0] + qv[1] + qv[2] + qv[3];
+        // run of 16 = 4 lanes, run of 32 = 8 lanes
+        int s16 = s4 + __builtin_amdgcn_mov_dpp(s4, DPP_QUAD_1032, 0xF, 0xF, false);
+        s16 += __builtin_amdgcn_mov_dpp(s16, DPP_QUAD_2301, 0xF, 0xF, false);
+        int s32 = s16 + __builtin_amdgcn_mov_dpp(s16, DPP_HALF_MIRROR, 0xF, 0xF, false);
+        const float d = amax / 127.0f;
+        const int64_t run = e0 / 32;
+        if ((lane & 3) == 0) a.ys16[(int64_t)row * (K / 16) + e0 / 16] = (int16_t)s16;
+        if ((lane & 7) == 0) {
+            a.xs[row * R32 + run] = (int16_t)s32;
+            a.d32[row * R32 + run] = d;
+            a.dbs[row * R32 + run] = d * (float)(int16_t)s32;
+        }
+    }
+    int any_bad = __syncthreads_or(bad ? 1 : 0);
+    if (threadIdx.x == 0) a.ok[row] = any_bad ? 0 : 1;
+}
+
+hipError_t launch_quantize_act(const float* x, int64_t rows, int64_t K, int block, const ActPtrs& a,
+                               hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    dim3 grid((unsigned)rows), blk(256);
+    if (block == 256)
+        hipLaunchKernelGGL(quantize_act_kernel<256>, grid, blk, 0, stream, x, K, a);
+    else
+        hipLaunchKernelGGL(quantize_act_kernel<32>, grid, blk, 0, stream, x, K, a);
+    return hipGetLastError();
+}
+
+}  // namespace mimg

@@ -1,0 +1,200 @@
+"""Python view of libmimg's C ABI (include/mimg.h).
+
+The reference's host side is Go: interp's fast paths (interp/fast.go:40-59)
+call the quantized products through `fastFunc`. Go is not in this image, so
+the Go cgo shim (go/mimg_fast.go) is shipped as source and this module plays
+its role for tests and benchmarks: the same calls, argument meaning and
+error behaviour (status > 0 = not handled, < 0 = error).
+
+Every product runs in libmimg.so on the GPU; there is no CPU fallback. If the
+library is missing or the device is not gfx950, calls raise.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmimg.so")
+
+F32, Q8_0, Q4_K, Q6_K = 1, 64, 66, 67
+BLOCK_ELEMS = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q6_K: 210}
+
+OK, NOT_HANDLED = 0, 1
+
+# Every exported symbol of include/mimg.h with (restype, argtypes).
+_P, _I64, _I, _U32, _U64 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint64
+SIGNATURES = {
+    "mimg_init": (_I, [_I]),
+    "mimg_shutdown": (None, []),
+    "mimg_last_error": (ctypes.c_char_p, []),
+    "mimg_version": (_I, []),
+    "mimg_register_weight": (_I, [_P, _U64, _U32, _I64, _I64, ctypes.POINTER(_U64)]),
+    "mimg_register_weight_device": (_I, [_P, _U64, _U32, _I64, _I64, ctypes.POINTER(_U64)]),
+    "mimg_release_weight": (_I, [_U64]),
+    "mimg_weight_info": (_I, [_U64, ctypes.POINTER(_P), ctypes.POINTER(_I64)]),
+    "mimg_dequant_matmul_a8": (_I, [_U64, _P, _I64, _P, _I, _P]),
+    "mimg_dequant_matmul": (_I, [_U64, _P, _I64, _P, _P]),
+    "mimg_dequantize": (_I, [_U32, _P, _U64, _P, _I64]),
+    "mimg_a8_workspace_bytes": (_U64, [_I64, _I64]),
+    "mimg_a8_workspace_offsets": (_I, [_I64, _I64, ctypes.POINTER(_U64)]),
+    "mimg_quantize_act_dev": (_I, [_P, _I64, _I64, _I, _P, _U64, _P]),
+    "mimg_linear_a8_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P, _U64, _P]),
+    "mimg_matmul_a8_quantized_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P, _U64, _P]),
+    "mimg_linear_f32_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
+    "mimg_dequantize_dev": (_I, [_U32, _P, _U64, _P, _I64, _P]),
+    "mimg_quantize_dev": (_I, [_U32, _P, _I64, _P, _U64, _P]),
+}
+
+
+class MimgError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"libmimg error {code}: {msg}")
+        self.code = code
+
+
+class NotHandled(MimgError):
+    pass
+
+
+_lib = None
+
+
+def load(path=LIB_PATH):
+    """Loads libmimg.so (no GPU call)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is not built: run `make -C mimir-model_amd` (or __graft_entry__.build())")
+        L = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _check(rc):
+    if rc != OK:
+        msg = load().mimg_last_error().decode(errors="replace")
+        if rc > 0:
+            raise NotHandled(rc, msg)
+        raise MimgError(rc, msg)
+
+
+_inited = False
+
+
+def init(device=0):
+    global _inited
+    if not _inited:
+        _check(load().mimg_init(device))
+        _inited = True
+
+
+def _p(a):
+    return None if a is None else ctypes.c_void_p(a.ctypes.data)
+
+
+class Weight:
+    """A weight matrix uploaded once, byte for byte, in its block layout."""
+
+    def __init__(self, data, dt, n, k, device=False):
+        init()
+        self.dt, self.n, self.k = dt, n, k
+        h = _U64()
+        if device:
+            # data: (device pointer, nbytes)
+            ptr, nbytes = data
+            _check(load().mimg_register_weight_device(ctypes.c_void_p(ptr), nbytes, dt, n, k, ctypes.byref(h)))
+            self._host = None
+        else:
+            self._host = np.ascontiguousarray(data, dtype=np.uint8)
+            _check(load().mimg_register_weight(_p(self._host), self._host.size, dt, n, k, ctypes.byref(h)))
+        self.handle = h.value
+
+    def info(self):
+        p, nref = _P(), _I64()
+        _check(load().mimg_weight_info(self.handle, ctypes.byref(p), ctypes.byref(nref)))
+        return p.value, nref.value
+
+    def release(self):
+        if self.handle:
+            _check(load().mimg_release_weight(self.handle))
+            self.handle = 0
+
+
+def dequant_matmul_a8(w, x, bias=None, block=256):
+    """dequant_matmul_a8.v1/v2 on host arrays: x [..., K] f32 -> y [..., N]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows = x.size // w.k
+    y = np.empty(x.shape[:-1] + (w.n,), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    _check(load().mimg_dequant_matmul_a8(w.handle, _p(x), rows, _p(b), block, _p(y)))
+    return y
+
+
+def dequant_matmul(w, x, bias=None):
+    """dequant_matmul.v1 on host arrays."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows = x.size // w.k
+    y = np.empty(x.shape[:-1] + (w.n,), np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    _check(load().mimg_dequant_matmul(w.handle, _p(x), rows, _p(b), _p(y)))
+    return y
+
+
+def dequantize(dt, raw, n):
+    init()
+    raw = np.ascontiguousarray(np.frombuffer(bytes(raw), np.uint8) if not isinstance(raw, np.ndarray) else raw, dtype=np.uint8)
+    out = np.empty(n, np.float32)
+    _check(load().mimg_dequantize(dt, _p(raw), raw.size, _p(out), n))
+    return out
+
+
+def a8_workspace_bytes(rows, k):
+    return int(load().mimg_a8_workspace_bytes(rows, k))
+
+
+def a8_workspace_offsets(rows, k):
+    off = (_U64 * 6)()
+    _check(load().mimg_a8_workspace_offsets(rows, k, off))
+    return [int(v) for v in off]
+
+
+# ---- device-pointer calls (pointers and streams as Python ints) ----------
+
+def quantize_act_dev(x_ptr, rows, k, block, ws_ptr, ws_bytes, stream):
+    _check(load().mimg_quantize_act_dev(_P(x_ptr), rows, k, block, _P(ws_ptr), ws_bytes, _P(stream)))
+
+
+def linear_a8_dev(w, x_ptr, rows, bias_ptr, block, y_ptr, ws_ptr, ws_bytes, stream):
+    _check(load().mimg_linear_a8_dev(w.handle, _P(x_ptr), rows, _P(bias_ptr) if bias_ptr else None, block,
+                                     _P(y_ptr), _P(ws_ptr), ws_bytes, _P(stream)))
+
+
+def matmul_a8_quantized_dev(w, x_ptr, rows, bias_ptr, block, y_ptr, ws_ptr, ws_bytes, stream):
+    _check(load().mimg_matmul_a8_quantized_dev(w.handle, _P(x_ptr), rows, _P(bias_ptr) if bias_ptr else None,
+                                               block, _P(y_ptr), _P(ws_ptr), ws_bytes, _P(stream)))
+
+
+def linear_f32_dev(w, x_ptr, rows, bias_ptr, y_ptr, stream):
+    _check(load().mimg_linear_f32_dev(w.handle, _P(x_ptr), rows, _P(bias_ptr) if bias_ptr else None,
+                                      _P(y_ptr), _P(stream)))
+
+
+def dequantize_dev(dt, src_ptr, nbytes, dst_ptr, n, stream):
+    _check(load().mimg_dequantize_dev(dt, _P(src_ptr), nbytes, _P(dst_ptr), n, _P(stream)))
+
+
+def quantize_dev(dt, x_ptr, n, dst_ptr, dst_bytes, stream):
+    """Encodes n f32 values into blocks of dt on the GPU (the reference
+    Quantize for Q8_0, quant.go:165-228; this repository's encoder for
+    Q4_K/Q6_K, which the reference lacks)."""
+    _check(load().mimg_quantize_dev(dt, _P(x_ptr), n, _P(dst_ptr), dst_bytes, _P(stream)))
+
+
+def row_bytes(dt, k):
+    return k // BLOCK_ELEMS[dt] * BLOCK_BYTES[dt]

@@ -1,0 +1,311 @@
+"""Parity of the HIP path (libmimg.so, called through the C ABI) with the CPU
+oracle on the same seeded inputs. The 8-bit block-256 products, the
+activation quantizer and the decoder must be bit-exact; the float32-path
+and block-32 kernels reproduce the reference's AVX2 lane order and are also
+compared bit for bit with the oracle's restatement of it."""
+import base64
+import json
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+Q8_0, Q4_K, Q6_K = 64, 66, 67
+
+
+def bits_equal(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    if a.shape != b.shape:
+        return False
+    same = a.view(np.uint32) == b.view(np.uint32)
+    both_nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all(same | both_nan))
+
+
+def first_diff(a, b):
+    a, b = np.asarray(a, np.float32).ravel(), np.asarray(b, np.float32).ravel()
+    idx = np.nonzero(a.view(np.uint32) != b.view(np.uint32))[0]
+    if idx.size == 0:
+        return "none"
+    i = idx[0]
+    return f"{idx.size} differ; first at {i}: {a[i]!r} vs {b[i]!r}"
+
+
+# ---------------------------------------------------------------- decode
+
+@pytest.mark.parametrize("dt,name", [(Q8_0, "q8_0"), (Q4_K, "q4_k"), (Q6_K, "q6_k")])
+def test_dequantize_golden(gpu, dt, name):
+    v = json.load(open(os.path.join(GOLDEN, "quant_golden.json")))[name]
+    raw = base64.b64decode(v["bytes"])
+    want = np.array(v["bits"], np.uint32)
+    got = gpu.dequantize(dt, raw, want.size)
+    assert np.array_equal(got.view(np.uint32), want)
+
+
+@pytest.mark.parametrize("dt", [Q8_0, Q4_K, Q6_K])
+def test_dequantize_random_bytes(gpu, oracle, dt):
+    """Random block bytes (every scale pattern, including subnormal, inf and
+    NaN f16 scales): GPU decode == oracle decode, bit for bit."""
+    rng = np.random.default_rng(dt)
+    nblk = 4096
+    be, bb = oracle.BLOCK_ELEMS[dt], oracle.BLOCK_BYTES[dt]
+    raw = rng.integers(0, 256, nblk * bb, dtype=np.uint8)
+    got = gpu.dequantize(dt, raw, nblk * be)
+    want = oracle.dequantize(dt, raw, nblk * be)
+    assert bits_equal(got, want), first_diff(got, want)
+
+
+def test_f16_scales_exhaustive(gpu, oracle):
+    """Every f16 bit pattern as a Q8_0 scale with quant 1: d*1 on the GPU
+    equals the oracle's exact conversion (subnormals included)."""
+    h = np.arange(65536, dtype=np.uint16)
+    raw = np.zeros((65536, 34), np.uint8)
+    raw[:, 0] = h & 0xFF
+    raw[:, 1] = h >> 8
+    raw[:, 2] = 1
+    got = gpu.dequantize(Q8_0, raw.ravel(), 65536 * 32).reshape(65536, 32)[:, 0]
+    want = oracle.f16_to_f32(h)
+    assert bits_equal(got, want), first_diff(got, want)
+
+
+# ------------------------------------------------------------- encoders
+
+@pytest.mark.parametrize("dt", [Q8_0, Q4_K, Q6_K])
+def test_encoder_gpu_equals_oracle(gpu, oracle, dt):
+    import hiprt
+
+    rng = np.random.default_rng(21)
+    n = 256 * 512
+    x = rng.standard_normal(n).astype(np.float32) * np.float32(0.02)
+    x[:256] *= 1000  # a block of larger values
+    x[256:512] = 0  # an all-zero block
+    nbytes = n // oracle.BLOCK_ELEMS[dt] * oracle.BLOCK_BYTES[dt]
+    xd = hiprt.DeviceBuffer.from_array(x)
+    out = hiprt.DeviceBuffer(nbytes)
+    s = hiprt.Stream()
+    gpu.quantize_dev(dt, xd.ptr, n, out.ptr, nbytes, s.handle)
+    s.sync()
+    assert np.array_equal(out.download(np.uint8), oracle.quantize(dt, x))
+
+
+# ---------------------------------------------------- activation quantizer
+
+@pytest.mark.parametrize("block", [256, 32])
+def test_quantize_act_bitexact(gpu, oracle, block):
+    import hiprt
+
+    rows, k = 7, 2048
+    rng = np.random.default_rng(block)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    x[1] *= np.float32(1e-30)
+    x[2] *= np.float32(1e15)
+    x[3, :256] = 0
+    x[4, 100] = np.nan
+    x[5, 1000] = np.float32(2.0 ** 61)
+    amax = np.abs(x[6, :block]).max()
+    x[6, 1:5] = np.float32([0.5, 1.5, 2.5, -3.5]) * amax / np.float32(127)
+    ws_bytes = gpu.a8_workspace_bytes(rows, k)
+    off = gpu.a8_workspace_offsets(rows, k)
+    ws = hiprt.DeviceBuffer(ws_bytes)
+    ws.zero()
+    xd = hiprt.DeviceBuffer.from_array(x)
+    s = hiprt.Stream()
+    gpu.quantize_act_dev(xd.ptr, rows, k, block, ws.ptr, ws_bytes, s.handle)
+    s.sync()
+    h = ws.download(np.uint8)
+    q = h[off[0]:off[0] + rows * k].view(np.int8).reshape(rows, k)
+    d = h[off[1]:off[1] + rows * k // 32 * 4].view(np.float32).reshape(rows, -1)
+    xs = h[off[2]:off[2] + rows * k // 32 * 2].view(np.int16).reshape(rows, -1)
+    ys = h[off[3]:off[3] + rows * k // 16 * 2].view(np.int16).reshape(rows, -1)
+    dbs = h[off[4]:off[4] + rows * k // 32 * 4].view(np.float32).reshape(rows, -1)
+    ok = h[off[5]:off[5] + rows * 4].view(np.int32)
+    for i in range(rows):
+        a = oracle.Act(x[i], block)
+        assert bool(ok[i]) == a.ok, i
+        if not a.ok:
+            continue
+        assert np.array_equal(q[i], a.q), i
+        assert bits_equal(d[i], a.d), i
+        assert np.array_equal(xs[i], a.xs), i
+        assert bits_equal(dbs[i], a.dbs), i
+        assert np.array_equal(ys[i], a.q.astype(np.int32).reshape(-1, 16).sum(1)), i
+
+
+# ------------------------------------------- block-256 8-bit products (GEMV)
+
+def _weights(oracle, dt, n, k, seed):
+    return oracle.synthetic_weight(dt, n, k, seed)
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K])
+@pytest.mark.parametrize("n,k", [(1, 256), (33, 2048), (200, 5632), (64, 14336), (4096, 512)])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 8])
+def test_linear_a8k_bitexact(gpu, oracle, dt, n, k, rows):
+    wb = _weights(oracle, dt, n, k, seed=n + k)
+    x = oracle.synthetic_acts(rows, k, seed=rows)
+    W = gpu.Weight(wb, dt, n, k)
+    got = gpu.dequant_matmul_a8(W, x, block=256)
+    want = oracle.linear_a8(x, wb, dt, n, k, block=256, threads=8)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K])
+@pytest.mark.parametrize("rows", [5, 6, 7, 9, 17])
+def test_linear_a8k_row_counts(gpu, oracle, dt, rows):
+    """Odd row counts and more than 8 rows (several launches) give the same
+    bits as the reference, which computes rows independently
+    (TestDequantMatmulA8RowsTogether, interp/transformer_test.go:303-349)."""
+    n, k = 96, 1024
+    wb = _weights(oracle, dt, n, k, seed=3)
+    x = oracle.synthetic_acts(rows, k, seed=rows + 100)
+    W = gpu.Weight(wb, dt, n, k)
+    got = gpu.dequant_matmul_a8(W, x, block=256)
+    want = oracle.linear_a8(x, wb, dt, n, k, block=256, threads=8)
+    assert bits_equal(got, want), first_diff(got, want)
+    one = np.stack([gpu.dequant_matmul_a8(W, x[i:i + 1], block=256)[0] for i in range(rows)])
+    assert bits_equal(got, one)
+    W.release()
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K])
+def test_linear_a8k_special_inputs(gpu, oracle, dt):
+    """The inputs of TestDotQ8KReference (reference q8k_test.go:104-187):
+    tiny and huge activations, a zero block, the largest finite f16 scales
+    with all-ones quants, subnormal f16 scales."""
+    from test_oracle import _special_rows
+
+    k = 5632
+    rng = np.random.default_rng(14)
+    x = rng.standard_normal((5, k)).astype(np.float32)
+    x[1] *= np.float32(1e-30)
+    x[2] *= np.float32(1e15)
+    x[3, :256] = 0
+    rows = [_special_rows(dt, k, t, rng, oracle) for t in range(3)]
+    wb = np.frombuffer(b"".join(rows), np.uint8)
+    W = gpu.Weight(wb, dt, 3, k)
+    got = gpu.dequant_matmul_a8(W, x, block=256)
+    want = oracle.linear_a8(x, wb, dt, 3, k, block=256)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K])
+@pytest.mark.parametrize("rows", [1, 3, 12])
+def test_linear_a8k_refusals_and_bias(gpu, oracle, dt, rows):
+    """Rows of x with NaN/Inf/huge values and rows of w with a non-finite
+    block scale take the float32 path (reference interp/fast.go:323-377);
+    bias is added as s + bias[j]."""
+    n, k = 40, 1024
+    wb = bytearray(_weights(oracle, dt, n, k, seed=8).tobytes())
+    rb = len(wb) // n
+    f = 208 if dt == Q6_K else 2  # Q4_K: dmin
+    for j, blk in ((5, 0), (17, 3)):
+        o = rb * j + blk * (210 if dt == Q6_K else 144) + f
+        wb[o:o + 2] = b"\x00\x7c" if j == 5 else b"\x01\x7e"  # +inf, NaN
+    wb = np.frombuffer(bytes(wb), np.uint8)
+    x = oracle.synthetic_acts(rows, k, seed=9)
+    x[0, 3] = np.nan
+    if rows > 2:
+        x[2, 700] = np.float32(1e30)
+    bias = np.random.default_rng(10).standard_normal(n).astype(np.float32)
+    W = gpu.Weight(wb, dt, n, k)
+    assert W.info()[1] == 2
+    got = gpu.dequant_matmul_a8(W, x, bias=bias, block=256)
+    want = oracle.linear_a8(x, wb, dt, n, k, bias=bias, block=256)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+
+
+def test_linear_a8k_llama_blocks(gpu, oracle):
+    """Weights written by llama.cpp's quantizer (reference testdata/llama)."""
+    z = np.load(os.path.join(GOLDEN, "llama_tensors.npz"))
+    for name in ("blk_0_attn_q_weight", "blk_0_ffn_down_weight", "output_weight", "token_embd_weight"):
+        raw, shape, dt = z[name + "__bytes"], z[name + "__shape"], int(z[name + "__dtype"][0])
+        n, k = int(shape[0]), int(shape[1])
+        x = oracle.synthetic_acts(3, k, seed=11)
+        W = gpu.Weight(raw, dt, n, k)
+        got = gpu.dequant_matmul_a8(W, x, block=256)
+        want = oracle.linear_a8(x, raw, dt, n, k, block=256)
+        W.release()
+        assert bits_equal(got, want), (name, first_diff(got, want))
+
+
+# ----------------------------------------------- Q8_0 x blocks of 32 (a8.v1)
+
+@pytest.mark.parametrize("rows", [1, 4, 8, 11])
+def test_linear_q8_0_a8_bitexact(gpu, oracle, rows):
+    n, k = 150, 4096 + 32
+    wb = _weights(oracle, Q8_0, n, k, seed=12)
+    x = oracle.synthetic_acts(rows, k, seed=13)
+    x[0, 40] = np.inf
+    bias = np.random.default_rng(1).standard_normal(n).astype(np.float32)
+    W = gpu.Weight(wb, Q8_0, n, k)
+    got = gpu.dequant_matmul_a8(W, x, bias=bias, block=32)
+    want = oracle.linear_a8(x, wb, Q8_0, n, k, bias=bias, block=32)
+    # Q8_0 with blocks of 256 has no 8-bit kernel: the float32 path
+    got256 = gpu.dequant_matmul_a8(W, x, block=256)
+    want256 = oracle.linear_a8(x, wb, Q8_0, n, k, block=256)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+    assert bits_equal(got256, want256), first_diff(got256, want256)
+
+
+# ------------------------------------------------- float32-activation path
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K, Q8_0])
+@pytest.mark.parametrize("rows", [1, 8, 9])
+def test_linear_f32_bitexact(gpu, oracle, dt, rows):
+    """dequant_matmul.v1: the fused order for <= 8 rows, decode-then-DotF32
+    for more (reference kernels.go:122-204)."""
+    n, k = 70, 1024
+    wb = _weights(oracle, dt, n, k, seed=14)
+    x = oracle.synthetic_acts(rows, k, seed=15)
+    bias = np.random.default_rng(2).standard_normal(n).astype(np.float32)
+    W = gpu.Weight(wb, dt, n, k)
+    got = gpu.dequant_matmul(W, x, bias=bias)
+    want = oracle.linear_f32(x, wb, dt, n, k, bias=bias)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+
+
+# ------------------------------------------------------------ errors
+
+def test_errors_are_reported_not_fatal(gpu, oracle):
+    wb = _weights(oracle, Q4_K, 4, 256, seed=1)
+    with pytest.raises(gpu.MimgError):
+        gpu.Weight(wb[:-1], Q4_K, 4, 256)  # wrong byte count
+    W = gpu.Weight(wb, Q4_K, 4, 256)
+    with pytest.raises(gpu.MimgError):
+        gpu.dequant_matmul_a8(W, np.zeros((1, 256), np.float32), block=64)  # block must be 32 or 256
+    # the same bytes register once
+    W2 = gpu.Weight(wb, Q4_K, 4, 256)
+    assert W2.handle == W.handle
+    W.release()
+
+
+# --------------------------------------------------- full-size shapes (cfg0/1)
+
+CFG1 = [  # (name, N, K, dtype, seed): Llama-3-8B layer, M = 1
+    ("q", 4096, 4096, Q4_K, 0), ("k", 1024, 4096, Q4_K, 1), ("v", 1024, 4096, Q6_K, 2),
+    ("o", 4096, 4096, Q4_K, 3), ("gate", 14336, 4096, Q4_K, 4), ("up", 14336, 4096, Q4_K, 5),
+    ("down", 4096, 14336, Q6_K, 6),
+]
+
+
+@pytest.mark.parametrize("name,n,k,dt,seed", CFG1)
+def test_cfg1_layer_shapes_bitexact(gpu, oracle, name, n, k, dt, seed):
+    """The BASELINE layer shapes at full size, M = 1 and M = 8: bit-exact."""
+    wb = _weights(oracle, dt, n, k, seed)
+    W = gpu.Weight(wb, dt, n, k)
+    for rows in (1, 8):
+        x = oracle.synthetic_acts(rows, k, seed=1)
+        got = gpu.dequant_matmul_a8(W, x, block=256)
+        want = oracle.linear_a8(x, wb, dt, n, k, block=256, threads=8)
+        assert bits_equal(got, want), (name, rows, first_diff(got, want))
+    W.release()
