@@ -56,16 +56,16 @@ def weight_bytes(n, k, dt):
     return n * (k // 256) * (144 if dt == Q4_K else 210)
 
 
-def step_bytes():
-    return sum(weight_bytes(n, k, dt) + k * 4 + n * 4 for _, n, k, dt, _, _ in CFG1)
+def step_bytes(rows=1):
+    return sum(weight_bytes(n, k, dt) + rows * (k * 4 + n * 4) for _, n, k, dt, _, _ in CFG1)
 
 
-def launch_bytes(n, k, dt):
-    """Algorithmic bytes of one GEMV launch at M = 1: the weight blocks, the
-    int8 quants, one f32 scale per 256, the per-32 (Q4_K) or per-16 (Q6_K)
-    int16 sums, and the f32 outputs."""
+def launch_bytes(n, k, dt, rows=1):
+    """Algorithmic bytes of one GEMV launch: the weight blocks, and per
+    activation row the int8 quants, one f32 scale per 256, the per-32 (Q4_K)
+    or per-16 (Q6_K) int16 sums, and the f32 outputs."""
     sums = (k // 32) * 2 if dt == Q4_K else (k // 16) * 2
-    return weight_bytes(n, k, dt) + k + (k // 256) * 4 + sums + n * 4
+    return weight_bytes(n, k, dt) + rows * (k + (k // 256) * 4 + sums + n * 4)
 
 
 def make_weights(stream, rotate, log):
@@ -99,7 +99,7 @@ def cpu_baseline(host_bytes, xs, seconds, log):
     import mimref
 
     threads = min(16, os.cpu_count() or 1)
-    nbytes = step_bytes()
+    nbytes = step_bytes(xs[0].shape[0])
 
     def one_layer(t):
         for name, n, k, dt, _, inp in CFG1:
@@ -142,6 +142,7 @@ def main():
     ap.add_argument("--steps", type=int, default=320)
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--rotate", type=int, default=32)
+    ap.add_argument("--rows", type=int, default=1, help="activation rows M (1 = cfg1; 8 = cfg4's batch 8)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
@@ -158,20 +159,21 @@ def main():
 
     mimg.init(0)
     stream = hiprt.Stream()
-    log(f"bench: cfg1 layer set, M=1, rotate {args.rotate}")
+    M = args.rows
+    log(f"bench: cfg1 layer set, M={M}, rotate {args.rotate}")
     layers, host_bytes = make_weights(stream, args.rotate, log)
 
-    xs = [np.random.default_rng(100 + i).standard_normal((1, k), dtype=np.float32) for i, k in enumerate(INPUT_K)]
+    xs = [np.random.default_rng(100 + i).standard_normal((M, k), dtype=np.float32) for i, k in enumerate(INPUT_K)]
     xd = [hiprt.DeviceBuffer.from_array(x) for x in xs]
-    ws_bytes = [mimg.a8_workspace_bytes(1, k) for k in INPUT_K]
+    ws_bytes = [mimg.a8_workspace_bytes(M, k) for k in INPUT_K]
     ws = [hiprt.DeviceBuffer(b) for b in ws_bytes]
-    yd = {name: hiprt.DeviceBuffer(n * 4) for name, n, _, _, _, _ in CFG1}
+    yd = {name: hiprt.DeviceBuffer(M * n * 4) for name, n, _, _, _, _ in CFG1}
 
     def enqueue_step(l):
         for i, k in enumerate(INPUT_K):
-            mimg.quantize_act_dev(xd[i].ptr, 1, k, 256, ws[i].ptr, ws_bytes[i], stream.handle)
+            mimg.quantize_act_dev(xd[i].ptr, M, k, 256, ws[i].ptr, ws_bytes[i], stream.handle)
         for name, n, k, dt, _, inp in CFG1:
-            mimg.matmul_a8_quantized_dev(layers[l][name], xd[inp].ptr, 1, None, 256, yd[name].ptr,
+            mimg.matmul_a8_quantized_dev(layers[l][name], xd[inp].ptr, M, None, 256, yd[name].ptr,
                                          ws[inp].ptr, ws_bytes[inp], stream.handle)
 
     if args.eager:
@@ -199,8 +201,8 @@ def main():
     wall = time.perf_counter() - t0
     ms_gpu = e0.elapsed_ms(e1)
     ms_per_step = ms_gpu / args.steps
-    value = step_bytes() / (ms_per_step * 1e-3) / 1e9
-    log(f"  timed: {args.steps} steps, {ms_per_step * 1e3:.2f} us/step (events), wall {wall * 1e3 / args.steps:.2f} us/step, {value:.1f} GB/s")
+    value = step_bytes(M) / (ms_per_step * 1e-3) / 1e9
+    log(f"  timed: {args.steps} steps, {ms_per_step * 1e3:.2f} us/step (events), wall {wall * 1e6 / args.steps:.2f} us/step, {value:.1f} GB/s")
 
     # Roofline of the dominant kernel: the Q4_K GEMV at the gate/up shape
     # (14336 x 4096, 33 MB), per-launch HIP events on the launch stream,
@@ -208,16 +210,16 @@ def main():
     def per_launch(name):
         _, n, k, dt, _, inp = next(c for c in CFG1 if c[0] == name)
         evs = [(hiprt.Event(), hiprt.Event()) for _ in range(args.roofline_launches)]
-        mimg.quantize_act_dev(xd[inp].ptr, 1, k, 256, ws[inp].ptr, ws_bytes[inp], stream.handle)
+        mimg.quantize_act_dev(xd[inp].ptr, M, k, 256, ws[inp].ptr, ws_bytes[inp], stream.handle)
         for i, (a, b) in enumerate(evs):
             a.record(stream)
-            mimg.matmul_a8_quantized_dev(layers[i % args.rotate][name], xd[inp].ptr, 1, None, 256, yd[name].ptr,
+            mimg.matmul_a8_quantized_dev(layers[i % args.rotate][name], xd[inp].ptr, M, None, 256, yd[name].ptr,
                                          ws[inp].ptr, ws_bytes[inp], stream.handle)
             b.record(stream)
         stream.sync()
         ts = np.array([a.elapsed_ms(b) for a, b in evs[4:]])
         us = float(np.mean(ts)) * 1e3
-        nbytes = launch_bytes(n, k, dt)
+        nbytes = launch_bytes(n, k, dt, M)
         return us, nbytes, nbytes / (us * 1e-6) / 1e9
 
     g_us, g_bytes, g_gbs = per_launch("gate")
@@ -247,9 +249,10 @@ def main():
         "dtype": "int8 x q4_k/q6_k, i32 block sums, f32 epilogue",
         "data": "synthetic (W ~ N(0,0.02^2) seeds 0..6 encoded Q4_K/Q6_K; x ~ N(0,1) seeds 100..103)",
         "config": {
-            "workload": "cfg1: Llama-3-8B decoder-layer linear set, M=1, Q4_K_M (q,k,o,gate,up Q4_K; v,down Q6_K), "
+            "workload": f"cfg1: Llama-3-8B decoder-layer linear set, M={M}, Q4_K_M (q,k,o,gate,up Q4_K; v,down Q6_K), "
                         "dequant_matmul_a8.v2 block=256",
-            "bytes_per_step": step_bytes(),
+            "rows": M,
+            "bytes_per_step": step_bytes(M),
             "rotation_layers": args.rotate,
             "graphs": not args.eager,
             "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
@@ -261,7 +264,7 @@ def main():
             "unit": "GB/s",
             "frac": round(g_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "gemv_a8k_kernel<Q4_K,1> at 14336x4096 (gate/up)",
+            "kernel": f"gemv_a8k_pairs_kernel<Q4_K,M={M}> at 14336x4096 (gate/up)",
             "launch_bytes": g_bytes,
             "avg_launch_us": round(g_us, 3),
             "q6k_down": {"avg_launch_us": round(d_us, 3), "launch_bytes": d_bytes, "achieved": round(d_gbs, 1)},

@@ -13,17 +13,29 @@
 // f32(S) is v_cvt_f32_i32 (round to nearest even), d*dx one f32 multiply,
 // fma one v_fma_f32, and the file is built with -ffp-contract=off.
 //
-// Mapping: a group of 8 lanes owns one weight row; a 256-thread workgroup
-// holds 32 groups (32 rows). For each block, lane l of the group loads 16
-// bytes of the block's quants (128-bit, coalesced) and computes its part of
-// S with v_dot4_i32_i8; the group sums the parts with three DPP steps
-// (integer, so exact in any order); every lane of the group then runs the
-// same serial float chain. The activation quants of up to 8 rows are staged
-// in LDS in tiles of blocks.
+// Two kernels compute the same bits:
+//
+// gemv_a8k_pairs_kernel (the default): a 256-thread workgroup owns R weight
+// rows. Its 32 groups of 8 lanes take the R*nb (row, block) pairs in turn,
+// U pairs at a time with all their weight loads issued before any compute,
+// so that many 128-bit loads per lane are in flight (the GEMV is bound by
+// HBM latency x bandwidth). For a pair, lane l of the group loads 16 bytes
+// of the block's quants, forms its part of S with v_dot4_i32_i8 against the
+// activation quants (read through L1, they are shared by all rows), and the
+// group sums the parts with three DPP steps (integer, so exact in any
+// order). The exact (S, M) and the two f32 scale products of every pair go
+// to LDS; then one lane per (row, activation row) runs the serial float
+// chain over the blocks in order.
+//
+// gemv_a8k_tiled_kernel: a group of 8 lanes owns one weight row and walks
+// its blocks in order, with the activation quants of up to 8 rows staged in
+// LDS in tiles of blocks.
 //
 // Rows of x the quantizer refused and rows of w with a non-finite block scale
 // take the float32 path (reference linearA8, interp/fast.go:323-377), in the
 // reference's AVX2 order (f32path.hpp).
+#include <cstdlib>
+
 #include "f32path.hpp"
 #include "mimg_device.hpp"
 #include "mimg_kernels.hpp"
@@ -56,7 +68,7 @@ struct KQ {
 };
 
 template <uint32_t DT, int M>
-__global__ __launch_bounds__(256) void gemv_a8k_kernel(GemvArgs A) {
+__global__ __launch_bounds__(256) void gemv_a8k_tiled_kernel(GemvArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int S16PB = KQ<DT>::S16PB;
     const int tb = A.tb;
@@ -183,12 +195,263 @@ __global__ __launch_bounds__(256) void gemv_a8k_kernel(GemvArgs A) {
     }
 }
 
+// One lane's share of a Q4_K block: lane l holds quant bytes 16l..16l+15 of
+// the block, i.e. chunk c = l/2, elements 64c+16h+[0,16) (low nibbles,
+// sub-block 2c) and 64c+32+16h+[0,16) (high nibbles, sub-block 2c+1), with
+// h = l%2; for the M term it takes sub-block l.
+struct Q4KLane {
+    uint32_t lo[4], hi[4];
+    int scl, sch, mm, yoff;
+    float d, dmin;
+};
+
+__device__ __forceinline__ Q4KLane q4k_lane(const u32x4& hdr, const u32x4& qv, int l) {
+    Q4KLane w;
+    const Q4KScales s = q4k_scales(hdr.y, hdr.z, hdr.w);
+    const int c = l >> 1, h = l & 1;
+    w.scl = (int)byte_of(s.sc, 2 * c);
+    w.sch = (int)byte_of(s.sc, 2 * c + 1);
+    w.mm = (int)byte_of(s.m, l);
+    w.d = f16_to_f32(hdr.x & 0xFFFFu);
+    w.dmin = f16_to_f32(hdr.x >> 16);
+    w.yoff = 64 * c + 16 * h;
+    const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        w.lo[k] = q[k] & 0x0F0F0F0Fu;
+        w.hi[k] = (q[k] >> 4) & 0x0F0F0F0Fu;
+    }
+    return w;
+}
+
+// The lane's part of S: sc_2c * sum(lo*y) + sc_2c+1 * sum(hi*y) (exact).
+__device__ __forceinline__ int q4k_part(const Q4KLane& w, const u32x4& ya, const u32x4& yh) {
+    int dl = sdot4(w.lo[0], ya.x, 0);
+    dl = sdot4(w.lo[1], ya.y, dl);
+    dl = sdot4(w.lo[2], ya.z, dl);
+    dl = sdot4(w.lo[3], ya.w, dl);
+    int dh = sdot4(w.hi[0], yh.x, 0);
+    dh = sdot4(w.hi[1], yh.y, dh);
+    dh = sdot4(w.hi[2], yh.z, dh);
+    dh = sdot4(w.hi[3], yh.w, dh);
+    return w.scl * dl + w.sch * dh;
+}
+
+// Raw loads of one lane's share of a Q6_K block (2-byte aligned blocks):
+// lane l = 4h + p takes ql bytes 64h+16p..+16 (elements eL..eL+15 in their
+// low nibbles and eH = eL+64.. in their high nibbles, eL = 128h+32(p/2)+16(p%2)),
+// the qh bytes 32h+16(p%2)..+16 and the block's scales and d.
+struct Q6KRaw {
+    u32x4 ql, qh;
+    uint32_t sw0, sw1, dbits;
+};
+
+__device__ __forceinline__ Q6KRaw q6k_load(const uint8_t* blk, int l) {
+    const int h = l >> 2, p = l & 3;
+    Q6KRaw r;
+    r.ql = load16_a2(blk + 64 * h + 16 * p);
+    r.qh = load16_a2(blk + 128 + 32 * h + 16 * (p & 1));
+    r.sw0 = load4_a2(blk + 192 + 8 * h);
+    r.sw1 = load4_a2(blk + 196 + 8 * h);
+    r.dbits = load_u16(blk + 208);
+    return r;
+}
+
+struct Q6KLane {
+    uint32_t vl[4], vh[4];
+    int scl, sch, eL;
+    float d;
+};
+
+__device__ __forceinline__ Q6KLane q6k_lane(const Q6KRaw& r, int l) {
+    const int h = l >> 2, p = l & 3, pp = p >> 1, p1 = p & 1;
+    Q6KLane w;
+    const int idx = 2 * pp + p1;
+    w.scl = (int)(int8_t)(r.sw0 >> (8 * idx));
+    w.sch = (int)(int8_t)(r.sw1 >> (8 * idx));
+    w.d = f16_to_f32(r.dbits);
+    w.eL = 128 * h + 32 * pp + 16 * p1;
+    const int shL = 2 * pp, shH = 4 + 2 * pp;
+    const uint32_t qlw[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};
+    const uint32_t qhw[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        w.vl[k] = (qlw[k] & 0x0F0F0F0Fu) | (((qhw[k] >> shL) & 0x03030303u) << 4);
+        w.vh[k] = ((qlw[k] >> 4) & 0x0F0F0F0Fu) | (((qhw[k] >> shH) & 0x03030303u) << 4);
+    }
+    return w;
+}
+
+// The lane's part of S: sc_L*(sum(q*y) - 32*sum(y)) + sc_H*(...) over its
+// two runs of 16 (exact); ysL/ysH are the runs' activation sums.
+__device__ __forceinline__ int q6k_part(const Q6KLane& w, const u32x4& ya, const u32x4& yh, int ysL, int ysH) {
+    int dl = sdot4(w.vl[0], ya.x, 0);
+    dl = sdot4(w.vl[1], ya.y, dl);
+    dl = sdot4(w.vl[2], ya.z, dl);
+    dl = sdot4(w.vl[3], ya.w, dl);
+    int dh = sdot4(w.vh[0], yh.x, 0);
+    dh = sdot4(w.vh[1], yh.y, dh);
+    dh = sdot4(w.vh[2], yh.z, dh);
+    dh = sdot4(w.vh[3], yh.w, dh);
+    return w.scl * (dl - 32 * ysL) + w.sch * (dh - 32 * ysH);
+}
+
+template <uint32_t DT, int M, int R>
+__global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    i32x4* part = (i32x4*)smem;  // [R][nb][M]: S, M term, bits(d*dx), bits(dmin*dx)
+    constexpr int U = 4;
+    const int g = threadIdx.x >> 3, l = threadIdx.x & 7;
+    const int nb = A.nb, row0 = blockIdx.x * R, npairs = R * nb;
+    const int64_t K = A.K, R32 = K / 32, R16 = K / 16;
+
+    for (int p0 = g; p0 < npairs; p0 += 32 * U) {
+        if (DT == DT_Q4_K) {
+            u32x4 hdr[U], qv[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int p = p0 + 32 * u;
+                if (p < npairs) {
+                    const int r = p / nb, b = p - r * nb;
+                    const int row = min(row0 + r, A.N - 1);
+                    const uint8_t* blk = A.W + (int64_t)row * A.rb + (int64_t)b * Q4K_BYTES;
+                    hdr[u] = *(const u32x4*)blk;
+                    qv[u] = *(const u32x4*)(blk + 16 + 16 * l);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int p = p0 + 32 * u;
+                if (p >= npairs) break;  // uniform within the group
+                const int r = p / nb, b = p - r * nb;
+                const Q4KLane w = q4k_lane(hdr[u], qv[u], l);
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    const int8_t* yb = A.q + m * K + (int64_t)b * 256 + w.yoff;
+                    const u32x4 ya = *(const u32x4*)yb;
+                    const u32x4 yh = *(const u32x4*)(yb + 32);
+                    const int S = group8_sum(q4k_part(w, ya, yh));
+                    const int Mt = group8_sum(w.mm * (int)A.s16[m * R32 + 8 * b + l]);
+                    const float dx = A.d32[m * R32 + 8 * b];
+                    if (l == 0) {
+                        i32x4 v;
+                        v.x = S;
+                        v.y = Mt;
+                        v.z = __float_as_int(w.d * dx);
+                        v.w = __float_as_int(w.dmin * dx);
+                        part[(r * nb + b) * M + m] = v;
+                    }
+                }
+            }
+        } else {
+            Q6KRaw raw[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int p = p0 + 32 * u;
+                if (p < npairs) {
+                    const int r = p / nb, b = p - r * nb;
+                    const int row = min(row0 + r, A.N - 1);
+                    raw[u] = q6k_load(A.W + (int64_t)row * A.rb + (int64_t)b * Q6K_BYTES, l);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int p = p0 + 32 * u;
+                if (p >= npairs) break;
+                const int r = p / nb, b = p - r * nb;
+                const Q6KLane w = q6k_lane(raw[u], l);
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    const int8_t* yb = A.q + m * K + (int64_t)b * 256;
+                    const u32x4 ya = *(const u32x4*)(yb + w.eL);
+                    const u32x4 yh = *(const u32x4*)(yb + w.eL + 64);
+                    const int16_t* ys = A.s16 + m * R16 + 16 * b;
+                    const int S = group8_sum(q6k_part(w, ya, yh, ys[w.eL >> 4], ys[(w.eL + 64) >> 4]));
+                    const float dx = A.d32[m * R32 + 8 * b];
+                    if (l == 0) {
+                        i32x4 v;
+                        v.x = S;
+                        v.y = 0;
+                        v.z = __float_as_int(w.d * dx);
+                        v.w = 0;
+                        part[(r * nb + b) * M + m] = v;
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // The serial float chain, one lane per (weight row, activation row).
+    const int t = threadIdx.x;
+    if (t < R * M) {
+        const int r = t / M, m = t - r * M, row = row0 + r;
+        if (row < A.N && A.wref[row] == 0 && A.ok[m]) {
+            float tot = 0.f, off = 0.f;
+            for (int b = 0; b < nb; b++) {
+                const i32x4 v = part[(r * nb + b) * M + m];
+                tot = __builtin_fmaf((float)v.x, __int_as_float(v.z), tot);
+                if (DT == DT_Q4_K) off = __builtin_fmaf((float)v.y, __int_as_float(v.w), off);
+            }
+            float res = DT == DT_Q4_K ? tot - off : tot;
+            if (A.bias) res += A.bias[row];
+            A.y[(int64_t)m * A.y_stride + row] = res;
+        }
+    }
+    // The float32 path for refused pairs, one group of eight lanes per pair.
+    for (int qq = g; qq < R * M; qq += 32) {
+        const int r = qq / M, m = qq - r * M, row = row0 + r;
+        if (row < A.N && (A.wref[row] != 0 || !A.ok[m])) {
+            float res = f32dot_g8<DT>(A.W + (int64_t)row * A.rb, A.x + (int64_t)m * K, K, A.fused != 0);
+            if (A.bias) res += A.bias[row];
+            if (l == 0) A.y[(int64_t)m * A.y_stride + row] = res;
+        }
+    }
+}
+
+// Kernel choice: 0 = pairs (default), 1 = tiled. MIMG_GEMV_VARIANT selects
+// the other for A/B timing; both give the same bits.
+static int gemv_variant() {
+    static const int v = [] {
+        const char* e = getenv("MIMG_GEMV_VARIANT");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
+}
+
+template <uint32_t DT, int M, int R>
+static hipError_t launch_pairs_r(GemvArgs A, hipStream_t stream) {
+    const size_t lds = (size_t)R * A.nb * M * 16;
+    dim3 grid((unsigned)((A.N + R - 1) / R)), blk(256);
+    hipLaunchKernelGGL((gemv_a8k_pairs_kernel<DT, M, R>), grid, blk, lds, stream, A);
+    return hipGetLastError();
+}
+
+// Rows per workgroup: enough (row, block) pairs to keep 32 groups busy, as
+// many workgroups as possible, and the pair table within 48 KB of LDS.
+static int pairs_rows(int N, int nb, int M) {
+    int R = 8;
+    while (R > 1 && ((N + R - 1) / R < 1024 || (size_t)R * nb * M * 16 > 48 * 1024)) R >>= 1;
+    return R;
+}
+
+template <uint32_t DT, int M>
+static hipError_t launch_pairs(GemvArgs A, hipStream_t stream) {
+    switch (pairs_rows(A.N, A.nb, M)) {
+    case 8: return launch_pairs_r<DT, M, 8>(A, stream);
+    case 4: return launch_pairs_r<DT, M, 4>(A, stream);
+    case 2: return launch_pairs_r<DT, M, 2>(A, stream);
+    default: return launch_pairs_r<DT, M, 1>(A, stream);
+    }
+}
+
 template <uint32_t DT, int M>
 static hipError_t launch_m(GemvArgs A, hipStream_t stream) {
+    if (gemv_variant() == 0 && (size_t)A.nb * M * 16 <= 48 * 1024) return launch_pairs<DT, M>(A, stream);
     A.tb = min(A.nb, max(1, 128 / M));
     const size_t lds = (size_t)M * A.tb * (256 + 4 + 2 * KQ<DT>::S16PB);
     dim3 grid((unsigned)((A.N + 31) / 32)), blk(256);
-    hipLaunchKernelGGL((gemv_a8k_kernel<DT, M>), grid, blk, lds, stream, A);
+    hipLaunchKernelGGL((gemv_a8k_tiled_kernel<DT, M>), grid, blk, lds, stream, A);
     return hipGetLastError();
 }
 

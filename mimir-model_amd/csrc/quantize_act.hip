@@ -10,22 +10,24 @@
 // ys16 = sum of each run of 16 (used by the Q6_K kernels for the bias of
 // 32); dbs = d*f32(xs).
 //
-// One workgroup per row; each wave takes one block of 256 elements at a time
-// (or eight blocks of 32), four elements per lane, float4 loads.
+// One workgroup per row, up to 16 waves; each wave takes one chunk of 256
+// elements at a time (one block of 256, or eight blocks of 32), four
+// elements per lane, float4 loads.
 #include "mimg_device.hpp"
 #include "mimg_kernels.hpp"
 
 namespace mimg {
 
 template <int BLOCK>
-__global__ __launch_bounds__(256) void quantize_act_kernel(const float* __restrict__ x, int64_t K,
-                                                           ActPtrs a) {
+__global__ __launch_bounds__(1024) void quantize_act_kernel(const float* __restrict__ x, int64_t K,
+                                                            ActPtrs a) {
     const int row = blockIdx.x;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nwaves = blockDim.x >> 6;
     const float* xr = x + (int64_t)row * K;
     const int64_t R32 = K / 32;
     bool bad = false;
-    for (int64_t c = wave; c * 256 < K; c += 4) {
+    for (int64_t c = wave; c * 256 < K; c += nwaves) {
         const int64_t e0 = c * 256 + 4 * lane;
         // blocks of 32: K is a multiple of 32, so each group of eight lanes
         // is wholly inside or outside the row (the DPP steps stay in-group)
@@ -84,7 +86,9 @@ __global__ __launch_bounds__(256) void quantize_act_kernel(const float* __restri
 hipError_t launch_quantize_act(const float* x, int64_t rows, int64_t K, int block, const ActPtrs& a,
                                hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
-    dim3 grid((unsigned)rows), blk(256);
+    const int64_t chunks = (K + 255) / 256;
+    const int waves = (int)(chunks < 16 ? chunks : 16);
+    dim3 grid((unsigned)rows), blk(64 * waves);
     if (block == 256)
         hipLaunchKernelGGL(quantize_act_kernel<256>, grid, blk, 0, stream, x, K, a);
     else
