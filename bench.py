@@ -169,12 +169,16 @@ def main():
     ws = [hiprt.DeviceBuffer(b) for b in ws_bytes]
     yd = {name: hiprt.DeviceBuffer(M * n * 4) for name, n, _, _, _, _ in CFG1}
 
+    # A decoder layer's calls: q, k and v share the attention input and gate
+    # and up the FFN input, so each pair/triple is one grouped call
+    # (dequant_matmul_a8.v2 each, bit for bit); o and down have inputs of
+    # their own.
+    groups = [[c for c in CFG1 if c[5] == i] for i in range(len(INPUT_K))]
+
     def enqueue_step(l):
-        for i, k in enumerate(INPUT_K):
-            mimg.quantize_act_dev(xd[i].ptr, M, k, 256, ws[i].ptr, ws_bytes[i], stream.handle)
-        for name, n, k, dt, _, inp in CFG1:
-            mimg.matmul_a8_quantized_dev(layers[l][name], xd[inp].ptr, M, None, 256, yd[name].ptr,
-                                         ws[inp].ptr, ws_bytes[inp], stream.handle)
+        for i, grp in enumerate(groups):
+            mimg.linear_a8_group_dev([layers[l][c[0]] for c in grp], xd[i].ptr, M, None, 256,
+                                     [yd[c[0]].ptr for c in grp], ws[i].ptr, ws_bytes[i], stream.handle)
 
     if args.eager:
         run_step = enqueue_step
@@ -208,18 +212,27 @@ def main():
     # (14336 x 4096, 33 MB), per-launch HIP events on the launch stream,
     # over distinct rotation copies so every launch reads from HBM.
     def per_launch(name):
+        """One call on one matrix, timed alone (HIP events on the stream the
+        kernel runs on). At M = 1 it is the single fused launch, whose
+        algorithmic bytes are the weights, x (f32) and y (f32); otherwise the
+        pre-quantized product launch alone (launch_bytes)."""
         _, n, k, dt, _, inp = next(c for c in CFG1 if c[0] == name)
         evs = [(hiprt.Event(), hiprt.Event()) for _ in range(args.roofline_launches)]
-        mimg.quantize_act_dev(xd[inp].ptr, M, k, 256, ws[inp].ptr, ws_bytes[inp], stream.handle)
+        if M > 1:
+            mimg.quantize_act_dev(xd[inp].ptr, M, k, 256, ws[inp].ptr, ws_bytes[inp], stream.handle)
         for i, (a, b) in enumerate(evs):
             a.record(stream)
-            mimg.matmul_a8_quantized_dev(layers[i % args.rotate][name], xd[inp].ptr, M, None, 256, yd[name].ptr,
-                                         ws[inp].ptr, ws_bytes[inp], stream.handle)
+            if M == 1:
+                mimg.linear_a8_dev(layers[i % args.rotate][name], xd[inp].ptr, M, None, 256, yd[name].ptr,
+                                   ws[inp].ptr, ws_bytes[inp], stream.handle)
+            else:
+                mimg.matmul_a8_quantized_dev(layers[i % args.rotate][name], xd[inp].ptr, M, None, 256,
+                                             yd[name].ptr, ws[inp].ptr, ws_bytes[inp], stream.handle)
             b.record(stream)
         stream.sync()
         ts = np.array([a.elapsed_ms(b) for a, b in evs[4:]])
         us = float(np.mean(ts)) * 1e3
-        nbytes = launch_bytes(n, k, dt, M)
+        nbytes = weight_bytes(n, k, dt) + k * 4 + n * 4 if M == 1 else launch_bytes(n, k, dt, M)
         return us, nbytes, nbytes / (us * 1e-6) / 1e9
 
     g_us, g_bytes, g_gbs = per_launch("gate")
@@ -264,7 +277,8 @@ def main():
             "unit": "GB/s",
             "frac": round(g_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": f"gemv_a8k_pairs_kernel<Q4_K,M={M}> at 14336x4096 (gate/up)",
+            "kernel": ("gemv_a8k_fused_kernel (quantize+GEMV, Q4_K, M=1)" if M == 1
+                       else f"gemv_a8k_pairs_kernel<Q4_K,M={M}>") + " at 14336x4096 (gate/up)",
             "launch_bytes": g_bytes,
             "avg_launch_us": round(g_us, 3),
             "q6k_down": {"avg_launch_us": round(d_us, 3), "launch_bytes": d_bytes, "achieved": round(d_gbs, 1)},

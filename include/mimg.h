@@ -134,6 +134,17 @@ int mimg_quantize_act_dev(const float *x, int64_t rows, int64_t k, int block, vo
 int mimg_linear_a8_dev(uint64_t w, const float *x, int64_t rows, const float *bias, int block, float *y,
                        void *ws, uint64_t ws_bytes, void *stream);
 
+/* mimg_linear_a8_dev for `count` (1..3) weights with the same K that share
+ * the activations x, e.g. the q, k and v projections of a decoder layer
+ * (reference importer/llama.go:423-534 writes them as three
+ * dequant_matmul_a8 calls on one input). y[i] (and bias[i], or bias NULL)
+ * belong to weight i. Equal, bit for bit, to the separate calls; with one
+ * activation row and blocks of 256 it is a single launch that quantizes x
+ * inside the kernel (ws may then be NULL). */
+int mimg_linear_a8_group_dev(const uint64_t *w, int count, const float *x, int64_t rows,
+                             const float *const *bias, int block, float *const *y, void *ws,
+                             uint64_t ws_bytes, void *stream);
+
 /* The product alone, for activations already quantized into ws by
  * mimg_quantize_act_dev with the same rows, K and block. */
 int mimg_matmul_a8_quantized_dev(uint64_t w, const float *x, int64_t rows, const float *bias, int block,

@@ -1,0 +1,275 @@
+// Decode GEMV for one activation row with the 8-bit quantization fused in:
+// dequant_matmul_a8.v2, block = 256, M = 1, Q4_K and Q6_K weights, for up
+// to three weight matrices that share the activation row (q, k, v of a
+// decoder layer; gate and up) in one launch.
+//
+// Each 256-thread workgroup owns R rows of one matrix. It first issues the
+// weight loads of its (row, block) pairs, then quantizes x into LDS while
+// they are in flight (every workgroup quantizes the same row the same way,
+// so no second launch and no global workspace), then forms the exact int32
+// block sums of its pairs (as gemv_kquant.hip) and runs the serial float
+// chain of each row in block order.
+//
+// Quantization (reference Q8.QuantizeBlocks, internal/kernels/q8.go:50-97):
+// per block of 256, amax = max|x| (the row is refused if any |x| is NaN or
+// above 2^60); q = RoundToEven(127 x / amax) of the exact quotient
+// (quant_rne.hpp); d = amax/127 (correctly rounded f32 division); per-16 and
+// per-32 sums of q.
+#include "f32path.hpp"
+#include "kquant_lane.hpp"
+#include "mimg_device.hpp"
+#include "mimg_kernels.hpp"
+
+namespace mimg {
+
+constexpr int DPP_ROW_ROR1 = 0x121, DPP_ROW_ROR2 = 0x122, DPP_ROW_ROR4 = 0x124, DPP_ROW_ROR8 = 0x128;
+
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), DPP_ROW_ROR8, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), DPP_ROW_ROR4, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), DPP_ROW_ROR2, 0xF, 0xF, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), DPP_ROW_ROR1, 0xF, 0xF, false)));
+    return v;
+}
+
+struct QuantLds {
+    int8_t* q;       // [K]
+    float* dx;       // [nb]
+    int16_t* xs;     // [K/32]
+    int16_t* ys16;   // [K/16]
+};
+
+// Quantizes one row of K f32 values into LDS; 16 threads (one DPP row) per
+// block of 256, 16 elements per thread. Returns this thread's refusal flag.
+__device__ __forceinline__ bool quantize_row_lds(const float* __restrict__ x, int nb, const QuantLds& Q) {
+    const int t = threadIdx.x, j = t & 15;
+    bool bad = false;
+    for (int b0 = 0; b0 < nb; b0 += 16) {
+        const int b = b0 + (t >> 4);
+        if (b >= nb) break;  // uniform within the DPP row
+        const float4* xp = (const float4*)(x + 256 * b + 16 * j);
+        const float4 v0 = xp[0], v1 = xp[1], v2 = xp[2], v3 = xp[3];
+        const float xv[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
+                              v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
+        float m = 0.f;
+        bool lbad = false;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float a = fabsf(xv[i]);
+            lbad |= !(a <= 0x1p60f);
+            m = fmaxf(m, a);
+        }
+        bad |= lbad;
+        const float amax = row16_max(m);
+        const bool quant = amax > 0.f && amax <= 0x1p60f;
+        const float inv = quant ? 1.0f / amax : 0.f;
+        uint32_t w[4] = {0, 0, 0, 0};
+        int s16 = 0;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int q = quant ? quant_rne(xv[i], amax, inv) : 0;
+            s16 += q;
+            w[i >> 2] |= (uint32_t)(q & 0xFF) << (8 * (i & 3));
+        }
+        *(u32x4*)(Q.q + 256 * b + 16 * j) = u32x4{w[0], w[1], w[2], w[3]};
+        const int s32 = s16 + __builtin_amdgcn_mov_dpp(s16, DPP_QUAD_1032, 0xF, 0xF, false);
+        Q.ys16[16 * b + j] = (int16_t)s16;
+        if ((j & 1) == 0) Q.xs[8 * b + (j >> 1)] = (int16_t)s32;
+        if (j == 0) Q.dx[b] = amax / 127.0f;
+    }
+    return bad;
+}
+
+struct FusedMat {
+    const uint8_t* W;
+    const uint8_t* wref;
+    const float* bias;
+    float* y;
+    int64_t rb;
+    int N;
+    uint32_t dt;
+    int R;       // rows per workgroup
+    int tile0;   // first workgroup of this matrix
+};
+
+struct FusedArgs {
+    FusedMat mat[3];
+    int nmat;
+    const float* x;
+    int64_t K;
+    int nb;
+};
+
+template <uint32_t DT>
+struct FusedRaw;
+template <>
+struct FusedRaw<DT_Q4_K> {
+    u32x4 hdr, qv;
+};
+template <>
+struct FusedRaw<DT_Q6_K> {
+    Q6KRaw raw;
+};
+
+template <uint32_t DT, int U>
+__device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F, int tile, uint8_t* smem) {
+    constexpr int BYTES = DT == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    const int nb = A.nb, R = F.R, np = R * nb;
+    const int64_t K = A.K;
+    const int g = threadIdx.x >> 3, l = threadIdx.x & 7;
+    const int row0 = tile * R;
+    QuantLds Q;
+    Q.q = (int8_t*)smem;
+    Q.dx = (float*)(smem + K);
+    Q.xs = (int16_t*)(Q.dx + nb);
+    Q.ys16 = (int16_t*)(Q.xs + K / 32);
+    i32x4* part = (i32x4*)(smem + ((K + nb * 4 + (K / 32) * 2 + (K / 16) * 2 + 15) & ~(int64_t)15));
+
+    // 1. The first U pairs' weights, unconditionally (clamped), in flight.
+    FusedRaw<DT> raw[U];
+    auto load = [&](int p0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int p = min(p0 + 32 * u, np - 1);
+            const int r = p / nb, b = p - r * nb;
+            const int row = min(row0 + r, F.N - 1);
+            const uint8_t* blk = F.W + (int64_t)row * F.rb + (int64_t)b * BYTES;
+            if constexpr (DT == DT_Q4_K) {
+                raw[u].hdr = *(const u32x4*)blk;
+                raw[u].qv = *(const u32x4*)(blk + 16 + 16 * l);
+            } else {
+                raw[u].raw = q6k_load(blk, l);
+            }
+        }
+    };
+    load(g);
+
+    // 2. Quantize x into LDS while the weights arrive.
+    const bool bad = quantize_row_lds(A.x, nb, Q);
+    const bool row_refused = __syncthreads_or(bad ? 1 : 0) != 0;
+
+    // 3. Exact block sums of this workgroup's pairs.
+    for (int p0 = g; p0 < np; p0 += 32 * U) {
+        if (p0 != g) load(p0);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int p = p0 + 32 * u;
+            if (p >= np) break;  // uniform within the group
+            const int r = p / nb, b = p - r * nb;
+            i32x4 v;
+            if constexpr (DT == DT_Q4_K) {
+                const Q4KLane w = q4k_lane(raw[u].hdr, raw[u].qv, l);
+                const int8_t* yb = Q.q + 256 * b + w.yoff;
+                v.x = group8_sum(q4k_part(w, *(const u32x4*)yb, *(const u32x4*)(yb + 32)));
+                v.y = group8_sum(w.mm * (int)Q.xs[8 * b + l]);
+                const float dx = Q.dx[b];
+                v.z = __float_as_int(w.d * dx);
+                v.w = __float_as_int(w.dmin * dx);
+            } else {
+                const Q6KLane w = q6k_lane(raw[u].raw, l);
+                const int8_t* yb = Q.q + 256 * b;
+                v.x = group8_sum(q6k_part(w, *(const u32x4*)(yb + w.eL), *(const u32x4*)(yb + w.eL + 64),
+                                          Q.ys16[16 * b + (w.eL >> 4)], Q.ys16[16 * b + ((w.eL + 64) >> 4)]));
+                v.y = 0;
+                v.z = __float_as_int(w.d * Q.dx[b]);
+                v.w = 0;
+            }
+            if (l == 0) part[r * nb + b] = v;
+        }
+    }
+    __syncthreads();
+
+    // 4. The serial float chain of each row, in block order.
+    const int t = threadIdx.x;
+    if (t < R) {
+        const int row = row0 + t;
+        if (row < F.N && F.wref[row] == 0 && !row_refused) {
+            float tot = 0.f, off = 0.f;
+            for (int b = 0; b < nb; b++) {
+                const i32x4 v = part[t * nb + b];
+                tot = __builtin_fmaf((float)v.x, __int_as_float(v.z), tot);
+                if (DT == DT_Q4_K) off = __builtin_fmaf((float)v.y, __int_as_float(v.w), off);
+            }
+            float res = DT == DT_Q4_K ? tot - off : tot;
+            if (F.bias) res += F.bias[row];
+            F.y[row] = res;
+        }
+    }
+    // 5. The float32 path for refused rows (fused order: one activation row).
+    for (int r = g; r < R; r += 32) {
+        const int row = row0 + r;
+        if (row < F.N && (F.wref[row] != 0 || row_refused)) {
+            float res = f32dot_g8<DT>(F.W + (int64_t)row * F.rb, A.x, K, true);
+            if (F.bias) res += F.bias[row];
+            if (l == 0) F.y[row] = res;
+        }
+    }
+}
+
+template <int U>
+__global__ __launch_bounds__(256) void gemv_a8k_fused_kernel(FusedArgs A) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    int mi = 0;
+    if (A.nmat > 1 && (int)blockIdx.x >= A.mat[1].tile0) mi = 1;
+    if (A.nmat > 2 && (int)blockIdx.x >= A.mat[2].tile0) mi = 2;
+    const FusedMat F = mi == 0 ? A.mat[0] : mi == 1 ? A.mat[1] : A.mat[2];
+    const int tile = (int)blockIdx.x - F.tile0;
+    if (F.dt == DT_Q4_K) fused_body<DT_Q4_K, U>(A, F, tile, smem);
+    else fused_body<DT_Q6_K, U>(A, F, tile, smem);
+}
+
+static size_t fused_lds_bytes(int64_t K, int nb, int maxR) {
+    size_t q = ((size_t)K + nb * 4 + (K / 32) * 2 + (K / 16) * 2 + 15) & ~(size_t)15;
+    return q + (size_t)maxR * nb * 16;
+}
+
+// Rows per workgroup for a matrix: pairs per workgroup at most 32*U*2 (two
+// load batches) and the pair table plus the quantized row within 48 KB.
+static int fused_rows(int nb, int64_t K) {
+    constexpr int U = 4;
+    int R = max(1, 32 * U / nb);
+    while (R > 1 && fused_lds_bytes(K, nb, R) > 48 * 1024) R >>= 1;
+    return R;
+}
+
+bool fused_gemv_ok(const DevWeight* const* ws, int nmat) {
+    if (nmat < 1 || nmat > 3) return false;
+    const int64_t K = ws[0]->k;
+    if (K % 256 || K > 16384) return false;
+    for (int i = 0; i < nmat; i++)
+        if (ws[i]->k != K || (ws[i]->dt != DT_Q4_K && ws[i]->dt != DT_Q6_K)) return false;
+    return fused_lds_bytes(K, (int)(K / 256), fused_rows((int)(K / 256), K)) <= 48 * 1024;
+}
+
+hipError_t launch_gemv_a8k_fused(const DevWeight* const* ws, int nmat, const float* x,
+                                 const float* const* bias, float* const* y, hipStream_t stream) {
+    if (!fused_gemv_ok(ws, nmat)) return hipErrorInvalidValue;
+    FusedArgs A;
+    A.nmat = nmat;
+    A.x = x;
+    A.K = ws[0]->k;
+    A.nb = (int)(A.K / 256);
+    int tiles = 0, maxR = 1;
+    for (int i = 0; i < 3; i++) {
+        FusedMat& F = A.mat[i];
+        const DevWeight& w = *ws[i < nmat ? i : 0];
+        F.W = w.data;
+        F.wref = w.wref;
+        F.bias = i < nmat ? bias[i] : nullptr;
+        F.y = i < nmat ? y[i] : nullptr;
+        F.rb = w.row_bytes;
+        F.N = (int)w.n;
+        F.dt = w.dt;
+        F.R = fused_rows(A.nb, A.K);
+        F.tile0 = tiles;
+        if (i < nmat) {
+            tiles += (F.N + F.R - 1) / F.R;
+            maxR = max(maxR, F.R);
+        }
+    }
+    const size_t lds = fused_lds_bytes(A.K, A.nb, maxR);
+    hipLaunchKernelGGL(gemv_a8k_fused_kernel<4>, dim3(tiles), dim3(256), lds, stream, A);
+    return hipGetLastError();
+}
+
+}  // namespace mimg

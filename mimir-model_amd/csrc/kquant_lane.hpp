@@ -1,0 +1,115 @@
+// Per-lane decode of Q4_K and Q6_K blocks for the 8-bit GEMV kernels: a
+// group of eight lanes shares one 256-element block; each helper gives one
+// lane its quants (as packed bytes for v_dot4_i32_i8), scales and the
+// activation offsets it multiplies. Integer results are exact.
+#pragma once
+
+#include "mimg_device.hpp"
+
+namespace mimg {
+
+// One lane's share of a Q4_K block: lane l holds quant bytes 16l..16l+15 of
+// the block, i.e. chunk c = l/2, elements 64c+16h+[0,16) (low nibbles,
+// sub-block 2c) and 64c+32+16h+[0,16) (high nibbles, sub-block 2c+1), with
+// h = l%2; for the M term it takes sub-block l.
+struct Q4KLane {
+    uint32_t lo[4], hi[4];
+    int scl, sch, mm, yoff;
+    float d, dmin;
+};
+
+__device__ __forceinline__ Q4KLane q4k_lane(const u32x4& hdr, const u32x4& qv, int l) {
+    Q4KLane w;
+    const Q4KScales s = q4k_scales(hdr.y, hdr.z, hdr.w);
+    const int c = l >> 1, h = l & 1;
+    w.scl = (int)byte_of(s.sc, 2 * c);
+    w.sch = (int)byte_of(s.sc, 2 * c + 1);
+    w.mm = (int)byte_of(s.m, l);
+    w.d = f16_to_f32(hdr.x & 0xFFFFu);
+    w.dmin = f16_to_f32(hdr.x >> 16);
+    w.yoff = 64 * c + 16 * h;
+    const uint32_t q[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        w.lo[k] = q[k] & 0x0F0F0F0Fu;
+        w.hi[k] = (q[k] >> 4) & 0x0F0F0F0Fu;
+    }
+    return w;
+}
+
+// The lane's part of S: sc_2c * sum(lo*y) + sc_2c+1 * sum(hi*y) (exact).
+__device__ __forceinline__ int q4k_part(const Q4KLane& w, const u32x4& ya, const u32x4& yh) {
+    int dl = sdot4(w.lo[0], ya.x, 0);
+    dl = sdot4(w.lo[1], ya.y, dl);
+    dl = sdot4(w.lo[2], ya.z, dl);
+    dl = sdot4(w.lo[3], ya.w, dl);
+    int dh = sdot4(w.hi[0], yh.x, 0);
+    dh = sdot4(w.hi[1], yh.y, dh);
+    dh = sdot4(w.hi[2], yh.z, dh);
+    dh = sdot4(w.hi[3], yh.w, dh);
+    return w.scl * dl + w.sch * dh;
+}
+
+// Raw loads of one lane's share of a Q6_K block (2-byte aligned blocks):
+// lane l = 4h + p takes ql bytes 64h+16p..+16 (elements eL..eL+15 in their
+// low nibbles and eH = eL+64.. in their high nibbles, eL = 128h+32(p/2)+16(p%2)),
+// the qh bytes 32h+16(p%2)..+16 and the block's scales and d.
+struct Q6KRaw {
+    u32x4 ql, qh;
+    int scl, sch;
+    uint32_t dbits;
+};
+
+// Seven loads per lane: ql and qh as 5 aligned dwords each, the two int8
+// scales of the lane's runs of 16 (sc[8h+idx] and sc[8h+idx+4], idx =
+// 2(p/2)+p%2) and d.
+__device__ __forceinline__ Q6KRaw q6k_load(const uint8_t* blk, int l) {
+    const int h = l >> 2, p = l & 3, idx = 2 * (p >> 1) + (p & 1);
+    Q6KRaw r;
+    r.ql = load16_a2(blk + 64 * h + 16 * p);
+    r.qh = load16_a2(blk + 128 + 32 * h + 16 * (p & 1));
+    r.scl = (int)(int8_t)blk[192 + 8 * h + idx];
+    r.sch = (int)(int8_t)blk[196 + 8 * h + idx];
+    r.dbits = load_u16(blk + 208);
+    return r;
+}
+
+struct Q6KLane {
+    uint32_t vl[4], vh[4];
+    int scl, sch, eL;
+    float d;
+};
+
+__device__ __forceinline__ Q6KLane q6k_lane(const Q6KRaw& r, int l) {
+    const int h = l >> 2, p = l & 3, pp = p >> 1, p1 = p & 1;
+    Q6KLane w;
+    w.scl = r.scl;
+    w.sch = r.sch;
+    w.d = f16_to_f32(r.dbits);
+    w.eL = 128 * h + 32 * pp + 16 * p1;
+    const int shL = 2 * pp, shH = 4 + 2 * pp;
+    const uint32_t qlw[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};
+    const uint32_t qhw[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        w.vl[k] = (qlw[k] & 0x0F0F0F0Fu) | (((qhw[k] >> shL) & 0x03030303u) << 4);
+        w.vh[k] = ((qlw[k] >> 4) & 0x0F0F0F0Fu) | (((qhw[k] >> shH) & 0x03030303u) << 4);
+    }
+    return w;
+}
+
+// The lane's part of S: sc_L*(sum(q*y) - 32*sum(y)) + sc_H*(...) over its
+// two runs of 16 (exact); ysL/ysH are the runs' activation sums.
+__device__ __forceinline__ int q6k_part(const Q6KLane& w, const u32x4& ya, const u32x4& yh, int ysL, int ysH) {
+    int dl = sdot4(w.vl[0], ya.x, 0);
+    dl = sdot4(w.vl[1], ya.y, dl);
+    dl = sdot4(w.vl[2], ya.z, dl);
+    dl = sdot4(w.vl[3], ya.w, dl);
+    int dh = sdot4(w.vh[0], yh.x, 0);
+    dh = sdot4(w.vh[1], yh.y, dh);
+    dh = sdot4(w.vh[2], yh.z, dh);
+    dh = sdot4(w.vh[3], yh.w, dh);
+    return w.scl * (dl - 32 * ysL) + w.sch * (dh - 32 * ysH);
+}
+
+}  // namespace mimg

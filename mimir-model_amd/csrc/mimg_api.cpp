@@ -5,6 +5,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -214,9 +215,12 @@ bool fused_q8_blocks(uint32_t dt, int block) {
 }
 
 // Everything after quantization: the product of the quantized rows.
-int matmul_quantized(const Weight* w, const float* x, int64_t rows, const float* bias, int block, float* y,
-                     const ActPtrs& a, hipStream_t s) {
-    const int64_t K = w->dw.k, N = w->dw.n, R32 = K / 32, R16 = K / 16;
+// The products of up to three weights (same K, each with an 8-bit kernel for
+// `block`) with activations already quantized into `a`: block-256 weights of
+// one dtype share a launch per chunk of 8 rows.
+int matmul_quantized(const Weight* const* w, int count, const float* x, int64_t rows, const float* const* bias,
+                     int block, float* const* y, const ActPtrs& a, hipStream_t s) {
+    const int64_t K = w[0]->dw.k, R32 = K / 32, R16 = K / 16;
     for (int64_t r0 = 0; r0 < rows; r0 += 8) {
         const int64_t mr = rows - r0 < 8 ? rows - r0 : 8;
         ActPtrs c;
@@ -226,12 +230,31 @@ int matmul_quantized(const Weight* w, const float* x, int64_t rows, const float*
         c.ys16 = a.ys16 + r0 * R16;
         c.dbs = a.dbs + r0 * R32;
         c.ok = a.ok + r0;
-        hipError_t e;
-        if (block == 256)
-            e = launch_gemv_a8k(w->dw, c, mr, rows, x + r0 * K, bias, y + r0 * N, N, s);
-        else
-            e = launch_gemv_q8_0_a8(w->dw, c, mr, rows, x + r0 * K, bias, y + r0 * N, N, s);
-        if (e != hipSuccess) return fail(MIMG_ERR_HIP, "product launch: %s", hipGetErrorString(e));
+        bool done[3] = {false, false, false};
+        for (int i = 0; i < count; i++) {
+            if (done[i]) continue;
+            hipError_t e;
+            if (block == 256) {
+                const DevWeight* dws[3];
+                const float* bs[3];
+                float* ys[3];
+                int n = 0;
+                for (int j = i; j < count; j++) {
+                    if (done[j] || w[j]->dw.dt != w[i]->dw.dt) continue;
+                    dws[n] = &w[j]->dw;
+                    bs[n] = bias ? bias[j] : nullptr;
+                    ys[n] = y[j] + r0 * w[j]->dw.n;
+                    done[j] = true;
+                    n++;
+                }
+                e = launch_gemv_a8k(dws, n, c, mr, rows, x + r0 * K, bs, ys, s);
+            } else {
+                const int64_t N = w[i]->dw.n;
+                e = launch_gemv_q8_0_a8(w[i]->dw, c, mr, rows, x + r0 * K, bias ? bias[i] : nullptr, y[i] + r0 * N, N, s);
+                done[i] = true;
+            }
+            if (e != hipSuccess) return fail(MIMG_ERR_HIP, "product launch: %s", hipGetErrorString(e));
+        }
     }
     return MIMG_OK;
 }
@@ -380,21 +403,94 @@ int mimg_matmul_a8_quantized_dev(uint64_t wh, const float* x, int64_t rows, cons
     if (!x || !y || !ws || !aligned(ws, 256)) return fail(MIMG_ERR_ARG, "null or misaligned pointer");
     ActLayout l = act_layout(rows, w->dw.k);
     if (ws_bytes < l.total) return fail(MIMG_ERR_WORKSPACE, "workspace %llu < %llu bytes", (unsigned long long)ws_bytes, (unsigned long long)l.total);
-    return matmul_quantized(w, x, rows, bias, block, y, act_ptrs((void*)ws, l), (hipStream_t)stream);
+    const Weight* ws1[1] = {w};
+    const float* bs1[1] = {bias};
+    float* ys1[1] = {y};
+    return matmul_quantized(ws1, 1, x, rows, bs1, block, ys1, act_ptrs((void*)ws, l), (hipStream_t)stream);
+}
+
+// When a single activation row is quantized inside the GEMV kernel: every
+// workgroup then quantizes the whole row, which pays while the group is
+// small (q/k/v, o); for long rows or many weight rows a separate quantize
+// launch costs less (measured on MI355X). MIMG_FUSED_MAXK / MIMG_FUSED_MAXN
+// override the limits, for tuning.
+static int64_t env_or(const char* name, int64_t dflt) {
+    const char* e = getenv(name);
+    return e ? (int64_t)atoll(e) : dflt;
+}
+static int64_t fused_max_k() {
+    static const int64_t v = env_or("MIMG_FUSED_MAXK", 4096);
+    return v;
+}
+static int64_t fused_max_n() {
+    static const int64_t v = env_or("MIMG_FUSED_MAXN", 8192);
+    return v;
+}
+
+int mimg_linear_a8_group_dev(const uint64_t* whs, int count, const float* x, int64_t rows, const float* const* bias,
+                             int block, float* const* y, void* ws, uint64_t ws_bytes, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!whs || !y || count < 1 || count > 3) return fail(MIMG_ERR_ARG, "a group holds 1 to 3 weights, got %d", count);
+    Weight* w[3];
+    const DevWeight* dw[3];
+    bool all_f32 = true, any_f32 = false;
+    for (int i = 0; i < count; i++) {
+        if ((rc = lookup(whs[i], &w[i]))) return rc;
+        if (w[i]->dw.k != w[0]->dw.k) return fail(MIMG_ERR_ARG, "the weights of a group must share K");
+        bool use_f32;
+        if ((rc = a8_checks(w[i], rows, block, &use_f32))) return rc;
+        all_f32 = all_f32 && use_f32;
+        any_f32 = any_f32 || use_f32;
+        dw[i] = &w[i]->dw;
+    }
+    if (rows == 0) return MIMG_OK;
+    if (!x || !aligned(x, 16)) return fail(MIMG_ERR_ARG, "x must be 16-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    int64_t total_n = 0;
+    for (int i = 0; i < count; i++) total_n += w[i]->dw.n;
+    if (!any_f32 && rows == 1 && block == 256 && w[0]->dw.k <= fused_max_k() && total_n <= fused_max_n() &&
+        fused_gemv_ok(dw, count)) {
+        float* ys[3];
+        const float* bs[3];
+        for (int i = 0; i < count; i++) {
+            ys[i] = y[i];
+            bs[i] = bias ? bias[i] : nullptr;
+        }
+        HIP_TRY(launch_gemv_a8k_fused(dw, count, x, bs, ys, s));
+        return MIMG_OK;
+    }
+    // The weights without an 8-bit kernel for `block` take the float32 path;
+    // the others share one quantization of x.
+    const Weight* wa[3];
+    const float* ba[3];
+    float* ya[3];
+    int na = 0;
+    for (int i = 0; i < count; i++) {
+        const float* bi = bias ? bias[i] : nullptr;
+        bool use_f32;
+        a8_checks(w[i], rows, block, &use_f32);
+        if (use_f32) {
+            if ((rc = mimg_linear_f32_dev(whs[i], x, rows, bi, y[i], stream))) return rc;
+            continue;
+        }
+        wa[na] = w[i];
+        ba[na] = bi;
+        ya[na] = y[i];
+        na++;
+    }
+    (void)all_f32;
+    if (na == 0) return MIMG_OK;
+    if ((rc = mimg_quantize_act_dev(x, rows, w[0]->dw.k, block, ws, ws_bytes, stream))) return rc;
+    ActLayout l = act_layout(rows, w[0]->dw.k);
+    return matmul_quantized(wa, na, x, rows, ba, block, ya, act_ptrs(ws, l), s);
 }
 
 int mimg_linear_a8_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, int block, float* y, void* ws,
                        uint64_t ws_bytes, void* stream) {
-    int rc = ensure_device();
-    if (rc) return rc;
-    Weight* w;
-    if ((rc = lookup(wh, &w))) return rc;
-    bool use_f32;
-    if ((rc = a8_checks(w, rows, block, &use_f32))) return rc;
-    if (use_f32) return mimg_linear_f32_dev(wh, x, rows, bias, y, stream);
-    if (rows == 0) return MIMG_OK;
-    if ((rc = mimg_quantize_act_dev(x, rows, w->dw.k, block, ws, ws_bytes, stream))) return rc;
-    return mimg_matmul_a8_quantized_dev(wh, x, rows, bias, block, y, ws, ws_bytes, stream);
+    const float* bs[1] = {bias};
+    float* ys[1] = {y};
+    return mimg_linear_a8_group_dev(&wh, 1, x, rows, bs, block, ys, ws, ws_bytes, stream);
 }
 
 int mimg_dequantize_dev(uint32_t dtype, const void* src, uint64_t len, float* dst, int64_t n, void* stream) {

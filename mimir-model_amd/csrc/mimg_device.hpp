@@ -120,3 +120,9 @@ __device__ __forceinline__ Q4KScales q4k_scales(uint32_t S0, uint32_t S1, uint32
 __device__ __forceinline__ uint32_t byte_of(uint64_t v, int j) { return (uint32_t)(v >> (8 * j)) & 0xFFu; }
 
 }  // namespace mimg
+
+#include "quant_rne.hpp"
+
+namespace mimg {
+
+}  // namespace mimg

@@ -43,11 +43,18 @@ hipError_t launch_quantize_act(const float* x, int64_t rows, int64_t K, int bloc
 hipError_t launch_weight_refusals(uint32_t dt, const uint8_t* w, int64_t n, int64_t k, uint8_t* wref,
                                   hipStream_t stream);
 
-// y[i*N+j] for act rows [0, rows) (rows <= 8 per launch, `total_rows` is the
-// row count of the whole call, which selects the float32 fallback's order).
-hipError_t launch_gemv_a8k(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows,
-                           const float* x, const float* bias, float* y, int64_t y_stride,
+// y_i[r*N_i+j] for act rows r in [0, rows) of up to three matrices of one
+// dtype and K (rows <= 8 per launch; `total_rows` is the row count of the
+// whole call, which selects the float32 fallback's order).
+hipError_t launch_gemv_a8k(const DevWeight* const* ws, int nmat, const ActPtrs& a, int64_t rows,
+                           int64_t total_rows, const float* x, const float* const* bias, float* const* y,
                            hipStream_t stream);
+
+// One activation row, quantized inside the kernel, against up to three
+// Q4_K/Q6_K matrices with the same K (gemv_fused.hip).
+bool fused_gemv_ok(const DevWeight* const* ws, int nmat);
+hipError_t launch_gemv_a8k_fused(const DevWeight* const* ws, int nmat, const float* x,
+                                 const float* const* bias, float* const* y, hipStream_t stream);
 
 hipError_t launch_gemv_q8_0_a8(const DevWeight& w, const ActPtrs& a, int64_t rows,
                                int64_t total_rows, const float* x, const float* bias, float* y,

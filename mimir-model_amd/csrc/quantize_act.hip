@@ -3,9 +3,8 @@
 // amaxQ8Go/quantQ8Go/sumsQ8Go at q8.go:237-273).
 //
 // Per block: amax = max|x|; the row is refused (ok = 0) if any |x| is NaN or
-// above 2^60; q = RoundToEven(127*f64(x)/f64(amax)) (0 when amax == 0), in
-// float64 with a correctly rounded division, so q is the exact quotient
-// rounded to nearest even; d = f32(amax)/127 (correctly rounded f32
+// above 2^60; q = RoundToEven(127*x/amax) of the exact quotient (0 when
+// amax == 0; quant_rne.hpp); d = f32(amax)/127 (correctly rounded f32
 // division), stored for each run of 32; xs = sum of each run of 32;
 // ys16 = sum of each run of 16 (used by the Q6_K kernels for the bias of
 // 32); dbs = d*f32(xs).
@@ -54,14 +53,9 @@ __global__ __launch_bounds__(1024) void quantize_act_kernel(const float* __restr
         bad |= bbad;
         const float xv[4] = {v.x, v.y, v.z, v.w};
         int qv[4];
-        for (int i = 0; i < 4; i++) {
-            if (lbad || amax == 0.f) {
-                qv[i] = 0;
-            } else {
-                double t = (127.0 * (double)xv[i]) / (double)amax;
-                qv[i] = (int)__builtin_rint(t);
-            }
-        }
+        const bool quant = !bbad && amax > 0.f;
+        const float inv = quant ? 1.0f / amax : 0.f;
+        for (int i = 0; i < 4; i++) qv[i] = quant ? quant_rne(xv[i], amax, inv) : 0;
         uint32_t packed = (uint32_t)(qv[0] & 0xFF) | ((uint32_t)(qv[1] & 0xFF) << 8) |
                           ((uint32_t)(qv[2] & 0xFF) << 16) | ((uint32_t)(qv[3] & 0xFF) << 24);
         *(uint32_t*)(a.q + (int64_t)row * K + e0) = packed;

@@ -41,6 +41,8 @@ SIGNATURES = {
     "mimg_a8_workspace_offsets": (_I, [_I64, _I64, ctypes.POINTER(_U64)]),
     "mimg_quantize_act_dev": (_I, [_P, _I64, _I64, _I, _P, _U64, _P]),
     "mimg_linear_a8_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P, _U64, _P]),
+    "mimg_linear_a8_group_dev": (_I, [ctypes.POINTER(_U64), _I, _P, _I64, ctypes.POINTER(_P), _I,
+                                      ctypes.POINTER(_P), _P, _U64, _P]),
     "mimg_matmul_a8_quantized_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P, _U64, _P]),
     "mimg_linear_f32_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
     "mimg_dequantize_dev": (_I, [_U32, _P, _U64, _P, _I64, _P]),
@@ -173,6 +175,16 @@ def quantize_act_dev(x_ptr, rows, k, block, ws_ptr, ws_bytes, stream):
 def linear_a8_dev(w, x_ptr, rows, bias_ptr, block, y_ptr, ws_ptr, ws_bytes, stream):
     _check(load().mimg_linear_a8_dev(w.handle, _P(x_ptr), rows, _P(bias_ptr) if bias_ptr else None, block,
                                      _P(y_ptr), _P(ws_ptr), ws_bytes, _P(stream)))
+
+
+def linear_a8_group_dev(weights, x_ptr, rows, bias_ptrs, block, y_ptrs, ws_ptr, ws_bytes, stream):
+    """Weights sharing one input (e.g. q, k, v): y_ptrs[i] = x . W_i^T (+ bias)."""
+    n = len(weights)
+    hs = (_U64 * n)(*[w.handle for w in weights])
+    ys = (_P * n)(*[_P(p) for p in y_ptrs])
+    bs = None if bias_ptrs is None else (_P * n)(*[_P(p) if p else None for p in bias_ptrs])
+    _check(load().mimg_linear_a8_group_dev(hs, n, _P(x_ptr), rows, bs, block, ys,
+                                           _P(ws_ptr) if ws_ptr else None, ws_bytes, _P(stream)))
 
 
 def matmul_a8_quantized_dev(w, x_ptr, rows, bias_ptr, block, y_ptr, ws_ptr, ws_bytes, stream):

@@ -236,6 +236,111 @@ def test_linear_a8k_llama_blocks(gpu, oracle):
         assert bits_equal(got, want), (name, first_diff(got, want))
 
 
+# ------------------------------------------- device entry points and groups
+
+def _dev_linear(gpu, weights, x, biases=None, group=True, prequant=False):
+    """Runs weights on x through the device entry points; returns [y_i]."""
+    import hiprt
+
+    rows, k = x.shape
+    xd = hiprt.DeviceBuffer.from_array(x)
+    ws_bytes = gpu.a8_workspace_bytes(rows, k)
+    ws = hiprt.DeviceBuffer(ws_bytes)
+    ys = [hiprt.DeviceBuffer(rows * w.n * 4) for w in weights]
+    bds = [None if b is None else hiprt.DeviceBuffer.from_array(b) for b in (biases or [None] * len(weights))]
+    s = hiprt.Stream()
+    if prequant:
+        gpu.quantize_act_dev(xd.ptr, rows, k, 256, ws.ptr, ws_bytes, s.handle)
+        for w, y, b in zip(weights, ys, bds):
+            gpu.matmul_a8_quantized_dev(w, xd.ptr, rows, b.ptr if b else None, 256, y.ptr, ws.ptr, ws_bytes, s.handle)
+    elif group:
+        gpu.linear_a8_group_dev(weights, xd.ptr, rows, [b.ptr if b else 0 for b in bds], 256,
+                                [y.ptr for y in ys], ws.ptr, ws_bytes, s.handle)
+    else:
+        for w, y, b in zip(weights, ys, bds):
+            gpu.linear_a8_dev(w, xd.ptr, rows, b.ptr if b else None, 256, y.ptr, ws.ptr, ws_bytes, s.handle)
+    s.sync()
+    return [y.download(np.float32).reshape(rows, w.n) for y, w in zip(ys, weights)]
+
+
+@pytest.mark.parametrize("rows", [1, 3])
+def test_group_qkv_bitexact(gpu, oracle, rows):
+    """q, k (Q4_K) and v (Q6_K) sharing one input in one grouped call (a single
+    fused launch at one row) equal the separate reference products."""
+    k = 4096
+    specs = [(Q4_K, 512, 21), (Q4_K, 128, 22), (Q6_K, 128, 23)]
+    wbs = [_weights(oracle, dt, n, k, seed) for dt, n, seed in specs]
+    W = [gpu.Weight(wb, dt, n, k) for wb, (dt, n, _) in zip(wbs, specs)]
+    x = oracle.synthetic_acts(rows, k, seed=24)
+    bias = [np.random.default_rng(i).standard_normal(n).astype(np.float32) for i, (_, n, _) in enumerate(specs)]
+    got = _dev_linear(gpu, W, x, biases=[bias[0], None, bias[2]])
+    for i, ((dt, n, _), wb) in enumerate(zip(specs, wbs)):
+        want = oracle.linear_a8(x, wb, dt, n, k, bias=bias[i] if i != 1 else None, block=256)
+        assert bits_equal(got[i], want), (i, first_diff(got[i], want))
+    for w in W:
+        w.release()
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K])
+@pytest.mark.parametrize("n,k", [(300, 14336), (4100, 4096), (7, 256)])
+def test_pairs_kernel_one_row_bitexact(gpu, oracle, dt, n, k):
+    """The pre-quantized path (quantize launch + pair kernel) at one row."""
+    wb = _weights(oracle, dt, n, k, seed=31)
+    W = gpu.Weight(wb, dt, n, k)
+    x = oracle.synthetic_acts(1, k, seed=32)
+    got = _dev_linear(gpu, [W], x, prequant=True)[0]
+    want = oracle.linear_a8(x, wb, dt, n, k, block=256)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K])
+def test_fused_refusals_large_k(gpu, oracle, dt):
+    """The fused one-row kernel at K = 14336 with a refused weight row, then
+    with a refused activation row (all products on the float32 path)."""
+    n, k = 96, 14336
+    wb = bytearray(_weights(oracle, dt, n, k, seed=33).tobytes())
+    rb = len(wb) // n
+    o = rb * 40 + 3 * (210 if dt == Q6_K else 144) + (208 if dt == Q6_K else 0)
+    wb[o:o + 2] = b"\x00\xfc"  # -inf
+    wb = np.frombuffer(bytes(wb), np.uint8)
+    W = gpu.Weight(wb, dt, n, k)
+    bias = np.random.default_rng(5).standard_normal(n).astype(np.float32)
+    x = oracle.synthetic_acts(1, k, seed=34)
+    got = _dev_linear(gpu, [W], x, biases=[bias], group=False)[0]
+    want = oracle.linear_a8(x, wb, dt, n, k, bias=bias, block=256)
+    assert bits_equal(got, want), first_diff(got, want)
+    x[0, 9999] = np.float32(3e19)  # above 2^60: the row is refused
+    got = _dev_linear(gpu, [W], x, biases=[bias], group=False)[0]
+    want = oracle.linear_a8(x, wb, dt, n, k, bias=bias, block=256)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+
+
+def test_fused_quantizer_ties(gpu, oracle):
+    """Activations on exact half-integer steps (127 x / amax = n + 1/2) and
+    next to them: the in-kernel quantizer must round exactly as the reference."""
+    k, n = 1024, 64
+    wb = _weights(oracle, Q4_K, n, k, seed=35)
+    W = gpu.Weight(wb, Q4_K, n, k)
+    rng = np.random.default_rng(36)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    for b in range(k // 256):
+        amax = np.float32(127 * 2.0 ** rng.integers(-3, 4))  # amax/127 a power of two: exact ties exist
+        blk = x[0, 256 * b:256 * b + 256]
+        blk[:] = np.clip(blk, -amax, amax)
+        blk[0] = amax
+        step = amax / np.float32(127)
+        for i, h in enumerate(np.arange(-20.5, 21.5, 1.0)):
+            blk[1 + i] = np.float32(h) * step
+            blk[100 + i] = np.nextafter(np.float32(h) * step, np.float32(np.inf))
+            blk[150 + i] = np.nextafter(np.float32(h) * step, np.float32(-np.inf))
+    got = _dev_linear(gpu, [W], x, group=False)[0]
+    want = oracle.linear_a8(x, wb, Q4_K, n, k, block=256)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+
+
 # ----------------------------------------------- Q8_0 x blocks of 32 (a8.v1)
 
 @pytest.mark.parametrize("rows", [1, 4, 8, 11])
