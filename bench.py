@@ -146,7 +146,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
-    ap.add_argument("--roofline-launches", type=int, default=128)
+    ap.add_argument("--roofline-replays", type=int, default=8,
+                    help="replays of the graph of --rotate single-kernel launches timed for the roofline")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -212,27 +213,32 @@ def main():
     # (14336 x 4096, 33 MB), per-launch HIP events on the launch stream,
     # over distinct rotation copies so every launch reads from HBM.
     def per_launch(name):
-        """One call on one matrix, timed alone (HIP events on the stream the
-        kernel runs on). At M = 1 it is the single fused launch, whose
-        algorithmic bytes are the weights, x (f32) and y (f32); otherwise the
-        pre-quantized product launch alone (launch_bytes)."""
+        """The GEMV kernel alone on one matrix: activations quantized once
+        beforehand, then a HIP graph of `rotate` back-to-back launches of the
+        pair kernel (one per rotation copy, so every launch reads its
+        weights from HBM), replayed --roofline-replays times between two
+        events on the launch stream. Returns the average time per launch
+        (graph time / launches, so the small gaps between kernels are
+        included), the algorithmic bytes per launch and their rate."""
         _, n, k, dt, _, inp = next(c for c in CFG1 if c[0] == name)
-        evs = [(hiprt.Event(), hiprt.Event()) for _ in range(args.roofline_launches)]
-        if M > 1:
-            mimg.quantize_act_dev(xd[inp].ptr, M, k, 256, ws[inp].ptr, ws_bytes[inp], stream.handle)
-        for i, (a, b) in enumerate(evs):
-            a.record(stream)
-            if M == 1:
-                mimg.linear_a8_dev(layers[i % args.rotate][name], xd[inp].ptr, M, None, 256, yd[name].ptr,
-                                   ws[inp].ptr, ws_bytes[inp], stream.handle)
-            else:
-                mimg.matmul_a8_quantized_dev(layers[i % args.rotate][name], xd[inp].ptr, M, None, 256,
+        mimg.quantize_act_dev(xd[inp].ptr, M, k, 256, ws[inp].ptr, ws_bytes[inp], stream.handle)
+
+        def launches():
+            for l in range(args.rotate):
+                mimg.matmul_a8_quantized_dev(layers[l][name], xd[inp].ptr, M, None, 256,
                                              yd[name].ptr, ws[inp].ptr, ws_bytes[inp], stream.handle)
-            b.record(stream)
-        stream.sync()
-        ts = np.array([a.elapsed_ms(b) for a, b in evs[4:]])
-        us = float(np.mean(ts)) * 1e3
-        nbytes = weight_bytes(n, k, dt) + k * 4 + n * 4 if M == 1 else launch_bytes(n, k, dt, M)
+
+        g = hiprt.Graph(stream, launches)
+        for _ in range(2):
+            g.launch(stream)
+        a, b = hiprt.Event(), hiprt.Event()
+        a.record(stream)
+        for _ in range(args.roofline_replays):
+            g.launch(stream)
+        b.record(stream)
+        b.sync()
+        us = a.elapsed_ms(b) * 1e3 / (args.roofline_replays * args.rotate)
+        nbytes = launch_bytes(n, k, dt, M)
         return us, nbytes, nbytes / (us * 1e-6) / 1e9
 
     g_us, g_bytes, g_gbs = per_launch("gate")
@@ -240,13 +246,15 @@ def main():
     log(f"  gate GEMV (Q4_K 14336x4096): {g_us:.2f} us/launch, {g_gbs:.0f} GB/s; "
         f"down GEMV (Q6_K 4096x14336): {d_us:.2f} us/launch, {d_gbs:.0f} GB/s")
 
+    # HBM bytes per launch of the same kernel at the same shape, from the
+    # rocprofv3 FETCH_SIZE / WRITE_SIZE passes summarised in profiles/ (the
+    # counters cannot be read from inside this process).
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "gemv_q4k_gate_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", f"gemv_pairs_q4k_gate_m{M}_traffic.md")
     if os.path.exists(tpath):
-        try:
-            traffic = json.load(open(tpath)).get("bytes_per_launch")
-        except (OSError, ValueError):
-            traffic = None
+        for line in open(tpath):
+            if line.startswith("bytes_per_launch:"):
+                traffic = int(line.split(":", 1)[1].strip())
 
     result = {
         "metric": METRIC,
@@ -277,8 +285,7 @@ def main():
             "unit": "GB/s",
             "frac": round(g_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": ("gemv_a8k_fused_kernel (quantize+GEMV, Q4_K, M=1)" if M == 1
-                       else f"gemv_a8k_pairs_kernel<Q4_K,M={M}>") + " at 14336x4096 (gate/up)",
+            "kernel": f"gemv_a8k_pairs_kernel<Q4_K,M={M}> at 14336x4096 (gate/up), pre-quantized activations",
             "launch_bytes": g_bytes,
             "avg_launch_us": round(g_us, 3),
             "q6k_down": {"avg_launch_us": round(d_us, 3), "launch_bytes": d_bytes, "achieved": round(d_gbs, 1)},

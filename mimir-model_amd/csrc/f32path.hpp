@@ -78,44 +78,78 @@ __device__ __forceinline__ float hsum_group8(float y0, float y1, float y2, float
 }
 
 // The float32 dot product of one weight row (K elements of dtype DT) with x,
-// in the reference's order; called by all eight lanes of a group.
+// in the reference's order; called by all eight lanes of a group. It serves
+// refused rows only, so it is written for few live registers (loops kept
+// rolled, each chunk's scales decoded once) rather than speed: it is inlined
+// into the 8-bit kernels and must not raise their register count.
 template <uint32_t DT>
 __device__ float f32dot_g8(const uint8_t* row, const float* x, int64_t K, bool fused) {
     const int l = threadIdx.x & 7;
     float Y[4] = {0.f, 0.f, 0.f, 0.f};
     if (!fused) {
+#pragma unroll 1
         for (int64_t s = 0; s < K / 32; s++)
+#pragma unroll
             for (int r = 0; r < 4; r++) {
                 int64_t e = 32 * s + 8 * r + l;
                 Y[r] = __builtin_fmaf(x[e], decode_weight<DT>(row, e), Y[r]);
             }
     } else if (DT == DT_Q4_K) {
-        for (int64_t b = 0; b < K / 256; b++)
-            for (int c = 0; c < 4; c++)
-                for (int st = 0; st < 4; st++) {
-                    int ra = (st & 1) ? 2 : 0;
-                    int i = 8 * st + l;
-                    const uint8_t* blk = row + b * Q4K_BYTES;
-                    float wl = q4k_weight(blk, 64 * c + i);
-                    float wh = q4k_weight(blk, 64 * c + 32 + i);
-                    Y[ra] = __builtin_fmaf(wl, x[256 * b + 64 * c + i], Y[ra]);
-                    Y[ra + 1] = __builtin_fmaf(wh, x[256 * b + 64 * c + 32 + i], Y[ra + 1]);
+#pragma unroll 1
+        for (int64_t b = 0; b < K / 256; b++) {
+            const uint8_t* blk = row + b * Q4K_BYTES;
+            const float d = f16_to_f32(load_u16(blk)), dmin = f16_to_f32(load_u16(blk + 2));
+#pragma unroll 1
+            for (int c = 0; c < 4; c++) {
+                // chunk c: sub-blocks 2c (low nibbles) and 2c+1 (high nibbles)
+                const uint8_t* s = blk + 4;
+                uint32_t sc0, m0, sc1, m1;
+                if (c < 2) {
+                    sc0 = s[2 * c] & 63, m0 = s[2 * c + 4] & 63;
+                    sc1 = s[2 * c + 1] & 63, m1 = s[2 * c + 5] & 63;
+                } else {
+                    const int j0 = 2 * c, j1 = 2 * c + 1;
+                    sc0 = (s[j0 + 4] & 0xF) | ((s[j0 - 4] >> 6) << 4), m0 = (s[j0 + 4] >> 4) | ((s[j0] >> 6) << 4);
+                    sc1 = (s[j1 + 4] & 0xF) | ((s[j1 - 4] >> 6) << 4), m1 = (s[j1 + 4] >> 4) | ((s[j1] >> 6) << 4);
                 }
+                const float s0 = d * (float)sc0, o0 = dmin * (float)m0;
+                const float s1 = d * (float)sc1, o1 = dmin * (float)m1;
+                const uint8_t* q = blk + 16 + 32 * c;
+                const float* xc = x + 256 * b + 64 * c;
+#pragma unroll 1
+                for (int st = 0; st < 4; st++) {
+                    const int i = 8 * st + l, ra = (st & 1) ? 2 : 0;
+                    const uint32_t byte = q[i];
+                    const float wl = s0 * (float)(byte & 0xF) - o0;
+                    const float wh = s1 * (float)(byte >> 4) - o1;
+                    Y[ra] = __builtin_fmaf(wl, xc[i], Y[ra]);
+                    Y[ra + 1] = __builtin_fmaf(wh, xc[32 + i], Y[ra + 1]);
+                }
+            }
+        }
     } else if (DT == DT_Q6_K) {
+#pragma unroll 1
         for (int64_t b = 0; b < K / 256; b++)
+#pragma unroll 1
             for (int h = 0; h < 2; h++)
+#pragma unroll 1
                 for (int st = 0; st < 4; st++)
+#pragma unroll
                     for (int p = 0; p < 4; p++) {
                         int e = 128 * h + 32 * p + 8 * st + l;
                         float w = q6k_weight(row + b * Q6K_BYTES, e);
                         Y[p] = __builtin_fmaf(w, x[256 * b + e], Y[p]);
                     }
     } else {
-        for (int64_t b = 0; b < K / 32; b++)
+#pragma unroll 1
+        for (int64_t b = 0; b < K / 32; b++) {
+            const float d = f16_to_f32(load_u16(row + b * Q80_BYTES));
+#pragma unroll
             for (int r = 0; r < 4; r++) {
-                float w = q8_0_weight(row + b * Q80_BYTES, 8 * r + l);
+                const float w = d * (float)(int8_t)row[b * Q80_BYTES + 2 + 8 * r + l];
                 Y[r] = __builtin_fmaf(w, x[32 * b + 8 * r + l], Y[r]);
             }
+        }
     }
     return hsum_group8(Y[0], Y[1], Y[2], Y[3]);
 }
