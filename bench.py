@@ -246,6 +246,17 @@ def main():
     log(f"  gate GEMV (Q4_K 14336x4096): {g_us:.2f} us/launch, {g_gbs:.0f} GB/s; "
         f"down GEMV (Q6_K 4096x14336): {d_us:.2f} us/launch, {d_gbs:.0f} GB/s")
 
+    # The host-memory entry point a cgo caller uses (x copied in, y copied
+    # back, the call returns when y is in host memory): PCIe- and
+    # synchronisation-inclusive time per gate call, for reference only.
+    hx = xs[2]
+    mimg.dequant_matmul_a8(layers[0]["gate"], hx)
+    t0 = time.perf_counter()
+    for i in range(args.rotate * 2):
+        mimg.dequant_matmul_a8(layers[i % args.rotate]["gate"], hx)
+    host_us = (time.perf_counter() - t0) * 1e6 / (args.rotate * 2)
+    log(f"  host-memory call (gate, x and y over PCIe, synchronous): {host_us:.1f} us/call")
+
     # HBM bytes per launch of the same kernel at the same shape, from the
     # rocprofv3 FETCH_SIZE / WRITE_SIZE passes summarised in profiles/ (the
     # counters cannot be read from inside this process).
@@ -289,6 +300,11 @@ def main():
             "launch_bytes": g_bytes,
             "avg_launch_us": round(g_us, 3),
             "q6k_down": {"avg_launch_us": round(d_us, 3), "launch_bytes": d_bytes, "achieved": round(d_gbs, 1)},
+        },
+        "host_api": {
+            "entry": "mimg_dequant_matmul_a8 (gate, host x and y)",
+            "us_per_call": round(host_us, 2),
+            "GB_per_s": round(launch_bytes(CFG1[4][1], CFG1[4][2], Q4_K, M) / (host_us * 1e-6) / 1e9, 1),
         },
     }
     if not args.no_cpu:
