@@ -73,11 +73,20 @@ struct KQ {
     static constexpr int S16PB = DT == DT_Q4_K ? 8 : 16;  // s16 entries per block
 };
 
-template <uint32_t DT, int M, int R>
+// Activation staging: with one activation row and K <= STAGE_MAXK the
+// workgroup copies the row's quants, block sums and scales into LDS behind
+// the pair table before computing, so the compute phase reads no global
+// memory (global reads issued after the weight loads would wait for all of
+// them, the load counter being in order).
+constexpr int STAGE_MAXK = 16384;
+
+template <uint32_t DT, int M, int R, bool STAGE>
 __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
     i32x4* part = (i32x4*)smem;  // [R][nb][M]: S, M term, bits(d*dx), bits(dmin*dx)
     constexpr int U = 4;
+    constexpr int S16PB = KQ<DT>::S16PB;
+    static_assert(!STAGE || M == 1, "staging holds one activation row");
     // This workgroup's matrix of the launch.
     int mi = 0;
     if (A.nmat > 1 && (int)blockIdx.x >= A.mat[1].tile0) mi = 1;
@@ -89,38 +98,89 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
     A.y = P.y;
     A.N = P.N;
     A.y_stride = P.N;
-    const int g = threadIdx.x >> 3, l = threadIdx.x & 7;
+    const int g = threadIdx.x >> 3, l = threadIdx.x & 7, t = threadIdx.x;
     const int nb = A.nb, row0 = ((int)blockIdx.x - P.tile0) * R, npairs = R * nb;
     const int64_t K = A.K, R32 = K / 32, R16 = K / 16;
 
-    for (int p0 = g; p0 < npairs; p0 += 32 * U) {
-        if (DT == DT_Q4_K) {
-            u32x4 hdr[U], qv[U];
+    // Staged row: q [K] int8, s16 [nb*S16PB] int16, dx [nb] f32.
+    int8_t* sq = (int8_t*)(smem + (size_t)R * nb * M * 16);
+    int16_t* ss = (int16_t*)(sq + K);
+    float* sdx = (float*)(ss + nb * S16PB);
+    const int nq = (int)(K / 16), ns = nb * S16PB / 8;
+    if constexpr (STAGE) {
+        // Straight into LDS (global_load_lds: lane i of a wave writes
+        // bytes [16i, 16i+16) after the wave's base), no registers held.
+        const int wave = t >> 6;
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int p = p0 + 32 * u;
-                if (p < npairs) {
-                    const int r = p / nb, b = p - r * nb;
-                    const int row = min(row0 + r, A.N - 1);
-                    const uint8_t* blk = A.W + (int64_t)row * A.rb + (int64_t)b * Q4K_BYTES;
+        for (int j = 0; j < STAGE_MAXK / 16 / 256; j++)
+            if (t + 256 * j < nq)
+                __builtin_amdgcn_global_load_lds((const u32x4*)A.q + t + 256 * j,
+                                                 (__attribute__((address_space(3))) void*)(sq + 1024 * wave + 4096 * j),
+                                                 16, 0, 0);
+        if (t < ns)
+            __builtin_amdgcn_global_load_lds((const u32x4*)A.s16 + t,
+                                             (__attribute__((address_space(3))) void*)((uint8_t*)ss + 1024 * wave), 16, 0, 0);
+        if (t < nb)
+            __builtin_amdgcn_global_load_lds(A.d32 + 8 * t, (__attribute__((address_space(3))) void*)(sdx + 64 * wave),
+                                             4, 0, 0);
+    }
+
+    // With staging the loop's trip count is the same for every group (the
+    // staging barrier sits in its first iteration).
+    const int pstart = STAGE ? 0 : g, poff = STAGE ? g : 0;
+    for (int p0 = pstart; p0 < npairs; p0 += 32 * U) {
+        // The weights of this group's next U pairs, all in flight.
+        u32x4 hdr[U], qv[U];
+        Q6KRaw raw[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int p = p0 + poff + 32 * u;
+            if (p < npairs) {
+                const int r = p / nb, b = p - r * nb;
+                const int row = min(row0 + r, A.N - 1);
+                const uint8_t* blk = A.W + (int64_t)row * A.rb + (int64_t)b * KQ<DT>::BYTES;
+                if constexpr (DT == DT_Q4_K) {
                     hdr[u] = *(const u32x4*)blk;
                     qv[u] = *(const u32x4*)(blk + 16 + 16 * l);
+                } else {
+                    raw[u] = q6k_load(blk, l);
                 }
             }
+        }
+        if constexpr (STAGE) {
+            if (p0 == 0) {
+                // The staged row and this wave's first weights have landed.
+                __builtin_amdgcn_s_waitcnt(0);
+                __syncthreads();
+            }
+        }
 #pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int p = p0 + 32 * u;
-                if (p >= npairs) break;  // uniform within the group
-                const int r = p / nb, b = p - r * nb;
+        for (int u = 0; u < U; u++) {
+            const int p = p0 + poff + 32 * u;
+            if (p >= npairs) break;  // uniform within the group
+            const int r = p / nb, b = p - r * nb;
+            if constexpr (DT == DT_Q4_K) {
                 const Q4KLane w = q4k_lane(hdr[u], qv[u], l);
 #pragma unroll
                 for (int m = 0; m < M; m++) {
-                    const int8_t* yb = A.q + m * K + (int64_t)b * 256 + w.yoff;
-                    const u32x4 ya = *(const u32x4*)yb;
-                    const u32x4 yh = *(const u32x4*)(yb + 32);
+                    u32x4 ya, yh;
+                    int xs;
+                    float dx;
+                    if constexpr (STAGE) {
+                        const int8_t* yb = sq + 256 * b + w.yoff;
+                        ya = *(const u32x4*)yb;
+                        yh = *(const u32x4*)(yb + 32);
+                        xs = ss[8 * b + l];
+                        dx = sdx[b];
+                    } else {
+                        const int8_t* yb = A.q + m * K + (int64_t)b * 256 + w.yoff;
+                        ya = *(const u32x4*)yb;
+                        yh = *(const u32x4*)(yb + 32);
+                        xs = A.s16[m * R32 + 8 * b + l];
+                        dx = A.d32[m * R32 + 8 * b];
+                    }
                     const int S = group8_sum(q4k_part(w, ya, yh));
-                    const int Mt = group8_sum(w.mm * (int)A.s16[m * R32 + 8 * b + l]);
-                    const float dx = A.d32[m * R32 + 8 * b];
+                    const int Mt = group8_sum(w.mm * xs);
                     if (l == 0) {
                         i32x4 v;
                         v.x = S;
@@ -130,32 +190,30 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
                         part[(r * nb + b) * M + m] = v;
                     }
                 }
-            }
-        } else {
-            Q6KRaw raw[U];
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int p = p0 + 32 * u;
-                if (p < npairs) {
-                    const int r = p / nb, b = p - r * nb;
-                    const int row = min(row0 + r, A.N - 1);
-                    raw[u] = q6k_load(A.W + (int64_t)row * A.rb + (int64_t)b * Q6K_BYTES, l);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < U; u++) {
-                const int p = p0 + 32 * u;
-                if (p >= npairs) break;
-                const int r = p / nb, b = p - r * nb;
+            } else {
                 const Q6KLane w = q6k_lane(raw[u], l);
 #pragma unroll
                 for (int m = 0; m < M; m++) {
-                    const int8_t* yb = A.q + m * K + (int64_t)b * 256;
-                    const u32x4 ya = *(const u32x4*)(yb + w.eL);
-                    const u32x4 yh = *(const u32x4*)(yb + w.eL + 64);
-                    const int16_t* ys = A.s16 + m * R16 + 16 * b;
-                    const int S = group8_sum(q6k_part(w, ya, yh, ys[w.eL >> 4], ys[(w.eL + 64) >> 4]));
-                    const float dx = A.d32[m * R32 + 8 * b];
+                    u32x4 ya, yh;
+                    int ysL, ysH;
+                    float dx;
+                    if constexpr (STAGE) {
+                        const int8_t* yb = sq + 256 * b;
+                        ya = *(const u32x4*)(yb + w.eL);
+                        yh = *(const u32x4*)(yb + w.eL + 64);
+                        ysL = ss[16 * b + (w.eL >> 4)];
+                        ysH = ss[16 * b + ((w.eL + 64) >> 4)];
+                        dx = sdx[b];
+                    } else {
+                        const int8_t* yb = A.q + m * K + (int64_t)b * 256;
+                        ya = *(const u32x4*)(yb + w.eL);
+                        yh = *(const u32x4*)(yb + w.eL + 64);
+                        const int16_t* ys = A.s16 + m * R16 + 16 * b;
+                        ysL = ys[w.eL >> 4];
+                        ysH = ys[(w.eL + 64) >> 4];
+                        dx = A.d32[m * R32 + 8 * b];
+                    }
+                    const int S = group8_sum(q6k_part(w, ya, yh, ysL, ysH));
                     if (l == 0) {
                         i32x4 v;
                         v.x = S;
@@ -171,7 +229,6 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
     __syncthreads();
 
     // The serial float chain, one lane per (weight row, activation row).
-    const int t = threadIdx.x;
     if (t < R * M) {
         const int r = t / M, m = t - r * M, row = row0 + r;
         if (row < A.N && A.wref[row] == 0 && A.ok[m]) {
@@ -204,8 +261,16 @@ static hipError_t launch_pairs_r(GemvArgs A, hipStream_t stream) {
         A.mat[i].tile0 = tiles;
         tiles += (A.mat[i].N + R - 1) / R;
     }
-    const size_t lds = (size_t)R * A.nb * M * 16;
-    hipLaunchKernelGGL((gemv_a8k_pairs_kernel<DT, M, R>), dim3((unsigned)tiles), dim3(256), lds, stream, A);
+    size_t lds = (size_t)R * A.nb * M * 16;
+    if constexpr (M == 1) {
+        if (A.K <= STAGE_MAXK) {
+            lds += (size_t)A.K + (size_t)A.nb * KQ<DT>::S16PB * 2 + (size_t)A.nb * 4;
+            hipLaunchKernelGGL((gemv_a8k_pairs_kernel<DT, M, R, true>), dim3((unsigned)tiles), dim3(256), lds,
+                               stream, A);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((gemv_a8k_pairs_kernel<DT, M, R, false>), dim3((unsigned)tiles), dim3(256), lds, stream, A);
     return hipGetLastError();
 }
 

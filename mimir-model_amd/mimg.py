@@ -15,7 +15,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmimg.so")
+# MIMG_LIB selects another build of the library (e.g. one made with other
+# compile-time tile parameters).
+LIB_PATH = os.environ.get("MIMG_LIB") or os.path.join(HERE, "libmimg.so")
 
 F32, Q8_0, Q4_K, Q6_K = 1, 64, 66, 67
 BLOCK_ELEMS = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
