@@ -39,45 +39,43 @@ struct QuantLds {
     int16_t* ys16;   // [K/16]
 };
 
-// Quantizes one row of K f32 values into LDS; 16 threads (one DPP row) per
-// block of 256, 16 elements per thread. Returns this thread's refusal flag.
-__device__ __forceinline__ bool quantize_row_lds(const float* __restrict__ x, int nb, const QuantLds& Q) {
-    const int t = threadIdx.x, j = t & 15;
+// Quantizes block b of the row into LDS from this thread's 16 values (16
+// threads, one DPP row, per block of 256; thread j of the row holds
+// elements 16j..16j+15). Returns this thread's refusal flag.
+__device__ __forceinline__ bool quantize_block_lds(const float4 (&v)[4], int b, int j, const QuantLds& Q) {
+    const float xv[16] = {v[0].x, v[0].y, v[0].z, v[0].w, v[1].x, v[1].y, v[1].z, v[1].w,
+                          v[2].x, v[2].y, v[2].z, v[2].w, v[3].x, v[3].y, v[3].z, v[3].w};
+    float m = 0.f;
     bool bad = false;
-    for (int b0 = 0; b0 < nb; b0 += 16) {
-        const int b = b0 + (t >> 4);
-        if (b >= nb) break;  // uniform within the DPP row
-        const float4* xp = (const float4*)(x + 256 * b + 16 * j);
-        const float4 v0 = xp[0], v1 = xp[1], v2 = xp[2], v3 = xp[3];
-        const float xv[16] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w,
-                              v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
-        float m = 0.f;
-        bool lbad = false;
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float a = fabsf(xv[i]);
-            lbad |= !(a <= 0x1p60f);
-            m = fmaxf(m, a);
-        }
-        bad |= lbad;
-        const float amax = row16_max(m);
-        const bool quant = amax > 0.f && amax <= 0x1p60f;
-        const float inv = quant ? 1.0f / amax : 0.f;
-        uint32_t w[4] = {0, 0, 0, 0};
-        int s16 = 0;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int q = quant ? quant_rne(xv[i], amax, inv) : 0;
-            s16 += q;
-            w[i >> 2] |= (uint32_t)(q & 0xFF) << (8 * (i & 3));
-        }
-        *(u32x4*)(Q.q + 256 * b + 16 * j) = u32x4{w[0], w[1], w[2], w[3]};
-        const int s32 = s16 + __builtin_amdgcn_mov_dpp(s16, DPP_QUAD_1032, 0xF, 0xF, false);
-        Q.ys16[16 * b + j] = (int16_t)s16;
-        if ((j & 1) == 0) Q.xs[8 * b + (j >> 1)] = (int16_t)s32;
-        if (j == 0) Q.dx[b] = amax / 127.0f;
+    for (int i = 0; i < 16; i++) {
+        const float a = fabsf(xv[i]);
+        bad |= !(a <= 0x1p60f);
+        m = fmaxf(m, a);
     }
+    const float amax = row16_max(m);
+    const bool quant = amax > 0.f && amax <= 0x1p60f;
+    const float inv = quant ? 1.0f / amax : 0.f;
+    uint32_t w[4] = {0, 0, 0, 0};
+    int s16 = 0;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const int q = quant ? quant_rne(xv[i], amax, inv) : 0;
+        s16 += q;
+        w[i >> 2] |= (uint32_t)(q & 0xFF) << (8 * (i & 3));
+    }
+    *(u32x4*)(Q.q + 256 * b + 16 * j) = u32x4{w[0], w[1], w[2], w[3]};
+    const int s32 = s16 + __builtin_amdgcn_mov_dpp(s16, DPP_QUAD_1032, 0xF, 0xF, false);
+    Q.ys16[16 * b + j] = (int16_t)s16;
+    if ((j & 1) == 0) Q.xs[8 * b + (j >> 1)] = (int16_t)s32;
+    if (j == 0) Q.dx[b] = amax / 127.0f;
     return bad;
+}
+
+__device__ __forceinline__ void load_x16(const float* __restrict__ x, int b, int j, float4 (&v)[4]) {
+    const float4* xp = (const float4*)(x + 256 * b + 16 * j);
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = xp[i];
 }
 
 struct FusedMat {
@@ -142,10 +140,20 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
             }
         }
     };
+    // The first 16 blocks of x are loaded before the weights: the load
+    // counter retires in order, so the quantizer, which needs only x, then
+    // waits for x alone while the weights are still in flight.
+    const int t = threadIdx.x, j = t & 15, bq = t >> 4;
+    float4 xv[4];
+    load_x16(A.x, min(bq, nb - 1), j, xv);
     load(g);
 
     // 2. Quantize x into LDS while the weights arrive.
-    const bool bad = quantize_row_lds(A.x, nb, Q);
+    bool bad = bq < nb ? quantize_block_lds(xv, bq, j, Q) : false;
+    for (int b = bq + 16; b < nb; b += 16) {  // rows longer than 4096
+        load_x16(A.x, b, j, xv);
+        bad |= quantize_block_lds(xv, b, j, Q);
+    }
     const bool row_refused = __syncthreads_or(bad ? 1 : 0) != 0;
 
     // 3. Exact block sums of this workgroup's pairs.
@@ -180,7 +188,6 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     __syncthreads();
 
     // 4. The serial float chain of each row, in block order.
-    const int t = threadIdx.x;
     if (t < R) {
         const int row = row0 + t;
         if (row < F.N && F.wref[row] == 0 && !row_refused) {

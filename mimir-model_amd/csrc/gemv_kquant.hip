@@ -132,19 +132,21 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
         // The weights of this group's next U pairs, all in flight.
         u32x4 hdr[U], qv[U];
         Q6KRaw raw[U];
+        // Unconditional (clamped) loads in straight-line code: a load in a
+        // conditional block makes the compiler wait for every earlier load
+        // before it (the blocks reuse registers), which would put the U
+        // pairs' HBM round trips in series.
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int p = p0 + poff + 32 * u;
-            if (p < npairs) {
-                const int r = p / nb, b = p - r * nb;
-                const int row = min(row0 + r, A.N - 1);
-                const uint8_t* blk = A.W + (int64_t)row * A.rb + (int64_t)b * KQ<DT>::BYTES;
-                if constexpr (DT == DT_Q4_K) {
-                    hdr[u] = *(const u32x4*)blk;
-                    qv[u] = *(const u32x4*)(blk + 16 + 16 * l);
-                } else {
-                    raw[u] = q6k_load(blk, l);
-                }
+            const int p = min(p0 + poff + 32 * u, npairs - 1);
+            const int r = p / nb, b = p - r * nb;
+            const int row = min(row0 + r, A.N - 1);
+            const uint8_t* blk = A.W + (int64_t)row * A.rb + (int64_t)b * KQ<DT>::BYTES;
+            if constexpr (DT == DT_Q4_K) {
+                hdr[u] = *(const u32x4*)blk;
+                qv[u] = *(const u32x4*)(blk + 16 + 16 * l);
+            } else {
+                raw[u] = q6k_load(blk, l);
             }
         }
         if constexpr (STAGE) {
@@ -156,8 +158,12 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int p = p0 + poff + 32 * u;
-            if (p >= npairs) break;  // uniform within the group
+            // Every loaded pair is consumed (a clamped duplicate past the end
+            // is computed and not stored), so no load is left pending across
+            // the loop's back edge, which would again cost a full wait.
+            const int pu = p0 + poff + 32 * u;
+            const bool store = pu < npairs;
+            const int p = min(pu, npairs - 1);
             const int r = p / nb, b = p - r * nb;
             if constexpr (DT == DT_Q4_K) {
                 const Q4KLane w = q4k_lane(hdr[u], qv[u], l);
@@ -181,7 +187,7 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
                     }
                     const int S = group8_sum(q4k_part(w, ya, yh));
                     const int Mt = group8_sum(w.mm * xs);
-                    if (l == 0) {
+                    if (l == 0 && store) {
                         i32x4 v;
                         v.x = S;
                         v.y = Mt;
@@ -214,7 +220,7 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
                         dx = A.d32[m * R32 + 8 * b];
                     }
                     const int S = group8_sum(q6k_part(w, ya, yh, ysL, ysH));
-                    if (l == 0) {
+                    if (l == 0 && store) {
                         i32x4 v;
                         v.x = S;
                         v.y = 0;

@@ -53,11 +53,14 @@ __device__ __forceinline__ int q4k_part(const Q4KLane& w, const u32x4& ya, const
 // Raw loads of one lane's share of a Q6_K block (2-byte aligned blocks):
 // lane l = 4h + p takes ql bytes 64h+16p..+16 (elements eL..eL+15 in their
 // low nibbles and eH = eL+64.. in their high nibbles, eL = 128h+32(p/2)+16(p%2)),
-// the qh bytes 32h+16(p%2)..+16 and the block's scales and d.
+// the qh bytes 32h+16(p%2)..+16 and the block's scales and d. The 16-byte
+// runs are kept as the five aligned dwords that hold them (both runs share
+// the block's misalignment); q6k_lane shifts them into place, so nothing
+// here waits for the loads to land.
 struct Q6KRaw {
-    u32x4 ql, qh;
+    uint32_t ql[5], qh[5];
     int scl, sch;
-    uint32_t dbits;
+    uint32_t dbits, shift;
 };
 
 // Seven loads per lane: ql and qh as 5 aligned dwords each, the two int8
@@ -66,8 +69,12 @@ struct Q6KRaw {
 __device__ __forceinline__ Q6KRaw q6k_load(const uint8_t* blk, int l) {
     const int h = l >> 2, p = l & 3, idx = 2 * (p >> 1) + (p & 1);
     Q6KRaw r;
-    r.ql = load16_a2(blk + 64 * h + 16 * p);
-    r.qh = load16_a2(blk + 128 + 32 * h + 16 * (p & 1));
+    const uint32_t* a = (const uint32_t*)__builtin_align_down(blk + 64 * h + 16 * p, 4);
+    const uint32_t* c = (const uint32_t*)__builtin_align_down(blk + 128 + 32 * h + 16 * (p & 1), 4);
+    const u32x4a4 av = *(const u32x4a4*)a, cv = *(const u32x4a4*)c;
+    r.ql[0] = av.x, r.ql[1] = av.y, r.ql[2] = av.z, r.ql[3] = av.w, r.ql[4] = a[4];
+    r.qh[0] = cv.x, r.qh[1] = cv.y, r.qh[2] = cv.z, r.qh[3] = cv.w, r.qh[4] = c[4];
+    r.shift = (uint32_t)((uintptr_t)blk & 3);
     r.scl = (int)(int8_t)blk[192 + 8 * h + idx];
     r.sch = (int)(int8_t)blk[196 + 8 * h + idx];
     r.dbits = load_u16(blk + 208);
@@ -88,8 +95,12 @@ __device__ __forceinline__ Q6KLane q6k_lane(const Q6KRaw& r, int l) {
     w.d = f16_to_f32(r.dbits);
     w.eL = 128 * h + 32 * pp + 16 * p1;
     const int shL = 2 * pp, shH = 4 + 2 * pp;
-    const uint32_t qlw[4] = {r.ql.x, r.ql.y, r.ql.z, r.ql.w};
-    const uint32_t qhw[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+    uint32_t qlw[4], qhw[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        qlw[k] = __builtin_amdgcn_alignbyte(r.ql[k + 1], r.ql[k], r.shift);
+        qhw[k] = __builtin_amdgcn_alignbyte(r.qh[k + 1], r.qh[k], r.shift);
+    }
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         w.vl[k] = (qlw[k] & 0x0F0F0F0Fu) | (((qhw[k] >> shL) & 0x03030303u) << 4);

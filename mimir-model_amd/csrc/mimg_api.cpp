@@ -218,6 +218,18 @@ bool fused_q8_blocks(uint32_t dt, int block) {
 // The products of up to three weights (same K, each with an 8-bit kernel for
 // `block`) with activations already quantized into `a`: block-256 weights of
 // one dtype share a launch per chunk of 8 rows.
+static int64_t env_or(const char* name, int64_t dflt) {
+    const char* e = getenv(name);
+    return e ? (int64_t)atoll(e) : dflt;
+}
+
+// Workgroups per CU of the tile-looping one-row GEMV (0: one workgroup per
+// tile instead). MIMG_TILES_WPC overrides, for tuning.
+static int64_t tiles_wpc() {
+    static const int64_t v = env_or("MIMG_TILES_WPC", 0);
+    return v;
+}
+
 int matmul_quantized(const Weight* const* w, int count, const float* x, int64_t rows, const float* const* bias,
                      int block, float* const* y, const ActPtrs& a, hipStream_t s) {
     const int64_t K = w[0]->dw.k, R32 = K / 32, R16 = K / 16;
@@ -247,7 +259,10 @@ int matmul_quantized(const Weight* const* w, int count, const float* x, int64_t 
                     done[j] = true;
                     n++;
                 }
-                e = launch_gemv_a8k(dws, n, c, mr, rows, x + r0 * K, bs, ys, s);
+                if (mr == 1 && tiles_wpc() > 0 && gemv_tiles_ok(*dws[0], 1))
+                    e = launch_gemv_a8k_tiles(dws, n, c, rows, x + r0 * K, bs, ys, (int)tiles_wpc(), s);
+                else
+                    e = launch_gemv_a8k(dws, n, c, mr, rows, x + r0 * K, bs, ys, s);
             } else {
                 const int64_t N = w[i]->dw.n;
                 e = launch_gemv_q8_0_a8(w[i]->dw, c, mr, rows, x + r0 * K, bias ? bias[i] : nullptr, y[i] + r0 * N, N, s);
@@ -414,10 +429,6 @@ int mimg_matmul_a8_quantized_dev(uint64_t wh, const float* x, int64_t rows, cons
 // small (q/k/v, o); for long rows or many weight rows a separate quantize
 // launch costs less (measured on MI355X). MIMG_FUSED_MAXK / MIMG_FUSED_MAXN
 // override the limits, for tuning.
-static int64_t env_or(const char* name, int64_t dflt) {
-    const char* e = getenv(name);
-    return e ? (int64_t)atoll(e) : dflt;
-}
 static int64_t fused_max_k() {
     static const int64_t v = env_or("MIMG_FUSED_MAXK", 4096);
     return v;
