@@ -71,6 +71,7 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
 constexpr int DPP_QUAD_1032 = 0xB1;  // lanes [1,0,3,2]
 constexpr int DPP_QUAD_2301 = 0x4E;  // lanes [2,3,0,1]
 constexpr int DPP_HALF_MIRROR = 0x141;
+constexpr int DPP_ROW_MIRROR = 0x140;   // lane i <-> 15-i within a row of 16
 
 __device__ __forceinline__ int dpp_i(int v, int ctrl) {
     switch (ctrl) {
