@@ -230,9 +230,28 @@ static int64_t tiles_wpc() {
     return v;
 }
 
+// Activation rows from which the blocks-of-256 products use the MFMA GEMM
+// instead of the GEMV in chunks of eight rows. MIMG_GEMM_MIN_ROWS
+// overrides, for tuning.
+static int64_t gemm_min_rows() {
+    static const int64_t v = env_or("MIMG_GEMM_MIN_ROWS", 16);
+    return v;
+}
+
 int matmul_quantized(const Weight* const* w, int count, const float* x, int64_t rows, const float* const* bias,
                      int block, float* const* y, const ActPtrs& a, hipStream_t s) {
     const int64_t K = w[0]->dw.k, R32 = K / 32, R16 = K / 16;
+    if (block == 256 && rows >= gemm_min_rows()) {
+        bool all = true;
+        for (int i = 0; i < count; i++) all = all && gemm_a8k_ok(w[i]->dw);
+        if (all) {
+            for (int i = 0; i < count; i++) {
+                hipError_t e = launch_gemm_a8k(w[i]->dw, a, rows, rows, x, bias ? bias[i] : nullptr, y[i], s);
+                if (e != hipSuccess) return fail(MIMG_ERR_HIP, "GEMM launch: %s", hipGetErrorString(e));
+            }
+            return MIMG_OK;
+        }
+    }
     for (int64_t r0 = 0; r0 < rows; r0 += 8) {
         const int64_t mr = rows - r0 < 8 ? rows - r0 : 8;
         ActPtrs c;

@@ -58,6 +58,12 @@ hipError_t launch_gemv_a8k_tiles(const DevWeight* const* ws, int nmat, const Act
                                  const float* x, const float* const* bias, float* const* y, int wgs_per_cu,
                                  hipStream_t stream);
 
+// Many activation rows (already quantized) against one Q4_K/Q6_K matrix,
+// on the int8 matrix cores (gemm_kquant.hip); bit-identical to the GEMV.
+bool gemm_a8k_ok(const DevWeight& w);
+hipError_t launch_gemm_a8k(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows, const float* x,
+                           const float* bias, float* y, hipStream_t stream);
+
 // One activation row, quantized inside the kernel, against up to three
 // Q4_K/Q6_K matrices with the same K (gemv_fused.hip).
 bool fused_gemv_ok(const DevWeight* const* ws, int nmat);

@@ -196,7 +196,24 @@ def test_linear_a8k_special_inputs(gpu, oracle, dt):
 
 
 @pytest.mark.parametrize("dt", [Q4_K, Q6_K])
-@pytest.mark.parametrize("rows", [1, 3, 12])
+@pytest.mark.parametrize("rows,n,k", [(16, 64, 256), (64, 100, 1024), (130, 300, 4096), (257, 129, 2048),
+                                      (128, 1024, 14336)])
+def test_gemm_a8k_bitexact(gpu, oracle, dt, rows, n, k):
+    """Prefill sizes (16 rows and more) run on the int8 MFMA GEMM: ragged
+    row and column counts, one and several 64x128 tiles, K from one block
+    to 56; bit for bit the reference, whose tile kernels equal its one-row
+    kernel (reference amx_test.go:41-141)."""
+    wb = _weights(oracle, dt, n, k, seed=rows + n)
+    x = oracle.synthetic_acts(rows, k, seed=rows + 1)
+    W = gpu.Weight(wb, dt, n, k)
+    got = gpu.dequant_matmul_a8(W, x, block=256)
+    want = oracle.linear_a8(x, wb, dt, n, k, block=256, threads=8)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K])
+@pytest.mark.parametrize("rows", [1, 3, 12, 40])
 def test_linear_a8k_refusals_and_bias(gpu, oracle, dt, rows):
     """Rows of x with NaN/Inf/huge values and rows of w with a non-finite
     block scale take the float32 path (reference interp/fast.go:323-377);
