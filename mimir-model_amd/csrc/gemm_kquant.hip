@@ -10,11 +10,13 @@
 // Q4_K), result tot - off (+ bias), as dotQ8KRef (q8k_test.go:38-102).
 //
 // Exact integer products on int8 MFMA: the scaled weight w = sc*q does not
-// fit int8 (Q4_K up to 945, Q6_K -4096..4064), so it is split as
-// w = 128*hi + lo with lo in [0,127] and hi in [0,7] (Q4_K) or [-32,31]
-// (Q6_K); S = 128*sum(hi*y) + sum(lo*y), each MFMA sum exact in int32
-// (|sum| < 2^31 for 256-element blocks). Q4_K's M term is a third MFMA plane
-// with A = m_s(k).
+// fit int8 (Q4_K up to 945, Q6_K -4096..4064), so it is split in two planes.
+// Q4_K: sc = 8*sh + sl (sh, sl <= 7), planes sh*q and sl*q (each <= 105),
+// S = 8*sum(sh*q*y) + sum(sl*q*y); the planes are the packed nibbles times
+// a constant. Q6_K: w = 128*hi + lo with lo in [0,127], hi in [-32,31],
+// S = 128*sum(hi*y) + sum(lo*y). Each MFMA sum is exact in int32 (|sum| <
+// 2^31 for 256-element blocks). Q4_K's M term is a third MFMA plane with
+// A = m_s(k).
 //
 // Tiling: a 256-thread workgroup owns 64 weight rows x 128 activation rows;
 // wave w takes weight rows 16w..16w+15 (the A operand: lane l holds row
@@ -39,9 +41,18 @@ namespace mimg {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int GM_BN = 64;    // weight rows per workgroup
-constexpr int GM_BM = 128;   // activation rows per workgroup
-constexpr int GM_TM = GM_BM / 16;
+#ifndef MIMG_GEMM_BM
+#define MIMG_GEMM_BM 128
+#endif
+#ifndef MIMG_GEMM_THREADS
+#define MIMG_GEMM_THREADS 512
+#endif
+constexpr int GM_T = MIMG_GEMM_THREADS;   // threads per workgroup (256: one wave per SIMD, 512: two)
+constexpr int GM_BN = 64;                 // weight rows per workgroup (4 waves of 16)
+constexpr int GM_BM = MIMG_GEMM_BM;       // activation rows per workgroup
+constexpr int GM_WM = GM_T / 256;         // waves along the activation rows
+constexpr int GM_TM = GM_BM / 16 / GM_WM; // activation tiles of 16 per wave
+constexpr int GM_ACH = GM_BM * 16 / GM_T; // activation copy instructions per thread per block
 
 template <uint32_t DT>
 struct GemmLayout {
@@ -49,12 +60,13 @@ struct GemmLayout {
     // copied as 9 chunks; Q6_K blocks (2-byte aligned) are copied as the 54
     // aligned dwords that cover them.
     static constexpr int WSLOT = DT == DT_Q4_K ? 144 : 216;
-    static constexpr int WBYTES = DT == DT_Q4_K ? 768 * 16 : 3584 * 4;  // incl. slack for unconditional copies
+    static constexpr int WDMA = DT == DT_Q4_K ? (GM_BN * 9 + GM_T - 1) / GM_T   // copy instructions per
+                                             : (GM_BN * 54 + GM_T - 1) / GM_T;  // thread per block
+    static constexpr int WBYTES = WDMA * GM_T * (DT == DT_Q4_K ? 16 : 4);  // incl. slack for unconditional copies
     static constexpr int ABYTES = GM_BM * 256;
-    static constexpr int DXBYTES = 256 * 4;
+    static constexpr int DXBYTES = GM_T * 4;
     static constexpr int BUF = WBYTES + ABYTES + DXBYTES;
-    static constexpr int WDMA = DT == DT_Q4_K ? 3 : 14;  // copy instructions per thread per block
-    static constexpr int NDMA = WDMA + 8 + 1;
+    static constexpr int NDMA = WDMA + GM_ACH + 1;
 };
 
 struct GemmArgs {
@@ -110,39 +122,39 @@ __device__ __forceinline__ void gm_barrier() {
 template <uint32_t DT>
 __device__ __forceinline__ void gemm_issue_block(const GemmArgs& A, int n0, int m0, int b, uint8_t* buf) {
     using L = GemmLayout<DT>;
-    const int t = threadIdx.x, wave = t >> 6;
+    const int t = threadIdx.x, wave = t >> 6;  // wave of the workgroup (0 .. GM_T/64-1)
     uint8_t* wl = buf;
     uint8_t* al = buf + L::WBYTES;
     uint8_t* dl = al + L::ABYTES;
     if constexpr (DT == DT_Q4_K) {
 #pragma unroll
         for (int i = 0; i < L::WDMA; i++) {
-            const int c = min(256 * i + t, GM_BN * 9 - 1);  // chunk of 16 bytes
+            const int c = min(GM_T * i + t, GM_BN * 9 - 1);  // chunk of 16 bytes
             const int r = c / 9, j = c - 9 * r;
             const int n = min(n0 + r, A.N - 1);
-            lds_copy16(A.W + (int64_t)n * A.rb + (int64_t)b * Q4K_BYTES + 16 * j, wl + 16 * (256 * i + 64 * wave));
+            lds_copy16(A.W + (int64_t)n * A.rb + (int64_t)b * Q4K_BYTES + 16 * j, wl + 16 * (GM_T * i + 64 * wave));
         }
     } else {
 #pragma unroll
         for (int i = 0; i < L::WDMA; i++) {
-            const int c = min(256 * i + t, GM_BN * 54 - 1);  // dword
+            const int c = min(GM_T * i + t, GM_BN * 54 - 1);  // dword
             const int r = c / 54, j = c - 54 * r;
             const int n = min(n0 + r, A.N - 1);
             const uint8_t* blk = A.W + (int64_t)n * A.rb + (int64_t)b * Q6K_BYTES;
             const uint8_t* base = (const uint8_t*)__builtin_align_down(blk, 4);
-            lds_copy4(base + 4 * j, wl + 4 * (256 * i + 64 * wave));
+            lds_copy4(base + 4 * j, wl + 4 * (GM_T * i + 64 * wave));
         }
     }
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int c = 256 * i + t;               // LDS chunk: row c/16, slot c%16
+    for (int i = 0; i < GM_ACH; i++) {
+        const int c = GM_T * i + t;              // LDS chunk: row c/16, slot c%16
         const int r = c >> 4, s = c & 15;
         const int m = min(m0 + r, A.M - 1);
-        lds_copy16(A.q + (int64_t)m * A.K + 256 * b + 16 * (s ^ (r & 15)), al + 16 * (256 * i + 64 * wave));
+        lds_copy16(A.q + (int64_t)m * A.K + 256 * b + 16 * (s ^ (r & 15)), al + 16 * (GM_T * i + 64 * wave));
     }
     {
         const int m = min(m0 + min(t, GM_BM - 1), A.M - 1);
-        lds_copy4(A.d32 + (int64_t)m * (A.K / 32) + 8 * b, dl + 4 * (64 * wave));
+        lds_copy4(A.d32 + (int64_t)m * (A.K / 32) + 8 * b, dl + 4 * (64 * wave));  // slots t >= GM_BM are slack
     }
 }
 
@@ -162,11 +174,12 @@ __device__ __forceinline__ uint32_t as_u32(s16x2 v) { return __builtin_bit_cast(
 __device__ __forceinline__ s16x2 as_s16x2(uint32_t v) { return __builtin_bit_cast(s16x2, v); }
 
 template <uint32_t DT>
-__global__ __launch_bounds__(256) void gemm_a8k_kernel(GemmArgs A) {
+__global__ __launch_bounds__(GM_T) void gemm_a8k_kernel(GemmArgs A) {
     using L = GemmLayout<DT>;
     __shared__ __align__(16) uint8_t smem[2 * L::BUF];
     __shared__ int flags[2];
-    const int t = threadIdx.x, wave = t >> 6, l = t & 63;
+    const int t = threadIdx.x, l = t & 63;
+    const int wn = (t >> 6) & 3, wm = t >> 8;  // this wave's weight rows 16wn.., activation tiles wm*GM_TM..
     const int ar = l & 15, G = l >> 4;
     const int n0 = blockIdx.x * GM_BN, m0 = blockIdx.y * GM_BM;
     const int nb = A.nb;
@@ -210,41 +223,48 @@ __global__ __launch_bounds__(256) void gemm_a8k_kernel(GemmArgs A) {
         // A operand row (weights): wave rows 16*wave + ar.
         float dC[4], dminC[4];
         if constexpr (DT == DT_Q4_K) {
-            const uint8_t* wr = wl + (16 * wave + ar) * L::WSLOT;
+            const uint8_t* wr = wl + (16 * wn + ar) * L::WSLOT;
             const uint32_t* sw = (const uint32_t*)(wr + 4);
             const Q4KScales s = q4k_scales(sw[0], sw[1], sw[2]);
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const uint32_t dd = *(const uint32_t*)(wl + (16 * wave + 4 * G + r) * L::WSLOT);
+                const uint32_t dd = *(const uint32_t*)(wl + (16 * wn + 4 * G + r) * L::WSLOT);
                 dC[r] = f16_to_f32(dd & 0xFFFFu);
                 dminC[r] = f16_to_f32(dd >> 16);
             }
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
+                // All B operands of this k step first: their LDS latency then
+                // hides under the unpacking of the A planes.
+                v4i bvs[GM_TM];
+#pragma unroll
+                for (int mt = 0; mt < GM_TM; mt++) {
+                    const int row = 16 * (wm * GM_TM + mt) + ar;
+                    bvs[mt] = *(const v4i*)(al + row * 256 + 16 * ((4 * ks + G) ^ (row & 15)));
+                }
                 const int sub = 2 * ks + (G >> 1);
                 const uint32_t sc = byte_of(s.sc, sub), mm = byte_of(s.m, sub);
                 const u32x4 qraw = *(const u32x4*)(wr + 16 + 32 * ks + 16 * (G & 1));
                 const uint32_t qd[4] = {qraw.x, qraw.y, qraw.z, qraw.w};
+                // sc = 8*sh + sl with sh, sl <= 7: sh*q and sl*q (q <= 15) are at
+                // most 105, so each plane is the packed nibbles times a small
+                // constant (16-bit lanes, no carry between the bytes).
+                const short sh = (short)(sc >> 3), sl = (short)(sc & 7);
+                const s16x2 shp = {sh, sh}, slp = {sl, sl};
+                const int shift = 4 * (G >> 1);  // low nibbles for G < 2, high for G >= 2
                 v4i aH, aL, aM;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    const uint32_t v = (G >> 1) ? (qd[k] >> 4) : qd[k];
-                    const uint32_t e = v & 0x000F000Fu, o = (v >> 8) & 0x000F000Fu;
-                    // 16-bit lanes of sc*q (at most 945: no carry between lanes)
-                    const uint32_t pe = e * sc, po = o * sc;
-                    uint32_t lo, hi;
-                    split4(pe, po, pe >> 7, po >> 7, lo, hi);
-                    aL[k] = (int)lo;
-                    aH[k] = (int)hi;
+                    const s16x2 nib = as_s16x2((qd[k] >> shift) & 0x0F0F0F0Fu);
+                    aH[k] = (int)as_u32(nib * shp);
+                    aL[k] = (int)as_u32(nib * slp);
                     aM[k] = (int)(mm * 0x01010101u);
                 }
 #pragma unroll
                 for (int mt = 0; mt < GM_TM; mt++) {
-                    const int row = 16 * mt + ar;
-                    const v4i bv = *(const v4i*)(al + row * 256 + 16 * ((4 * ks + G) ^ (row & 15)));
-                    accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bv, accH[mt], 0, 0, 0);
-                    accL[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, bv, accL[mt], 0, 0, 0);
-                    accM[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aM, bv, accM[mt], 0, 0, 0);
+                    accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bvs[mt], accH[mt], 0, 0, 0);
+                    accL[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, bvs[mt], accL[mt], 0, 0, 0);
+                    accM[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aM, bvs[mt], accM[mt], 0, 0, 0);
                 }
             }
         } else {
@@ -254,7 +274,7 @@ __global__ __launch_bounds__(256) void gemm_a8k_kernel(GemmArgs A) {
                 const uint8_t* blk = A.W + (int64_t)n * A.rb + (int64_t)b * Q6K_BYTES;
                 return wl + row * L::WSLOT + ((uintptr_t)blk & 3);
             };
-            const uint8_t* wr = wbyte_addr(16 * wave + ar);
+            const uint8_t* wr = wbyte_addr(16 * wn + ar);
             const uint32_t rsh = (uint32_t)((uintptr_t)wr & 3);
             const uint32_t* wra = (const uint32_t*)(wr - rsh);
             auto rd16 = [&](int off) -> u32x4 {  // 16 bytes at wr + off (off % 4 == 0)
@@ -264,12 +284,20 @@ __global__ __launch_bounds__(256) void gemm_a8k_kernel(GemmArgs A) {
             };
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const uint8_t* wc = wbyte_addr(16 * wave + 4 * G + r);
+                const uint8_t* wc = wbyte_addr(16 * wn + 4 * G + r);
                 dC[r] = f16_to_f32((uint32_t)wc[208] | ((uint32_t)wc[209] << 8));
                 dminC[r] = 0.f;
             }
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) {
+                // All B operands of this k step first: their LDS latency then
+                // hides under the unpacking of the A planes.
+                v4i bvs[GM_TM];
+#pragma unroll
+                for (int mt = 0; mt < GM_TM; mt++) {
+                    const int row = 16 * (wm * GM_TM + mt) + ar;
+                    bvs[mt] = *(const v4i*)(al + row * 256 + 16 * ((4 * ks + G) ^ (row & 15)));
+                }
                 const int h = ks >> 1, p = 2 * (ks & 1) + (G >> 1);
                 const u32x4 ql = rd16(64 * h + 32 * (p & 1) + 16 * (G & 1));
                 const u32x4 qh = rd16(128 + 32 * h + 16 * (G & 1));
@@ -291,10 +319,8 @@ __global__ __launch_bounds__(256) void gemm_a8k_kernel(GemmArgs A) {
                 }
 #pragma unroll
                 for (int mt = 0; mt < GM_TM; mt++) {
-                    const int row = 16 * mt + ar;
-                    const v4i bv = *(const v4i*)(al + row * 256 + 16 * ((4 * ks + G) ^ (row & 15)));
-                    accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bv, accH[mt], 0, 0, 0);
-                    accL[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, bv, accL[mt], 0, 0, 0);
+                    accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bvs[mt], accH[mt], 0, 0, 0);
+                    accL[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, bvs[mt], accL[mt], 0, 0, 0);
                 }
             }
         }
@@ -302,10 +328,10 @@ __global__ __launch_bounds__(256) void gemm_a8k_kernel(GemmArgs A) {
         // The block's float step, per output in block order.
 #pragma unroll
         for (int mt = 0; mt < GM_TM; mt++) {
-            const float dx = dl[16 * mt + ar];
+            const float dx = dl[16 * (wm * GM_TM + mt) + ar];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int S = (accH[mt][r] << 7) + accL[mt][r];
+                const int S = (accH[mt][r] << (DT == DT_Q4_K ? 3 : 7)) + accL[mt][r];
                 tot[mt][r] = __builtin_fmaf((float)S, dC[r] * dx, tot[mt][r]);
                 if (DT == DT_Q4_K) off[mt][r] = __builtin_fmaf((float)accM[mt][r], dminC[r] * dx, off[mt][r]);
             }
@@ -318,11 +344,11 @@ __global__ __launch_bounds__(256) void gemm_a8k_kernel(GemmArgs A) {
     }
 
     // Outputs: lane holds rows n = n0 + 16*wave + 4G + r of column m.
-    const int nbase = n0 + 16 * wave + 4 * G;
+    const int nbase = n0 + 16 * wn + 4 * G;
     const int refused = flags[0];
 #pragma unroll
     for (int mt = 0; mt < GM_TM; mt++) {
-        const int m = m0 + 16 * mt + ar;
+        const int m = m0 + 16 * (wm * GM_TM + mt) + ar;
         if (m >= A.M) continue;
         if (refused && A.ok[m] == 0) continue;
 #pragma unroll
@@ -339,7 +365,7 @@ __global__ __launch_bounds__(256) void gemm_a8k_kernel(GemmArgs A) {
     // Refused pairs of the tile: the float32 path, one group of eight lanes
     // per (row, activation row).
     const int g = t >> 3;
-    for (int pidx = g; pidx < GM_BN * GM_BM; pidx += 32) {
+    for (int pidx = g; pidx < GM_BN * GM_BM; pidx += GM_T / 8) {
         const int n = n0 + pidx % GM_BN, m = m0 + pidx / GM_BN;
         if (n >= A.N || m >= A.M) continue;
         if (A.wref[n] == 0 && A.ok[m] != 0) continue;
@@ -373,9 +399,9 @@ hipError_t launch_gemm_a8k(const DevWeight& w, const ActPtrs& a, int64_t rows, i
     A.fused = total_rows <= 8;
     dim3 grid((unsigned)((w.n + GM_BN - 1) / GM_BN), (unsigned)((rows + GM_BM - 1) / GM_BM));
     if (w.dt == DT_Q4_K)
-        hipLaunchKernelGGL(gemm_a8k_kernel<DT_Q4_K>, grid, dim3(256), 0, stream, A);
+        hipLaunchKernelGGL(gemm_a8k_kernel<DT_Q4_K>, grid, dim3(GM_T), 0, stream, A);
     else
-        hipLaunchKernelGGL(gemm_a8k_kernel<DT_Q6_K>, grid, dim3(256), 0, stream, A);
+        hipLaunchKernelGGL(gemm_a8k_kernel<DT_Q6_K>, grid, dim3(GM_T), 0, stream, A);
     return hipGetLastError();
 }
 
