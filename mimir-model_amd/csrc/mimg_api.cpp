@@ -284,7 +284,12 @@ int matmul_quantized(const Weight* const* w, int count, const float* x, int64_t 
                     e = launch_gemv_a8k(dws, n, c, mr, rows, x + r0 * K, bs, ys, s);
             } else {
                 const int64_t N = w[i]->dw.n;
-                e = launch_gemv_q8_0_a8(w[i]->dw, c, mr, rows, x + r0 * K, bias ? bias[i] : nullptr, y[i] + r0 * N, N, s);
+                if (w[i]->dw.dt == DT_Q8_0)
+                    e = launch_gemv_q8_0_a8(w[i]->dw, c, mr, rows, x + r0 * K, bias ? bias[i] : nullptr,
+                                            y[i] + r0 * N, N, s);
+                else
+                    e = launch_gemv_kq_a8_b32(w[i]->dw, c, mr, rows, x + r0 * K, bias ? bias[i] : nullptr,
+                                              y[i] + r0 * N, N, s);
                 done[i] = true;
             }
             if (e != hipSuccess) return fail(MIMG_ERR_HIP, "product launch: %s", hipGetErrorString(e));
@@ -304,8 +309,6 @@ int a8_checks(const Weight* w, int64_t rows, int block, bool* use_f32) {
         *use_f32 = true;
         return MIMG_OK;
     }
-    if (block == 32 && w->dw.dt != DT_Q8_0)
-        return fail(MIMG_NOT_HANDLED, "%s with activation blocks of 32 has no GPU kernel yet", dt_name(w->dw.dt));
     return MIMG_OK;
 }
 

@@ -74,6 +74,12 @@ hipError_t launch_gemv_q8_0_a8(const DevWeight& w, const ActPtrs& a, int64_t row
                                int64_t total_rows, const float* x, const float* bias, float* y,
                                int64_t y_stride, hipStream_t stream);
 
+// Q4_K/Q6_K x 8-bit activations in blocks of 32, rows <= 8 per launch
+// (gemv_kquant_b32.hip).
+hipError_t launch_gemv_kq_a8_b32(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows,
+                                 const float* x, const float* bias, float* y, int64_t y_stride,
+                                 hipStream_t stream);
+
 hipError_t launch_linear_f32(const DevWeight& w, const float* x, int64_t rows, const float* bias,
                              float* y, hipStream_t stream);
 

@@ -378,6 +378,29 @@ def test_linear_q8_0_a8_bitexact(gpu, oracle, rows):
     assert bits_equal(got256, want256), first_diff(got256, want256)
 
 
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K])
+@pytest.mark.parametrize("rows", [1, 3, 8, 11])
+def test_linear_kquant_a8_block32_bitexact(gpu, oracle, dt, rows):
+    """Q4_K/Q6_K with activation blocks of 32 (dequant_matmul_a8.v1): the
+    lane order of dotQ4KQ8AVX2/dotQ6KQ8AVX2 as the oracle restates it, bit
+    for bit, with a refused activation row (float32 path), a weight row with
+    a non-finite scale, bias, and more than 8 rows (DotF32 fallback order)."""
+    n, k = 70, 2048
+    wb = bytearray(_weights(oracle, dt, n, k, seed=21).tobytes())
+    rb = len(wb) // n
+    o = rb * 9 + (208 if dt == Q6_K else 0)
+    wb[o:o + 2] = b"\x00\x7c"  # row 9: +inf block scale
+    wb = np.frombuffer(bytes(wb), np.uint8)
+    x = oracle.synthetic_acts(rows, k, seed=22)
+    x[rows - 1, 7] = np.nan
+    bias = np.random.default_rng(23).standard_normal(n).astype(np.float32)
+    W = gpu.Weight(wb, dt, n, k)
+    got = gpu.dequant_matmul_a8(W, x, bias=bias, block=32)
+    want = oracle.linear_a8(x, wb, dt, n, k, bias=bias, block=32)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+
+
 # ------------------------------------------------- float32-activation path
 
 @pytest.mark.parametrize("dt", [Q4_K, Q6_K, Q8_0])
