@@ -37,6 +37,7 @@ import mimg  # noqa: E402
 
 METRIC = "Q4_K GEMV GB/s (% of HBM peak); decode tok/s at 8B Q4_K_M; prefill TFLOP/s"
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8
 Q4_K, Q6_K = mimg.Q4_K, mimg.Q6_K
 
 # (name, N, K, dtype, weight seed, input index)
@@ -146,6 +147,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
+    ap.add_argument("--prefill-rows", default="512,2048",
+                    help="activation rows of the prefill GEMM measurements (comma list; empty to skip)")
     ap.add_argument("--roofline-replays", type=int, default=8,
                     help="replays of the graph of --rotate single-kernel launches timed for the roofline")
     args = ap.parse_args()
@@ -246,6 +249,43 @@ def main():
     log(f"  gate GEMV (Q4_K 14336x4096): {g_us:.2f} us/launch, {g_gbs:.0f} GB/s; "
         f"down GEMV (Q6_K 4096x14336): {d_us:.2f} us/launch, {d_gbs:.0f} GB/s")
 
+    # Prefill: the gate (Q4_K) and down (Q6_K) products
+    # at M activation rows on the int8 MFMA GEMM, activations quantized
+    # beforehand; a graph of --rotate launches over the rotation copies.
+    # Ops = 2*M*N*K; the fraction is of MI355X's dense int8 peak.
+    def prefill(name, rows):
+        _, n, k, dt, _, _ = next(c for c in CFG1 if c[0] == name)
+        xp = hiprt.DeviceBuffer.from_array(np.random.default_rng(200 + rows).standard_normal((rows, k), dtype=np.float32))
+        wsb = mimg.a8_workspace_bytes(rows, k)
+        wsp = hiprt.DeviceBuffer(wsb)
+        yp = hiprt.DeviceBuffer(rows * n * 4)
+        mimg.quantize_act_dev(xp.ptr, rows, k, 256, wsp.ptr, wsb, stream.handle)
+
+        def launches():
+            for l in range(args.rotate):
+                mimg.matmul_a8_quantized_dev(layers[l][name], xp.ptr, rows, None, 256, yp.ptr, wsp.ptr, wsb,
+                                             stream.handle)
+
+        g = hiprt.Graph(stream, launches)
+        g.launch(stream)
+        a, b = hiprt.Event(), hiprt.Event()
+        a.record(stream)
+        g.launch(stream)
+        b.record(stream)
+        b.sync()
+        us = a.elapsed_ms(b) * 1e3 / args.rotate
+        for buf in (xp, wsp, yp):
+            buf.free()
+        tops = 2.0 * rows * n * k / (us * 1e-6) / 1e12
+        return {"us_per_launch": round(us, 2), "TOP_per_s": round(tops, 1),
+                "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+
+    prefill_res = {}
+    for rows in [int(r) for r in args.prefill_rows.split(",") if r]:
+        for name in ("gate", "down"):
+            prefill_res[f"{name}_M{rows}"] = prefill(name, rows)
+            log(f"  prefill {name} M={rows}: {prefill_res[f'{name}_M{rows}']}")
+
     # The host-memory entry point a cgo caller uses (x copied in, y copied
     # back, the call returns when y is in host memory): PCIe- and
     # synchronisation-inclusive time per gate call, for reference only.
@@ -300,6 +340,11 @@ def main():
             "launch_bytes": g_bytes,
             "avg_launch_us": round(g_us, 3),
             "q6k_down": {"avg_launch_us": round(d_us, 3), "launch_bytes": d_bytes, "achieved": round(d_gbs, 1)},
+        },
+        "prefill": {
+            "workload": "cfg2: gate 14336x4096 Q4_K and down 4096x14336 Q6_K, dequant_matmul_a8.v2 block=256, "
+                        "int8 MFMA GEMM (bit-identical to the GEMV), activations quantized beforehand",
+            "results": prefill_res,
         },
         "host_api": {
             "entry": "mimg_dequant_matmul_a8 (gate, host x and y)",
