@@ -72,7 +72,11 @@ int mimg_version(void);
  * read (interp/interp.go:101-122 -> file.go:394-398): the same (host, len,
  * dtype, n, k) returns the same handle without a second upload, so a Go
  * caller may pass W.Data of every call (its mmap slice is stable for the
- * Program's life). len must equal n * (k / block_elems) * block_bytes. */
+ * Program's life). A hit is checked against a sampled fingerprint of the
+ * bytes (64 samples and both ends), so other bytes later mapped at the same
+ * address (a file closed and another opened) are uploaded afresh. Each call
+ * adds a reference; mimg_release_weight drops one. len must equal
+ * n * (k / block_elems) * block_bytes. */
 int mimg_register_weight(const void *host, uint64_t len, uint32_t dtype, int64_t n, int64_t k,
                          uint64_t *handle);
 
@@ -82,7 +86,7 @@ int mimg_register_weight(const void *host, uint64_t len, uint32_t dtype, int64_t
 int mimg_register_weight_device(const void *dev, uint64_t len, uint32_t dtype, int64_t n, int64_t k,
                                 uint64_t *handle);
 
-/* Frees a weight's device buffer. */
+/* Drops one reference of a registration; the last frees the device buffer. */
 int mimg_release_weight(uint64_t handle);
 
 /* Device address of a weight's bytes and the number of its rows that the
@@ -165,6 +169,66 @@ int mimg_dequantize_dev(uint32_t dtype, const void *src, uint64_t len, float *ds
  * and these two are this library's own, for synthetic weights. */
 int mimg_quantize_dev(uint32_t dtype, const float *src, int64_t n, void *dst, uint64_t dst_len,
                       void *stream);
+
+/* ---- decoder-step ops on device buffers ---------------------------------
+ * The other fast paths of the graph the reference's importer writes for a
+ * llama/qwen2 model (reference importer/llama.go:317-547, interp/fast.go:40-59),
+ * so that a decoder step's activations stay on the GPU between the linear
+ * layers. Float results follow the reference's formulas; they are checked
+ * against the reference fixture's float64-oracle logits within its own
+ * tolerances, not bit for bit. */
+
+/* embedding.v1 (reference interp/fast.go:818-842): out[t] = the decoded row
+ * ids[t] of a registered table [V, E] (Q4_K, Q6_K, Q8_0 or F32). */
+int mimg_embedding_dev(uint64_t table, const int32_t *ids, int64_t T, float *out, void *stream);
+
+/* rms_norm.v1 (reference interp/fast.go:434-485), with the graph's residual
+ * add before it (importer/llama.go:512-514, 520): if resid is not NULL,
+ * x += resid (written back); then y = rms_norm(x) * scale (scale may be NULL).
+ * x, y: [rows, n]. */
+int mimg_rms_norm_dev(float *x, const float *resid, const float *scale, float eps, int64_t rows, int64_t n, float *y,
+                      void *stream);
+
+/* rope.v1 (reference interp/fast.go:507-557, transformer.go:257-324) in place
+ * on x [T, heads, d]: angles pos[t] * inv_freq[i] in f64 (inv_freq: device
+ * f64 [rotary/2], theta^(-2i/rotary)); adjacent pairs if interleaved. */
+int mimg_rope_dev(float *x, const int64_t *pos, const double *inv_freq, int64_t T, int heads, int d, int rotary,
+                  int interleaved, void *stream);
+
+/* The cache scatter of the graph (reference importer/llama.go:489-503): k, v
+ * [T, kv_heads, d] into kcache/vcache [kv_heads, context, d] at the cache
+ * indices pos[t] (slot * per-slot context + position with several slots),
+ * rounded to f16 when f16 != 0 (the caches are then f16). Rows whose index
+ * is outside 0..context-1 are not stored. */
+int mimg_kv_store_dev(const float *k, const float *v, const int64_t *pos, int64_t T, int kv_heads, int d,
+                      int64_t context, void *kcache, void *vcache, int f16, void *stream);
+
+/* attention.v1 (f32 cache) / attention.v2 (f16 cache) with the graph's
+ * mask (reference interp/fast.go:559-700, importer/llama.go:364-395):
+ * query t of head h sees the cache entries kstart[t]..kend[t] (inclusive;
+ * kstart may be NULL for 0) of kv head h / (heads / kv_heads), as the mask
+ * of a cache with one or several sequences ("slots") allows; scale
+ * 1/sqrt(d). q, out: [T, heads, d]. d <= 512, at most 8192 visible keys
+ * (the range is clipped to the cache row and to 8192 keys; a query that
+ * sees nothing gets zeros). */
+int mimg_attention_dev(const float *q, const void *kcache, const void *vcache, const int64_t *kend,
+                       const int64_t *kstart, int64_t T, int heads, int kv_heads, int d, int64_t context, int f16,
+                       float *out, void *stream);
+
+/* One step of the greedy loop on the device (reference cmd/mim-run/main.go
+ * generate, 184-257), for n sequences: ids[i] = chosen[i], out[count*n+i] =
+ * chosen[i] while count < cap (out holds cap*n ids), pos[i] += 1,
+ * cache_index[i] += 1 (if not NULL), count += 1. So a captured decode step
+ * needs no host round trip. */
+int mimg_greedy_advance_dev(const int32_t *chosen, int32_t *ids, int64_t *pos, int64_t *cache_index, int32_t *out,
+                            int32_t *count, int cap, int n, void *stream);
+
+/* swiglu.v1 (reference interp/fast.go:487-498): out = silu(g) * u. */
+int mimg_swiglu_dev(const float *g, const float *u, float *out, int64_t n, void *stream);
+
+/* Greedy choice (reference cmd/mim-run/main.go:184-192): out[r] = the first
+ * index of the largest value of row r of x [rows, n]. */
+int mimg_argmax_dev(const float *x, int64_t rows, int64_t n, int32_t *out, void *stream);
 
 #ifdef __cplusplus
 }

@@ -49,6 +49,8 @@ struct Weight {
     uint64_t len = 0;
     bool has_key = false;
     std::tuple<uintptr_t, uint64_t, uint32_t, int64_t, int64_t> key;
+    uint64_t fp = 0;    // sampled fingerprint of the host bytes (has_key)
+    int64_t refs = 1;   // registrations not yet released
 };
 
 std::mutex g_mu;
@@ -144,6 +146,30 @@ int check_shape(uint32_t dtype, uint64_t len, int64_t n, int64_t k) {
     return MIMG_OK;
 }
 
+// A cheap fingerprint of host bytes: 64 evenly spaced 8-byte samples and
+// the first and last 64 bytes, mixed with splitmix64's finaliser. It tells
+// a registered buffer from other bytes later mapped at the same address (a
+// closed and reopened file) without reading the whole tensor on each call.
+static uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+static uint64_t fingerprint(const uint8_t* p, uint64_t len) {
+    uint64_t h = mix64(len);
+    auto take = [&](uint64_t off) {
+        uint64_t v = 0;
+        const uint64_t m = len - off < 8 ? len - off : 8;
+        memcpy(&v, p + off, m);
+        h = mix64(h ^ v ^ (off << 1));
+    };
+    for (uint64_t o = 0; o < 64 && o < len; o += 8) take(o);
+    for (uint64_t o = len > 64 ? len - 64 : 0; o < len; o += 8) take(o);
+    if (len > 8)
+        for (uint64_t i = 0; i < 64; i++) take(i * (len - 8) / 63);
+    return h;
+}
+
 int register_impl(const void* src, uint64_t len, uint32_t dtype, int64_t n, int64_t k, bool from_host,
                   uint64_t* handle) {
     if (!handle || !src) return fail(MIMG_ERR_ARG, "null pointer");
@@ -151,12 +177,21 @@ int register_impl(const void* src, uint64_t len, uint32_t dtype, int64_t n, int6
     if (rc) return rc;
     if ((rc = ensure_device())) return rc;
     auto key = std::make_tuple((uintptr_t)src, len, dtype, n, k);
+    const uint64_t fp = from_host ? fingerprint((const uint8_t*)src, len) : 0;
     if (from_host) {
         std::lock_guard<std::mutex> lk(g_mu);
         auto it = g_keys.find(key);
         if (it != g_keys.end()) {
-            *handle = it->second;
-            return MIMG_OK;
+            Weight* old = g_weights[it->second];
+            if (old->fp == fp) {
+                old->refs++;
+                *handle = it->second;
+                return MIMG_OK;
+            }
+            // other bytes at a registered address: the old entry keeps its
+            // handle until released, the key goes to a fresh upload
+            old->has_key = false;
+            g_keys.erase(it);
         }
     }
     Weight* w = new Weight();
@@ -189,16 +224,19 @@ int register_impl(const void* src, uint64_t len, uint32_t dtype, int64_t n, int6
     w->dw.n_refused = refused;
     w->has_key = from_host;
     w->key = key;
+    w->fp = fp;
     std::lock_guard<std::mutex> lk(g_mu);
     if (from_host) {
         auto it = g_keys.find(key);
-        if (it != g_keys.end()) {  // another thread registered it meanwhile
+        if (it != g_keys.end() && g_weights[it->second]->fp == fp) {  // another thread registered it meanwhile
             (void)hipFree(w->data);
             (void)hipFree(w->wref);
             delete w;
+            g_weights[it->second]->refs++;
             *handle = it->second;
             return MIMG_OK;
         }
+        if (it != g_keys.end()) g_weights[it->second]->has_key = false;
         g_keys[key] = g_next;
     }
     g_weights[g_next] = w;
@@ -366,6 +404,7 @@ int mimg_release_weight(uint64_t handle) {
     auto it = g_weights.find(handle);
     if (it == g_weights.end()) return fail(MIMG_ERR_HANDLE, "unknown weight handle %llu", (unsigned long long)handle);
     Weight* w = it->second;
+    if (--w->refs > 0) return MIMG_OK;
     if (w->has_key) g_keys.erase(w->key);
     g_weights.erase(it);
     HIP_TRY(hipDeviceSynchronize());
@@ -537,6 +576,100 @@ int mimg_dequantize_dev(uint32_t dtype, const void* src, uint64_t len, float* ds
                     (long long)(n / be * block_bytes(dtype)), (unsigned long long)len);
     if (n == 0) return MIMG_OK;
     HIP_TRY(launch_dequantize(dtype, (const uint8_t*)src, n, dst, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+// ---- decoder-step ops ------------------------------------------------------
+
+int mimg_embedding_dev(uint64_t table, const int32_t* ids, int64_t T, float* out, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    Weight* w;
+    if ((rc = lookup(table, &w))) return rc;
+    if (T < 0 || T > (1 << 30)) return fail(MIMG_ERR_ARG, "T = %lld", (long long)T);
+    if (T == 0) return MIMG_OK;
+    if (!ids || !out) return fail(MIMG_ERR_ARG, "null pointer");
+    HIP_TRY(launch_embed_rows(w->dw.dt, w->dw.data, w->dw.row_bytes, ids, (int)T, (int)w->dw.n, w->dw.k, out,
+                              (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_rms_norm_dev(float* x, const float* resid, const float* scale, float eps, int64_t rows, int64_t n, float* y,
+                      void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (rows < 0 || n <= 0 || rows > (1 << 30)) return fail(MIMG_ERR_ARG, "rows %lld, n %lld", (long long)rows, (long long)n);
+    if (rows == 0) return MIMG_OK;
+    if (!x || !y) return fail(MIMG_ERR_ARG, "null pointer");
+    HIP_TRY(launch_rms_norm(x, resid, scale, eps, rows, n, y, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_rope_dev(float* x, const int64_t* pos, const double* inv_freq, int64_t T, int heads, int d, int rotary,
+                  int interleaved, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (T < 0 || heads <= 0 || d <= 0 || rotary <= 0 || rotary % 2 || rotary > d)
+        return fail(MIMG_ERR_ARG, "rope: T %lld, heads %d, D %d, rotary %d", (long long)T, heads, d, rotary);
+    if (T == 0) return MIMG_OK;
+    if (!x || !pos || !inv_freq) return fail(MIMG_ERR_ARG, "null pointer");
+    HIP_TRY(launch_rope(x, pos, inv_freq, (int)T, heads, d, rotary, interleaved, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_kv_store_dev(const float* k, const float* v, const int64_t* pos, int64_t T, int kv_heads, int d,
+                      int64_t context, void* kcache, void* vcache, int f16, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (T < 0 || kv_heads <= 0 || d <= 0 || context <= 0) return fail(MIMG_ERR_ARG, "kv store shape");
+    if (T == 0) return MIMG_OK;
+    if (!k || !v || !pos || !kcache || !vcache) return fail(MIMG_ERR_ARG, "null pointer");
+    HIP_TRY(launch_kv_store(k, v, pos, (int)T, kv_heads, d, context, kcache, vcache, f16, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_attention_dev(const float* q, const void* kcache, const void* vcache, const int64_t* kend,
+                       const int64_t* kstart, int64_t T, int heads, int kv_heads, int d, int64_t context, int f16,
+                       float* out, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (T < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || d <= 0 || d > 512 || context <= 0)
+        return fail(MIMG_ERR_ARG, "attention: heads %d, kv heads %d, D %d, context %lld (D <= 512)", heads, kv_heads, d,
+                    (long long)context);
+    if (T == 0) return MIMG_OK;
+    if (!q || !kcache || !vcache || !kend || !out) return fail(MIMG_ERR_ARG, "null pointer");
+    HIP_TRY(launch_attention(q, kcache, vcache, kend, kstart, (int)T, heads, kv_heads, d, context, f16, out,
+                             (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_greedy_advance_dev(const int32_t* chosen, int32_t* ids, int64_t* pos, int64_t* cache_index, int32_t* out,
+                            int32_t* count, int cap, int n, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (n < 1 || n > 1024 || cap < 0) return fail(MIMG_ERR_ARG, "greedy advance: %d sequences (1..1024), cap %d", n, cap);
+    if (!chosen || !ids || !pos || !out || !count) return fail(MIMG_ERR_ARG, "null pointer");
+    HIP_TRY(launch_greedy_advance(chosen, ids, pos, cache_index, out, count, cap, n, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_swiglu_dev(const float* g, const float* u, float* out, int64_t n, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (n < 0) return fail(MIMG_ERR_ARG, "n = %lld", (long long)n);
+    if (n == 0) return MIMG_OK;
+    if (!g || !u || !out) return fail(MIMG_ERR_ARG, "null pointer");
+    HIP_TRY(launch_swiglu(g, u, out, n, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_argmax_dev(const float* x, int64_t rows, int64_t n, int32_t* out, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (rows < 0 || n <= 0 || n >= (1ll << 31)) return fail(MIMG_ERR_ARG, "argmax: rows %lld, n %lld", (long long)rows, (long long)n);
+    if (rows == 0) return MIMG_OK;
+    if (!x || !out) return fail(MIMG_ERR_ARG, "null pointer");
+    HIP_TRY(launch_argmax(x, rows, n, out, (hipStream_t)stream));
     return MIMG_OK;
 }
 

@@ -83,6 +83,22 @@ hipError_t launch_gemv_kq_a8_b32(const DevWeight& w, const ActPtrs& a, int64_t r
 hipError_t launch_linear_f32(const DevWeight& w, const float* x, int64_t rows, const float* bias,
                              float* y, hipStream_t stream);
 
+// Decoder-step ops (decoder_ops.hip).
+hipError_t launch_embed_rows(uint32_t dt, const uint8_t* table, int64_t row_bytes, const int32_t* ids, int T, int V,
+                             int64_t E, float* out, hipStream_t s);
+hipError_t launch_rms_norm(float* x, const float* resid, const float* scale, float eps, int64_t rows, int64_t n, float* y,
+                           hipStream_t s);
+hipError_t launch_rope(float* x, const int64_t* pos, const double* inv_freq, int T, int heads, int D, int rotary,
+                       int interleaved, hipStream_t s);
+hipError_t launch_kv_store(const float* k, const float* v, const int64_t* pos, int T, int Hkv, int D, int64_t C, void* kc,
+                           void* vc, int f16, hipStream_t s);
+hipError_t launch_attention(const float* q, const void* kc, const void* vc, const int64_t* kend, const int64_t* kstart,
+                            int T, int H, int Hkv, int D, int64_t C, int f16, float* out, hipStream_t s);
+hipError_t launch_greedy_advance(const int32_t* chosen, int32_t* ids, int64_t* pos, int64_t* cidx, int32_t* out,
+                                 int32_t* count, int cap, int n, hipStream_t s);
+hipError_t launch_swiglu(const float* g, const float* u, float* out, int64_t n, hipStream_t s);
+hipError_t launch_argmax(const float* x, int64_t rows, int64_t n, int32_t* out, hipStream_t s);
+
 hipError_t launch_dequantize(uint32_t dt, const uint8_t* src, int64_t n_elems, float* dst,
                              hipStream_t stream);
 

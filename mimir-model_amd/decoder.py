@@ -1,0 +1,258 @@
+"""Greedy llama/qwen2 decoding with every op on the GPU, through libmimg.
+
+The forward pass is the graph the reference's importer writes for a llama
+or qwen2 model (reference importer/llama.go:317-547) run the way its interp
+fast paths run it: embedding.v1, rms_norm.v1, the quantized linears
+(dequant_matmul_a8.v2 / .v1 with 8-bit activations, dequant_matmul.v1
+without), rope.v1, the cache scatter, attention.v1/.v2 with the causal and
+slot mask, swiglu.v1, and the greedy loop of cmd/mim-run/main.go:184-257.
+Activations, the key-value cache and the chosen tokens stay in device
+memory; a decode step is one HIP graph replay with no host round trip.
+
+Several sequences ("slots", reference LlamaOptions.Slots,
+importer/llama.go:306-310) share one cache of slots * context positions:
+the token at position p of slot s goes to cache index s*context + p and sees
+the keys s*context .. s*context + p.
+
+There is no CPU fallback: every op is a libmimg call, which raises if the
+library or a gfx950 GPU is missing.
+"""
+import numpy as np
+
+import hiprt
+import mimg
+
+F32 = mimg.F32
+
+
+class Config:
+    """The model shape (reference importer/llama.go LlamaConfig)."""
+
+    def __init__(self, arch="llama", layers=1, embed=256, ffn=256, heads=4, kv_heads=None, rope_dims=None,
+                 rope_theta=10000.0, norm_eps=1e-5, context=64, **_):
+        self.arch, self.layers, self.embed, self.ffn = arch, int(layers), int(embed), int(ffn)
+        self.heads = int(heads)
+        self.kv_heads = int(kv_heads or heads)
+        self.head_dim = self.embed // self.heads
+        self.rope_dims = int(rope_dims or self.head_dim)
+        self.rope_theta, self.norm_eps, self.context = float(rope_theta), float(norm_eps), int(context)
+        # llama rotates adjacent pairs, qwen2 the two halves
+        # (reference interp/transformer.go:257-324)
+        self.interleaved = arch != "qwen2"
+        if self.embed % self.heads or self.heads % self.kv_heads or self.rope_dims % 2:
+            raise ValueError(f"inconsistent shape: embed {embed}, heads {heads}, kv heads {kv_heads}, rope {rope_dims}")
+
+
+def inv_freq(cfg):
+    """theta^(-2i/r) in f64, i < r/2 (reference interp/fast.go:507-557)."""
+    r = cfg.rope_dims
+    return np.array([cfg.rope_theta ** (-2.0 * i / r) for i in range(r // 2)], np.float64)
+
+
+class Decoder:
+    """One model on the GPU with its key-value cache.
+
+    tensors: {GGUF tensor name: (dtype, shape, data)}, where data is the
+    block bytes (np.uint8) of a quantized matrix, an np.float32 array for a
+    norm scale or bias, or an already registered mimg.Weight.
+    """
+
+    def __init__(self, config, tensors, a8=True, cache_f16=False, max_rows=64, slots=1):
+        c = self.c = config if isinstance(config, Config) else Config(**config)
+        self.a8, self.f16, self.slots = bool(a8), bool(cache_f16), int(slots)
+        self.R = int(max_rows)
+        mimg.init()
+        self.stream = hiprt.Stream()
+        self.w, self.vec = {}, {}
+        for name, (dt, shape, data) in tensors.items():
+            if isinstance(data, mimg.Weight):
+                self.w[name] = data
+            elif dt == F32:
+                if len(shape) != 1:
+                    raise mimg.NotHandled(1, f"{name}: f32 matrices are not handled")
+                self.vec[name] = hiprt.DeviceBuffer.from_array(np.ascontiguousarray(data, np.float32))
+            else:
+                self.w[name] = mimg.Weight(data, dt, int(shape[0]), int(shape[1]))
+        self.head = self.w.get("output.weight") or self.w["token_embd.weight"]
+        self.vocab = self.w["token_embd.weight"].n
+        E, F, H, Hkv, D, R = c.embed, c.ffn, c.heads, c.kv_heads, c.head_dim, self.R
+        self.cache_len = self.slots * c.context
+        esz = 2 if self.f16 else 4
+        B = hiprt.DeviceBuffer
+        self.kc = [B(Hkv * self.cache_len * D * esz) for _ in range(c.layers)]
+        self.vc = [B(Hkv * self.cache_len * D * esz) for _ in range(c.layers)]
+        for buf in self.kc + self.vc:
+            buf.zero()
+        self.invf = B.from_array(inv_freq(c))
+        self.x, self.h, self.ao = B(R * E * 4), B(R * E * 4), B(R * E * 4)
+        self.q, self.o = B(R * H * D * 4), B(R * H * D * 4)
+        self.k, self.v = B(R * Hkv * D * 4), B(R * Hkv * D * 4)
+        self.g, self.u = B(R * F * 4), B(R * F * 4)
+        self.logits = B(R * self.vocab * 4)
+        self.ids, self.pos = B(R * 4), B(R * 8)
+        self.cidx, self.kstart = B(R * 8), B(R * 8)
+        self.chosen, self.count = B(R * 4), B(4)
+        self.out, self.out_cap = None, 0
+        kmax = max(E, H * D, F)
+        self.ws_bytes = mimg.a8_workspace_bytes(R, kmax)
+        self.ws = B(self.ws_bytes)
+        self.graphs = {}
+
+    # ---- the graph's ops ---------------------------------------------------
+
+    def _block(self, w):
+        return 256 if w.dt in (mimg.Q4_K, mimg.Q6_K) else 32
+
+    def _linears(self, names, x, rows, ys, biases=None):
+        """ys[i] = x . W_i^T (+ bias_i) for weights sharing the input x."""
+        ws = [self.w[n] for n in names]
+        bs = [None if b is None or b not in self.vec else self.vec[b].ptr for b in (biases or [None] * len(names))]
+        s = self.stream.handle
+        if not self.a8:
+            for w, b, y in zip(ws, bs, ys):
+                mimg.linear_f32_dev(w, x, rows, b, y, s)
+            return
+        blocks = {self._block(w) for w in ws}
+        if len(ws) > 1 and len(blocks) == 1:
+            mimg.linear_a8_group_dev(ws, x, rows, bs if any(bs) else None, blocks.pop(), ys, self.ws.ptr,
+                                     self.ws_bytes, s)
+            return
+        for w, b, y in zip(ws, bs, ys):
+            mimg.linear_a8_dev(w, x, rows, b, self._block(w), y, self.ws.ptr, self.ws_bytes, s)
+
+    def _forward(self, T):
+        """Enqueues the forward pass of the T rows in ids/pos/cidx/kstart;
+        logits [T, vocab] land in self.logits."""
+        c, s = self.c, self.stream.handle
+        E, F, H, Hkv, D = c.embed, c.ffn, c.heads, c.kv_heads, c.head_dim
+        kstart = self.kstart.ptr if self.slots > 1 else None
+        mimg.embedding_dev(self.w["token_embd.weight"], self.ids.ptr, T, self.x.ptr, s)
+        resid = None  # the previous sublayer's output, added to x by the next norm
+        for l in range(c.layers):
+            p = f"blk.{l}."
+            mimg.rms_norm_dev(self.x.ptr, resid, self.vec[p + "attn_norm.weight"].ptr, c.norm_eps, T, E,
+                              self.h.ptr, s)
+            self._linears([p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"], self.h.ptr, T,
+                          [self.q.ptr, self.k.ptr, self.v.ptr],
+                          [p + "attn_q.bias", p + "attn_k.bias", p + "attn_v.bias"])
+            mimg.rope_dev(self.q.ptr, self.pos.ptr, self.invf.ptr, T, H, D, c.rope_dims, c.interleaved, s)
+            mimg.rope_dev(self.k.ptr, self.pos.ptr, self.invf.ptr, T, Hkv, D, c.rope_dims, c.interleaved, s)
+            mimg.kv_store_dev(self.k.ptr, self.v.ptr, self.cidx.ptr, T, Hkv, D, self.cache_len, self.kc[l].ptr,
+                              self.vc[l].ptr, self.f16, s)
+            mimg.attention_dev(self.q.ptr, self.kc[l].ptr, self.vc[l].ptr, self.cidx.ptr, kstart, T, H, Hkv, D,
+                               self.cache_len, self.f16, self.o.ptr, s)
+            self._linears([p + "attn_output.weight"], self.o.ptr, T, [self.ao.ptr])
+            mimg.rms_norm_dev(self.x.ptr, self.ao.ptr, self.vec[p + "ffn_norm.weight"].ptr, c.norm_eps, T, E,
+                              self.h.ptr, s)
+            self._linears([p + "ffn_gate.weight", p + "ffn_up.weight"], self.h.ptr, T, [self.g.ptr, self.u.ptr])
+            mimg.swiglu_dev(self.g.ptr, self.u.ptr, self.g.ptr, T * F, s)
+            self._linears([p + "ffn_down.weight"], self.g.ptr, T, [self.ao.ptr])
+            resid = self.ao.ptr
+        mimg.rms_norm_dev(self.x.ptr, resid, self.vec["output_norm.weight"].ptr, c.norm_eps, T, E, self.h.ptr, s)
+        if self.a8:
+            mimg.linear_a8_dev(self.head, self.h.ptr, T, None, self._block(self.head), self.logits.ptr, self.ws.ptr,
+                               self.ws_bytes, s)
+        else:
+            mimg.linear_f32_dev(self.head, self.h.ptr, T, None, self.logits.ptr, s)
+
+    def _set_rows(self, tokens, positions, slots=None):
+        tokens = np.asarray(tokens, np.int32).ravel()
+        positions = np.asarray(positions, np.int64).ravel()
+        T = tokens.size
+        if T == 0 or T > self.R or positions.size != T:
+            raise ValueError(f"{T} tokens with {positions.size} positions (1..{self.R})")
+        slots = np.zeros(T, np.int64) if slots is None else np.asarray(slots, np.int64).ravel()
+        if slots.size != T or slots.min() < 0 or slots.max() >= self.slots:
+            raise ValueError(f"slots {slots} (0..{self.slots - 1})")
+        if positions.min() < 0 or positions.max() >= self.c.context:
+            raise ValueError(f"positions outside 0..{self.c.context - 1}")
+        start = slots * self.c.context
+        self.stream.sync()
+        self.ids.upload(tokens)
+        self.pos.upload(positions)
+        self.cidx.upload(start + positions)
+        self.kstart.upload(start)
+        return T
+
+    # ---- API -----------------------------------------------------------------
+
+    def forward(self, tokens, positions, slots=None):
+        """Logits [T, vocab] (host) for the tokens at the positions; the
+        cache is updated (reference Session.Step)."""
+        T = self._set_rows(tokens, positions, slots)
+        self._forward(T)
+        self.stream.sync()
+        return self.logits.download(np.float32, T * self.vocab).reshape(T, self.vocab)
+
+    def _decode_graph(self, n):
+        g = self.graphs.get(n)
+        if g is None:
+            def step():
+                self._forward(n)
+                mimg.argmax_dev(self.logits.ptr, n, self.vocab, self.chosen.ptr, self.stream.handle)
+                mimg.greedy_advance_dev(self.chosen.ptr, self.ids.ptr, self.pos.ptr, self.cidx.ptr, self.out.ptr,
+                                        self.count.ptr, self.out_cap, n, self.stream.handle)
+            g = self.graphs[n] = hiprt.Graph(self.stream, step)
+        return g
+
+    def _ensure_out(self, cap, n):
+        if self.out is None or self.out_cap < cap or self.out.nbytes < cap * n * 4:
+            self.out = hiprt.DeviceBuffer(cap * n * 4)
+            self.out_cap = cap
+            self.graphs = {}  # captured with the old buffer
+
+    def generate(self, prompts, n_new, slots=None, graph=True):
+        """Greedy continuation of each prompt (one per slot, all of the same
+        length): n_new tokens each, [len(prompts), n_new] (reference
+        cmd/mim-run/main.go generate). The prompts run as one batch of
+        rows; every decode step is a graph replay."""
+        prompts = np.atleast_2d(np.asarray(prompts, np.int32))
+        n, P = prompts.shape
+        if n > self.slots:
+            raise ValueError(f"{n} prompts, {self.slots} slots")
+        if P + n_new - 1 > self.c.context:
+            raise ValueError(f"{P} + {n_new} tokens exceed the context {self.c.context}")
+        slots = np.arange(n) if slots is None else np.asarray(slots)
+        self._ensure_out(max(n_new, 1), n)
+        s = self.stream.handle
+        # the prompts: n*P rows in chunks of at most R
+        rows_tok = prompts.ravel()
+        rows_pos = np.tile(np.arange(P, dtype=np.int64), n)
+        rows_slot = np.repeat(slots, P)
+        last = None
+        for c0 in range(0, n * P, self.R):
+            T = self._set_rows(rows_tok[c0:c0 + self.R], rows_pos[c0:c0 + self.R], rows_slot[c0:c0 + self.R])
+            self._forward(T)
+            last = (c0, T)
+        # the last row of each prompt: pick, then continue from position P
+        self.stream.sync()
+        lg = self.logits.download(np.float32, last[1] * self.vocab).reshape(last[1], self.vocab)
+        ends = [i * P + P - 1 for i in range(n)]
+        first = []
+        for e in ends:
+            if e < last[0]:
+                raise ValueError("with several prompts, the prompts must fit in one batch of rows")
+            first.append(int(np.argmax(lg[e - last[0]])))
+        self.chosen.upload(np.array(first, np.int32))
+        self._set_rows(np.array(first, np.int32), np.full(n, P - 1), slots)
+        self.count.upload(np.zeros(1, np.int32))
+        mimg.greedy_advance_dev(self.chosen.ptr, self.ids.ptr, self.pos.ptr, self.cidx.ptr, self.out.ptr,
+                                self.count.ptr, self.out_cap, n, s)
+        if graph:
+            g = self._decode_graph(n)
+            for _ in range(n_new - 1):
+                g.launch(self.stream)
+        else:
+            for _ in range(n_new - 1):
+                self._forward(n)
+                mimg.argmax_dev(self.logits.ptr, n, self.vocab, self.chosen.ptr, s)
+                mimg.greedy_advance_dev(self.chosen.ptr, self.ids.ptr, self.pos.ptr, self.cidx.ptr, self.out.ptr,
+                                        self.count.ptr, self.out_cap, n, s)
+        self.stream.sync()
+        return self.out.download(np.int32, n_new * n).reshape(n_new, n).T.copy()
+
+    def reset(self):
+        """Clears the cache (a new session)."""
+        self.stream.sync()
+        for buf in self.kc + self.vc:
+            buf.zero()

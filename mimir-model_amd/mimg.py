@@ -49,6 +49,14 @@ SIGNATURES = {
     "mimg_linear_f32_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
     "mimg_dequantize_dev": (_I, [_U32, _P, _U64, _P, _I64, _P]),
     "mimg_quantize_dev": (_I, [_U32, _P, _I64, _P, _U64, _P]),
+    "mimg_embedding_dev": (_I, [_U64, _P, _I64, _P, _P]),
+    "mimg_rms_norm_dev": (_I, [_P, _P, _P, ctypes.c_float, _I64, _I64, _P, _P]),
+    "mimg_rope_dev": (_I, [_P, _P, _P, _I64, _I, _I, _I, _I, _P]),
+    "mimg_kv_store_dev": (_I, [_P, _P, _P, _I64, _I, _I, _I64, _P, _P, _I, _P]),
+    "mimg_attention_dev": (_I, [_P, _P, _P, _P, _P, _I64, _I, _I, _I, _I64, _I, _P, _P]),
+    "mimg_greedy_advance_dev": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _P]),
+    "mimg_swiglu_dev": (_I, [_P, _P, _P, _I64, _P]),
+    "mimg_argmax_dev": (_I, [_P, _I64, _I64, _P, _P]),
 }
 
 
@@ -129,6 +137,13 @@ class Weight:
             _check(load().mimg_release_weight(self.handle))
             self.handle = 0
 
+    def __del__(self):
+        # each Weight holds one reference of its registration
+        try:
+            self.release()
+        except Exception:
+            pass
+
 
 def dequant_matmul_a8(w, x, bias=None, block=256):
     """dequant_matmul_a8.v1/v2 on host arrays: x [..., K] f32 -> y [..., N]."""
@@ -208,6 +223,48 @@ def quantize_dev(dt, x_ptr, n, dst_ptr, dst_bytes, stream):
     Quantize for Q8_0, quant.go:165-228; this repository's encoder for
     Q4_K/Q6_K, which the reference lacks)."""
     _check(load().mimg_quantize_dev(dt, _P(x_ptr), n, _P(dst_ptr), dst_bytes, _P(stream)))
+
+
+def _o(ptr):
+    return _P(ptr) if ptr else None
+
+
+# ---- the other ops of a decoder step (device pointers, as above) ----------
+
+def embedding_dev(table, ids_ptr, T, out_ptr, stream):
+    _check(load().mimg_embedding_dev(table.handle, _P(ids_ptr), T, _P(out_ptr), _P(stream)))
+
+
+def rms_norm_dev(x_ptr, resid_ptr, scale_ptr, eps, rows, n, y_ptr, stream):
+    _check(load().mimg_rms_norm_dev(_P(x_ptr), _o(resid_ptr), _o(scale_ptr), eps, rows, n, _P(y_ptr), _P(stream)))
+
+
+def rope_dev(x_ptr, pos_ptr, inv_freq_ptr, T, heads, d, rotary, interleaved, stream):
+    _check(load().mimg_rope_dev(_P(x_ptr), _P(pos_ptr), _P(inv_freq_ptr), T, heads, d, rotary, int(interleaved),
+                                _P(stream)))
+
+
+def kv_store_dev(k_ptr, v_ptr, pos_ptr, T, kv_heads, d, context, kc_ptr, vc_ptr, f16, stream):
+    _check(load().mimg_kv_store_dev(_P(k_ptr), _P(v_ptr), _P(pos_ptr), T, kv_heads, d, context, _P(kc_ptr),
+                                    _P(vc_ptr), int(f16), _P(stream)))
+
+
+def attention_dev(q_ptr, kc_ptr, vc_ptr, kend_ptr, kstart_ptr, T, heads, kv_heads, d, context, f16, out_ptr, stream):
+    _check(load().mimg_attention_dev(_P(q_ptr), _P(kc_ptr), _P(vc_ptr), _P(kend_ptr), _o(kstart_ptr), T, heads,
+                                     kv_heads, d, context, int(f16), _P(out_ptr), _P(stream)))
+
+
+def greedy_advance_dev(chosen_ptr, ids_ptr, pos_ptr, cidx_ptr, out_ptr, count_ptr, cap, n, stream):
+    _check(load().mimg_greedy_advance_dev(_P(chosen_ptr), _P(ids_ptr), _P(pos_ptr), _o(cidx_ptr), _P(out_ptr),
+                                          _P(count_ptr), cap, n, _P(stream)))
+
+
+def swiglu_dev(g_ptr, u_ptr, out_ptr, n, stream):
+    _check(load().mimg_swiglu_dev(_P(g_ptr), _P(u_ptr), _P(out_ptr), n, _P(stream)))
+
+
+def argmax_dev(x_ptr, rows, n, out_ptr, stream):
+    _check(load().mimg_argmax_dev(_P(x_ptr), rows, n, _P(out_ptr), _P(stream)))
 
 
 def row_bytes(dt, k):

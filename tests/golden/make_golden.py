@@ -14,6 +14,12 @@ Fixtures (data only: inputs and expected outputs):
                            tensors of testdata/llama/tiny-q4km.gguf (blocks
                            written by llama.cpp's quantizer), read with a
                            minimal GGUF v3 header parser.
+  {llama,qwen2}_model.npz  every tensor of testdata/{llama,qwen2}/tiny-q4km.gguf
+                           (block bytes, or f32 values), for the decoder tests.
+  {llama,qwen2}_expected.json  the model configuration read from the GGUF
+                           metadata and the reference's expected outputs
+                           (testdata/*/expected.json: prompt ids, greedy ids,
+                           float64-oracle logits, llama.cpp's deviation).
 
 Usage: python tests/golden/make_golden.py [/root/reference]
 """
@@ -27,8 +33,9 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 
 
-def gguf_tensors(path):
-    """Returns {name: (ggml_type, shape, raw bytes)} of a GGUF v2/v3 file."""
+def gguf_tensors(path, with_meta=False):
+    """Returns {name: (ggml_type, shape, raw bytes)} of a GGUF v2/v3 file
+    (and the metadata dict, with_meta)."""
     with open(path, "rb") as f:
         data = f.read()
     off = 0
@@ -64,10 +71,13 @@ def gguf_tensors(path):
     assert version in (2, 3), version
     n_tensors, n_kv = rd("Q"), rd("Q")
     align = 32
+    meta = {}
     for _ in range(n_kv):
         key = rstr()
         t = rd("I")
         v = rval(t)
+        if not key.startswith("tokenizer."):
+            meta[key] = v
         if key == "general.alignment":
             align = int(v)
     infos = []
@@ -89,7 +99,41 @@ def gguf_tensors(path):
         n = int(np.prod(dims))
         nbytes = n // be * bb
         out[name] = (t, [int(d) for d in reversed(dims)], data[base + o: base + o + nbytes])
-    return out
+    return (out, meta) if with_meta else out
+
+
+def write_model(ref, fx):
+    """The decoder fixtures of testdata/<fx> (model tensors, config, expected)."""
+    t, meta = gguf_tensors(os.path.join(ref, f"testdata/{fx}/tiny-q4km.gguf"), with_meta=True)
+    arrays = {}
+    for name, (gt, shape, raw) in sorted(t.items()):
+        key = name.replace(".", "_")
+        if gt == 0:
+            arrays[key + "__f32"] = np.frombuffer(raw, np.float32).reshape(shape)
+        else:
+            arrays[key + "__bytes"] = np.frombuffer(raw, np.uint8)
+            arrays[key + "__dtype"] = np.array([{8: 64, 12: 66, 14: 67}[gt]], np.int64)
+        arrays[key + "__shape"] = np.array(shape, np.int64)
+    np.savez_compressed(os.path.join(HERE, f"{fx}_model.npz"), **arrays)
+    arch = meta["general.architecture"]
+    cfg = {
+        "arch": arch,
+        "layers": meta[f"{arch}.block_count"],
+        "embed": meta[f"{arch}.embedding_length"],
+        "ffn": meta[f"{arch}.feed_forward_length"],
+        "heads": meta[f"{arch}.attention.head_count"],
+        "kv_heads": meta.get(f"{arch}.attention.head_count_kv", meta[f"{arch}.attention.head_count"]),
+        "rope_dims": meta.get(f"{arch}.rope.dimension_count"),
+        "rope_theta": meta.get(f"{arch}.rope.freq_base", 10000.0),
+        "norm_eps": meta[f"{arch}.attention.layer_norm_rms_epsilon"],
+        "context": meta[f"{arch}.context_length"],
+    }
+    e = json.load(open(os.path.join(ref, f"testdata/{fx}/expected.json")))
+    out = {"config": cfg, "vocab": e["vocab"], "prompt_ids": e["prompt_ids"], "greedy": e["greedy"],
+           "prompt_logits": e["prompt_logits"], "greedy_logits": e["greedy_logits"],
+           "llama_cpp_max_diff": e["llama_cpp_max_diff"]}
+    json.dump(out, open(os.path.join(HERE, f"{fx}_expected.json"), "w"))
+    print("wrote", fx, cfg)
 
 
 def main(ref):
@@ -113,6 +157,8 @@ def main(ref):
         arrays[key + "__dtype"] = np.array([66 if gt == 12 else 67], np.int64)
     np.savez_compressed(os.path.join(HERE, "llama_tensors.npz"), **arrays)
     print("wrote", len(names), "tensors:", ", ".join(names))
+    for fx in ("llama", "qwen2"):
+        write_model(ref, fx)
 
 
 if __name__ == "__main__":

@@ -454,3 +454,42 @@ def test_cfg1_layer_shapes_bitexact(gpu, oracle, name, n, k, dt, seed):
         want = oracle.linear_a8(x, wb, dt, n, k, block=256, threads=8)
         assert bits_equal(got, want), (name, rows, first_diff(got, want))
     W.release()
+
+
+# ------------------------------------------------------ weight registration
+
+def test_register_same_bytes_shares_and_other_bytes_upload(gpu, oracle):
+    """The same (address, length, dtype, shape) returns the same handle with
+    one more reference; other bytes written at that address (a file closed
+    and another mapped there) are uploaded afresh, and the old handle keeps
+    computing with its own copy until released."""
+    import ctypes
+
+    lib = gpu.load()
+    n, k = 64, 512
+    buf = np.ascontiguousarray(oracle.synthetic_weight(Q4_K, n, k, seed=31))
+    first = buf.copy()
+    x = oracle.synthetic_acts(1, k, seed=32)
+
+    def reg():
+        h = ctypes.c_uint64()
+        assert lib.mimg_register_weight(buf.ctypes.data, buf.size, Q4_K, n, k, ctypes.byref(h)) == 0
+        return h.value
+
+    def run(h):
+        y = np.empty((1, n), np.float32)
+        assert lib.mimg_dequant_matmul_a8(h, x.ctypes.data, 1, None, 256, y.ctypes.data) == 0
+        return y
+
+    h1 = reg()
+    assert reg() == h1                      # second reference, no upload
+    assert lib.mimg_release_weight(h1) == 0  # drops one: still valid
+    assert bits_equal(run(h1), oracle.linear_a8(x, first, Q4_K, n, k, block=256))
+    buf[:] = oracle.synthetic_weight(Q4_K, n, k, seed=33)  # new bytes, same address
+    h2 = reg()
+    assert h2 != h1
+    assert bits_equal(run(h2), oracle.linear_a8(x, buf, Q4_K, n, k, block=256))
+    assert bits_equal(run(h1), oracle.linear_a8(x, first, Q4_K, n, k, block=256))
+    assert lib.mimg_release_weight(h1) == 0
+    assert lib.mimg_release_weight(h1) < 0   # gone
+    assert lib.mimg_release_weight(h2) == 0
