@@ -19,6 +19,16 @@ graph. Timed region: exactly --steps steps between two synchronisations.
 
 value = bytes per step / time per step, bytes by BASELINE.md's formula
 (sum of N*(K/QK)*block_bytes + K*4 + N*4 over the seven matrices).
+
+The "decode" section runs whole greedy generation on the GPU decoder
+(mimir-model_amd/decoder.py) with random Q4_K_M weights of two model shapes
+(BASELINE.json configs[3] and [4]): a Llama-3.2-1B shape with a 32-token
+prompt (uniform ids, seed 7) and 128 new tokens, and a Llama-3-8B shape
+with a 512-token prompt and 256 new tokens at batch 1 and at batch 8 (eight
+sequences in eight cache slots), f16 key-value cache. Reported: decode
+tokens/s (every sequence's new tokens over the device time of the decode
+steps), prompt tokens/s, and the weight bytes a decode step reads over the
+step time.
 """
 import argparse
 import json
@@ -137,6 +147,47 @@ def cpu_baseline(host_bytes, xs, seconds, log):
     }
 
 
+def decode_bench(name, log):
+    """Greedy generation on the GPU decoder with a random model of the
+    named shape (module docstring)."""
+    import decoder
+    import synthetic
+
+    cfg = dict(synthetic.LLAMA_1B if name == "llama1b" else synthetic.LLAMA_8B)
+    runs = [(32, 128, 1)] if name == "llama1b" else [(512, 256, 1), (512, 256, 8)]
+    cfg["context"] = max(p + n for p, n, _ in runs)
+    t0 = time.time()
+    tensors = synthetic.build(cfg, seed=1, log=log)
+    slots = max(b for _, _, b in runs)
+    rows = max(min(p * b, 512) for p, _, b in runs)
+    dec = decoder.Decoder(cfg, tensors, a8=True, cache_f16=True, max_rows=rows, slots=slots)
+    log(f"  {name}: model and decoder ready in {time.time() - t0:.1f} s")
+    step_bytes_tok = synthetic.weight_bytes(cfg, per_token=True)
+    out = {}
+    for P, n_new, batch in runs:
+        prompts = np.random.default_rng(7).integers(0, cfg["vocab"], (batch, P)).astype(np.int32)
+        dec.generate(prompts, 4)  # warm up: captures the decode graph
+        dec.reset()
+        tm = {}
+        ids = dec.generate(prompts, n_new, timing=tm)
+        dec.reset()
+        step_ms = tm["decode_ms"] / tm["decode_steps"]
+        key = f"{name}_P{P}_N{n_new}_B{batch}"
+        out[key] = {
+            "decode_tok_per_s": round(batch * tm["decode_steps"] / (tm["decode_ms"] * 1e-3), 1),
+            "ms_per_step": round(step_ms, 4),
+            "prompt_tok_per_s": round(tm["prompt_rows"] / (tm["prompt_ms"] * 1e-3), 1),
+            "prompt_ms": round(tm["prompt_ms"], 3),
+            "weight_GB_per_s": round(step_bytes_tok / (step_ms * 1e-3) / 1e9, 1),
+            "weight_bytes_per_step": step_bytes_tok,
+            "first_ids": ids[0, :8].tolist(),
+        }
+        log(f"  {key}: {out[key]}")
+    del dec
+    tensors.clear()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -149,6 +200,8 @@ def main():
     ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
     ap.add_argument("--prefill-rows", default="512,2048",
                     help="activation rows of the prefill GEMM measurements (comma list; empty to skip)")
+    ap.add_argument("--decode", default="llama1b,llama8b",
+                    help="whole-model decode runs (comma list of llama1b, llama8b; empty to skip)")
     ap.add_argument("--roofline-replays", type=int, default=8,
                     help="replays of the graph of --rotate single-kernel launches timed for the roofline")
     args = ap.parse_args()
@@ -184,6 +237,7 @@ def main():
             mimg.linear_a8_group_dev([layers[l][c[0]] for c in grp], xd[i].ptr, M, None, 256,
                                      [yd[c[0]].ptr for c in grp], ws[i].ptr, ws_bytes[i], stream.handle)
 
+    graphs = []
     if args.eager:
         run_step = enqueue_step
     else:
@@ -352,6 +406,13 @@ def main():
             "GB_per_s": round(launch_bytes(CFG1[4][1], CFG1[4][2], Q4_K, M) / (host_us * 1e-6) / 1e9, 1),
         },
     }
+    del graphs
+    layers.clear()
+    decode_res = {}
+    for name in [d for d in args.decode.split(",") if d]:
+        decode_res.update(decode_bench(name, log))
+    if decode_res:
+        result["decode"] = decode_res
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(host_bytes, xs, args.cpu_seconds, log)
     print(json.dumps(result), flush=True)

@@ -170,6 +170,11 @@ int mimg_dequantize_dev(uint32_t dtype, const void *src, uint64_t len, float *ds
 int mimg_quantize_dev(uint32_t dtype, const float *src, int64_t n, void *dst, uint64_t dst_len,
                       void *stream);
 
+/* n values ~ N(0, stdv^2) into dst (device), a function of (seed, index)
+ * only. No reference counterpart: it builds the random weights of the
+ * benchmark models (N(0, 0.02^2) before encoding) on the device. */
+int mimg_synthetic_normal_dev(uint64_t seed, float stdv, float *dst, int64_t n, void *stream);
+
 /* ---- decoder-step ops on device buffers ---------------------------------
  * The other fast paths of the graph the reference's importer writes for a
  * llama/qwen2 model (reference importer/llama.go:317-547, interp/fast.go:40-59),
@@ -208,9 +213,12 @@ int mimg_kv_store_dev(const float *k, const float *v, const int64_t *pos, int64_
  * query t of head h sees the cache entries kstart[t]..kend[t] (inclusive;
  * kstart may be NULL for 0) of kv head h / (heads / kv_heads), as the mask
  * of a cache with one or several sequences ("slots") allows; scale
- * 1/sqrt(d). q, out: [T, heads, d]. d <= 512, at most 8192 visible keys
- * (the range is clipped to the cache row and to 8192 keys; a query that
- * sees nothing gets zeros). */
+ * 1/sqrt(d). q, out: [T, heads, d]. Bit for bit the reference's attendRow
+ * with its AVX2 kernels (interp/fast.go:728-751; scores, Cephes expf sum
+ * and ordered weighted sum of internal/kernels/attn_amd64.s:12-468).
+ * d a multiple of 8, at most 512; at most 8192 visible keys (the range is
+ * clipped to the cache row and to 8192 keys; a query that sees nothing gets
+ * zeros, a non-finite largest score NaN). */
 int mimg_attention_dev(const float *q, const void *kcache, const void *vcache, const int64_t *kend,
                        const int64_t *kstart, int64_t T, int heads, int kv_heads, int d, int64_t context, int f16,
                        float *out, void *stream);
@@ -223,8 +231,13 @@ int mimg_attention_dev(const float *q, const void *kcache, const void *vcache, c
 int mimg_greedy_advance_dev(const int32_t *chosen, int32_t *ids, int64_t *pos, int64_t *cache_index, int32_t *out,
                             int32_t *count, int cap, int n, void *stream);
 
-/* swiglu.v1 (reference interp/fast.go:487-498): out = silu(g) * u. */
-int mimg_swiglu_dev(const float *g, const float *u, float *out, int64_t n, void *stream);
+/* swiglu.v1 (reference interp/fast.go:487-498): out = silu(g) * u, bit for
+ * bit as the reference computes it with GOMAXPROCS = procs: its parallel()
+ * cuts the n elements into pieces of max(1, n / (min(procs, n) * 8))
+ * (interp/pool.go:33-51) and SiluMulF32 (internal/kernels/attn.go:63-76)
+ * takes the first len&~7 of each piece through the AVX2 formula
+ * (attn_amd64.s:459-535), the rest through float64. */
+int mimg_swiglu_dev(const float *g, const float *u, float *out, int64_t n, int procs, void *stream);
 
 /* Greedy choice (reference cmd/mim-run/main.go:184-192): out[r] = the first
  * index of the largest value of row r of x [rows, n]. */

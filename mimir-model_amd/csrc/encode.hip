@@ -124,6 +124,38 @@ __global__ void encode_q6_k_kernel(const float* __restrict__ src, int64_t nb, ui
     blk[209] = (uint8_t)(hd >> 8);
 }
 
+// Synthetic N(0, std^2) values for benchmark models: element pair i comes
+// from one 64-bit hash of (seed, i) (splitmix64's finaliser) through the
+// Box-Muller transform, so the values depend on (seed, i) only, not on the
+// launch shape.
+__device__ __forceinline__ uint64_t splitmix_fin(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+__global__ void normal_fill_kernel(uint64_t seed, float stdv, float* __restrict__ dst, int64_t n) {
+    const int64_t pairs = (n + 1) / 2;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < pairs; i += (int64_t)gridDim.x * blockDim.x) {
+        const uint64_t h = splitmix_fin(splitmix_fin(seed) ^ (0x9e3779b97f4a7c15ull * (uint64_t)(i + 1)));
+        const float u1 = (float)((h >> 40) + 1) * 0x1p-24f;     // (0, 1]
+        const float u2 = (float)((h >> 16) & 0xFFFFFF) * 0x1p-24f;  // [0, 1)
+        const float r = stdv * sqrtf(-2.f * logf(u1));
+        float sn, cs;
+        sincosf(6.2831853f * u2, &sn, &cs);
+        dst[2 * i] = r * cs;
+        if (2 * i + 1 < n) dst[2 * i + 1] = r * sn;
+    }
+}
+
+hipError_t launch_normal_fill(uint64_t seed, float stdv, float* dst, int64_t n, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int64_t pairs = (n + 1) / 2;
+    const unsigned grid = (unsigned)((pairs + 255) / 256 < 16384 ? (pairs + 255) / 256 : 16384);
+    hipLaunchKernelGGL(normal_fill_kernel, dim3(grid), dim3(256), 0, stream, seed, stdv, dst, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_encode(uint32_t dt, const float* x, int64_t n, uint8_t* dst, hipStream_t stream) {
     int64_t be = dt == DT_Q8_0 ? 32 : 256;
     int64_t nb = n / be;

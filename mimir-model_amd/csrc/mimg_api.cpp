@@ -633,9 +633,9 @@ int mimg_attention_dev(const float* q, const void* kcache, const void* vcache, c
                        float* out, void* stream) {
     int rc = ensure_device();
     if (rc) return rc;
-    if (T < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || d <= 0 || d > 512 || context <= 0)
-        return fail(MIMG_ERR_ARG, "attention: heads %d, kv heads %d, D %d, context %lld (D <= 512)", heads, kv_heads, d,
-                    (long long)context);
+    if (T < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || d <= 0 || d > 512 || d % 8 || context <= 0)
+        return fail(MIMG_ERR_ARG, "attention: heads %d, kv heads %d, D %d, context %lld (D a multiple of 8, <= 512)",
+                    heads, kv_heads, d, (long long)context);
     if (T == 0) return MIMG_OK;
     if (!q || !kcache || !vcache || !kend || !out) return fail(MIMG_ERR_ARG, "null pointer");
     HIP_TRY(launch_attention(q, kcache, vcache, kend, kstart, (int)T, heads, kv_heads, d, context, f16, out,
@@ -653,13 +653,17 @@ int mimg_greedy_advance_dev(const int32_t* chosen, int32_t* ids, int64_t* pos, i
     return MIMG_OK;
 }
 
-int mimg_swiglu_dev(const float* g, const float* u, float* out, int64_t n, void* stream) {
+int mimg_swiglu_dev(const float* g, const float* u, float* out, int64_t n, int procs, void* stream) {
     int rc = ensure_device();
     if (rc) return rc;
     if (n < 0) return fail(MIMG_ERR_ARG, "n = %lld", (long long)n);
     if (n == 0) return MIMG_OK;
     if (!g || !u || !out) return fail(MIMG_ERR_ARG, "null pointer");
-    HIP_TRY(launch_swiglu(g, u, out, n, (hipStream_t)stream));
+    // the reference's piece size (interp/pool.go:33-39)
+    const int64_t w = procs < n ? procs : n;
+    int64_t chunk = n;
+    if (w > 1) chunk = n / (w * 8) > 1 ? n / (w * 8) : 1;
+    HIP_TRY(launch_swiglu(g, u, out, n, chunk, (hipStream_t)stream));
     return MIMG_OK;
 }
 
@@ -670,6 +674,16 @@ int mimg_argmax_dev(const float* x, int64_t rows, int64_t n, int32_t* out, void*
     if (rows == 0) return MIMG_OK;
     if (!x || !out) return fail(MIMG_ERR_ARG, "null pointer");
     HIP_TRY(launch_argmax(x, rows, n, out, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_synthetic_normal_dev(uint64_t seed, float stdv, float* dst, int64_t n, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (n < 0) return fail(MIMG_ERR_ARG, "n = %lld", (long long)n);
+    if (n == 0) return MIMG_OK;
+    if (!dst) return fail(MIMG_ERR_ARG, "null pointer");
+    HIP_TRY(launch_normal_fill(seed, stdv, dst, n, (hipStream_t)stream));
     return MIMG_OK;
 }
 

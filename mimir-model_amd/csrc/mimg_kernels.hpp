@@ -96,12 +96,13 @@ hipError_t launch_attention(const float* q, const void* kc, const void* vc, cons
                             int T, int H, int Hkv, int D, int64_t C, int f16, float* out, hipStream_t s);
 hipError_t launch_greedy_advance(const int32_t* chosen, int32_t* ids, int64_t* pos, int64_t* cidx, int32_t* out,
                                  int32_t* count, int cap, int n, hipStream_t s);
-hipError_t launch_swiglu(const float* g, const float* u, float* out, int64_t n, hipStream_t s);
+hipError_t launch_swiglu(const float* g, const float* u, float* out, int64_t n, int64_t chunk, hipStream_t s);
 hipError_t launch_argmax(const float* x, int64_t rows, int64_t n, int32_t* out, hipStream_t s);
 
 hipError_t launch_dequantize(uint32_t dt, const uint8_t* src, int64_t n_elems, float* dst,
                              hipStream_t stream);
 
 hipError_t launch_encode(uint32_t dt, const float* x, int64_t n, uint8_t* dst, hipStream_t stream);
+hipError_t launch_normal_fill(uint64_t seed, float stdv, float* dst, int64_t n, hipStream_t stream);
 
 }  // namespace mimg

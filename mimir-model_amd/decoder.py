@@ -54,12 +54,16 @@ class Decoder:
 
     tensors: {GGUF tensor name: (dtype, shape, data)}, where data is the
     block bytes (np.uint8) of a quantized matrix, an np.float32 array for a
-    norm scale or bias, or an already registered mimg.Weight.
+    norm scale or bias, or an already registered mimg.Weight. procs is the
+    GOMAXPROCS of the reference run to reproduce (its swiglu results depend
+    on it).
     """
 
-    def __init__(self, config, tensors, a8=True, cache_f16=False, max_rows=64, slots=1):
+    def __init__(self, config, tensors, a8=True, cache_f16=False, max_rows=64, slots=1, procs=16):
         c = self.c = config if isinstance(config, Config) else Config(**config)
         self.a8, self.f16, self.slots = bool(a8), bool(cache_f16), int(slots)
+        # the reference's GOMAXPROCS: swiglu's results follow its piece split
+        self.procs = int(procs)
         self.R = int(max_rows)
         mimg.init()
         self.stream = hiprt.Stream()
@@ -120,13 +124,19 @@ class Decoder:
         for w, b, y in zip(ws, bs, ys):
             mimg.linear_a8_dev(w, x, rows, b, self._block(w), y, self.ws.ptr, self.ws_bytes, s)
 
-    def _forward(self, T):
-        """Enqueues the forward pass of the T rows in ids/pos/cidx/kstart;
-        logits [T, vocab] land in self.logits."""
+    def _forward(self, T, ids=None, pos=None, cidx=None, kstart=None, head_rows=None):
+        """Enqueues the forward pass of T rows (device arrays of token ids,
+        positions, cache indices and slot starts; by default the decoder's
+        own). Logits land in self.logits: all T rows, or with head_rows =
+        [(row, logits row)] only those rows (the head is the largest matrix;
+        generation needs the last row of each prompt only)."""
         c, s = self.c, self.stream.handle
         E, F, H, Hkv, D = c.embed, c.ffn, c.heads, c.kv_heads, c.head_dim
-        kstart = self.kstart.ptr if self.slots > 1 else None
-        mimg.embedding_dev(self.w["token_embd.weight"], self.ids.ptr, T, self.x.ptr, s)
+        ids = ids or self.ids.ptr
+        pos = pos or self.pos.ptr
+        cidx = cidx or self.cidx.ptr
+        kstart = (kstart or self.kstart.ptr) if self.slots > 1 else None
+        mimg.embedding_dev(self.w["token_embd.weight"], ids, T, self.x.ptr, s)
         resid = None  # the previous sublayer's output, added to x by the next norm
         for l in range(c.layers):
             p = f"blk.{l}."
@@ -135,25 +145,27 @@ class Decoder:
             self._linears([p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"], self.h.ptr, T,
                           [self.q.ptr, self.k.ptr, self.v.ptr],
                           [p + "attn_q.bias", p + "attn_k.bias", p + "attn_v.bias"])
-            mimg.rope_dev(self.q.ptr, self.pos.ptr, self.invf.ptr, T, H, D, c.rope_dims, c.interleaved, s)
-            mimg.rope_dev(self.k.ptr, self.pos.ptr, self.invf.ptr, T, Hkv, D, c.rope_dims, c.interleaved, s)
-            mimg.kv_store_dev(self.k.ptr, self.v.ptr, self.cidx.ptr, T, Hkv, D, self.cache_len, self.kc[l].ptr,
+            mimg.rope_dev(self.q.ptr, pos, self.invf.ptr, T, H, D, c.rope_dims, c.interleaved, s)
+            mimg.rope_dev(self.k.ptr, pos, self.invf.ptr, T, Hkv, D, c.rope_dims, c.interleaved, s)
+            mimg.kv_store_dev(self.k.ptr, self.v.ptr, cidx, T, Hkv, D, self.cache_len, self.kc[l].ptr,
                               self.vc[l].ptr, self.f16, s)
-            mimg.attention_dev(self.q.ptr, self.kc[l].ptr, self.vc[l].ptr, self.cidx.ptr, kstart, T, H, Hkv, D,
+            mimg.attention_dev(self.q.ptr, self.kc[l].ptr, self.vc[l].ptr, cidx, kstart, T, H, Hkv, D,
                                self.cache_len, self.f16, self.o.ptr, s)
             self._linears([p + "attn_output.weight"], self.o.ptr, T, [self.ao.ptr])
             mimg.rms_norm_dev(self.x.ptr, self.ao.ptr, self.vec[p + "ffn_norm.weight"].ptr, c.norm_eps, T, E,
                               self.h.ptr, s)
             self._linears([p + "ffn_gate.weight", p + "ffn_up.weight"], self.h.ptr, T, [self.g.ptr, self.u.ptr])
-            mimg.swiglu_dev(self.g.ptr, self.u.ptr, self.g.ptr, T * F, s)
+            mimg.swiglu_dev(self.g.ptr, self.u.ptr, self.g.ptr, T * F, self.procs, s)
             self._linears([p + "ffn_down.weight"], self.g.ptr, T, [self.ao.ptr])
             resid = self.ao.ptr
         mimg.rms_norm_dev(self.x.ptr, resid, self.vec["output_norm.weight"].ptr, c.norm_eps, T, E, self.h.ptr, s)
-        if self.a8:
-            mimg.linear_a8_dev(self.head, self.h.ptr, T, None, self._block(self.head), self.logits.ptr, self.ws.ptr,
-                               self.ws_bytes, s)
-        else:
-            mimg.linear_f32_dev(self.head, self.h.ptr, T, None, self.logits.ptr, s)
+        V = self.vocab
+        for src, dst, n in ([(0, 0, T)] if head_rows is None else [(r, d, 1) for r, d in head_rows]):
+            xh, yh = self.h.ptr + src * E * 4, self.logits.ptr + dst * V * 4
+            if self.a8:
+                mimg.linear_a8_dev(self.head, xh, n, None, self._block(self.head), yh, self.ws.ptr, self.ws_bytes, s)
+            else:
+                mimg.linear_f32_dev(self.head, xh, n, None, yh, s)
 
     def _set_rows(self, tokens, positions, slots=None):
         tokens = np.asarray(tokens, np.int32).ravel()
@@ -184,15 +196,18 @@ class Decoder:
         self.stream.sync()
         return self.logits.download(np.float32, T * self.vocab).reshape(T, self.vocab)
 
+    def _decode_step(self, n):
+        """One greedy step of n sequences: forward of the tokens in ids,
+        pick, append, advance."""
+        self._forward(n)
+        mimg.argmax_dev(self.logits.ptr, n, self.vocab, self.chosen.ptr, self.stream.handle)
+        mimg.greedy_advance_dev(self.chosen.ptr, self.ids.ptr, self.pos.ptr, self.cidx.ptr, self.out.ptr,
+                                self.count.ptr, self.out_cap, n, self.stream.handle)
+
     def _decode_graph(self, n):
         g = self.graphs.get(n)
         if g is None:
-            def step():
-                self._forward(n)
-                mimg.argmax_dev(self.logits.ptr, n, self.vocab, self.chosen.ptr, self.stream.handle)
-                mimg.greedy_advance_dev(self.chosen.ptr, self.ids.ptr, self.pos.ptr, self.cidx.ptr, self.out.ptr,
-                                        self.count.ptr, self.out_cap, n, self.stream.handle)
-            g = self.graphs[n] = hiprt.Graph(self.stream, step)
+            g = self.graphs[n] = hiprt.Graph(self.stream, lambda: self._decode_step(n))
         return g
 
     def _ensure_out(self, cap, n):
@@ -201,54 +216,61 @@ class Decoder:
             self.out_cap = cap
             self.graphs = {}  # captured with the old buffer
 
-    def generate(self, prompts, n_new, slots=None, graph=True):
+    def generate(self, prompts, n_new, slots=None, graph=True, timing=None):
         """Greedy continuation of each prompt (one per slot, all of the same
         length): n_new tokens each, [len(prompts), n_new] (reference
-        cmd/mim-run/main.go generate). The prompts run as one batch of
-        rows; every decode step is a graph replay."""
+        cmd/mim-run/main.go generate). The prompt rows run in batches of at
+        most max_rows, the first pick is made on the device, and every
+        decode step is one graph replay. With a dict as timing, it receives
+        the device times of the prompt (to the first pick) and of the
+        decode steps."""
         prompts = np.atleast_2d(np.asarray(prompts, np.int32))
         n, P = prompts.shape
-        if n > self.slots:
-            raise ValueError(f"{n} prompts, {self.slots} slots")
-        if P + n_new - 1 > self.c.context:
+        if n > self.slots or n > self.R:
+            raise ValueError(f"{n} prompts, {self.slots} slots, {self.R} rows")
+        if P < 1 or P + n_new - 1 > self.c.context:
             raise ValueError(f"{P} + {n_new} tokens exceed the context {self.c.context}")
-        slots = np.arange(n) if slots is None else np.asarray(slots)
+        slots = np.arange(n, dtype=np.int64) if slots is None else np.asarray(slots, np.int64)
+        if slots.size != n or slots.min() < 0 or slots.max() >= self.slots:
+            raise ValueError(f"slots {slots}")
         self._ensure_out(max(n_new, 1), n)
         s = self.stream.handle
-        # the prompts: n*P rows in chunks of at most R
-        rows_tok = prompts.ravel()
+        C = self.c.context
+        # every prompt row's inputs, and the state of the first decode step
+        B = hiprt.DeviceBuffer
         rows_pos = np.tile(np.arange(P, dtype=np.int64), n)
-        rows_slot = np.repeat(slots, P)
-        last = None
-        for c0 in range(0, n * P, self.R):
-            T = self._set_rows(rows_tok[c0:c0 + self.R], rows_pos[c0:c0 + self.R], rows_slot[c0:c0 + self.R])
-            self._forward(T)
-            last = (c0, T)
-        # the last row of each prompt: pick, then continue from position P
+        rows_start = np.repeat(slots * C, P)
+        p_ids, p_pos = B.from_array(prompts.ravel()), B.from_array(rows_pos)
+        p_cidx, p_start = B.from_array(rows_start + rows_pos), B.from_array(rows_start)
         self.stream.sync()
-        lg = self.logits.download(np.float32, last[1] * self.vocab).reshape(last[1], self.vocab)
-        ends = [i * P + P - 1 for i in range(n)]
-        first = []
-        for e in ends:
-            if e < last[0]:
-                raise ValueError("with several prompts, the prompts must fit in one batch of rows")
-            first.append(int(np.argmax(lg[e - last[0]])))
-        self.chosen.upload(np.array(first, np.int32))
-        self._set_rows(np.array(first, np.int32), np.full(n, P - 1), slots)
+        self.pos.upload(np.full(n, P - 1, np.int64))
+        self.cidx.upload(slots * C + P - 1)
+        self.kstart.upload(slots * C)
         self.count.upload(np.zeros(1, np.int32))
+        ev = [hiprt.Event() for _ in range(3)]
+        ev[0].record(self.stream)
+        for c0 in range(0, n * P, self.R):
+            T = min(self.R, n * P - c0)
+            heads = [(i * P + P - 1 - c0, i) for i in range(n) if c0 <= i * P + P - 1 < c0 + T]
+            self._forward(T, p_ids.ptr + 4 * c0, p_pos.ptr + 8 * c0, p_cidx.ptr + 8 * c0, p_start.ptr + 8 * c0,
+                          head_rows=heads)
+        mimg.argmax_dev(self.logits.ptr, n, self.vocab, self.chosen.ptr, s)
         mimg.greedy_advance_dev(self.chosen.ptr, self.ids.ptr, self.pos.ptr, self.cidx.ptr, self.out.ptr,
                                 self.count.ptr, self.out_cap, n, s)
-        if graph:
+        ev[1].record(self.stream)
+        if graph and n_new > 1:
             g = self._decode_graph(n)
             for _ in range(n_new - 1):
                 g.launch(self.stream)
         else:
             for _ in range(n_new - 1):
-                self._forward(n)
-                mimg.argmax_dev(self.logits.ptr, n, self.vocab, self.chosen.ptr, s)
-                mimg.greedy_advance_dev(self.chosen.ptr, self.ids.ptr, self.pos.ptr, self.cidx.ptr, self.out.ptr,
-                                        self.count.ptr, self.out_cap, n, s)
+                self._decode_step(n)
+        ev[2].record(self.stream)
         self.stream.sync()
+        if timing is not None:
+            timing["prompt_ms"] = ev[0].elapsed_ms(ev[1])
+            timing["decode_ms"] = ev[1].elapsed_ms(ev[2])
+            timing["prompt_rows"], timing["decode_steps"] = n * P, n_new - 1
         return self.out.download(np.int32, n_new * n).reshape(n_new, n).T.copy()
 
     def reset(self):

@@ -49,13 +49,14 @@ SIGNATURES = {
     "mimg_linear_f32_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
     "mimg_dequantize_dev": (_I, [_U32, _P, _U64, _P, _I64, _P]),
     "mimg_quantize_dev": (_I, [_U32, _P, _I64, _P, _U64, _P]),
+    "mimg_synthetic_normal_dev": (_I, [_U64, ctypes.c_float, _P, _I64, _P]),
     "mimg_embedding_dev": (_I, [_U64, _P, _I64, _P, _P]),
     "mimg_rms_norm_dev": (_I, [_P, _P, _P, ctypes.c_float, _I64, _I64, _P, _P]),
     "mimg_rope_dev": (_I, [_P, _P, _P, _I64, _I, _I, _I, _I, _P]),
     "mimg_kv_store_dev": (_I, [_P, _P, _P, _I64, _I, _I, _I64, _P, _P, _I, _P]),
     "mimg_attention_dev": (_I, [_P, _P, _P, _P, _P, _I64, _I, _I, _I, _I64, _I, _P, _P]),
     "mimg_greedy_advance_dev": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _P]),
-    "mimg_swiglu_dev": (_I, [_P, _P, _P, _I64, _P]),
+    "mimg_swiglu_dev": (_I, [_P, _P, _P, _I64, _I, _P]),
     "mimg_argmax_dev": (_I, [_P, _I64, _I64, _P, _P]),
 }
 
@@ -225,6 +226,10 @@ def quantize_dev(dt, x_ptr, n, dst_ptr, dst_bytes, stream):
     _check(load().mimg_quantize_dev(dt, _P(x_ptr), n, _P(dst_ptr), dst_bytes, _P(stream)))
 
 
+def synthetic_normal_dev(seed, std, dst_ptr, n, stream):
+    _check(load().mimg_synthetic_normal_dev(seed, std, _P(dst_ptr), n, _P(stream)))
+
+
 def _o(ptr):
     return _P(ptr) if ptr else None
 
@@ -259,8 +264,9 @@ def greedy_advance_dev(chosen_ptr, ids_ptr, pos_ptr, cidx_ptr, out_ptr, count_pt
                                           _P(count_ptr), cap, n, _P(stream)))
 
 
-def swiglu_dev(g_ptr, u_ptr, out_ptr, n, stream):
-    _check(load().mimg_swiglu_dev(_P(g_ptr), _P(u_ptr), _P(out_ptr), n, _P(stream)))
+def swiglu_dev(g_ptr, u_ptr, out_ptr, n, procs, stream):
+    """procs: the reference's GOMAXPROCS, which fixes its piece split."""
+    _check(load().mimg_swiglu_dev(_P(g_ptr), _P(u_ptr), _P(out_ptr), n, procs, _P(stream)))
 
 
 def argmax_dev(x_ptr, rows, n, out_ptr, stream):

@@ -11,18 +11,22 @@ Each op follows the reference's fast path:
                  x1*c - x2*s, x2*c + x1*s in f32; adjacent pairs for llama
                  ("interleaved"), halves for qwen2 (interp/fast.go:507-557,
                  transformer.go:257-324)
-  attention.v1/2 keys j <= position visible (the graph's mask), scores
-                 f32(q.k)*f32(1/sqrt(D)), e = f32(exp(f64(s - max))), o = (sum e v)/sum e
-                 (interp/fast.go:569-700, internal/kernels/attn.go:44-61); GQA
-                 head h reads kv head h/(H/Hkv); with the cache in f16 the new
-                 keys and values are rounded to f16 first (llama.go:489-499)
-  swiglu.v1      f32(f64(g)/(1+exp(-f64(g)))*f64(u)) (internal/kernels/attn.go:63-73)
+  attention.v1/2 keys j <= position visible (the graph's mask); attendRow
+                 with the AVX2 kernels: scores, Cephes expf sum, ordered
+                 weighted sum (interp/fast.go:559-751, attn_amd64.s), the C
+                 restatement mimref.attention; GQA head h reads kv head
+                 h/(H/Hkv); with the cache in f16 the new keys and values are
+                 rounded to f16 as they are stored (llama.go:489-499)
+  swiglu.v1      SiluMulF32 over the pieces of parallel() for GOMAXPROCS =
+                 procs (interp/fast.go:487-498, attn.go:63-76), mimref.silu_mul
   linears        dequant_matmul_a8.v2 (block 256) for Q4_K/Q6_K, v1 (block
                  32) otherwise, with a8; dequant_matmul.v1 without
                  (llama.go:264-280); the oracle's C linear_a8/linear_f32.
-Dot products inside attention and the f64 sums use numpy's summation
-order, not the reference's lanes: the checks on this oracle are the
-reference fixture's tolerances (float64-oracle logits), not bits.
+The f64 sums of rms_norm use numpy's order and the f64 cos/sin/exp come
+from numpy/libm rather than Go's math package: after rounding to f32 these
+agree with the reference except with probability ~1e-7 per value. Checks:
+the reference fixtures' tolerances (float64-oracle logits) and
+tests/test_oracle_decoder.py.
 """
 import numpy as np
 
@@ -77,42 +81,26 @@ def rope(x, cos, sin, rotary, interleaved):
     return y
 
 
-def attention(q, kc, vc, positions, kv_heads):
-    """q: [T, H, D]; kc/vc: [Hkv, C, D] f32 (already rounded when f16);
-    query t sees keys 0..positions[t]."""
-    T, H, D = q.shape
-    G = H // kv_heads
-    scale = np.float32(1.0 / np.sqrt(D))
-    out = np.zeros((T, H, D), np.float32)
-    for t in range(T):
-        end = int(positions[t]) + 1
-        for h in range(H):
-            k = kc[h // G, :end]
-            v = vc[h // G, :end]
-            s = (k @ q[t, h]).astype(np.float32) * scale
-            mx = s.max()
-            e = np.exp((s - mx).astype(np.float64)).astype(np.float32)
-            tot = np.float32(0)
-            for ev in e:  # sequential f32 sum, as ExpSumF32's tail
-                tot = np.float32(tot + ev)
-            out[t, h] = (e @ v).astype(np.float32) / tot
-    return out
+def attention(q, kc, vc, positions, kv_heads, kstart=None):
+    """q: [T, H, D]; kc/vc: [Hkv, C, D] float32 or float16; query t sees
+    cache entries kstart[t] (default 0) .. positions[t]."""
+    return mimref.attention(q, kc, vc, np.asarray(positions, np.int64), kstart)
 
 
-def swiglu(g, u):
-    g64 = g.astype(np.float64)
-    return (g64 / (1.0 + np.exp(-g64)) * u.astype(np.float64)).astype(np.float32)
+def swiglu(g, u, procs=16):
+    return mimref.silu_mul(g, u, procs).reshape(np.shape(g))
 
 
 class Decoder:
     """The forward pass with a key-value cache, on the CPU."""
 
-    def __init__(self, model, a8=True, cache_f16=False, threads=8):
-        self.m, self.a8, self.f16, self.threads = model, a8, cache_f16, threads
+    def __init__(self, model, a8=True, cache_f16=False, threads=8, procs=16):
+        self.m, self.a8, self.f16, self.threads, self.procs = model, a8, cache_f16, threads, procs
         c = model.c
         C = c["context"]
-        self.kc = [np.zeros((c["kv_heads"], C, c["head_dim"]), np.float32) for _ in range(c["layers"])]
-        self.vc = [np.zeros((c["kv_heads"], C, c["head_dim"]), np.float32) for _ in range(c["layers"])]
+        cdt = np.float16 if cache_f16 else np.float32
+        self.kc = [np.zeros((c["kv_heads"], C, c["head_dim"]), cdt) for _ in range(c["layers"])]
+        self.vc = [np.zeros((c["kv_heads"], C, c["head_dim"]), cdt) for _ in range(c["layers"])]
 
     def linear(self, x, name, bias=None):
         dt, shape, w = self.m.t[name]
@@ -150,16 +138,13 @@ class Decoder:
             v = self.linear(h, p + "attn_v.weight", bias("attn_v.bias")).reshape(T, Hkv, D)
             q = rope(q, cos, sin, c["rope_dims"], inter)
             k = rope(k, cos, sin, c["rope_dims"], inter)
-            if self.f16:
-                k = k.astype(np.float16).astype(np.float32)
-                v = v.astype(np.float16).astype(np.float32)
             for i, pos in enumerate(positions):
-                self.kc[l][:, pos] = k[i]
+                self.kc[l][:, pos] = k[i]  # rounded to f16 (RNE) with an f16 cache
                 self.vc[l][:, pos] = v[i]
             o = attention(q, self.kc[l], self.vc[l], positions, Hkv).reshape(T, H * D)
             x = (x + self.linear(o, p + "attn_output.weight")).astype(np.float32)
             h = rms_norm(x, m.t[p + "ffn_norm.weight"][2], c["norm_eps"])
-            a = swiglu(self.linear(h, p + "ffn_gate.weight"), self.linear(h, p + "ffn_up.weight"))
+            a = swiglu(self.linear(h, p + "ffn_gate.weight"), self.linear(h, p + "ffn_up.weight"), self.procs)
             x = (x + self.linear(a, p + "ffn_down.weight")).astype(np.float32)
         x = rms_norm(x, m.t["output_norm.weight"][2], c["norm_eps"])
         head = "output.weight" if "output.weight" in m.t else "token_embd.weight"

@@ -787,3 +787,177 @@ int mref_linear_a8(const float *x, int64_t rows, const uint8_t *w, uint32_t dt, 
     free(ok);
     return MREF_OK;
 }
+
+/* ---- the decoder ops around the linears ---------------------------------
+ * Restated from the reference's attention and swiglu fast paths
+ * (interp/fast.go:487-498, 559-751; internal/kernels/attn.go:24-140) with
+ * the AVX2 kernels they call on amd64 (attn_amd64.s:12-535): the float32
+ * operation order is the one of those kernels, so a GPU kernel following
+ * the same order gives the same bits. Parity: pinned by the reference
+ * fixtures' expected logits (cmd/mim-run/main_test.go tolerances) and by the
+ * checks of tests/test_oracle_decoder.py (closed forms, float64 brute
+ * force, planted mistakes); the AVX2 bits themselves cannot be run here. */
+
+/* Cephes' expf as expSumF32AVX2 evaluates it (attn_amd64.s:81-240): t is
+ * clamped to lo, t = f*ln2 + r with f = rint(t*log2e) and ln2 in two parts,
+ * exp(r) = 1 + r + r^2 P(r), times 2^f built in the exponent; t < lo (and
+ * NaN) gives 0. */
+static inline float cephes_exp_avx2(float t) {
+    const float lo = bits_f32(0xc2aeac4fu), log2e = bits_f32(0x3fb8aa3bu);
+    const float c1 = bits_f32(0x3f318000u), c2 = bits_f32(0xb95e8083u);
+    const int keep = t >= lo;          /* VCMPPS GE_OQ: false for NaN */
+    const float tt = t > lo ? t : lo;  /* VMAXPS: the second operand (lo) for NaN */
+    const float f = rintf(tt * log2e);
+    float r = fmaf(-f, c1, tt);
+    r = fmaf(-f, c2, r);
+    const float r2 = r * r;
+    float p = bits_f32(0x39506967u);
+    p = fmaf(p, r, bits_f32(0x3ab743ceu));
+    p = fmaf(p, r, bits_f32(0x3c088908u));
+    p = fmaf(p, r, bits_f32(0x3d2aa9c1u));
+    p = fmaf(p, r, bits_f32(0x3e2aaaaau));
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r2, r);
+    p = p + 1.0f;
+    const float two_f = bits_f32((uint32_t)((int32_t)f + 127) << 23);
+    const float e = p * two_f;
+    return keep ? e : 0.0f;
+}
+
+/* ExpSumF32 (attn.go:41-56): the first n&~7 through expSumF32AVX2 (eight
+ * lane sums, HSUM ((s0+s4)+(s1+s5))+((s2+s6)+(s3+s7))), the rest
+ * f32(exp(f64(x-m))) added in order. x[i] becomes its exponential. */
+float mref_expsum_f32(float *x, int64_t n, float m) {
+    float s = 0.0f;
+    int64_t i = 0;
+    if (n >= 8) {
+        const int64_t nv = n & ~(int64_t)7;
+        float lane[8] = {0};
+        for (; i < nv; i += 8)
+            for (int c = 0; c < 8; c++) {
+                const float e = cephes_exp_avx2(x[i + c] - m);
+                x[i + c] = e;
+                lane[c] = lane[c] + e;
+            }
+        s = ((lane[0] + lane[4]) + (lane[1] + lane[5])) + ((lane[2] + lane[6]) + (lane[3] + lane[7]));
+    }
+    for (; i < n; i++) {
+        const float e = (float)exp((double)(x[i] - m));
+        x[i] = e;
+        s += e;
+    }
+    return s;
+}
+
+static inline float kv_val(const float *f32, const uint16_t *f16, int64_t i) {
+    return f16 ? mref_f16_to_f32(f16[i]) : f32[i];
+}
+
+/* ScoresF32/ScoresF16 with scoresF32AVX2/scoresF16AVX2 (attn_amd64.s:12-78,
+ * 312-385), D a multiple of 8: lane c of a row accumulates q[8m+c]*k[8m+c]
+ * by fma over m. Rows go in fours from the first, reduced as
+ * ((l0+l1)+(l2+l3))+((l4+l5)+(l6+l7)); the last n%4 rows one by one, as
+ * ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)); then times scale. */
+void mref_scores(const float *q, const float *k32, const uint16_t *k16, int64_t n, int d, float scale,
+                 float *out) {
+    const int64_t n4 = n - n % 4;
+    for (int64_t j = 0; j < n; j++) {
+        float l[8] = {0};
+        for (int m = 0; m < d / 8; m++)
+            for (int c = 0; c < 8; c++) l[c] = fmaf(q[8 * m + c], kv_val(k32, k16, j * d + 8 * m + c), l[c]);
+        const float s = j < n4 ? ((l[0] + l[1]) + (l[2] + l[3])) + ((l[4] + l[5]) + (l[6] + l[7]))
+                               : ((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7]));
+        out[j] = s * scale;
+    }
+}
+
+/* attendRow (fast.go:728-751) over n visible rows of k and v (f32, or f16
+ * when k16/v16 are given), D a multiple of 8: scores, their max, ExpSumF32,
+ * WeightedSum (wsumF32AVX2/wsumF16AVX2, attn_amd64.s:244-307, 390-468: per
+ * element acc = fma(e_j, v_j, acc) over the rows in order), o = acc / sum.
+ * When the largest score is not finite the reference leaves the row to its
+ * scalar loop, whose result is then NaN throughout; this restatement writes
+ * NaN. sc holds n floats of scratch. */
+void mref_attend_row(const float *q, const float *k32, const uint16_t *k16, const float *v32, const uint16_t *v16,
+                     int64_t n, int d, float scale, float *sc, float *o) {
+    mref_scores(q, k32, k16, n, d, scale, sc);
+    float mx = -INFINITY;
+    for (int64_t j = 0; j < n; j++)
+        if (sc[j] > mx || sc[j] != sc[j]) mx = sc[j];
+    if (n == 0 || isinf(mx) || mx != mx) {
+        for (int i = 0; i < d; i++) o[i] = n == 0 ? 0.0f : NAN;
+        return;
+    }
+    const float sum = mref_expsum_f32(sc, n, mx);
+    for (int i = 0; i < d; i++) {
+        float acc = 0.0f;
+        for (int64_t j = 0; j < n; j++) acc = fmaf(sc[j], kv_val(v32, v16, j * d + i), acc);
+        o[i] = acc / sum;
+    }
+}
+
+/* The attention of a decoder step over a cache [kv_heads][context][d]
+ * (f32, or f16 bits when f16): query t of head h sees the entries
+ * kstart[t]..kend[t] of kv head h / (heads / kv_heads). q, out [T][heads][d]. */
+int mref_attention(const float *q, const void *kc, const void *vc, const int64_t *kend, const int64_t *kstart,
+                   int64_t T, int heads, int kv_heads, int d, int64_t context, int f16, float *out, int threads) {
+    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads || d <= 0 || d % 8) return MREF_ERR_ARG;
+    const float scale = (float)(1.0 / sqrt((double)d));
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(dynamic, 1) if (threads > 1)
+#endif
+    for (int64_t th = 0; th < T * heads; th++) {
+        const int64_t t = th / heads;
+        const int h = (int)(th % heads), hk = h / (heads / kv_heads);
+        int64_t k0 = kstart ? kstart[t] : 0;
+        if (k0 < 0) k0 = 0;
+        if (k0 >= context) k0 = context - 1;
+        int64_t n = kend[t] + 1 - k0;
+        if (n > context - k0) n = context - k0;
+        if (n < 0) n = 0;
+        const int64_t base = ((int64_t)hk * context + k0) * d;
+        float *sc = (float *)malloc((size_t)(n > 0 ? n : 1) * 4);
+        mref_attend_row(q + th * d, f16 ? NULL : (const float *)kc + base, f16 ? (const uint16_t *)kc + base : NULL,
+                        f16 ? NULL : (const float *)vc + base, f16 ? (const uint16_t *)vc + base : NULL, n, d, scale,
+                        sc, out + th * d);
+        free(sc);
+    }
+    return MREF_OK;
+}
+
+/* silu(x) * b as siluMulF32AVX2 computes it (attn_amd64.s:459-535):
+ * h = exp(-|x|/2) by the Cephes steps above, e = h*h, silu = x / (1+e) for
+ * x >= 0 and ((x*h)*h) / (1+e) below, then times b. */
+static inline float silu_mul_avx2(float x, float b) {
+    const float t = -fabsf(x) * 0.5f;
+    const float h = cephes_exp_avx2(t);
+    const float e1 = h * h + 1.0f;
+    const float y = (x * h) * h;
+    const float num = x >= 0.0f ? x : y;
+    return (num / e1) * b;
+}
+
+/* swiglu.v1 (fast.go:487-498): parallel() splits the n elements into pieces
+ * of max(1, n / (w*8)), w = min(procs, n) (interp/pool.go:33-51, 79-97; one
+ * piece when w <= 1), and SiluMulF32 (attn.go:63-76) runs on each piece:
+ * its first len&~7 elements through siluMulF32AVX2 (when len >= 8), the
+ * rest as f32(f64(a)/(1+exp(-f64(a)))*f64(b)). So the result depends on
+ * the reference's GOMAXPROCS, given here as procs. */
+void mref_silu_mul(const float *a, const float *b, float *out, int64_t n, int procs) {
+    const int64_t w = procs < n ? procs : n;
+    int64_t chunk = n;
+    if (w > 1) {
+        chunk = n / (w * 8);
+        if (chunk < 1) chunk = 1;
+    }
+    for (int64_t lo = 0; lo < n; lo += chunk) {
+        const int64_t len = lo + chunk < n ? chunk : n - lo;
+        const int64_t nv = len >= 8 ? len & ~(int64_t)7 : 0;
+        for (int64_t i = 0; i < len; i++) {
+            const float x = a[lo + i], y = b[lo + i];
+            out[lo + i] = i < nv ? silu_mul_avx2(x, y)
+                                 : (float)((double)x / (1.0 + exp(-(double)x)) * (double)y);
+        }
+    }
+}

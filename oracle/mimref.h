@@ -75,6 +75,16 @@ int mref_linear_a8(const float *x, int64_t rows, const uint8_t *w, uint32_t dt, 
 int mref_linear_f32(const float *x, int64_t rows, const uint8_t *w, uint32_t dt, int64_t n,
                     int64_t k, const float *bias, float *y, int threads);
 
+/* decoder ops (interp/fast.go:487-498, 559-751 with attn_amd64.s) */
+float mref_expsum_f32(float *x, int64_t n, float m);
+void mref_scores(const float *q, const float *k32, const uint16_t *k16, int64_t n, int d, float scale,
+                 float *out);
+void mref_attend_row(const float *q, const float *k32, const uint16_t *k16, const float *v32, const uint16_t *v16,
+                     int64_t n, int d, float scale, float *sc, float *o);
+int mref_attention(const float *q, const void *kc, const void *vc, const int64_t *kend, const int64_t *kstart,
+                   int64_t T, int heads, int kv_heads, int d, int64_t context, int f16, float *out, int threads);
+void mref_silu_mul(const float *a, const float *b, float *out, int64_t n, int procs);
+
 /* exact fused-multiply-add check helper (fma of floats, for tests) */
 float mref_fmaf(float a, float b, float c);
 

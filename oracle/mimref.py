@@ -54,6 +54,11 @@ def lib():
             "mref_linear_a8": (I, [P, I64, P, U32, I64, I64, P, I, P, I]),
             "mref_linear_f32": (I, [P, I64, P, U32, I64, I64, P, P, I]),
             "mref_fmaf": (F, [F, F, F]),
+            "mref_expsum_f32": (F, [P, I64, F]),
+            "mref_scores": (None, [P, P, P, I64, I, F, P]),
+            "mref_attend_row": (None, [P, P, P, P, P, I64, I, F, P, P]),
+            "mref_attention": (I, [P, P, P, P, P, I64, I, I, I, I64, I, P, I]),
+            "mref_silu_mul": (None, [P, P, P, I64, I]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -189,3 +194,54 @@ def synthetic_weight(dt, n, k, seed, scale=0.02):
 def synthetic_acts(rows, k, seed):
     """x ~ N(0, 1) in f32 from numpy's PCG64 (default_rng(seed))."""
     return np.random.default_rng(seed).standard_normal((rows, k), dtype=np.float32)
+
+
+# ---- decoder ops (interp/fast.go:487-498, 559-751 with attn_amd64.s) ----
+
+def expsum_f32(x, m):
+    """ExpSumF32: (exponentials, their sum)."""
+    x = np.ascontiguousarray(x, np.float32).copy()
+    s = lib().mref_expsum_f32(_p(x), x.size, float(np.float32(m)))
+    return x, np.float32(s)
+
+
+def scores(q, k, scale):
+    """ScoresF32 (k f32 [n, d]) or ScoresF16 (k float16 [n, d])."""
+    q = np.ascontiguousarray(q, np.float32)
+    n, d = k.shape
+    out = np.empty(n, np.float32)
+    if k.dtype == np.float16:
+        k16 = np.ascontiguousarray(k).view(np.uint16)
+        lib().mref_scores(_p(q), None, _p(k16), n, d, float(np.float32(scale)), _p(out))
+    else:
+        k32 = np.ascontiguousarray(k, np.float32)
+        lib().mref_scores(_p(q), _p(k32), None, n, d, float(np.float32(scale)), _p(out))
+    return out
+
+
+def attention(q, kc, vc, kend, kstart=None, threads=1):
+    """q [T, H, D] f32; kc, vc [Hkv, C, D] float32 or float16; query t sees
+    cache entries kstart[t]..kend[t] of its kv head."""
+    q = np.ascontiguousarray(q, np.float32)
+    T, H, D = q.shape
+    Hkv, C, _ = kc.shape
+    f16 = kc.dtype == np.float16
+    kc = np.ascontiguousarray(kc).view(np.uint16) if f16 else np.ascontiguousarray(kc, np.float32)
+    vc = np.ascontiguousarray(vc).view(np.uint16) if f16 else np.ascontiguousarray(vc, np.float32)
+    ke = np.ascontiguousarray(kend, np.int64)
+    ks = None if kstart is None else np.ascontiguousarray(kstart, np.int64)
+    out = np.empty_like(q)
+    rc = lib().mref_attention(_p(q), _p(kc), _p(vc), _p(ke), _p(ks), T, H, Hkv, D, C, int(f16), _p(out), threads)
+    if rc != 0:
+        raise ValueError(f"mref_attention: {rc}")
+    return out
+
+
+def silu_mul(a, b, procs):
+    """swiglu.v1 with the piece split of GOMAXPROCS = procs."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    out = np.empty_like(a)
+    lib().mref_silu_mul(_p(a), _p(b), _p(out), a.size, procs)
+    return out
+
