@@ -147,7 +147,7 @@ def cpu_baseline(host_bytes, xs, seconds, log):
     }
 
 
-def decode_bench(name, log):
+def decode_bench(name, log, graph=True):
     """Greedy generation on the GPU decoder with a random model of the
     named shape (module docstring)."""
     import decoder
@@ -166,10 +166,10 @@ def decode_bench(name, log):
     out = {}
     for P, n_new, batch in runs:
         prompts = np.random.default_rng(7).integers(0, cfg["vocab"], (batch, P)).astype(np.int32)
-        dec.generate(prompts, 4)  # warm up: captures the decode graph
+        dec.generate(prompts, 4, graph=graph)  # warm up: captures the decode graph
         dec.reset()
         tm = {}
-        ids = dec.generate(prompts, n_new, timing=tm)
+        ids = dec.generate(prompts, n_new, timing=tm, graph=graph)
         dec.reset()
         step_ms = tm["decode_ms"] / tm["decode_steps"]
         key = f"{name}_P{P}_N{n_new}_B{batch}"
@@ -181,6 +181,7 @@ def decode_bench(name, log):
             "weight_GB_per_s": round(step_bytes_tok / (step_ms * 1e-3) / 1e9, 1),
             "weight_bytes_per_step": step_bytes_tok,
             "first_ids": ids[0, :8].tolist(),
+            "graphs": graph,
         }
         log(f"  {key}: {out[key]}")
     del dec
@@ -410,7 +411,7 @@ def main():
     layers.clear()
     decode_res = {}
     for name in [d for d in args.decode.split(",") if d]:
-        decode_res.update(decode_bench(name, log))
+        decode_res.update(decode_bench(name, log, graph=not args.eager))
     if decode_res:
         result["decode"] = decode_res
     if not args.no_cpu:

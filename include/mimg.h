@@ -154,6 +154,41 @@ int mimg_linear_a8_group_dev(const uint64_t *w, int count, const float *x, int64
 int mimg_matmul_a8_quantized_dev(uint64_t w, const float *x, int64_t rows, const float *bias, int block,
                                  float *y, const void *ws, uint64_t ws_bytes, void *stream);
 
+/* mimg_matmul_a8_quantized_dev for a group of 1 to 3 weights sharing K and
+ * the quantized activations (e.g. q, k and v after
+ * mimg_rms_norm_quant_dev); bias may be NULL or hold NULLs. No reference
+ * counterpart beyond the per-weight fast path it equals bit for bit. */
+int mimg_matmul_a8_quantized_group_dev(const uint64_t *w, int count, const float *x, int64_t rows,
+                                       const float *const *bias, int block, float *const *y, const void *ws,
+                                       uint64_t ws_bytes, void *stream);
+
+/* rms_norm.v1 (reference interp/fast.go:434-485, with the residual add
+ * before it) and the 8-bit quantizer of dequant_matmul_a8 (q8.go:50-97) on
+ * its output, in one launch: if resid is not NULL, x += resid (written
+ * back); y = rms_norm(x) * scale is written and quantized into ws (the
+ * layout of mimg_quantize_act_dev for rows, n, block). Equal, bit for bit,
+ * to mimg_rms_norm_dev followed by mimg_quantize_act_dev, except that the
+ * f64 sum of squares may round differently (~1e-16 relative). x, y, resid,
+ * scale 16-byte aligned; n a multiple of block, at most 32768. */
+int mimg_rms_norm_quant_dev(float *x, const float *resid, const float *scale, float eps, int64_t rows, int64_t n,
+                            float *y, int block, void *ws, uint64_t ws_bytes, void *stream);
+
+/* swiglu.v1 over g, u [rows, n] (as mimg_swiglu_dev over rows*n elements
+ * with GOMAXPROCS = procs) and the 8-bit quantizer on its output, in one
+ * launch: out is written and quantized into ws. Bit for bit the two calls.
+ * 16-byte aligned; n a multiple of block, at most 32768. */
+int mimg_swiglu_quant_dev(const float *g, const float *u, float *out, int64_t rows, int64_t n, int procs, int block,
+                          void *ws, uint64_t ws_bytes, void *stream);
+
+/* rope.v1 on q [T, heads, d] (in place) and k [T, kv_heads, d], and the
+ * cache scatter of the rotated k and of v into kcache/vcache at
+ * cache_index[t], in one launch: bit for bit mimg_rope_dev on q and k then
+ * mimg_kv_store_dev (reference importer/llama.go:364-503). k is left as
+ * it was. */
+int mimg_rope_kv_dev(float *q, const float *k, const float *v, const int64_t *pos, const int64_t *cache_index,
+                     const double *inv_freq, int64_t T, int heads, int kv_heads, int d, int rotary, int interleaved,
+                     int64_t context, void *kcache, void *vcache, int f16, void *stream);
+
 /* mimg_dequant_matmul on device buffers. */
 int mimg_linear_f32_dev(uint64_t w, const float *x, int64_t rows, const float *bias, float *y,
                         void *stream);
@@ -216,12 +251,15 @@ int mimg_kv_store_dev(const float *k, const float *v, const int64_t *pos, int64_
  * 1/sqrt(d). q, out: [T, heads, d]. Bit for bit the reference's attendRow
  * with its AVX2 kernels (interp/fast.go:728-751; scores, Cephes expf sum
  * and ordered weighted sum of internal/kernels/attn_amd64.s:12-468).
- * d a multiple of 8, at most 512; at most 8192 visible keys (the range is
- * clipped to the cache row and to 8192 keys; a query that sees nothing gets
- * zeros, a non-finite largest score NaN). */
+ * d a multiple of 8, at most 512. The visible range is clipped to the
+ * cache row and to max_keys (1..8192; the per-sequence context); a query
+ * that sees nothing gets zeros, a non-finite largest score NaN. ws: device
+ * scratch of mimg_attention_workspace_bytes(T, heads, max_keys) bytes
+ * (the scores). */
+uint64_t mimg_attention_workspace_bytes(int64_t T, int heads, int64_t max_keys);
 int mimg_attention_dev(const float *q, const void *kcache, const void *vcache, const int64_t *kend,
-                       const int64_t *kstart, int64_t T, int heads, int kv_heads, int d, int64_t context, int f16,
-                       float *out, void *stream);
+                       const int64_t *kstart, int64_t T, int heads, int kv_heads, int d, int64_t context,
+                       int64_t max_keys, int f16, float *out, void *ws, uint64_t ws_bytes, void *stream);
 
 /* One step of the greedy loop on the device (reference cmd/mim-run/main.go
  * generate, 184-257), for n sequences: ids[i] = chosen[i], out[count*n+i] =
@@ -240,7 +278,9 @@ int mimg_greedy_advance_dev(const int32_t *chosen, int32_t *ids, int64_t *pos, i
 int mimg_swiglu_dev(const float *g, const float *u, float *out, int64_t n, int procs, void *stream);
 
 /* Greedy choice (reference cmd/mim-run/main.go:184-192): out[r] = the first
- * index of the largest value of row r of x [rows, n]. */
+ * index of the largest value of row r of x [rows, n], as the reference's
+ * loop from index 0 with x > v[best]: NaNs are never chosen, and a row
+ * whose first value is NaN gives 0. */
 int mimg_argmax_dev(const float *x, int64_t rows, int64_t n, int32_t *out, void *stream);
 
 #ifdef __cplusplus

@@ -19,24 +19,12 @@
 //   swiglu.v1     SiluMulF32 over the reference's pieces (fast.go:487-498,
 //                 attn.go:63-76, attn_amd64.s:459-535): bit for bit
 //   argmax        first index of the largest logit (cmd/mim-run/main.go:184-192)
+#include "decoder_math.hpp"
 #include "f32path.hpp"
 #include "mimg_device.hpp"
 #include "mimg_kernels.hpp"
 
 namespace mimg {
-
-__device__ __forceinline__ double wave_sum_f64(double v) {
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
-__device__ __forceinline__ float wave_sum_f32(float v) {
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
-__device__ __forceinline__ float wave_max_f32(float v) {
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
 
 // Rows of the embedding table for the given tokens: out[t][e].
 template <uint32_t DT>
@@ -52,36 +40,77 @@ __global__ void embed_rows_kernel(const uint8_t* __restrict__ table, int64_t row
 }
 
 // One 256-thread workgroup per row: x += resid (if given, written back to
-// x), then y = rms_norm(x) * scale.
+// x), then y = rms_norm(x) * scale. Rows of up to RMS_REG*256*4 elements
+// with n % 4 == 0 are held in registers (one pass over memory); longer or
+// ragged rows take a second pass.
+constexpr int RMS_REG = 8;
 __global__ __launch_bounds__(256) void rms_norm_kernel(float* __restrict__ x, const float* __restrict__ resid,
                                                        const float* __restrict__ scale, float eps, int64_t n,
                                                        float* __restrict__ y) {
     __shared__ double part[4];
-    __shared__ float inv_s;
     float* xr = x + (int64_t)blockIdx.x * n;
     const float* rr = resid ? resid + (int64_t)blockIdx.x * n : nullptr;
     float* yr = y + (int64_t)blockIdx.x * n;
+    const int tid = threadIdx.x;
+    const bool inreg = n % 4 == 0 && n <= (int64_t)RMS_REG * 256 * 4;
+    float4 v[RMS_REG];
     double ss = 0.0;
-    for (int64_t i = threadIdx.x; i < n; i += 256) {
-        float v = xr[i];
-        if (rr) {
-            v = v + rr[i];
-            xr[i] = v;
+    if (inreg) {
+        const int64_t n4 = n / 4;
+#pragma unroll
+        for (int k = 0; k < RMS_REG; k++) {
+            const int64_t i = tid + 256 * k;
+            if (i < n4) {
+                v[k] = ((const float4*)xr)[i];
+                if (rr) {
+                    const float4 r4 = ((const float4*)rr)[i];
+                    v[k].x = v[k].x + r4.x;
+                    v[k].y = v[k].y + r4.y;
+                    v[k].z = v[k].z + r4.z;
+                    v[k].w = v[k].w + r4.w;
+                    ((float4*)xr)[i] = v[k];
+                }
+                ss += (double)v[k].x * (double)v[k].x + (double)v[k].y * (double)v[k].y +
+                      (double)v[k].z * (double)v[k].z + (double)v[k].w * (double)v[k].w;
+            }
         }
-        ss += (double)v * (double)v;
+    } else {
+        for (int64_t i = tid; i < n; i += 256) {
+            float e = xr[i];
+            if (rr) {
+                e = e + rr[i];
+                xr[i] = e;
+            }
+            ss += (double)e * (double)e;
+        }
     }
     ss = wave_sum_f64(ss);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const double tot = (part[0] + part[1]) + (part[2] + part[3]);
-        inv_s = (float)(1.0 / sqrt((double)(float)(tot / (double)n) + (double)eps));
-    }
-    __syncthreads();
-    const float inv = inv_s;
-    for (int64_t i = threadIdx.x; i < n; i += 256) {
-        const float v = xr[i] * inv;
-        yr[i] = scale ? v * scale[i] : v;
+    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float inv = (float)(1.0 / sqrt((double)(float)(tot / (double)n) + (double)eps));
+    if (inreg) {
+        const int64_t n4 = n / 4;
+#pragma unroll
+        for (int k = 0; k < RMS_REG; k++) {
+            const int64_t i = tid + 256 * k;
+            if (i < n4) {
+                float4 o = {v[k].x * inv, v[k].y * inv, v[k].z * inv, v[k].w * inv};
+                if (scale) {
+                    const float4 s4 = ((const float4*)scale)[i];
+                    o.x = o.x * s4.x;
+                    o.y = o.y * s4.y;
+                    o.z = o.z * s4.z;
+                    o.w = o.w * s4.w;
+                }
+                ((float4*)yr)[i] = o;
+            }
+        }
+    } else {
+        for (int64_t i = tid; i < n; i += 256) {
+            const float e = xr[i] * inv;
+            yr[i] = scale ? e * scale[i] : e;
+        }
     }
 }
 
@@ -129,155 +158,319 @@ __global__ void kv_store_kernel(const float* __restrict__ k, const float* __rest
     }
 }
 
-__device__ __forceinline__ float kv_at(const void* c, int64_t i, int f16) {
-    return f16 ? (float)((const _Float16*)c)[i] : ((const float*)c)[i];
-}
 
-// Cephes' expf as the reference's expSumF32AVX2 evaluates it
-// (attn_amd64.s:81-240): t clamped to lo, f = rint(t*log2e), r = t - f*ln2
-// with ln2 in two parts (fma), exp(r) = 1 + r + r^2 P(r), times 2^f put in
-// the exponent; t < lo (and NaN) gives 0.
-__device__ __forceinline__ float cephes_exp(float t) {
-    const float lo = __uint_as_float(0xc2aeac4fu), log2e = __uint_as_float(0x3fb8aa3bu);
-    const float c1 = __uint_as_float(0x3f318000u), c2 = __uint_as_float(0xb95e8083u);
-    const bool keep = t >= lo;
-    const float tt = t > lo ? t : lo;
-    const float f = __builtin_rintf(tt * log2e);
-    float r = __builtin_fmaf(-f, c1, tt);
-    r = __builtin_fmaf(-f, c2, r);
-    const float r2 = r * r;
-    float p = __uint_as_float(0x39506967u);
-    p = __builtin_fmaf(p, r, __uint_as_float(0x3ab743ceu));
-    p = __builtin_fmaf(p, r, __uint_as_float(0x3c088908u));
-    p = __builtin_fmaf(p, r, __uint_as_float(0x3d2aa9c1u));
-    p = __builtin_fmaf(p, r, __uint_as_float(0x3e2aaaaau));
-    p = __builtin_fmaf(p, r, 0.5f);
-    p = __builtin_fmaf(p, r2, r);
-    p = p + 1.0f;
-    const float e = p * __uint_as_float((uint32_t)((int32_t)f + 127) << 23);
-    return keep ? e : 0.0f;
-}
-
-// attention.v1/.v2 for one query row and head, in the reference's attendRow
-// order (interp/fast.go:728-751 with attn_amd64.s), so the result is the
-// reference's bit for bit. One 256-thread workgroup per (query t, head h)
-// over cache entries kstart[t]..kend[t] of kv head h / (H / Hkv), D a
-// multiple of 8 (at most 512), at most ATT_MAXC visible keys.
-//   scores  eight lanes per key: lane c sums q[8m+c]*k[8m+c] by fma over m;
-//           keys go in fours from the first, reduced
-//           ((l0+l1)+(l2+l3))+((l4+l5)+(l6+l7)), the last n%4 keys as
-//           ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)); times scale
-//   expsum  Cephes exp of s - max for the first n&~7 keys, eight stride-8
-//           lane sums in key order, HSUM, then the tail keys with the f64
-//           exp added in order
-//   wsum    thread d: acc = fma(e_j, v_j[d], acc) over the keys in order;
-//           o[d] = acc / sum
-// A non-finite largest score gives NaN (the reference's scalar loop ends
-// in NaN then); no visible key gives zeros.
-constexpr int ATT_MAXC = 8192;
-__global__ __launch_bounds__(256) void attention_kernel(const float* __restrict__ q, const void* kc, const void* vc,
-                                                        const int64_t* __restrict__ kend,
-                                                        const int64_t* __restrict__ kstart, int H, int Hkv, int D,
-                                                        int64_t C, int f16, float* __restrict__ out) {
-    __shared__ float sc[ATT_MAXC];
-    __shared__ float qs[512];
-    __shared__ float red[4];
-    __shared__ int nan_any;
-    __shared__ float lane_sum[8];
-    const int t = blockIdx.y, h = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-    const int hk = h / (H / Hkv);
-    // visible keys, indexed from k0; kept inside the cache row and LDS
-    const int64_t k0 = kstart ? (kstart[t] < 0 ? 0 : (kstart[t] >= C ? C - 1 : kstart[t])) : 0;
-    int64_t n = kend[t] + 1 - k0;
-    if (n > C - k0) n = C - k0;
-    if (n > ATT_MAXC) n = ATT_MAXC;
-    const int64_t cbase = (int64_t)hk * C + k0;
-    const float scale = (float)(1.0 / sqrt((double)D));
-    float* orow = out + ((int64_t)t * H + h) * D;
-    if (n <= 0) {
-        for (int d = tid; d < D; d += 256) orow[d] = 0.f;
+// rope.v1 on q and k and the cache scatter of k and v in one launch (the
+// graph's rope of q and k and its cache update, importer/llama.go:364-503):
+// a workgroup per (row t, head), heads 0..H-1 of q, then Hkv of k, then Hkv
+// of v; thread i takes one pair of dims: (2i, 2i+1) when interleaved, else
+// (i, i + rotary/2) for i < rotary/2 and two adjacent dims past the rotary
+// ones. q is rotated in place; k (rotated) and v go to the caches at cidx[t]
+// (rounded to f16 with an f16 cache; rows outside the cache are not stored).
+template <bool F16>
+__global__ void rope_kv_kernel(float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+                               const int64_t* __restrict__ pos, const int64_t* __restrict__ cidx,
+                               const double* __restrict__ inv_freq, int H, int Hkv, int D, int rotary, int interleaved,
+                               int64_t C, void* kc, void* vc) {
+    const int t = blockIdx.y, hh = blockIdx.x, i = threadIdx.x;
+    if (i >= D / 2) return;
+    const int h2 = rotary / 2;
+    int a, b;
+    if (interleaved) {
+        a = 2 * i;
+        b = 2 * i + 1;
+    } else if (i < h2) {
+        a = i;
+        b = i + h2;
+    } else {
+        a = rotary + 2 * (i - h2);
+        b = a + 1;
+    }
+    const bool rot = i < h2;
+    float* row;
+    const float* src;
+    if (hh < H) {
+        row = q + ((int64_t)t * H + hh) * D;
+        src = row;
+    } else if (hh < H + Hkv) {
+        row = nullptr;
+        src = k + ((int64_t)t * Hkv + (hh - H)) * D;
+    } else {
+        row = nullptr;
+        src = v + ((int64_t)t * Hkv + (hh - H - Hkv)) * D;
+    }
+    float xa = src[a], xb = src[b];
+    if (rot && hh < H + Hkv) {
+        const double ang = (double)pos[t] * inv_freq[i];
+        const float c = (float)cos(ang), sn = (float)sin(ang);
+        const float x1 = xa, x2 = xb;
+        xa = x1 * c - x2 * sn;
+        xb = x2 * c + x1 * sn;
+    }
+    if (row) {
+        row[a] = xa;
+        row[b] = xb;
         return;
     }
-    const float* qr = q + ((int64_t)t * H + h) * D;
-    for (int d = tid; d < D; d += 256) qs[d] = qr[d];
-    if (tid == 0) nan_any = 0;
-    __syncthreads();
-    // scores: 32 groups of eight lanes, a key per group
-    const int c = lane & 7, gbase = lane & ~7, grp = tid >> 3;
-    const int64_t n4 = n - n % 4;
-    for (int64_t j0 = 0; j0 < n; j0 += 32) {
-        const int64_t j = j0 + grp;
-        const int64_t jj = j < n ? j : n - 1;  // groups past the end recompute the last key, unstored
-        const int64_t base = (cbase + jj) * D;
-        float l = 0.f;
-        for (int m = 0; m < D / 8; m++) l = __builtin_fmaf(qs[8 * m + c], kv_at(kc, base + 8 * m + c, f16), l);
-        const bool four = jj < n4;
-        const int x1 = four ? 1 : 4, x2 = four ? 2 : 1, x3 = four ? 4 : 2;
-        float p = l + __shfl(l, gbase + (c ^ x1));
-        p = p + __shfl(p, gbase + (c ^ x2));
-        p = p + __shfl(p, gbase + (c ^ x3));
-        if (c == 0 && j < n) sc[j] = p * scale;
+    const int64_t p = cidx[t];
+    if (p < 0 || p >= C) return;
+    const int hk = hh < H + Hkv ? hh - H : hh - H - Hkv;
+    const int64_t at = ((int64_t)hk * C + p) * D;
+    void* cache = hh < H + Hkv ? kc : vc;
+    if constexpr (F16) {
+        ((_Float16*)cache)[at + a] = (_Float16)xa;
+        ((_Float16*)cache)[at + b] = (_Float16)xb;
+    } else {
+        ((float*)cache)[at + a] = xa;
+        ((float*)cache)[at + b] = xb;
     }
-    __syncthreads();
+}
+
+// attention.v1/.v2 in the reference's attendRow order (interp/fast.go:728-751
+// with attn_amd64.s), bit for bit, as two kernels:
+//   att_scores  a workgroup per (64-key tile, head h, query t): eight lanes
+//               per key, lane c sums q[8m+c]*k[8m+c] by fma over m; keys go
+//               in fours from the first visible one, reduced
+//               ((l0+l1)+(l2+l3))+((l4+l5)+(l6+l7)), the last n%4 keys as
+//               ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)); times scale; into the
+//               workspace row of (t, h)
+//   att_wsum    a workgroup per (slice of DS dims, head h, query t): max,
+//               Cephes exp of s - max for the first n&~7 keys (eight
+//               stride-8 lane sums in key order, then HSUM), the f64 exp
+//               for the tail added in order; then for each dim d of the
+//               slice acc = fma(e_j, v_j[d], acc) over the keys in order
+//               (the values staged through LDS, as many keys at a time as
+//               fit beside the scores in 64 KB), and
+//               o[d] = acc / sum
+// The visible keys of query t are cache entries kstart[t]..kend[t] (kstart
+// 0 when null) of kv head h / (H / Hkv), clipped to the cache row and to
+// maxk (the workspace row). A non-finite largest score gives NaN (the
+// reference's scalar loop ends in NaN then); no visible key gives zeros.
+constexpr int ATT_MAXC = 8192;
+
+struct AttRange {
+    int64_t k0, n;
+};
+__device__ __forceinline__ AttRange att_range(const int64_t* kend, const int64_t* kstart, int t, int64_t C,
+                                              int64_t maxk) {
+    AttRange r;
+    r.k0 = kstart ? (kstart[t] < 0 ? 0 : (kstart[t] >= C ? C - 1 : kstart[t])) : 0;
+    int64_t n = kend[t] + 1 - r.k0;
+    if (n > C - r.k0) n = C - r.k0;
+    if (n > maxk) n = maxk;
+    r.n = n < 0 ? 0 : n;
+    return r;
+}
+
+template <bool F16>
+__device__ __forceinline__ float kv_load(const void* c, int64_t i) {
+    if constexpr (F16) return (float)((const _Float16*)c)[i];
+    else return ((const float*)c)[i];
+}
+
+// The score of one key from the eight lanes' chains l (lane c of the group
+// holds l_c): ((l0+l1)+(l2+l3))+((l4+l5)+(l6+l7)) for keys in the groups of
+// four, ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) for the last n%4; lane 0 of the
+// group returns it.
+__device__ __forceinline__ float att_reduce8(float l, bool four, int gbase, int c) {
+    const int x1 = four ? 1 : 4, x2 = four ? 2 : 1, x3 = four ? 4 : 2;
+    float p = l + __shfl(l, gbase + (c ^ x1));
+    p = p + __shfl(p, gbase + (c ^ x2));
+    return p + __shfl(p, gbase + (c ^ x3));
+}
+
+// DM = D/8 for D = 64 or 128 (unrolled; every load of a lane in flight at
+// once), 0 for other multiples of 8.
+template <bool F16, int DM>
+__global__ __launch_bounds__(256) void att_scores_kernel(const float* __restrict__ q, const void* kc,
+                                                         const int64_t* __restrict__ kend,
+                                                         const int64_t* __restrict__ kstart, int H, int Hkv, int D,
+                                                         int64_t C, int64_t maxk, float* __restrict__ ws) {
+    const int tile = blockIdx.x, h = blockIdx.y, t = blockIdx.z;
+    const AttRange r = att_range(kend, kstart, t, C, maxk);
+    if ((int64_t)tile * 64 >= r.n) return;
+    const int hk = h / (H / Hkv);
+    const int lane = threadIdx.x & 63, c = lane & 7, gbase = lane & ~7, grp = threadIdx.x >> 3;
+    const int64_t n4 = r.n - r.n % 4;
+    const int64_t cbase = (int64_t)hk * C + r.k0;
+    const float scale = (float)(1.0 / sqrt((double)D));
+    const float* qr = q + ((int64_t)t * H + h) * D;
+    float* out = ws + ((int64_t)t * H + h) * maxk;
+    // two keys per group; past the end the last key is recomputed, unstored
+    const int64_t j0 = (int64_t)tile * 64 + grp, j1 = j0 + 32;
+    const int64_t a0 = cbase + (j0 < r.n ? j0 : r.n - 1), a1 = cbase + (j1 < r.n ? j1 : r.n - 1);
+    float l0 = 0.f, l1 = 0.f;
+    if constexpr (DM > 0) {
+        float qv[DM], k0v[DM], k1v[DM];
+#pragma unroll
+        for (int m = 0; m < DM; m++) {
+            qv[m] = qr[8 * m + c];
+            k0v[m] = kv_load<F16>(kc, a0 * D + 8 * m + c);
+            k1v[m] = kv_load<F16>(kc, a1 * D + 8 * m + c);
+        }
+#pragma unroll
+        for (int m = 0; m < DM; m++) {
+            l0 = __builtin_fmaf(qv[m], k0v[m], l0);
+            l1 = __builtin_fmaf(qv[m], k1v[m], l1);
+        }
+    } else {
+        for (int m = 0; m < D / 8; m++) {
+            const float qm = qr[8 * m + c];
+            l0 = __builtin_fmaf(qm, kv_load<F16>(kc, a0 * D + 8 * m + c), l0);
+            l1 = __builtin_fmaf(qm, kv_load<F16>(kc, a1 * D + 8 * m + c), l1);
+        }
+    }
+    const float p0 = att_reduce8(l0, j0 < n4, gbase, c);
+    const float p1 = att_reduce8(l1, j1 < n4, gbase, c);
+    if (c == 0) {
+        if (j0 < r.n) out[j0] = p0 * scale;
+        if (j1 < r.n) out[j1] = p1 * scale;
+    }
+}
+
+// LDS of att_wsum: the scores (maxk floats, padded to 4) and up to
+// ATT_VBYTES of values as f32; the first chunk of values is loaded into
+// registers (at most ATT_VREGS 16-byte pieces a thread) while the
+// exponentials are computed.
+constexpr int ATT_VBYTES = 48 * 1024;
+constexpr int ATT_LDS_MAX = 64 * 1024;
+constexpr int ATT_VREGS = 12;
+
+template <int DS, bool F16>
+__global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int64_t* __restrict__ kend,
+                                                       const int64_t* __restrict__ kstart, int H, int Hkv, int D,
+                                                       int64_t C, int64_t maxk, int vch,
+                                                       const float* __restrict__ ws, float* __restrict__ out) {
+    extern __shared__ float att_lds[];
+    __shared__ float red[4];
+    __shared__ float lane_sum[8];
+    __shared__ int nan_any;
+    constexpr int PER_ROW = F16 ? DS / 8 : DS / 4;  // 16-byte pieces per row of the slice
+    float* sc = att_lds;
+    float* vb = att_lds + ((maxk + 3) & ~(int64_t)3);
+    const int d0 = blockIdx.x * DS, h = blockIdx.y, t = blockIdx.z, tid = threadIdx.x, w = tid >> 6;
+    const AttRange r = att_range(kend, kstart, t, C, maxk);
+    const int64_t n = r.n;
+    float* orow = out + ((int64_t)t * H + h) * D + d0;
+    if (n <= 0) {
+        if (tid < DS) orow[tid] = 0.f;
+        return;
+    }
+    const int hk = h / (H / Hkv);
+    const int64_t vbase = ((int64_t)hk * C + r.k0) * D + d0;
+    const int64_t rows0 = n < vch ? n : vch;
+    // the first chunk of values, into registers
+    uint4 vr[ATT_VREGS];
+#pragma unroll
+    for (int k = 0; k < ATT_VREGS; k++) {
+        const int64_t i = tid + 256 * k;
+        const int64_t row = i / PER_ROW, piece = i % PER_ROW;
+        if (row < rows0) {
+            if constexpr (F16) vr[k] = *(const uint4*)((const _Float16*)vc + vbase + row * D + piece * 8);
+            else vr[k] = *(const uint4*)((const float*)vc + vbase + row * D + piece * 4);
+        }
+    }
+    const float* srow = ws + ((int64_t)t * H + h) * maxk;
+    if (tid == 0) nan_any = 0;
     float mx = -INFINITY;
     int isnan_local = 0;
     for (int64_t j = tid; j < n; j += 256) {
-        const float v = sc[j];
+        const float v = srow[j];
+        sc[j] = v;
         isnan_local |= v != v;
         mx = fmaxf(mx, v);
     }
     mx = wave_max_f32(mx);
-    if (lane == 0) red[w] = mx;
+    __syncthreads();  // nan_any cleared before it is set
+    if ((tid & 63) == 0) red[w] = mx;
     if (isnan_local) nan_any = 1;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     if (nan_any || __builtin_isinf(mx)) {
-        for (int d = tid; d < D; d += 256) orow[d] = __builtin_nanf("");
+        if (tid < DS) orow[tid] = __builtin_nanf("");
         return;
     }
-    // exponentials: the vector part through Cephes, the tail through f64 exp
     const int64_t nv = n >= 8 ? (n & ~(int64_t)7) : 0;
     for (int64_t j = tid; j < n; j += 256) {
         const float x = sc[j] - mx;
         sc[j] = j < nv ? cephes_exp(x) : (float)exp((double)x);
     }
+    // the first chunk of values into LDS as f32
+#pragma unroll
+    for (int k = 0; k < ATT_VREGS; k++) {
+        const int64_t i = tid + 256 * k;
+        const int64_t row = i / PER_ROW, piece = i % PER_ROW;
+        if (row < rows0) {
+            if constexpr (F16) {
+                const uint32_t wv[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
+                float* dst = vb + row * DS + piece * 8;
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    dst[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
+                    dst[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
+                }
+            } else {
+                *(uint4*)(vb + row * DS + piece * 4) = vr[k];
+            }
+        }
+    }
     __syncthreads();
+    // eight stride-8 lane sums in key order, then HSUM and the tail
     if (tid < 8) {
         float s = 0.f;
-        for (int64_t j = tid; j < nv; j += 8) s = s + sc[j];
+        int64_t j = tid;
+        for (; j + 56 < nv; j += 64) {
+            float e[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) e[u] = sc[j + 8 * u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) s = s + e[u];
+        }
+        for (; j < nv; j += 8) s = s + sc[j];
         lane_sum[tid] = s;
     }
     __syncthreads();
     float sum = ((lane_sum[0] + lane_sum[4]) + (lane_sum[1] + lane_sum[5])) +
                 ((lane_sum[2] + lane_sum[6]) + (lane_sum[3] + lane_sum[7]));
-    if (nv == 0) sum = 0.f;
     for (int64_t j = nv; j < n; j++) sum = sum + sc[j];
-    // o[d] = (sum_j e_j v_j[d]) / sum, the keys in order
-    for (int d = tid; d < D; d += 256) {
-        const int64_t vb = cbase * D + d;
-        float acc = 0.f;
-        int64_t j = 0;
-        for (; j + 4 <= n; j += 4) {
-            const float v0 = kv_at(vc, vb + (j + 0) * D, f16), v1 = kv_at(vc, vb + (j + 1) * D, f16);
-            const float v2 = kv_at(vc, vb + (j + 2) * D, f16), v3 = kv_at(vc, vb + (j + 3) * D, f16);
-            acc = __builtin_fmaf(sc[j], v0, acc);
-            acc = __builtin_fmaf(sc[j + 1], v1, acc);
-            acc = __builtin_fmaf(sc[j + 2], v2, acc);
-            acc = __builtin_fmaf(sc[j + 3], v3, acc);
+    float acc = 0.f;
+    for (int64_t c0 = 0; c0 < n; c0 += vch) {
+        const int64_t rows = n - c0 < vch ? n - c0 : vch;
+        if (c0 > 0) {  // later chunks (long contexts): stage, then sum
+            __syncthreads();
+            for (int64_t i = tid; i < rows * PER_ROW; i += 256) {
+                const int64_t row = i / PER_ROW, piece = i % PER_ROW;
+                if constexpr (F16) {
+                    const uint4 raw = *(const uint4*)((const _Float16*)vc + vbase + (c0 + row) * D + piece * 8);
+                    const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+                    float* dst = vb + row * DS + piece * 8;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        dst[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
+                        dst[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
+                    }
+                } else {
+                    *(uint4*)(vb + row * DS + piece * 4) = *(const uint4*)((const float*)vc + vbase + (c0 + row) * D + piece * 4);
+                }
+            }
+            __syncthreads();
         }
-        for (; j < n; j++) acc = __builtin_fmaf(sc[j], kv_at(vc, vb + j * D, f16), acc);
-        orow[d] = acc / sum;
+        if (tid < DS) {
+            const float* e = sc + c0;
+            int64_t j = 0;
+            for (; j + 8 <= rows; j += 8) {
+                float ev[8], vv[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    ev[u] = e[j + u];
+                    vv[u] = vb[(j + u) * DS + tid];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++) acc = __builtin_fmaf(ev[u], vv[u], acc);
+            }
+            for (; j < rows; j++) acc = __builtin_fmaf(e[j], vb[j * DS + tid], acc);
+        }
     }
-}
-
-// silu(x) * b as the reference's siluMulF32AVX2 (attn_amd64.s:459-535):
-// h = exp(-|x|/2) by the Cephes steps, silu = x/(1+h*h) for x >= 0 and
-// ((x*h)*h)/(1+h*h) below, then times b.
-__device__ __forceinline__ float silu_mul_vec(float x, float b) {
-    const float hh = cephes_exp(-__builtin_fabsf(x) * 0.5f);
-    const float e1 = hh * hh + 1.0f;
-    const float y = (x * hh) * hh;
-    return ((x >= 0.f ? x : y) / e1) * b;
+    if (tid < DS) orow[tid] = acc / sum;
 }
 
 // swiglu.v1 (reference interp/fast.go:487-498): the reference splits the n
@@ -287,58 +480,78 @@ __device__ __forceinline__ float silu_mul_vec(float x, float b) {
 // f32(f64(g)/(1+exp(-f64(g)))*f64(u)).
 __global__ void swiglu_kernel(const float* __restrict__ g, const float* __restrict__ u, float* __restrict__ out, int64_t n,
                               int64_t chunk) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t lo = i / chunk * chunk;
-        const int64_t len = lo + chunk < n ? chunk : n - lo;
-        const int64_t nv = len >= 8 ? (len & ~(int64_t)7) : 0;
-        const float x = g[i], y = u[i];
-        if (i - lo < nv) {
-            out[i] = silu_mul_vec(x, y);
-        } else {
-            const double a = (double)x;
-            out[i] = (float)(a / (1.0 + exp(-a)) * (double)y);
-        }
-    }
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = swiglu_at(g[i], u[i], i, n, chunk);
 }
 
 // One 1024-thread workgroup per row of logits: the first index of the max.
+// Each thread scans its elements in increasing index order (eight 16-byte
+// loads in flight when the row is 16-byte aligned), keeping the first index
+// of its largest value; the group then reduces lexicographically (larger
+// value, then smaller index). As the reference's loop (best = 0; x >
+// v[best]): NaNs are never chosen, and a row whose first value is NaN gives 0.
+__device__ __forceinline__ void am_take(float v, int i, float& best, int& idx, int none) {
+    if (idx == none ? v == v : v > best) {
+        best = v;
+        idx = i;
+    }
+}
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, int64_t n, int32_t* __restrict__ out) {
     __shared__ float bv[16];
     __shared__ int bi[16];
     const float* r = x + (int64_t)blockIdx.x * n;
+    const int none = (int)n;
     float best = -INFINITY;
-    int idx = (int)n;  // none yet
-    for (int i = threadIdx.x; i < (int)n; i += 1024) {
-        const float v = r[i];
-        if (idx == n || v > best) {
-            best = v;
-            idx = i;
+    int idx = none;
+    const int tid = threadIdx.x;
+    int i0 = 0;
+    if (((uintptr_t)r & 15) == 0) {
+        // thread tid takes the float4s tid, tid+1024, ... in order: its
+        // indices increase, so its first maximum is kept
+        const int n4 = (int)(n / 4);
+        for (int b = 0; b < n4; b += 8 * 1024) {
+            float4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i = b + k * 1024 + tid;
+                v[k] = i < n4 ? ((const float4*)r)[i] : make_float4(NAN, NAN, NAN, NAN);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int i = 4 * (b + k * 1024 + tid);
+                am_take(v[k].x, i, best, idx, none);
+                am_take(v[k].y, i + 1, best, idx, none);
+                am_take(v[k].z, i + 2, best, idx, none);
+                am_take(v[k].w, i + 3, best, idx, none);
+            }
         }
+        i0 = n4 * 4;
     }
-    // lexicographic (larger value, then smaller index) across the group
+    for (int i = i0 + tid; i < (int)n; i += 1024) am_take(r[i], i, best, idx, none);
     for (int off = 32; off >= 1; off >>= 1) {
         const float ov = __shfl_xor(best, off);
         const int oi = __shfl_xor(idx, off);
-        if (oi < n && (idx == n || ov > best || (ov == best && oi < idx))) {
+        if (oi != none && (idx == none || ov > best || (ov == best && oi < idx))) {
             best = ov;
             idx = oi;
         }
     }
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
+    const int w = tid >> 6;
+    if ((tid & 63) == 0) {
         bv[w] = best;
         bi[w] = idx;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         float b = bv[0];
-        int i0 = bi[0];
+        int i0b = bi[0];
         for (int k = 1; k < 16; k++)
-            if (bi[k] < n && (i0 == n || bv[k] > b || (bv[k] == b && bi[k] < i0))) {
+            if (bi[k] != none && (i0b == none || bv[k] > b || (bv[k] == b && bi[k] < i0b))) {
                 b = bv[k];
-                i0 = bi[k];
+                i0b = bi[k];
             }
-        out[blockIdx.x] = (int32_t)(i0 == n ? 0 : i0);
+        // the reference starts from index 0, which no NaN-led row leaves
+        out[blockIdx.x] = (int32_t)(i0b == none || r[0] != r[0] ? 0 : i0b);
     }
 }
 
@@ -403,11 +616,58 @@ hipError_t launch_kv_store(const float* k, const float* v, const int64_t* pos, i
     return hipGetLastError();
 }
 
+template <bool F16>
+static void launch_att_scores(dim3 grid, const float* q, const void* kc, const int64_t* kend, const int64_t* kstart,
+                              int H, int Hkv, int D, int64_t C, int64_t maxk, float* ws, hipStream_t s) {
+    if (D == 64)
+        hipLaunchKernelGGL((att_scores_kernel<F16, 8>), grid, dim3(256), 0, s, q, kc, kend, kstart, H, Hkv, D, C, maxk, ws);
+    else if (D == 128)
+        hipLaunchKernelGGL((att_scores_kernel<F16, 16>), grid, dim3(256), 0, s, q, kc, kend, kstart, H, Hkv, D, C, maxk, ws);
+    else
+        hipLaunchKernelGGL((att_scores_kernel<F16, 0>), grid, dim3(256), 0, s, q, kc, kend, kstart, H, Hkv, D, C, maxk, ws);
+}
+
+template <int DS, bool F16>
+static void launch_att_wsum(int T, int H, int Hkv, int D, int64_t C, int64_t maxk, const void* vc, const int64_t* kend,
+                            const int64_t* kstart, const float* ws, float* out, hipStream_t s) {
+    constexpr int PER_ROW = F16 ? DS / 8 : DS / 4;
+    const int64_t sc_bytes = ((maxk + 3) & ~(int64_t)3) * 4;
+    int64_t vch = (ATT_LDS_MAX - 256 - sc_bytes) / (DS * 4);
+    if (vch > ATT_VBYTES / (DS * 4)) vch = ATT_VBYTES / (DS * 4);
+    if (vch > (int64_t)ATT_VREGS * 256 / PER_ROW) vch = (int64_t)ATT_VREGS * 256 / PER_ROW;
+    const size_t lds = (size_t)(sc_bytes + vch * DS * 4);
+    hipLaunchKernelGGL((att_wsum_kernel<DS, F16>), dim3((unsigned)(D / DS), (unsigned)H, (unsigned)T), dim3(256), lds, s,
+                       vc, kend, kstart, H, Hkv, D, C, maxk, (int)vch, ws, out);
+}
+
 hipError_t launch_attention(const float* q, const void* kc, const void* vc, const int64_t* kend, const int64_t* kstart,
-                            int T, int H, int Hkv, int D, int64_t C, int f16, float* out, hipStream_t s) {
-    if (D > 512 || D % 8 || H % Hkv) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)H, (unsigned)T), dim3(256), 0, s, q, kc, vc, kend, kstart, H, Hkv,
-                       D, C, f16, out);
+                            int T, int H, int Hkv, int D, int64_t C, int64_t maxk, int f16, float* out, float* ws,
+                            hipStream_t s) {
+    if (D > 512 || D % 8 || H % Hkv || maxk < 1 || maxk > ATT_MAXC || T < 1) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((maxk + 63) / 64), (unsigned)H, (unsigned)T);
+    if (f16) launch_att_scores<true>(grid, q, kc, kend, kstart, H, Hkv, D, C, maxk, ws, s);
+    else launch_att_scores<false>(grid, q, kc, kend, kstart, H, Hkv, D, C, maxk, ws, s);
+    if (D % 16 == 0) {
+        if (f16) launch_att_wsum<16, true>(T, H, Hkv, D, C, maxk, vc, kend, kstart, ws, out, s);
+        else launch_att_wsum<16, false>(T, H, Hkv, D, C, maxk, vc, kend, kstart, ws, out, s);
+    } else {
+        if (f16) launch_att_wsum<8, true>(T, H, Hkv, D, C, maxk, vc, kend, kstart, ws, out, s);
+        else launch_att_wsum<8, false>(T, H, Hkv, D, C, maxk, vc, kend, kstart, ws, out, s);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_kv(float* q, const float* k, const float* v, const int64_t* pos, const int64_t* cidx,
+                          const double* inv_freq, int T, int H, int Hkv, int D, int rotary, int interleaved, int64_t C,
+                          void* kc, void* vc, int f16, hipStream_t s) {
+    if (D % 2 || D > 1024 || rotary > D || rotary % 2 || (!interleaved && (D - rotary) % 2)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(H + 2 * Hkv), (unsigned)T), blk((unsigned)((D / 2 + 63) / 64 * 64));
+    if (f16)
+        hipLaunchKernelGGL(rope_kv_kernel<true>, grid, blk, 0, s, q, k, v, pos, cidx, inv_freq, H, Hkv, D, rotary,
+                           interleaved, C, kc, vc);
+    else
+        hipLaunchKernelGGL(rope_kv_kernel<false>, grid, blk, 0, s, q, k, v, pos, cidx, inv_freq, H, Hkv, D, rotary,
+                           interleaved, C, kc, vc);
     return hipGetLastError();
 }
 

@@ -454,6 +454,92 @@ int mimg_quantize_act_dev(const float* x, int64_t rows, int64_t k, int block, vo
     return MIMG_OK;
 }
 
+static int qa_checks(int64_t rows, int64_t k, int block, const void* ws, uint64_t ws_bytes, ActLayout* l) {
+    if (block != 32 && block != 256) return fail(MIMG_ERR_ARG, "block must be 32 or 256, got %d", block);
+    if (rows < 0 || k <= 0 || k % block) return fail(MIMG_ERR_ARG, "K = %lld with blocks of %d", (long long)k, block);
+    if (k > 32768) return fail(MIMG_ERR_ARG, "K = %lld: the fused producers take rows of at most 32768", (long long)k);
+    if (rows == 0) return MIMG_OK;
+    if (!ws || !aligned(ws, 256)) return fail(MIMG_ERR_ARG, "ws must be 256-byte aligned");
+    *l = act_layout(rows, k);
+    if (ws_bytes < l->total)
+        return fail(MIMG_ERR_WORKSPACE, "workspace %llu < %llu bytes", (unsigned long long)ws_bytes, (unsigned long long)l->total);
+    return MIMG_OK;
+}
+
+int mimg_rms_norm_quant_dev(float* x, const float* resid, const float* scale, float eps, int64_t rows, int64_t n,
+                            float* y, int block, void* ws, uint64_t ws_bytes, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    ActLayout l;
+    if ((rc = qa_checks(rows, n, block, ws, ws_bytes, &l)) || rows == 0) return rc;
+    if (!x || !y || !aligned(x, 16) || !aligned(y, 16) || (resid && !aligned(resid, 16)) || (scale && !aligned(scale, 16)))
+        return fail(MIMG_ERR_ARG, "x, y, resid and scale must be 16-byte aligned");
+    HIP_TRY(launch_norm_quantize_act(x, resid, scale, eps, y, rows, n, block, act_ptrs(ws, l), (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_swiglu_quant_dev(const float* g, const float* u, float* out, int64_t rows, int64_t n, int procs, int block,
+                          void* ws, uint64_t ws_bytes, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    ActLayout l;
+    if ((rc = qa_checks(rows, n, block, ws, ws_bytes, &l)) || rows == 0) return rc;
+    if (!g || !u || !out || !aligned(g, 16) || !aligned(u, 16) || !aligned(out, 16))
+        return fail(MIMG_ERR_ARG, "g, u and out must be 16-byte aligned");
+    const int64_t total = rows * n, w = procs < total ? procs : total;
+    int64_t chunk = total;
+    if (w > 1) chunk = total / (w * 8) > 1 ? total / (w * 8) : 1;
+    HIP_TRY(launch_swiglu_quantize_act(g, u, out, chunk, rows, n, block, act_ptrs(ws, l), (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_rope_kv_dev(float* q, const float* k, const float* v, const int64_t* pos, const int64_t* cache_index,
+                     const double* inv_freq, int64_t T, int heads, int kv_heads, int d, int rotary, int interleaved,
+                     int64_t context, void* kcache, void* vcache, int f16, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (T < 0 || T > 65535 || heads <= 0 || kv_heads <= 0 || d <= 0 || d % 2 || d > 1024 || rotary <= 0 ||
+        rotary % 2 || rotary > d || context <= 0)
+        return fail(MIMG_ERR_ARG, "rope_kv: T %lld, heads %d, kv heads %d, D %d, rotary %d", (long long)T, heads, kv_heads,
+                    d, rotary);
+    if (T == 0) return MIMG_OK;
+    if (!q || !k || !v || !pos || !cache_index || !inv_freq || !kcache || !vcache)
+        return fail(MIMG_ERR_ARG, "null pointer");
+    HIP_TRY(launch_rope_kv(q, k, v, pos, cache_index, inv_freq, (int)T, heads, kv_heads, d, rotary, interleaved, context,
+                           kcache, vcache, f16, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_matmul_a8_quantized_group_dev(const uint64_t* whs, int count, const float* x, int64_t rows,
+                                       const float* const* bias, int block, float* const* y, const void* ws,
+                                       uint64_t ws_bytes, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!whs || !y || count < 1 || count > 3) return fail(MIMG_ERR_ARG, "a group holds 1 to 3 weights, got %d", count);
+    const Weight* w[3];
+    for (int i = 0; i < count; i++) {
+        Weight* wi;
+        if ((rc = lookup(whs[i], &wi))) return rc;
+        bool use_f32;
+        if ((rc = a8_checks(wi, rows, block, &use_f32))) return rc;
+        if (use_f32) return fail(MIMG_ERR_ARG, "%s has no 8-bit kernel for blocks of %d", dt_name(wi->dw.dt), block);
+        if (wi->dw.k != (i ? w[0]->dw.k : wi->dw.k)) return fail(MIMG_ERR_ARG, "the weights of a group must share K");
+        w[i] = wi;
+    }
+    if (rows == 0) return MIMG_OK;
+    if (!x || !ws || !aligned(ws, 256)) return fail(MIMG_ERR_ARG, "null or misaligned pointer");
+    ActLayout l = act_layout(rows, w[0]->dw.k);
+    if (ws_bytes < l.total)
+        return fail(MIMG_ERR_WORKSPACE, "workspace %llu < %llu bytes", (unsigned long long)ws_bytes, (unsigned long long)l.total);
+    const float* bs[3];
+    float* ys[3];
+    for (int i = 0; i < count; i++) {
+        bs[i] = bias ? bias[i] : nullptr;
+        ys[i] = y[i];
+    }
+    return matmul_quantized(w, count, x, rows, bs, block, ys, act_ptrs((void*)ws, l), (hipStream_t)stream);
+}
+
 int mimg_linear_f32_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, float* y, void* stream) {
     int rc = ensure_device();
     if (rc) return rc;
@@ -628,18 +714,29 @@ int mimg_kv_store_dev(const float* k, const float* v, const int64_t* pos, int64_
     return MIMG_OK;
 }
 
+uint64_t mimg_attention_workspace_bytes(int64_t T, int heads, int64_t max_keys) {
+    if (T < 0 || heads <= 0 || max_keys <= 0) return 0;
+    return ((uint64_t)T * (uint64_t)heads * (uint64_t)max_keys * 4 + 255) & ~(uint64_t)255;
+}
+
 int mimg_attention_dev(const float* q, const void* kcache, const void* vcache, const int64_t* kend,
-                       const int64_t* kstart, int64_t T, int heads, int kv_heads, int d, int64_t context, int f16,
-                       float* out, void* stream) {
+                       const int64_t* kstart, int64_t T, int heads, int kv_heads, int d, int64_t context,
+                       int64_t max_keys, int f16, float* out, void* ws, uint64_t ws_bytes, void* stream) {
     int rc = ensure_device();
     if (rc) return rc;
-    if (T < 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads || d <= 0 || d > 512 || d % 8 || context <= 0)
-        return fail(MIMG_ERR_ARG, "attention: heads %d, kv heads %d, D %d, context %lld (D a multiple of 8, <= 512)",
-                    heads, kv_heads, d, (long long)context);
+    if (T < 0 || T > 65535 || heads <= 0 || heads > 65535 || kv_heads <= 0 || heads % kv_heads || d <= 0 || d > 512 ||
+        d % 8 || context <= 0)
+        return fail(MIMG_ERR_ARG, "attention: T %lld, heads %d, kv heads %d, D %d, context %lld (D a multiple of 8, <= 512)",
+                    (long long)T, heads, kv_heads, d, (long long)context);
+    if (max_keys < 1 || max_keys > 8192)
+        return fail(MIMG_ERR_ARG, "attention: max_keys %lld (1..8192)", (long long)max_keys);
     if (T == 0) return MIMG_OK;
-    if (!q || !kcache || !vcache || !kend || !out) return fail(MIMG_ERR_ARG, "null pointer");
-    HIP_TRY(launch_attention(q, kcache, vcache, kend, kstart, (int)T, heads, kv_heads, d, context, f16, out,
-                             (hipStream_t)stream));
+    if (!q || !kcache || !vcache || !kend || !out || !ws) return fail(MIMG_ERR_ARG, "null pointer");
+    if (ws_bytes < mimg_attention_workspace_bytes(T, heads, max_keys))
+        return fail(MIMG_ERR_WORKSPACE, "attention workspace %llu < %llu bytes", (unsigned long long)ws_bytes,
+                    (unsigned long long)mimg_attention_workspace_bytes(T, heads, max_keys));
+    HIP_TRY(launch_attention(q, kcache, vcache, kend, kstart, (int)T, heads, kv_heads, d, context, max_keys, f16, out,
+                             (float*)ws, (hipStream_t)stream));
     return MIMG_OK;
 }
 

@@ -39,6 +39,21 @@ struct DevWeight {
 
 hipError_t launch_quantize_act(const float* x, int64_t rows, int64_t K, int block, const ActPtrs& a,
                                hipStream_t stream);
+// The producer of a quantized row fused into the quantizer (quantize_act.hip).
+struct QaSource {
+    const float* aux = nullptr;    // rms_norm: the residual (or null); swiglu: u
+    const float* scale = nullptr;  // rms_norm: the scale (or null)
+    float eps = 0.f;
+    float* y = nullptr;            // the produced rows
+    int64_t chunk = 1, total = 0;  // swiglu: the reference's piece size, rows*K
+};
+hipError_t launch_norm_quantize_act(float* x, const float* resid, const float* scale, float eps, float* y,
+                                    int64_t rows, int64_t K, int block, const ActPtrs& a, hipStream_t stream);
+hipError_t launch_swiglu_quantize_act(const float* g, const float* u, float* y, int64_t chunk, int64_t rows,
+                                      int64_t K, int block, const ActPtrs& a, hipStream_t stream);
+hipError_t launch_rope_kv(float* q, const float* k, const float* v, const int64_t* pos, const int64_t* cidx,
+                          const double* inv_freq, int T, int H, int Hkv, int D, int rotary, int interleaved, int64_t C,
+                          void* kc, void* vc, int f16, hipStream_t s);
 
 hipError_t launch_weight_refusals(uint32_t dt, const uint8_t* w, int64_t n, int64_t k, uint8_t* wref,
                                   hipStream_t stream);
@@ -93,7 +108,8 @@ hipError_t launch_rope(float* x, const int64_t* pos, const double* inv_freq, int
 hipError_t launch_kv_store(const float* k, const float* v, const int64_t* pos, int T, int Hkv, int D, int64_t C, void* kc,
                            void* vc, int f16, hipStream_t s);
 hipError_t launch_attention(const float* q, const void* kc, const void* vc, const int64_t* kend, const int64_t* kstart,
-                            int T, int H, int Hkv, int D, int64_t C, int f16, float* out, hipStream_t s);
+                            int T, int H, int Hkv, int D, int64_t C, int64_t maxk, int f16, float* out, float* ws,
+                            hipStream_t s);
 hipError_t launch_greedy_advance(const int32_t* chosen, int32_t* ids, int64_t* pos, int64_t* cidx, int32_t* out,
                                  int32_t* count, int cap, int n, hipStream_t s);
 hipError_t launch_swiglu(const float* g, const float* u, float* out, int64_t n, int64_t chunk, hipStream_t s);

@@ -77,6 +77,8 @@ class Decoder:
                 self.vec[name] = hiprt.DeviceBuffer.from_array(np.ascontiguousarray(data, np.float32))
             else:
                 self.w[name] = mimg.Weight(data, dt, int(shape[0]), int(shape[1]))
+        if c.context > 8192:
+            raise ValueError(f"context {c.context}: attention handles at most 8192 positions per sequence")
         self.head = self.w.get("output.weight") or self.w["token_embd.weight"]
         self.vocab = self.w["token_embd.weight"].n
         E, F, H, Hkv, D, R = c.embed, c.ffn, c.heads, c.kv_heads, c.head_dim, self.R
@@ -100,6 +102,8 @@ class Decoder:
         kmax = max(E, H * D, F)
         self.ws_bytes = mimg.a8_workspace_bytes(R, kmax)
         self.ws = B(self.ws_bytes)
+        self.att_ws_bytes = mimg.attention_workspace_bytes(R, H, c.context)
+        self.att_ws = B(self.att_ws_bytes)
         self.graphs = {}
 
     # ---- the graph's ops ---------------------------------------------------
@@ -124,6 +128,27 @@ class Decoder:
         for w, b, y in zip(ws, bs, ys):
             mimg.linear_a8_dev(w, x, rows, b, self._block(w), y, self.ws.ptr, self.ws_bytes, s)
 
+    def _norm_linears(self, resid, norm, T, names, ys, biases=None, single_fused=False):
+        """x += resid; h = rms_norm(x) * scale; ys[i] = h . W_i^T (+ bias_i).
+        With 8-bit activations and one block size for the group, the norm
+        and the quantization of h are one launch and the products take the
+        quantized h (bit for bit the separate ops); at one row, q/k/v
+        (single_fused) instead use the GEMV that quantizes inside."""
+        c, s = self.c, self.stream.handle
+        E = c.embed
+        ws = [self.w[n] for n in names]
+        blocks = {self._block(w) for w in ws}
+        if self.a8 and len(blocks) == 1 and not (single_fused and T == 1) and E <= 32768:
+            block = blocks.pop()
+            mimg.rms_norm_quant_dev(self.x.ptr, resid, self.vec[norm].ptr, c.norm_eps, T, E, self.h.ptr, block,
+                                    self.ws.ptr, self.ws_bytes, s)
+            bs = [None if b is None or b not in self.vec else self.vec[b].ptr for b in (biases or [None] * len(names))]
+            mimg.matmul_a8_quantized_group_dev(ws, self.h.ptr, T, bs if any(bs) else None, block, ys, self.ws.ptr,
+                                               self.ws_bytes, s)
+            return
+        mimg.rms_norm_dev(self.x.ptr, resid, self.vec[norm].ptr, c.norm_eps, T, E, self.h.ptr, s)
+        self._linears(names, self.h.ptr, T, ys, biases)
+
     def _forward(self, T, ids=None, pos=None, cidx=None, kstart=None, head_rows=None):
         """Enqueues the forward pass of T rows (device arrays of token ids,
         positions, cache indices and slot starts; by default the decoder's
@@ -140,26 +165,36 @@ class Decoder:
         resid = None  # the previous sublayer's output, added to x by the next norm
         for l in range(c.layers):
             p = f"blk.{l}."
-            mimg.rms_norm_dev(self.x.ptr, resid, self.vec[p + "attn_norm.weight"].ptr, c.norm_eps, T, E,
-                              self.h.ptr, s)
-            self._linears([p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"], self.h.ptr, T,
-                          [self.q.ptr, self.k.ptr, self.v.ptr],
-                          [p + "attn_q.bias", p + "attn_k.bias", p + "attn_v.bias"])
-            mimg.rope_dev(self.q.ptr, pos, self.invf.ptr, T, H, D, c.rope_dims, c.interleaved, s)
-            mimg.rope_dev(self.k.ptr, pos, self.invf.ptr, T, Hkv, D, c.rope_dims, c.interleaved, s)
-            mimg.kv_store_dev(self.k.ptr, self.v.ptr, cidx, T, Hkv, D, self.cache_len, self.kc[l].ptr,
-                              self.vc[l].ptr, self.f16, s)
+            qkv = [p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"]
+            qkv_b = [p + "attn_q.bias", p + "attn_k.bias", p + "attn_v.bias"]
+            self._norm_linears(resid, p + "attn_norm.weight", T, qkv, [self.q.ptr, self.k.ptr, self.v.ptr], qkv_b,
+                               single_fused=True)
+            mimg.rope_kv_dev(self.q.ptr, self.k.ptr, self.v.ptr, pos, cidx, self.invf.ptr, T, H, Hkv, D, c.rope_dims,
+                             c.interleaved, self.cache_len, self.kc[l].ptr, self.vc[l].ptr, self.f16, s)
             mimg.attention_dev(self.q.ptr, self.kc[l].ptr, self.vc[l].ptr, cidx, kstart, T, H, Hkv, D,
-                               self.cache_len, self.f16, self.o.ptr, s)
+                               self.cache_len, c.context, self.f16, self.o.ptr, self.att_ws.ptr, self.att_ws_bytes, s)
             self._linears([p + "attn_output.weight"], self.o.ptr, T, [self.ao.ptr])
-            mimg.rms_norm_dev(self.x.ptr, self.ao.ptr, self.vec[p + "ffn_norm.weight"].ptr, c.norm_eps, T, E,
-                              self.h.ptr, s)
-            self._linears([p + "ffn_gate.weight", p + "ffn_up.weight"], self.h.ptr, T, [self.g.ptr, self.u.ptr])
-            mimg.swiglu_dev(self.g.ptr, self.u.ptr, self.g.ptr, T * F, self.procs, s)
-            self._linears([p + "ffn_down.weight"], self.g.ptr, T, [self.ao.ptr])
+            self._norm_linears(self.ao.ptr, p + "ffn_norm.weight", T, [p + "ffn_gate.weight", p + "ffn_up.weight"],
+                               [self.g.ptr, self.u.ptr])
+            down = self.w[p + "ffn_down.weight"]
+            if self.a8 and self._block(down) in (32, 256) and F <= 32768:
+                mimg.swiglu_quant_dev(self.g.ptr, self.u.ptr, self.g.ptr, T, F, self.procs, self._block(down),
+                                      self.ws.ptr, self.ws_bytes, s)
+                mimg.matmul_a8_quantized_group_dev([down], self.g.ptr, T, None, self._block(down), [self.ao.ptr],
+                                                   self.ws.ptr, self.ws_bytes, s)
+            else:
+                mimg.swiglu_dev(self.g.ptr, self.u.ptr, self.g.ptr, T * F, self.procs, s)
+                self._linears([p + "ffn_down.weight"], self.g.ptr, T, [self.ao.ptr])
             resid = self.ao.ptr
-        mimg.rms_norm_dev(self.x.ptr, resid, self.vec["output_norm.weight"].ptr, c.norm_eps, T, E, self.h.ptr, s)
         V = self.vocab
+        if head_rows is None and self.a8 and E <= 32768:
+            block = self._block(self.head)
+            mimg.rms_norm_quant_dev(self.x.ptr, resid, self.vec["output_norm.weight"].ptr, c.norm_eps, T, E,
+                                    self.h.ptr, block, self.ws.ptr, self.ws_bytes, s)
+            mimg.matmul_a8_quantized_group_dev([self.head], self.h.ptr, T, None, block, [self.logits.ptr], self.ws.ptr,
+                                               self.ws_bytes, s)
+            return
+        mimg.rms_norm_dev(self.x.ptr, resid, self.vec["output_norm.weight"].ptr, c.norm_eps, T, E, self.h.ptr, s)
         for src, dst, n in ([(0, 0, T)] if head_rows is None else [(r, d, 1) for r, d in head_rows]):
             xh, yh = self.h.ptr + src * E * 4, self.logits.ptr + dst * V * 4
             if self.a8:

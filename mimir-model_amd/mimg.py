@@ -50,11 +50,17 @@ SIGNATURES = {
     "mimg_dequantize_dev": (_I, [_U32, _P, _U64, _P, _I64, _P]),
     "mimg_quantize_dev": (_I, [_U32, _P, _I64, _P, _U64, _P]),
     "mimg_synthetic_normal_dev": (_I, [_U64, ctypes.c_float, _P, _I64, _P]),
+    "mimg_matmul_a8_quantized_group_dev": (_I, [ctypes.POINTER(_U64), _I, _P, _I64, ctypes.POINTER(_P), _I,
+                                                ctypes.POINTER(_P), _P, _U64, _P]),
+    "mimg_rms_norm_quant_dev": (_I, [_P, _P, _P, ctypes.c_float, _I64, _I64, _P, _I, _P, _U64, _P]),
+    "mimg_swiglu_quant_dev": (_I, [_P, _P, _P, _I64, _I64, _I, _I, _P, _U64, _P]),
+    "mimg_rope_kv_dev": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _I64, _P, _P, _I, _P]),
     "mimg_embedding_dev": (_I, [_U64, _P, _I64, _P, _P]),
     "mimg_rms_norm_dev": (_I, [_P, _P, _P, ctypes.c_float, _I64, _I64, _P, _P]),
     "mimg_rope_dev": (_I, [_P, _P, _P, _I64, _I, _I, _I, _I, _P]),
     "mimg_kv_store_dev": (_I, [_P, _P, _P, _I64, _I, _I, _I64, _P, _P, _I, _P]),
-    "mimg_attention_dev": (_I, [_P, _P, _P, _P, _P, _I64, _I, _I, _I, _I64, _I, _P, _P]),
+    "mimg_attention_workspace_bytes": (_U64, [_I64, _I, _I64]),
+    "mimg_attention_dev": (_I, [_P, _P, _P, _P, _P, _I64, _I, _I, _I, _I64, _I64, _I, _P, _P, _U64, _P]),
     "mimg_greedy_advance_dev": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _P]),
     "mimg_swiglu_dev": (_I, [_P, _P, _P, _I64, _I, _P]),
     "mimg_argmax_dev": (_I, [_P, _I64, _I64, _P, _P]),
@@ -210,6 +216,32 @@ def matmul_a8_quantized_dev(w, x_ptr, rows, bias_ptr, block, y_ptr, ws_ptr, ws_b
                                                block, _P(y_ptr), _P(ws_ptr), ws_bytes, _P(stream)))
 
 
+def matmul_a8_quantized_group_dev(weights, x_ptr, rows, bias_ptrs, block, y_ptrs, ws_ptr, ws_bytes, stream):
+    n = len(weights)
+    hs = (_U64 * n)(*[w.handle for w in weights])
+    ys = (_P * n)(*[_P(p) for p in y_ptrs])
+    bs = None if bias_ptrs is None else (_P * n)(*[_P(p) if p else None for p in bias_ptrs])
+    _check(load().mimg_matmul_a8_quantized_group_dev(hs, n, _P(x_ptr), rows, bs, block, ys, _P(ws_ptr), ws_bytes,
+                                                     _P(stream)))
+
+
+def rms_norm_quant_dev(x_ptr, resid_ptr, scale_ptr, eps, rows, n, y_ptr, block, ws_ptr, ws_bytes, stream):
+    _check(load().mimg_rms_norm_quant_dev(_P(x_ptr), _o(resid_ptr), _o(scale_ptr), eps, rows, n, _P(y_ptr), block,
+                                          _P(ws_ptr), ws_bytes, _P(stream)))
+
+
+def swiglu_quant_dev(g_ptr, u_ptr, out_ptr, rows, n, procs, block, ws_ptr, ws_bytes, stream):
+    _check(load().mimg_swiglu_quant_dev(_P(g_ptr), _P(u_ptr), _P(out_ptr), rows, n, procs, block, _P(ws_ptr),
+                                        ws_bytes, _P(stream)))
+
+
+def rope_kv_dev(q_ptr, k_ptr, v_ptr, pos_ptr, cidx_ptr, inv_freq_ptr, T, heads, kv_heads, d, rotary, interleaved,
+                context, kc_ptr, vc_ptr, f16, stream):
+    _check(load().mimg_rope_kv_dev(_P(q_ptr), _P(k_ptr), _P(v_ptr), _P(pos_ptr), _P(cidx_ptr), _P(inv_freq_ptr), T,
+                                   heads, kv_heads, d, rotary, int(interleaved), context, _P(kc_ptr), _P(vc_ptr),
+                                   int(f16), _P(stream)))
+
+
 def linear_f32_dev(w, x_ptr, rows, bias_ptr, y_ptr, stream):
     _check(load().mimg_linear_f32_dev(w.handle, _P(x_ptr), rows, _P(bias_ptr) if bias_ptr else None,
                                       _P(y_ptr), _P(stream)))
@@ -254,9 +286,15 @@ def kv_store_dev(k_ptr, v_ptr, pos_ptr, T, kv_heads, d, context, kc_ptr, vc_ptr,
                                     _P(vc_ptr), int(f16), _P(stream)))
 
 
-def attention_dev(q_ptr, kc_ptr, vc_ptr, kend_ptr, kstart_ptr, T, heads, kv_heads, d, context, f16, out_ptr, stream):
+def attention_workspace_bytes(T, heads, max_keys):
+    return int(load().mimg_attention_workspace_bytes(T, heads, max_keys))
+
+
+def attention_dev(q_ptr, kc_ptr, vc_ptr, kend_ptr, kstart_ptr, T, heads, kv_heads, d, context, max_keys, f16,
+                  out_ptr, ws_ptr, ws_bytes, stream):
     _check(load().mimg_attention_dev(_P(q_ptr), _P(kc_ptr), _P(vc_ptr), _P(kend_ptr), _o(kstart_ptr), T, heads,
-                                     kv_heads, d, context, int(f16), _P(out_ptr), _P(stream)))
+                                     kv_heads, d, context, max_keys, int(f16), _P(out_ptr), _o(ws_ptr), ws_bytes,
+                                     _P(stream)))
 
 
 def greedy_advance_dev(chosen_ptr, ids_ptr, pos_ptr, cidx_ptr, out_ptr, count_ptr, cap, n, stream):

@@ -98,12 +98,11 @@ def test_rope(gpu, rt, interleaved):
 @pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
 @pytest.mark.parametrize("T,H,Hkv,D,slots", [(1, 32, 8, 64, 1), (6, 4, 2, 64, 1), (3, 8, 8, 128, 2), (4, 4, 1, 32, 3),
                                              (5, 2, 1, 8, 1), (2, 4, 2, 256, 1)])
-def test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, slots):
+def test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, slots, C=48):
     """The cache scatter (exact) and attention against the C restatement of
     the reference's attendRow with its AVX2 kernels, bit for bit; visible
     ranges of every length mod 4 and mod 8 (the scores' groups of four and
     the exp sum's vector part and tail)."""
-    C = 48
     rng = np.random.default_rng(T * 100 + H + D)
     L = slots * C
     # a cache already holding rows, then T new rows at the given positions
@@ -118,10 +117,12 @@ def test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, slo
     kc, vc = dev(rt, base[0]), dev(rt, base[1])
     dk, dv, dq, dc, ds = dev(rt, k), dev(rt, v), dev(rt, q), dev(rt, cidx), dev(rt, (slot * C).astype(np.int64))
     out = rt.DeviceBuffer(q.nbytes)
+    wsb = gpu.attention_workspace_bytes(T, H, C)
+    ws = rt.DeviceBuffer(wsb)
     s = rt.Stream()
     gpu.kv_store_dev(dk.ptr, dv.ptr, dc.ptr, T, Hkv, D, L, kc.ptr, vc.ptr, f16, s.handle)
-    gpu.attention_dev(dq.ptr, kc.ptr, vc.ptr, dc.ptr, ds.ptr if slots > 1 else None, T, H, Hkv, D, L, f16, out.ptr,
-                      s.handle)
+    gpu.attention_dev(dq.ptr, kc.ptr, vc.ptr, dc.ptr, ds.ptr if slots > 1 else None, T, H, Hkv, D, L, C, f16, out.ptr,
+                      ws.ptr, wsb, s.handle)
     s.sync()
     wk, wv = base[0].copy(), base[1].copy()
     for t in range(T):
@@ -134,6 +135,13 @@ def test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, slo
     want = oracle.attention(q, wk, wv, cidx, slot * C if slots > 1 else None)
     got = out.download(np.float32).reshape(T, H, D)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), float(np.max(np.abs(got - want)))
+
+
+@pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
+@pytest.mark.parametrize("C,D", [(700, 128), (1100, 64), (300, 8)])
+def test_attention_long_context_bitexact(gpu, oracle, rt, f16, C, D):
+    """Long visible ranges: many score tiles and several value chunks."""
+    test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, 3, 4, 2, D, 1, C=C)
 
 
 @pytest.mark.parametrize("n,procs", [(3 * 8192 + 5, 16), (1792, 16), (100, 4), (100, 1), (4096, 7), (7, 16)])
@@ -167,6 +175,17 @@ def test_argmax_first_index(gpu, rt):
     s.sync()
     got = do.download(np.int32)
     assert got.tolist() == [int(np.argmax(r)) for r in x] == [got[0], 77, 0, n - 1]
+    # the reference's loop (best = 0; x > v[best]): NaNs are never chosen,
+    # a NaN first value gives 0; odd lengths (unaligned rows)
+    y = rng.standard_normal((3, 1001)).astype(np.float32)
+    y[0, 5] = np.nan
+    y[1, 0] = np.nan
+    y[2, :] = np.nan
+    dy, dz = dev(rt, y), rt.DeviceBuffer(3 * 4)
+    gpu.argmax_dev(dy.ptr, 3, 1001, dz.ptr, s.handle)
+    s.sync()
+    want0 = int(np.nanargmax(y[0]))
+    assert dz.download(np.int32).tolist() == [want0, 0, 0]
 
 
 def test_greedy_advance(gpu, rt):
@@ -296,3 +315,113 @@ def test_llama1b_shape_greedy_matches_oracle(gpu, cache_f16):
         if i + 1 < n_new:
             lg = ref.forward([want[-1]], [32 + i])[0]
     assert got == want
+
+
+# ------------------------------------------------------ fused launches
+
+def _ws_bytes(gpu, ws, rows, k):
+    """The quantized activations in a workspace, as raw bytes per array."""
+    off = gpu.a8_workspace_offsets(rows, k)
+    raw = ws.download(np.uint8, gpu.a8_workspace_bytes(rows, k))
+    sizes = [rows * k, rows * (k // 32) * 4, rows * (k // 32) * 2, rows * (k // 16) * 2, rows * (k // 32) * 4, rows * 4]
+    return [raw[o:o + n].tobytes() for o, n in zip(off, sizes)]
+
+
+@pytest.mark.parametrize("rows,n,block,resid", [(1, 4096, 256, True), (5, 2048, 256, False), (3, 1024, 32, True),
+                                                (2, 8192, 256, True)])
+def test_rms_norm_quant_equals_two_launches(gpu, rt, rows, n, block, resid):
+    rng = np.random.default_rng(rows * n + block)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    r = rng.standard_normal((rows, n)).astype(np.float32)
+    sc = rng.standard_normal(n).astype(np.float32)
+    s = rt.Stream()
+    wsb = gpu.a8_workspace_bytes(rows, n)
+    outs = []
+    for fused in (False, True):
+        dx, dr, dsc, dy, ws = dev(rt, x), dev(rt, r), dev(rt, sc), rt.DeviceBuffer(x.nbytes), rt.DeviceBuffer(wsb)
+        ws.zero()
+        if fused:
+            gpu.rms_norm_quant_dev(dx.ptr, dr.ptr if resid else None, dsc.ptr, 1e-5, rows, n, dy.ptr, block, ws.ptr, wsb,
+                                   s.handle)
+        else:
+            gpu.rms_norm_dev(dx.ptr, dr.ptr if resid else None, dsc.ptr, 1e-5, rows, n, dy.ptr, s.handle)
+            gpu.quantize_act_dev(dy.ptr, rows, n, block, ws.ptr, wsb, s.handle)
+        s.sync()
+        outs.append((dx.download(np.float32), dy.download(np.float32), _ws_bytes(gpu, ws, rows, n)))
+    (x0, y0, q0), (x1, y1, q1) = outs
+    assert np.array_equal(x0, x1)
+    assert np.array_equal(y0.view(np.uint32), y1.view(np.uint32))
+    assert q0 == q1
+
+
+@pytest.mark.parametrize("rows,n,block,procs", [(1, 14336, 256, 16), (4, 8192, 256, 7), (3, 1792, 32, 16)])
+def test_swiglu_quant_equals_two_launches(gpu, rt, rows, n, block, procs):
+    rng = np.random.default_rng(rows + n)
+    g = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+    u = rng.standard_normal((rows, n)).astype(np.float32)
+    s = rt.Stream()
+    wsb = gpu.a8_workspace_bytes(rows, n)
+    outs = []
+    for fused in (False, True):
+        dg, du, do, ws = dev(rt, g), dev(rt, u), rt.DeviceBuffer(g.nbytes), rt.DeviceBuffer(wsb)
+        ws.zero()
+        if fused:
+            gpu.swiglu_quant_dev(dg.ptr, du.ptr, do.ptr, rows, n, procs, block, ws.ptr, wsb, s.handle)
+        else:
+            gpu.swiglu_dev(dg.ptr, du.ptr, do.ptr, rows * n, procs, s.handle)
+            gpu.quantize_act_dev(do.ptr, rows, n, block, ws.ptr, wsb, s.handle)
+        s.sync()
+        outs.append((do.download(np.float32), _ws_bytes(gpu, ws, rows, n)))
+    assert np.array_equal(outs[0][0].view(np.uint32), outs[1][0].view(np.uint32))
+    assert outs[0][1] == outs[1][1]
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("T,H,Hkv,D,rot,inter", [(1, 32, 8, 128, 128, True), (5, 4, 2, 64, 32, False),
+                                                 (3, 8, 8, 64, 64, False), (2, 4, 1, 80, 48, True)])
+def test_rope_kv_equals_three_launches(gpu, rt, f16, T, H, Hkv, D, rot, inter):
+    rng = np.random.default_rng(T * D + rot)
+    C = 40
+    q = rng.standard_normal((T, H, D)).astype(np.float32)
+    k = rng.standard_normal((T, Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((T, Hkv, D)).astype(np.float32)
+    pos = np.array([3, 17, 0, 39, 21][:T], np.int64)
+    cidx = pos.copy()
+    invf = np.array([500000.0 ** (-2.0 * i / rot) for i in range(rot // 2)], np.float64)
+    cdt = np.float16 if f16 else np.float32
+    s = rt.Stream()
+    outs = []
+    for fused in (False, True):
+        dq, dk, dv, dp, dc, di = dev(rt, q), dev(rt, k), dev(rt, v), dev(rt, pos), dev(rt, cidx), dev(rt, invf)
+        kc, vc = dev(rt, np.zeros((Hkv, C, D), cdt)), dev(rt, np.zeros((Hkv, C, D), cdt))
+        if fused:
+            gpu.rope_kv_dev(dq.ptr, dk.ptr, dv.ptr, dp.ptr, dc.ptr, di.ptr, T, H, Hkv, D, rot, inter, C, kc.ptr, vc.ptr,
+                            f16, s.handle)
+        else:
+            gpu.rope_dev(dq.ptr, dp.ptr, di.ptr, T, H, D, rot, inter, s.handle)
+            gpu.rope_dev(dk.ptr, dp.ptr, di.ptr, T, Hkv, D, rot, inter, s.handle)
+            gpu.kv_store_dev(dk.ptr, dv.ptr, dc.ptr, T, Hkv, D, C, kc.ptr, vc.ptr, f16, s.handle)
+        s.sync()
+        outs.append([b.download(np.uint8).tobytes() for b in (dq, kc, vc)])
+    assert outs[0] == outs[1]
+
+
+def test_matmul_quantized_group_equals_single(gpu, oracle, rt):
+    rows, k = 3, 1024
+    specs = [(Q4_K, 300), (Q4_K, 100), (Q6_K, 120)]
+    wbs = [oracle.synthetic_weight(dt, n, k, seed=40 + i) for i, (dt, n) in enumerate(specs)]
+    W = [gpu.Weight(wb, dt, n, k) for wb, (dt, n) in zip(wbs, specs)]
+    x = oracle.synthetic_acts(rows, k, seed=44)
+    bias = np.random.default_rng(45).standard_normal(300).astype(np.float32)
+    s = rt.Stream()
+    wsb = gpu.a8_workspace_bytes(rows, k)
+    dx, ws, db = dev(rt, x), rt.DeviceBuffer(wsb), dev(rt, bias)
+    ys = [rt.DeviceBuffer(rows * n * 4) for _, n in specs]
+    gpu.quantize_act_dev(dx.ptr, rows, k, 256, ws.ptr, wsb, s.handle)
+    gpu.matmul_a8_quantized_group_dev(W, dx.ptr, rows, [db.ptr, None, None], 256, [y.ptr for y in ys], ws.ptr, wsb,
+                                      s.handle)
+    s.sync()
+    for i, ((dt, n), wb) in enumerate(zip(specs, wbs)):
+        want = oracle.linear_a8(x, wb, dt, n, k, bias=bias if i == 0 else None, block=256)
+        got = ys[i].download(np.float32).reshape(rows, n)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), i
