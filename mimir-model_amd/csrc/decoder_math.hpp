@@ -60,13 +60,33 @@ __device__ __forceinline__ float silu_mul_vec(float x, float b) {
 // `chunk` elements (parallel(), interp/pool.go:33-51): the first len&~7 of
 // a piece through the vector formula, the rest through float64
 // (SiluMulF32, internal/kernels/attn.go:63-76).
-__device__ __forceinline__ float swiglu_at(float g, float u, int64_t i, int64_t n, int64_t chunk) {
-    const int64_t lo = i / chunk * chunk;
+__device__ __forceinline__ float swiglu_in_piece(float g, float u, int64_t i, int64_t lo, int64_t n, int64_t chunk) {
     const int64_t len = lo + chunk < n ? chunk : n - lo;
     const int64_t nv = len >= 8 ? (len & ~(int64_t)7) : 0;
     if (i - lo < nv) return silu_mul_vec(g, u);
     const double a = (double)g;
     return (float)(a / (1.0 + exp(-a)) * (double)u);
+}
+__device__ __forceinline__ int64_t piece_start(int64_t i, int64_t chunk) {
+    // n < 2^32 in practice: a 32-bit division is far cheaper than a 64-bit one
+    if (((uint64_t)i | (uint64_t)chunk) < 0x100000000ull) return (int64_t)((uint32_t)i / (uint32_t)chunk) * chunk;
+    return i / chunk * chunk;
+}
+__device__ __forceinline__ float swiglu_at(float g, float u, int64_t i, int64_t n, int64_t chunk) {
+    return swiglu_in_piece(g, u, i, piece_start(i, chunk), n, chunk);
+}
+// Four consecutive elements i..i+3: one division for the four.
+__device__ __forceinline__ float4 swiglu4(float4 g, float4 u, int64_t i, int64_t n, int64_t chunk) {
+    int64_t lo = piece_start(i, chunk);
+    float4 o;
+    o.x = swiglu_in_piece(g.x, u.x, i, lo, n, chunk);
+    while (i + 1 - lo >= chunk) lo += chunk;
+    o.y = swiglu_in_piece(g.y, u.y, i + 1, lo, n, chunk);
+    while (i + 2 - lo >= chunk) lo += chunk;
+    o.z = swiglu_in_piece(g.z, u.z, i + 2, lo, n, chunk);
+    while (i + 3 - lo >= chunk) lo += chunk;
+    o.w = swiglu_in_piece(g.w, u.w, i + 3, lo, n, chunk);
+    return o;
 }
 
 }  // namespace mimg

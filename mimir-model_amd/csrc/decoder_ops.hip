@@ -373,7 +373,25 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
     if (tid == 0) nan_any = 0;
     float mx = -INFINITY;
     int isnan_local = 0;
-    for (int64_t j = tid; j < n; j += 256) {
+    {
+        // the first 1024 scores in one round of loads (clamped, unstored past n)
+        float sv[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int64_t j = tid + 256 * k;
+            sv[k] = srow[j < n ? j : n - 1];
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int64_t j = tid + 256 * k;
+            if (j < n) {
+                sc[j] = sv[k];
+                isnan_local |= sv[k] != sv[k];
+                mx = fmaxf(mx, sv[k]);
+            }
+        }
+    }
+    for (int64_t j = tid + 1024; j < n; j += 256) {
         const float v = srow[j];
         sc[j] = v;
         isnan_local |= v != v;
@@ -394,7 +412,10 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
         const float x = sc[j] - mx;
         sc[j] = j < nv ? cephes_exp(x) : (float)exp((double)x);
     }
-    // the first chunk of values into LDS as f32
+    // the first chunk of values into LDS as f32, dim-major (vb[d][j], rows of
+    // vstride = vch + 4 floats: the chain reads four keys of one dim at once,
+    // and the sixteen lanes' rows fall in distinct banks)
+    const int64_t vstride = vch + 4;
 #pragma unroll
     for (int k = 0; k < ATT_VREGS; k++) {
         const int64_t i = tid + 256 * k;
@@ -402,14 +423,18 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
         if (row < rows0) {
             if constexpr (F16) {
                 const uint32_t wv[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
-                float* dst = vb + row * DS + piece * 8;
+                float* dst = vb + piece * 8 * vstride + row;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    dst[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
-                    dst[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
+                    dst[(2 * e) * vstride] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
+                    dst[(2 * e + 1) * vstride] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
                 }
             } else {
-                *(uint4*)(vb + row * DS + piece * 4) = vr[k];
+                const float fv[4] = {__uint_as_float(vr[k].x), __uint_as_float(vr[k].y), __uint_as_float(vr[k].z),
+                                     __uint_as_float(vr[k].w)};
+                float* dst = vb + piece * 4 * vstride + row;
+#pragma unroll
+                for (int e = 0; e < 4; e++) dst[e * vstride] = fv[e];
             }
         }
     }
@@ -418,12 +443,12 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
     if (tid < 8) {
         float s = 0.f;
         int64_t j = tid;
-        for (; j + 56 < nv; j += 64) {
-            float e[8];
+        for (; j + 120 < nv; j += 128) {
+            float e[16];
 #pragma unroll
-            for (int u = 0; u < 8; u++) e[u] = sc[j + 8 * u];
+            for (int u = 0; u < 16; u++) e[u] = sc[j + 8 * u];
 #pragma unroll
-            for (int u = 0; u < 8; u++) s = s + e[u];
+            for (int u = 0; u < 16; u++) s = s + e[u];
         }
         for (; j < nv; j += 8) s = s + sc[j];
         lane_sum[tid] = s;
@@ -442,32 +467,44 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
                 if constexpr (F16) {
                     const uint4 raw = *(const uint4*)((const _Float16*)vc + vbase + (c0 + row) * D + piece * 8);
                     const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
-                    float* dst = vb + row * DS + piece * 8;
+                    float* dst = vb + piece * 8 * vstride + row;
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        dst[2 * e] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
-                        dst[2 * e + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
+                        dst[(2 * e) * vstride] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
+                        dst[(2 * e + 1) * vstride] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
                     }
                 } else {
-                    *(uint4*)(vb + row * DS + piece * 4) = *(const uint4*)((const float*)vc + vbase + (c0 + row) * D + piece * 4);
+                    const float4 v4 = *(const float4*)((const float*)vc + vbase + (c0 + row) * D + piece * 4);
+                    float* dst = vb + piece * 4 * vstride + row;
+                    dst[0] = v4.x;
+                    dst[vstride] = v4.y;
+                    dst[2 * vstride] = v4.z;
+                    dst[3 * vstride] = v4.w;
                 }
             }
             __syncthreads();
         }
         if (tid < DS) {
+            // the chain in key order, four keys per LDS read of each operand
             const float* e = sc + c0;
+            const float* vd = vb + tid * vstride;
             int64_t j = 0;
-            for (; j + 8 <= rows; j += 8) {
-                float ev[8], vv[8];
+            for (; j + 16 <= rows; j += 16) {
+                float4 ev[4], vv[4];
 #pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    ev[u] = e[j + u];
-                    vv[u] = vb[(j + u) * DS + tid];
+                for (int u = 0; u < 4; u++) {
+                    ev[u] = *(const float4*)(e + j + 4 * u);
+                    vv[u] = *(const float4*)(vd + j + 4 * u);
                 }
 #pragma unroll
-                for (int u = 0; u < 8; u++) acc = __builtin_fmaf(ev[u], vv[u], acc);
+                for (int u = 0; u < 4; u++) {
+                    acc = __builtin_fmaf(ev[u].x, vv[u].x, acc);
+                    acc = __builtin_fmaf(ev[u].y, vv[u].y, acc);
+                    acc = __builtin_fmaf(ev[u].z, vv[u].z, acc);
+                    acc = __builtin_fmaf(ev[u].w, vv[u].w, acc);
+                }
             }
-            for (; j < rows; j++) acc = __builtin_fmaf(e[j], vb[j * DS + tid], acc);
+            for (; j < rows; j++) acc = __builtin_fmaf(e[j], vd[j], acc);
         }
     }
     if (tid < DS) orow[tid] = acc / sum;
@@ -632,10 +669,12 @@ static void launch_att_wsum(int T, int H, int Hkv, int D, int64_t C, int64_t max
                             const int64_t* kstart, const float* ws, float* out, hipStream_t s) {
     constexpr int PER_ROW = F16 ? DS / 8 : DS / 4;
     const int64_t sc_bytes = ((maxk + 3) & ~(int64_t)3) * 4;
-    int64_t vch = (ATT_LDS_MAX - 256 - sc_bytes) / (DS * 4);
-    if (vch > ATT_VBYTES / (DS * 4)) vch = ATT_VBYTES / (DS * 4);
+    // values: DS rows of vch + 4 floats (vch a multiple of 4)
+    int64_t vch = (ATT_LDS_MAX - 256 - sc_bytes) / (DS * 4) - 4;
+    if (vch > ATT_VBYTES / (DS * 4) - 4) vch = ATT_VBYTES / (DS * 4) - 4;
     if (vch > (int64_t)ATT_VREGS * 256 / PER_ROW) vch = (int64_t)ATT_VREGS * 256 / PER_ROW;
-    const size_t lds = (size_t)(sc_bytes + vch * DS * 4);
+    vch &= ~(int64_t)3;
+    const size_t lds = (size_t)(sc_bytes + DS * (vch + 4) * 4);
     hipLaunchKernelGGL((att_wsum_kernel<DS, F16>), dim3((unsigned)(D / DS), (unsigned)H, (unsigned)T), dim3(256), lds, s,
                        vc, kend, kstart, H, Hkv, D, C, maxk, (int)vch, ws, out);
 }

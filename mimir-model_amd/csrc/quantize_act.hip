@@ -80,10 +80,7 @@ __global__ __launch_bounds__(1024) void quantize_act_kernel(const float* __restr
                           (double)vv[i].z * (double)vv[i].z + (double)vv[i].w * (double)vv[i].w;
             } else {
                 const int64_t gi = (int64_t)row * K + (live ? e0 : 0);
-                vv[i].x = swiglu_at(vv[i].x, aux[i].x, gi, src.total, src.chunk);
-                vv[i].y = swiglu_at(vv[i].y, aux[i].y, gi + 1, src.total, src.chunk);
-                vv[i].z = swiglu_at(vv[i].z, aux[i].z, gi + 2, src.total, src.chunk);
-                vv[i].w = swiglu_at(vv[i].w, aux[i].w, gi + 3, src.total, src.chunk);
+                vv[i] = swiglu4(vv[i], aux[i], gi, src.total, src.chunk);
                 if (live) *(float4*)(src.y + gi) = vv[i];
             }
         }
