@@ -19,6 +19,8 @@
 //   swiglu.v1     SiluMulF32 over the reference's pieces (fast.go:487-498,
 //                 attn.go:63-76, attn_amd64.s:459-535): bit for bit
 //   argmax        first index of the largest logit (cmd/mim-run/main.go:184-192)
+#include <type_traits>
+
 #include "decoder_math.hpp"
 #include "f32path.hpp"
 #include "mimg_device.hpp"
@@ -327,12 +329,12 @@ __global__ __launch_bounds__(256) void att_scores_kernel(const float* __restrict
     }
 }
 
-// LDS of att_wsum: the scores (maxk floats, padded to 4) and up to
-// ATT_VBYTES of values as f32; the first chunk of values is loaded into
-// registers (at most ATT_VREGS 16-byte pieces a thread) while the
-// exponentials are computed.
-constexpr int ATT_VBYTES = 48 * 1024;
-constexpr int ATT_LDS_MAX = 64 * 1024;
+// LDS of att_wsum: the scores (maxk floats, padded to 4) and a chunk of
+// values in the cache's own type (f16 or f32), dim-major, within ATT_LDS
+// bytes (more only when the scores need it) so that several workgroups fit
+// on a CU; the first chunk of values is loaded into registers (at most
+// ATT_VREGS 16-byte pieces a thread) while the exponentials are computed.
+constexpr int ATT_LDS = 32 * 1024;
 constexpr int ATT_VREGS = 12;
 
 template <int DS, bool F16>
@@ -345,8 +347,9 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
     __shared__ float lane_sum[8];
     __shared__ int nan_any;
     constexpr int PER_ROW = F16 ? DS / 8 : DS / 4;  // 16-byte pieces per row of the slice
+    using VT = typename std::conditional<F16, _Float16, float>::type;
     float* sc = att_lds;
-    float* vb = att_lds + ((maxk + 3) & ~(int64_t)3);
+    VT* vb = (VT*)(att_lds + ((maxk + 3) & ~(int64_t)3));
     const int d0 = blockIdx.x * DS, h = blockIdx.y, t = blockIdx.z, tid = threadIdx.x, w = tid >> 6;
     const AttRange r = att_range(kend, kstart, t, C, maxk);
     const int64_t n = r.n;
@@ -412,10 +415,10 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
         const float x = sc[j] - mx;
         sc[j] = j < nv ? cephes_exp(x) : (float)exp((double)x);
     }
-    // the first chunk of values into LDS as f32, dim-major (vb[d][j], rows of
-    // vstride = vch + 4 floats: the chain reads four keys of one dim at once,
-    // and the sixteen lanes' rows fall in distinct banks)
-    const int64_t vstride = vch + 4;
+    // the first chunk of values into LDS, dim-major (vb[d][j], rows of
+    // vstride = vch + 16 bytes' worth of elements: the chain reads four keys
+    // of one dim at once, and the sixteen lanes' rows fall in distinct banks)
+    const int64_t vstride = vch + (F16 ? 8 : 4);
 #pragma unroll
     for (int k = 0; k < ATT_VREGS; k++) {
         const int64_t i = tid + 256 * k;
@@ -423,16 +426,16 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
         if (row < rows0) {
             if constexpr (F16) {
                 const uint32_t wv[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
-                float* dst = vb + piece * 8 * vstride + row;
+                VT* dst = vb + piece * 8 * vstride + row;
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    dst[(2 * e) * vstride] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
-                    dst[(2 * e + 1) * vstride] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
+                    dst[(2 * e) * vstride] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
+                    dst[(2 * e + 1) * vstride] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
                 }
             } else {
                 const float fv[4] = {__uint_as_float(vr[k].x), __uint_as_float(vr[k].y), __uint_as_float(vr[k].z),
                                      __uint_as_float(vr[k].w)};
-                float* dst = vb + piece * 4 * vstride + row;
+                VT* dst = vb + piece * 4 * vstride + row;
 #pragma unroll
                 for (int e = 0; e < 4; e++) dst[e * vstride] = fv[e];
             }
@@ -467,15 +470,15 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
                 if constexpr (F16) {
                     const uint4 raw = *(const uint4*)((const _Float16*)vc + vbase + (c0 + row) * D + piece * 8);
                     const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
-                    float* dst = vb + piece * 8 * vstride + row;
+                    VT* dst = vb + piece * 8 * vstride + row;
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
-                        dst[(2 * e) * vstride] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
-                        dst[(2 * e + 1) * vstride] = (float)__builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
+                        dst[(2 * e) * vstride] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
+                        dst[(2 * e + 1) * vstride] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
                     }
                 } else {
                     const float4 v4 = *(const float4*)((const float*)vc + vbase + (c0 + row) * D + piece * 4);
-                    float* dst = vb + piece * 4 * vstride + row;
+                    VT* dst = vb + piece * 4 * vstride + row;
                     dst[0] = v4.x;
                     dst[vstride] = v4.y;
                     dst[2 * vstride] = v4.z;
@@ -487,14 +490,22 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
         if (tid < DS) {
             // the chain in key order, four keys per LDS read of each operand
             const float* e = sc + c0;
-            const float* vd = vb + tid * vstride;
+            const VT* vd = vb + tid * vstride;
             int64_t j = 0;
             for (; j + 16 <= rows; j += 16) {
                 float4 ev[4], vv[4];
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
                     ev[u] = *(const float4*)(e + j + 4 * u);
-                    vv[u] = *(const float4*)(vd + j + 4 * u);
+                    if constexpr (F16) {
+                        const uint2 h = *(const uint2*)(vd + j + 4 * u);
+                        vv[u] = make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xFFFF)),
+                                            (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16)),
+                                            (float)__builtin_bit_cast(_Float16, (uint16_t)(h.y & 0xFFFF)),
+                                            (float)__builtin_bit_cast(_Float16, (uint16_t)(h.y >> 16)));
+                    } else {
+                        vv[u] = *(const float4*)(vd + j + 4 * u);
+                    }
                 }
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
@@ -504,7 +515,7 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
                     acc = __builtin_fmaf(ev[u].w, vv[u].w, acc);
                 }
             }
-            for (; j < rows; j++) acc = __builtin_fmaf(e[j], vd[j], acc);
+            for (; j < rows; j++) acc = __builtin_fmaf(e[j], (float)vd[j], acc);
         }
     }
     if (tid < DS) orow[tid] = acc / sum;
@@ -668,13 +679,16 @@ template <int DS, bool F16>
 static void launch_att_wsum(int T, int H, int Hkv, int D, int64_t C, int64_t maxk, const void* vc, const int64_t* kend,
                             const int64_t* kstart, const float* ws, float* out, hipStream_t s) {
     constexpr int PER_ROW = F16 ? DS / 8 : DS / 4;
+    constexpr int64_t ESZ = F16 ? 2 : 4, PAD = F16 ? 8 : 4;
     const int64_t sc_bytes = ((maxk + 3) & ~(int64_t)3) * 4;
-    // values: DS rows of vch + 4 floats (vch a multiple of 4)
-    int64_t vch = (ATT_LDS_MAX - 256 - sc_bytes) / (DS * 4) - 4;
-    if (vch > ATT_VBYTES / (DS * 4) - 4) vch = ATT_VBYTES / (DS * 4) - 4;
+    // values: DS rows of vch + PAD elements (vch a multiple of 8); at least
+    // 64 keys a chunk, the rest of ATT_LDS otherwise
+    int64_t budget = ATT_LDS - 256;
+    if (budget < sc_bytes + DS * (64 + PAD) * ESZ) budget = sc_bytes + DS * (64 + PAD) * ESZ;
+    int64_t vch = (budget - sc_bytes) / (DS * ESZ) - PAD;
     if (vch > (int64_t)ATT_VREGS * 256 / PER_ROW) vch = (int64_t)ATT_VREGS * 256 / PER_ROW;
-    vch &= ~(int64_t)3;
-    const size_t lds = (size_t)(sc_bytes + DS * (vch + 4) * 4);
+    vch &= ~(int64_t)7;
+    const size_t lds = (size_t)(sc_bytes + DS * (vch + PAD) * ESZ);
     hipLaunchKernelGGL((att_wsum_kernel<DS, F16>), dim3((unsigned)(D / DS), (unsigned)H, (unsigned)T), dim3(256), lds, s,
                        vc, kend, kstart, H, Hkv, D, C, maxk, (int)vch, ws, out);
 }
