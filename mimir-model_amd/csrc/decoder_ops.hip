@@ -281,52 +281,192 @@ __device__ __forceinline__ float att_reduce8(float l, bool four, int gbase, int 
 }
 
 // DM = D/8 for D = 64 or 128 (unrolled; every load of a lane in flight at
-// once), 0 for other multiples of 8.
-template <bool F16, int DM>
+// once), 0 for other multiples of 8. QT queries per workgroup (rows
+// QT*z .. QT*z + QT-1 of T): when they share the first visible cache entry
+// (rows of one sequence), each key is loaded once for all of them.
+template <bool F16, int DM, int QT>
 __global__ __launch_bounds__(256) void att_scores_kernel(const float* __restrict__ q, const void* kc,
                                                          const int64_t* __restrict__ kend,
-                                                         const int64_t* __restrict__ kstart, int H, int Hkv, int D,
-                                                         int64_t C, int64_t maxk, float* __restrict__ ws) {
-    const int tile = blockIdx.x, h = blockIdx.y, t = blockIdx.z;
-    const AttRange r = att_range(kend, kstart, t, C, maxk);
-    if ((int64_t)tile * 64 >= r.n) return;
+                                                         const int64_t* __restrict__ kstart, int T, int H, int Hkv,
+                                                         int D, int64_t C, int64_t maxk, float* __restrict__ ws) {
+    const int tile = blockIdx.x, h = blockIdx.y;
+    AttRange r[QT];
+    int64_t nmax = 0;
+#pragma unroll
+    for (int i = 0; i < QT; i++) {
+        const int t = QT * blockIdx.z + i;
+        r[i] = t < T ? att_range(kend, kstart, t, C, maxk) : AttRange{0, 0};
+        nmax = r[i].n > nmax ? r[i].n : nmax;
+    }
+    if ((int64_t)tile * 64 >= nmax) return;
+    int i0 = 0;  // the first query with keys (nmax > 0)
+    while (r[i0].n == 0) i0++;
+    bool same = true;
+#pragma unroll
+    for (int i = 0; i < QT; i++) same = same && (r[i].n == 0 || r[i].k0 == r[i0].k0);
     const int hk = h / (H / Hkv);
     const int lane = threadIdx.x & 63, c = lane & 7, gbase = lane & ~7, grp = threadIdx.x >> 3;
-    const int64_t n4 = r.n - r.n % 4;
-    const int64_t cbase = (int64_t)hk * C + r.k0;
     const float scale = (float)(1.0 / sqrt((double)D));
-    const float* qr = q + ((int64_t)t * H + h) * D;
-    float* out = ws + ((int64_t)t * H + h) * maxk;
-    // two keys per group; past the end the last key is recomputed, unstored
     const int64_t j0 = (int64_t)tile * 64 + grp, j1 = j0 + 32;
-    const int64_t a0 = cbase + (j0 < r.n ? j0 : r.n - 1), a1 = cbase + (j1 < r.n ? j1 : r.n - 1);
-    float l0 = 0.f, l1 = 0.f;
-    if constexpr (DM > 0) {
-        float qv[DM], k0v[DM], k1v[DM];
+    constexpr int DMR = DM > 0 ? DM : 1;
+    // one query: dot products of q with keys at a0, a1 (cache entries)
+    auto query_scores = [&](int i, const float* kv0, const float* kv1, int64_t a0, int64_t a1) {
+        const int t = QT * blockIdx.z + i;
+        const float* qr = q + ((int64_t)t * H + h) * D;
+        float l0 = 0.f, l1 = 0.f;
+        if constexpr (DM > 0) {
 #pragma unroll
-        for (int m = 0; m < DM; m++) {
-            qv[m] = qr[8 * m + c];
-            k0v[m] = kv_load<F16>(kc, a0 * D + 8 * m + c);
-            k1v[m] = kv_load<F16>(kc, a1 * D + 8 * m + c);
+            for (int m = 0; m < DM; m++) {
+                const float qm = qr[8 * m + c];
+                l0 = __builtin_fmaf(qm, kv0[m], l0);
+                l1 = __builtin_fmaf(qm, kv1[m], l1);
+            }
+        } else {
+            for (int m = 0; m < D / 8; m++) {
+                const float qm = qr[8 * m + c];
+                l0 = __builtin_fmaf(qm, kv_load<F16>(kc, a0 * D + 8 * m + c), l0);
+                l1 = __builtin_fmaf(qm, kv_load<F16>(kc, a1 * D + 8 * m + c), l1);
+            }
         }
+        const int64_t n = r[i].n, n4 = n - n % 4;
+        const float p0 = att_reduce8(l0, j0 < n4, gbase, c);
+        const float p1 = att_reduce8(l1, j1 < n4, gbase, c);
+        float* out = ws + ((int64_t)t * H + h) * maxk;
+        if (c == 0) {
+            if (j0 < n) out[j0] = p0 * scale;
+            if (j1 < n) out[j1] = p1 * scale;
+        }
+    };
+    auto load_keys = [&](int64_t base, int64_t n, float* kv0, float* kv1, int64_t& a0, int64_t& a1) {
+        // past the end the last key is recomputed, unstored
+        a0 = base + (j0 < n ? j0 : n - 1);
+        a1 = base + (j1 < n ? j1 : n - 1);
+        if constexpr (DM > 0) {
 #pragma unroll
-        for (int m = 0; m < DM; m++) {
-            l0 = __builtin_fmaf(qv[m], k0v[m], l0);
-            l1 = __builtin_fmaf(qv[m], k1v[m], l1);
+            for (int m = 0; m < DM; m++) {
+                kv0[m] = kv_load<F16>(kc, a0 * D + 8 * m + c);
+                kv1[m] = kv_load<F16>(kc, a1 * D + 8 * m + c);
+            }
         }
+    };
+    float kv0[DMR], kv1[DMR];
+    int64_t a0, a1;
+    if (same) {
+        load_keys((int64_t)hk * C + r[i0].k0, nmax, kv0, kv1, a0, a1);
+#pragma unroll
+        for (int i = 0; i < QT; i++)
+            if ((int64_t)tile * 64 < r[i].n) query_scores(i, kv0, kv1, a0, a1);
     } else {
-        for (int m = 0; m < D / 8; m++) {
-            const float qm = qr[8 * m + c];
-            l0 = __builtin_fmaf(qm, kv_load<F16>(kc, a0 * D + 8 * m + c), l0);
-            l1 = __builtin_fmaf(qm, kv_load<F16>(kc, a1 * D + 8 * m + c), l1);
+        for (int i = 0; i < QT; i++) {
+            if ((int64_t)tile * 64 >= r[i].n) continue;
+            load_keys((int64_t)hk * C + r[i].k0, r[i].n, kv0, kv1, a0, a1);
+            query_scores(i, kv0, kv1, a0, a1);
         }
     }
-    const float p0 = att_reduce8(l0, j0 < n4, gbase, c);
-    const float p1 = att_reduce8(l1, j1 < n4, gbase, c);
-    if (c == 0) {
-        if (j0 < r.n) out[j0] = p0 * scale;
-        if (j1 < r.n) out[j1] = p1 * scale;
+}
+
+// Many queries (prefill): a workgroup per (64 dims, head, four queries),
+// wave w for query 4z + w, lane for one dim. The waves share each staged
+// chunk of values when their queries share the first visible cache entry;
+// otherwise the chunks are staged per query. Per query the steps are those
+// of att_wsum_kernel (max, Cephes exp with eight stride-8 lane sums and the
+// f64 tail, then acc = fma(e_j, v_j[d], acc) in key order).
+// keys per staged chunk of values: 16 KB of LDS
+template <bool F16>
+constexpr int attq_vc() {
+    return F16 ? 128 : 64;
+}
+
+template <bool F16>
+__global__ __launch_bounds__(256) void att_wsum_q4_kernel(const void* vc, const int64_t* __restrict__ kend,
+                                                          const int64_t* __restrict__ kstart, int T, int H, int Hkv,
+                                                          int D, int64_t C, int64_t maxk,
+                                                          const float* __restrict__ ws, float* __restrict__ out) {
+    extern __shared__ float att_lds[];
+    __shared__ int64_t k0s[4], ns[4];
+    using VT = typename std::conditional<F16, _Float16, float>::type;
+    const int64_t mkp = (maxk + 3) & ~(int64_t)3;
+    const int d0 = blockIdx.x * 64, h = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const int t = 4 * blockIdx.z + w;
+    float* sw = att_lds + w * mkp;
+    VT* vb = (VT*)(att_lds + 4 * mkp);
+    const AttRange r = t < T ? att_range(kend, kstart, t, C, maxk) : AttRange{0, 0};
+    const int64_t n = r.n;
+    if (lane == 0) {
+        k0s[w] = r.k0;
+        ns[w] = n;
     }
+    // this wave's scores, max and NaN check
+    const float* srow = ws + ((int64_t)(t < T ? t : 0) * H + h) * maxk;
+    float mx = -INFINITY;
+    int bad = 0;
+    for (int64_t j = lane; j < n; j += 64) {
+        const float v = srow[j];
+        sw[j] = v;
+        bad |= v != v;
+        mx = fmaxf(mx, v);
+    }
+    mx = wave_max_f32(mx);
+    bad = __any(bad) || __builtin_isinf(mx);
+    const int64_t nv = n >= 8 ? (n & ~(int64_t)7) : 0;
+    if (!bad)
+        for (int64_t j = lane; j < n; j += 64) {
+            const float x = sw[j] - mx;
+            sw[j] = j < nv ? cephes_exp(x) : (float)exp((double)x);
+        }
+    __syncthreads();
+    float s = 0.f;
+    if (lane < 8)
+        for (int64_t j = lane; j < nv; j += 8) s = s + sw[j];
+    float sum = ((__shfl(s, 0) + __shfl(s, 4)) + (__shfl(s, 1) + __shfl(s, 5))) +
+                ((__shfl(s, 2) + __shfl(s, 6)) + (__shfl(s, 3) + __shfl(s, 7)));
+    for (int64_t j = nv; j < n; j++) sum = sum + sw[j];
+    int64_t nmax = 0;
+    int first = -1;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        nmax = ns[i] > nmax ? ns[i] : nmax;
+        if (first < 0 && ns[i] > 0) first = i;
+    }
+    bool same = true;
+#pragma unroll
+    for (int i = 0; i < 4; i++) same = same && (ns[i] == 0 || k0s[i] == k0s[first < 0 ? 0 : first]);
+    constexpr int VC = attq_vc<F16>();
+    const int hk = h / (H / Hkv);
+    float acc = 0.f;
+    constexpr int PER_ROW = F16 ? 8 : 16;  // 16-byte pieces per row of 64 dims
+    for (int pass = 0; pass < (same ? 1 : 4); pass++) {
+        const int src = same ? (first < 0 ? 0 : first) : pass;
+        const int64_t pn = same ? nmax : ns[pass];
+        const int64_t vbase = ((int64_t)hk * C + k0s[src]) * D + d0;
+        const bool mine = same || pass == w;
+        for (int64_t c0 = 0; c0 < pn; c0 += VC) {
+            const int64_t rows = pn - c0 < VC ? pn - c0 : VC;
+            __syncthreads();  // the previous chunk has been used
+            for (int64_t i = tid; i < rows * PER_ROW; i += 256) {
+                const int64_t row = i / PER_ROW, piece = i % PER_ROW;
+                const uint4 raw = *(const uint4*)((const VT*)vc + vbase + (c0 + row) * D + piece * (16 / sizeof(VT)));
+                *(uint4*)(vb + row * 64 + piece * (16 / sizeof(VT))) = raw;
+            }
+            __syncthreads();
+            if (mine && !bad && c0 < n) {
+                const int64_t e1 = n - c0 < rows ? n - c0 : rows;
+                const float* e = sw + c0;
+                int64_t j = 0;
+                for (; j + 4 <= e1; j += 4) {
+                    const float4 ev = *(const float4*)(e + j);
+                    const float v0 = (float)vb[(j + 0) * 64 + lane], v1 = (float)vb[(j + 1) * 64 + lane];
+                    const float v2 = (float)vb[(j + 2) * 64 + lane], v3 = (float)vb[(j + 3) * 64 + lane];
+                    acc = __builtin_fmaf(ev.x, v0, acc);
+                    acc = __builtin_fmaf(ev.y, v1, acc);
+                    acc = __builtin_fmaf(ev.z, v2, acc);
+                    acc = __builtin_fmaf(ev.w, v3, acc);
+                }
+                for (; j < e1; j++) acc = __builtin_fmaf(e[j], (float)vb[j * 64 + lane], acc);
+            }
+        }
+    }
+    if (t < T) out[((int64_t)t * H + h) * D + d0 + lane] = n <= 0 ? 0.f : (bad ? __builtin_nanf("") : acc / sum);
 }
 
 // LDS of att_wsum: the scores (maxk floats, padded to 4) and a chunk of
@@ -664,15 +804,18 @@ hipError_t launch_kv_store(const float* k, const float* v, const int64_t* pos, i
     return hipGetLastError();
 }
 
-template <bool F16>
+template <bool F16, int QT>
 static void launch_att_scores(dim3 grid, const float* q, const void* kc, const int64_t* kend, const int64_t* kstart,
-                              int H, int Hkv, int D, int64_t C, int64_t maxk, float* ws, hipStream_t s) {
+                              int T, int H, int Hkv, int D, int64_t C, int64_t maxk, float* ws, hipStream_t s) {
     if (D == 64)
-        hipLaunchKernelGGL((att_scores_kernel<F16, 8>), grid, dim3(256), 0, s, q, kc, kend, kstart, H, Hkv, D, C, maxk, ws);
+        hipLaunchKernelGGL((att_scores_kernel<F16, 8, QT>), grid, dim3(256), 0, s, q, kc, kend, kstart, T, H, Hkv, D, C,
+                           maxk, ws);
     else if (D == 128)
-        hipLaunchKernelGGL((att_scores_kernel<F16, 16>), grid, dim3(256), 0, s, q, kc, kend, kstart, H, Hkv, D, C, maxk, ws);
+        hipLaunchKernelGGL((att_scores_kernel<F16, 16, QT>), grid, dim3(256), 0, s, q, kc, kend, kstart, T, H, Hkv, D, C,
+                           maxk, ws);
     else
-        hipLaunchKernelGGL((att_scores_kernel<F16, 0>), grid, dim3(256), 0, s, q, kc, kend, kstart, H, Hkv, D, C, maxk, ws);
+        hipLaunchKernelGGL((att_scores_kernel<F16, 0, QT>), grid, dim3(256), 0, s, q, kc, kend, kstart, T, H, Hkv, D, C,
+                           maxk, ws);
 }
 
 template <int DS, bool F16>
@@ -697,9 +840,26 @@ hipError_t launch_attention(const float* q, const void* kc, const void* vc, cons
                             int T, int H, int Hkv, int D, int64_t C, int64_t maxk, int f16, float* out, float* ws,
                             hipStream_t s) {
     if (D > 512 || D % 8 || H % Hkv || maxk < 1 || maxk > ATT_MAXC || T < 1) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)((maxk + 63) / 64), (unsigned)H, (unsigned)T);
-    if (f16) launch_att_scores<true>(grid, q, kc, kend, kstart, H, Hkv, D, C, maxk, ws, s);
-    else launch_att_scores<false>(grid, q, kc, kend, kstart, H, Hkv, D, C, maxk, ws, s);
+    // many queries: four per workgroup, sharing the key and value loads
+    const bool many = T >= 16 && D % 64 == 0 && maxk <= 2048;
+    const unsigned tiles = (unsigned)((maxk + 63) / 64);
+    if (many) {
+        const dim3 grid(tiles, (unsigned)H, (unsigned)((T + 3) / 4));
+        if (f16) launch_att_scores<true, 4>(grid, q, kc, kend, kstart, T, H, Hkv, D, C, maxk, ws, s);
+        else launch_att_scores<false, 4>(grid, q, kc, kend, kstart, T, H, Hkv, D, C, maxk, ws, s);
+        const size_t lds = (size_t)(4 * ((maxk + 3) & ~(int64_t)3) * 4 + (f16 ? attq_vc<true>() * 64 * 2 : attq_vc<false>() * 64 * 4));
+        const dim3 g2((unsigned)(D / 64), (unsigned)H, (unsigned)((T + 3) / 4));
+        if (f16)
+            hipLaunchKernelGGL(att_wsum_q4_kernel<true>, g2, dim3(256), lds, s, vc, kend, kstart, T, H, Hkv, D, C, maxk,
+                               ws, out);
+        else
+            hipLaunchKernelGGL(att_wsum_q4_kernel<false>, g2, dim3(256), lds, s, vc, kend, kstart, T, H, Hkv, D, C, maxk,
+                               ws, out);
+        return hipGetLastError();
+    }
+    const dim3 grid(tiles, (unsigned)H, (unsigned)T);
+    if (f16) launch_att_scores<true, 1>(grid, q, kc, kend, kstart, T, H, Hkv, D, C, maxk, ws, s);
+    else launch_att_scores<false, 1>(grid, q, kc, kend, kstart, T, H, Hkv, D, C, maxk, ws, s);
     if (D % 16 == 0) {
         if (f16) launch_att_wsum<16, true>(T, H, Hkv, D, C, maxk, vc, kend, kstart, ws, out, s);
         else launch_att_wsum<16, false>(T, H, Hkv, D, C, maxk, vc, kend, kstart, ws, out, s);

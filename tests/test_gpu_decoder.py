@@ -425,3 +425,34 @@ def test_matmul_quantized_group_equals_single(gpu, oracle, rt):
         want = oracle.linear_a8(x, wb, dt, n, k, bias=bias if i == 0 else None, block=256)
         got = ys[i].download(np.float32).reshape(rows, n)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), i
+
+
+@pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
+@pytest.mark.parametrize("T,slots,D", [(20, 1, 64), (37, 1, 128), (24, 3, 64), (18, 2, 128)])
+def test_attention_many_queries_bitexact(gpu, oracle, rt, f16, T, slots, D):
+    """Prompt-like batches (T >= 16 rows: four queries per workgroup): rows of
+    one sequence at consecutive positions (the causal prefill), and rows of
+    several slots interleaved, against the C restatement bit for bit."""
+    H, Hkv, C = 4, 2, 64
+    rng = np.random.default_rng(T + slots + D)
+    L = slots * C
+    cdt = np.float16 if f16 else np.float32
+    kc = (rng.standard_normal((Hkv, L, D)) * 2).astype(cdt)
+    vc = rng.standard_normal((Hkv, L, D)).astype(cdt)
+    q = rng.standard_normal((T, H, D)).astype(np.float32)
+    slot = np.arange(T) % slots if slots > 1 else np.zeros(T, np.int64)
+    pos = np.arange(T) // slots if slots > 1 else np.arange(T)
+    pos = pos.astype(np.int64) + 3
+    cidx = (slot * C + pos).astype(np.int64)
+    kstart = (slot * C).astype(np.int64)
+    dq, dk, dv, de, ds = dev(rt, q), dev(rt, kc), dev(rt, vc), dev(rt, cidx), dev(rt, kstart)
+    out = rt.DeviceBuffer(q.nbytes)
+    wsb = gpu.attention_workspace_bytes(T, H, C)
+    ws = rt.DeviceBuffer(wsb)
+    s = rt.Stream()
+    gpu.attention_dev(dq.ptr, dk.ptr, dv.ptr, de.ptr, ds.ptr if slots > 1 else None, T, H, Hkv, D, L, C, f16, out.ptr,
+                      ws.ptr, wsb, s.handle)
+    s.sync()
+    want = oracle.attention(q, kc, vc, cidx, kstart if slots > 1 else None)
+    got = out.download(np.float32).reshape(T, H, D)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), float(np.max(np.abs(got - want)))
