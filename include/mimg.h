@@ -86,7 +86,24 @@ int mimg_register_weight(const void *host, uint64_t len, uint32_t dtype, int64_t
 int mimg_register_weight_device(const void *dev, uint64_t len, uint32_t dtype, int64_t n, int64_t k,
                                 uint64_t *handle);
 
-/* Drops one reference of a registration; the last frees the device buffer. */
+/* The container's weights section uploaded whole (reference File.Weights(),
+ * file.go:401-404; spec/container.md sections 6.3 and 7: one contiguous,
+ * aligned byte range): len bytes from host into one device buffer in one
+ * transfer, followed by 256 zero bytes; *dev receives its address. Tensors
+ * keep their offsets in it, so each weight is a view (below). */
+int mimg_upload_weights(const void *host, uint64_t len, void **dev);
+
+/* Frees an uploaded weights section; fails while views of it are registered. */
+int mimg_free_weights(void *dev);
+
+/* A weight matrix inside an uploaded weights section, at device address dev
+ * (section base + the tensor's offset): as mimg_register_weight, without a
+ * copy. Its handle is released with mimg_release_weight. */
+int mimg_register_weight_view(const void *dev, uint64_t len, uint32_t dtype, int64_t n, int64_t k,
+                              uint64_t *handle);
+
+/* Drops one reference of a registration; the last frees the device buffer
+ * (a view's flags only). */
 int mimg_release_weight(uint64_t handle);
 
 /* Device address of a weight's bytes and the number of its rows that the

@@ -47,11 +47,17 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 #ifndef MIMG_GEMM_THREADS
 #define MIMG_GEMM_THREADS 512
 #endif
+#ifndef MIMG_GEMM_NW
+#define MIMG_GEMM_NW 4
+#endif
 constexpr int GM_T = MIMG_GEMM_THREADS;   // threads per workgroup (256: one wave per SIMD, 512: two)
-constexpr int GM_BN = 64;                 // weight rows per workgroup (4 waves of 16)
+constexpr int GM_NW = MIMG_GEMM_NW;       // waves along the weight rows (16 rows each)
+constexpr int GM_BN = 16 * GM_NW;         // weight rows per workgroup
 constexpr int GM_BM = MIMG_GEMM_BM;       // activation rows per workgroup
-constexpr int GM_WM = GM_T / 256;         // waves along the activation rows
+constexpr int GM_WM = GM_T / 64 / GM_NW;  // waves along the activation rows
 constexpr int GM_TM = GM_BM / 16 / GM_WM; // activation tiles of 16 per wave
+static_assert(GM_WM * GM_NW * 64 == GM_T && GM_TM * GM_WM * 16 == GM_BM && GM_T >= GM_BN && GM_T >= GM_BM,
+              "GEMM tile shape");
 constexpr int GM_ACH = GM_BM * 16 / GM_T; // activation copy instructions per thread per block
 
 template <uint32_t DT>
@@ -179,7 +185,7 @@ __global__ __launch_bounds__(GM_T) void gemm_a8k_kernel(GemmArgs A) {
     __shared__ __align__(16) uint8_t smem[2 * L::BUF];
     __shared__ int flags[2];
     const int t = threadIdx.x, l = t & 63;
-    const int wn = (t >> 6) & 3, wm = t >> 8;  // this wave's weight rows 16wn.., activation tiles wm*GM_TM..
+    const int wn = (t >> 6) % GM_NW, wm = (t >> 6) / GM_NW;  // this wave's weight rows 16wn.., activation tiles wm*GM_TM..
     const int ar = l & 15, G = l >> 4;
     const int n0 = blockIdx.x * GM_BN, m0 = blockIdx.y * GM_BM;
     const int nb = A.nb;

@@ -51,7 +51,15 @@ struct Weight {
     std::tuple<uintptr_t, uint64_t, uint32_t, int64_t, int64_t> key;
     uint64_t fp = 0;    // sampled fingerprint of the host bytes (has_key)
     int64_t refs = 1;   // registrations not yet released
+    uint8_t* view_of = nullptr;  // a view into this uploaded weights section (data not owned)
 };
+
+// Weights sections uploaded whole (mimg_upload_weights): device base -> (length, live views).
+struct Upload {
+    uint64_t len;
+    int64_t views;
+};
+std::map<uintptr_t, Upload> g_uploads;
 
 std::mutex g_mu;
 int g_device = -1;
@@ -408,9 +416,90 @@ int mimg_release_weight(uint64_t handle) {
     if (w->has_key) g_keys.erase(w->key);
     g_weights.erase(it);
     HIP_TRY(hipDeviceSynchronize());
-    (void)hipFree(w->data);
+    if (w->view_of) g_uploads[(uintptr_t)w->view_of].views--;
+    else (void)hipFree(w->data);
     (void)hipFree(w->wref);
     delete w;
+    return MIMG_OK;
+}
+
+int mimg_upload_weights(const void* host, uint64_t len, void** dev) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!host || !dev || len == 0) return fail(MIMG_ERR_ARG, "null pointer or empty section");
+    uint8_t* d = nullptr;
+    hipError_t e = hipMalloc((void**)&d, len + WEIGHT_PAD);
+    if (e == hipSuccess) e = hipMemset(d + len, 0, WEIGHT_PAD);
+    if (e == hipSuccess) e = hipMemcpy(d, host, len, hipMemcpyHostToDevice);  // one transfer
+    if (e != hipSuccess) {
+        if (d) (void)hipFree(d);
+        return fail(MIMG_ERR_HIP, "weights upload (%llu bytes): %s", (unsigned long long)len, hipGetErrorString(e));
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_uploads[(uintptr_t)d] = Upload{len, 0};
+    *dev = d;
+    return MIMG_OK;
+}
+
+int mimg_free_weights(void* dev) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = g_uploads.find((uintptr_t)dev);
+    if (it == g_uploads.end()) return fail(MIMG_ERR_ARG, "not an uploaded weights section");
+    if (it->second.views > 0)
+        return fail(MIMG_ERR_ARG, "%lld weight views of this section are still registered", (long long)it->second.views);
+    g_uploads.erase(it);
+    HIP_TRY(hipDeviceSynchronize());
+    (void)hipFree(dev);
+    return MIMG_OK;
+}
+
+int mimg_register_weight_view(const void* dev, uint64_t len, uint32_t dtype, int64_t n, int64_t k, uint64_t* handle) {
+    if (!handle || !dev) return fail(MIMG_ERR_ARG, "null pointer");
+    int rc = check_shape(dtype, len, n, k);
+    if (rc) return rc;
+    if ((rc = ensure_device())) return rc;
+    uint8_t* base = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_uploads.upper_bound((uintptr_t)dev);
+        if (it != g_uploads.begin()) {
+            --it;
+            const uintptr_t b = it->first, p = (uintptr_t)dev;
+            if (p >= b && p - b <= it->second.len && len <= it->second.len - (p - b)) base = (uint8_t*)b;
+        }
+        if (!base) return fail(MIMG_ERR_ARG, "the view is not inside an uploaded weights section");
+    }
+    Weight* w = new Weight();
+    hipError_t e = hipMalloc((void**)&w->wref, (size_t)n);
+    if (e == hipSuccess) e = launch_weight_refusals(dtype, (const uint8_t*)dev, n, k, w->wref, nullptr);
+    std::vector<uint8_t> flags;
+    if (e == hipSuccess) {
+        flags.resize((size_t)n);
+        e = hipMemcpy(flags.data(), w->wref, (size_t)n, hipMemcpyDeviceToHost);
+    }
+    if (e != hipSuccess) {
+        if (w->wref) (void)hipFree(w->wref);
+        delete w;
+        return fail(MIMG_ERR_HIP, "weight view: %s", hipGetErrorString(e));
+    }
+    int64_t refused = 0;
+    for (uint8_t f : flags) refused += f;
+    w->data = (uint8_t*)dev;
+    w->view_of = base;
+    w->len = len;
+    w->dw.dt = dtype;
+    w->dw.n = n;
+    w->dw.k = k;
+    w->dw.row_bytes = k / block_elems(dtype) * block_bytes(dtype);
+    w->dw.data = w->data;
+    w->dw.wref = w->wref;
+    w->dw.n_refused = refused;
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_uploads[(uintptr_t)base].views++;
+    g_weights[g_next] = w;
+    *handle = g_next++;
     return MIMG_OK;
 }
 

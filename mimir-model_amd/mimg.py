@@ -50,6 +50,9 @@ SIGNATURES = {
     "mimg_dequantize_dev": (_I, [_U32, _P, _U64, _P, _I64, _P]),
     "mimg_quantize_dev": (_I, [_U32, _P, _I64, _P, _U64, _P]),
     "mimg_synthetic_normal_dev": (_I, [_U64, ctypes.c_float, _P, _I64, _P]),
+    "mimg_upload_weights": (_I, [_P, _U64, ctypes.POINTER(_P)]),
+    "mimg_free_weights": (_I, [_P]),
+    "mimg_register_weight_view": (_I, [_P, _U64, _U32, _I64, _I64, ctypes.POINTER(_U64)]),
     "mimg_matmul_a8_quantized_group_dev": (_I, [ctypes.POINTER(_U64), _I, _P, _I64, ctypes.POINTER(_P), _I,
                                                 ctypes.POINTER(_P), _P, _U64, _P]),
     "mimg_rms_norm_quant_dev": (_I, [_P, _P, _P, ctypes.c_float, _I64, _I64, _P, _I, _P, _U64, _P]),
@@ -120,11 +123,16 @@ def _p(a):
 class Weight:
     """A weight matrix uploaded once, byte for byte, in its block layout."""
 
-    def __init__(self, data, dt, n, k, device=False):
+    def __init__(self, data, dt, n, k, device=False, view=False):
         init()
         self.dt, self.n, self.k = dt, n, k
         h = _U64()
-        if device:
+        if view:
+            # data: (device address inside an uploaded weights section, nbytes)
+            ptr, nbytes = data
+            _check(load().mimg_register_weight_view(ctypes.c_void_p(ptr), nbytes, dt, n, k, ctypes.byref(h)))
+            self._host = None
+        elif device:
             # data: (device pointer, nbytes)
             ptr, nbytes = data
             _check(load().mimg_register_weight_device(ctypes.c_void_p(ptr), nbytes, dt, n, k, ctypes.byref(h)))
@@ -150,6 +158,27 @@ class Weight:
             self.release()
         except Exception:
             pass
+
+
+class WeightsSection:
+    """A container's weights section uploaded whole (mimg_upload_weights)."""
+
+    def __init__(self, host):
+        init()
+        host = np.ascontiguousarray(np.frombuffer(host, np.uint8) if not isinstance(host, np.ndarray) else host)
+        p = _P()
+        _check(load().mimg_upload_weights(_p(host), host.size, ctypes.byref(p)))
+        self.ptr, self.nbytes = p.value, host.size
+
+    def view(self, offset, nbytes, dt, n, k):
+        if offset < 0 or offset + nbytes > self.nbytes:
+            raise ValueError(f"view [{offset}, +{nbytes}) outside the section of {self.nbytes} bytes")
+        return Weight((self.ptr + offset, nbytes), dt, n, k, view=True)
+
+    def free(self):
+        if self.ptr:
+            _check(load().mimg_free_weights(_P(self.ptr)))
+            self.ptr = 0
 
 
 def dequant_matmul_a8(w, x, bias=None, block=256):

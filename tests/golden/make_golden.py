@@ -20,6 +20,11 @@ Fixtures (data only: inputs and expected outputs):
                            metadata and the reference's expected outputs
                            (testdata/*/expected.json: prompt ids, greedy ids,
                            float64-oracle logits, llama.cpp's deviation).
+  tiny-llama.mim, tiny-llama.expected.json
+                           the reference's compatibility fixture
+                           (testdata/compat/0.2-0.1/): a container written by
+                           its importer and the Go executor's logits for two
+                           runs, copied byte for byte.
 
 Usage: python tests/golden/make_golden.py [/root/reference]
 """
@@ -159,6 +164,12 @@ def main(ref):
     print("wrote", len(names), "tensors:", ", ".join(names))
     for fx in ("llama", "qwen2"):
         write_model(ref, fx)
+    for name in ("tiny-llama.mim", "tiny-llama.expected.json"):
+        with open(os.path.join(ref, "testdata/compat/0.2-0.1", name), "rb") as f:
+            data = f.read()
+        with open(os.path.join(HERE, name), "wb") as f:
+            f.write(data)
+        print("copied", name, len(data), "bytes")
 
 
 if __name__ == "__main__":

@@ -456,3 +456,41 @@ def test_attention_many_queries_bitexact(gpu, oracle, rt, f16, T, slots, D):
     want = oracle.attention(q, kc, vc, cidx, kstart if slots > 1 else None)
     got = out.download(np.float32).reshape(T, H, D)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), float(np.max(np.abs(got - want)))
+
+
+def test_container_upload_runs_match_the_go_executor(gpu):
+    """8(f)(3)/(4): the reference's importer output (a .mim container with
+    its weights, metadata and graph) opened, its weights section uploaded in
+    one transfer with every matrix a view at its offset, and the two runs of
+    its compatibility fixture (a 7-token prompt, then one decode step at
+    position 7) decoded on the GPU: every logit within 2e-5 of the largest
+    of the Go executor's (the fixture's own tolerance)."""
+    import binascii
+    import json
+    import os
+
+    import container
+    import decoder
+    from conftest import GOLDEN
+
+    exp = json.load(open(os.path.join(GOLDEN, "tiny-llama.expected.json")))
+    f = container.MimFile(os.path.join(GOLDEN, "tiny-llama.mim"))
+    sec, tensors = f.upload()
+    dec = decoder.Decoder(f.llama_config(), tensors, a8=False, max_rows=16)
+
+    def arr(d, dt):
+        return np.frombuffer(binascii.unhexlify(d["data"]), dt)
+
+    for run in exp["runs"]:
+        toks = arr(run["inputs"]["tokens"], np.int32)
+        pos = arr(run["inputs"]["positions"], np.int64)
+        want = arr(run["outputs"]["logits"], np.float32)
+        got = dec.forward(toks, pos).ravel()
+        ok, worst, allowed = fm.near(got, want, float(run["outputs"]["logits"]["tol"]))
+        assert ok, f"{worst} > {allowed}"
+    del dec
+    for t in list(tensors.values()):
+        if isinstance(t[2], gpu.Weight):
+            t[2].release()
+    sec.free()
+    f.close()
