@@ -81,10 +81,10 @@ class MimFile:
     def close(self):
         try:
             self.buf.release()
-        except Exception:
-            pass
-        if isinstance(self._m, mmap.mmap):
-            self._m.close()
+            if isinstance(self._m, mmap.mmap):
+                self._m.close()
+        except BufferError:
+            pass  # arrays still view the mapping; it closes when they go
         self._f.close()
 
     # ---- parsing, in the order of spec/container.md section 9 -------------
@@ -302,17 +302,14 @@ class MimFile:
             out[key] = v
         return out
 
-    def llama_config(self):
-        """The decoder shape from the metadata an import writes
-        (reference importer/llama.go LlamaConfigOf)."""
-        m = self.metadata()
-        arch = m.get("general.architecture", "llama")
-        g = lambda k, d=None: m.get(f"{arch}.{k}", d)
-        return dict(arch=arch, layers=g("block_count"), embed=g("embedding_length"), ffn=g("feed_forward_length"),
-                    heads=g("attention.head_count"), kv_heads=g("attention.head_count_kv"),
-                    rope_dims=g("rope.dimension_count"), rope_theta=g("rope.freq_base", 10000.0),
-                    norm_eps=g("attention.layer_norm_rms_epsilon", 1e-5),
-                    context=m.get("mim.context_length", g("context_length")))
+    def llama_config(self, context=0):
+        """The decoder shape from the metadata an import writes (reference
+        importer/llama.go LlamaConfigOf); the cache length is the file's
+        `mim.context_length` unless given."""
+        import decoder
+
+        md = self.metadata()
+        return decoder.config_from_metadata(md, context or md.get("mim.context_length", 0))
 
     def upload(self):
         """The weights section to the device in one transfer, and every

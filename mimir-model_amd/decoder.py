@@ -43,6 +43,54 @@ class Config:
             raise ValueError(f"inconsistent shape: embed {embed}, heads {heads}, kv heads {kv_heads}, rope {rope_dims}")
 
 
+MAX_CONTEXT = 1 << 20
+
+
+def config_from_metadata(md, context=0):
+    """The decoder shape of a llama or qwen2 model from its metadata, as the
+    reference's importer reads it (importer/llama.go LlamaConfigOf): the
+    required keys must be positive and at most 2^24, head counts must
+    divide, rope scaling is not supported, the context is the model's own
+    unless given."""
+    arch = md.get("general.architecture")
+    if arch not in ("llama", "qwen2"):
+        raise ValueError(f'architecture {arch!r}: only "llama" and "qwen2" graphs can be built')
+
+    def req(key):
+        v = md.get(f"{arch}.{key}")
+        if isinstance(v, bool) or not isinstance(v, int) or v <= 0 or v > 1 << 24:
+            raise ValueError(f"metadata {arch}.{key} is missing or invalid")
+        return v
+
+    c = dict(arch=arch, layers=req("block_count"), embed=req("embedding_length"), ffn=req("feed_forward_length"),
+             heads=req("attention.head_count"))
+    max_ctx = req("context_length")
+    c["kv_heads"] = req("attention.head_count_kv") if f"{arch}.attention.head_count_kv" in md else c["heads"]
+    if c["embed"] % c["heads"] or c["heads"] % c["kv_heads"]:
+        raise ValueError(f"embedding length {c['embed']}, {c['heads']} heads and {c['kv_heads']} key-value heads "
+                         "do not divide")
+    head_dim = c["embed"] // c["heads"]
+    c["rope_dims"] = head_dim
+    if f"{arch}.rope.dimension_count" in md:
+        c["rope_dims"] = req("rope.dimension_count")
+        if c["rope_dims"] % 2 or c["rope_dims"] > head_dim:
+            raise ValueError(f"rope dimension count {c['rope_dims']} for head size {head_dim}")
+    c["rope_theta"] = float(md.get(f"{arch}.rope.freq_base", 10000.0))
+    t = md.get(f"{arch}.rope.scaling.type")
+    if isinstance(t, str) and t != "none":
+        raise ValueError(f"rope scaling {t!r} is not supported yet")
+    eps = md.get(f"{arch}.attention.layer_norm_rms_epsilon")
+    if not isinstance(eps, float) or eps <= 0:
+        raise ValueError(f"metadata {arch}.attention.layer_norm_rms_epsilon is missing or invalid")
+    # the importer stores f32 metadata widened to f64; the graph's rms_norm
+    # attribute keeps it, and rms_norm.v1 rounds it to f32
+    c["norm_eps"] = eps
+    c["context"] = context if context > 0 else max_ctx
+    if c["context"] > MAX_CONTEXT:
+        raise ValueError(f"context length {c['context']} exceeds {MAX_CONTEXT}")
+    return c
+
+
 def inv_freq(cfg):
     """theta^(-2i/r) in f64, i < r/2 (reference interp/fast.go:507-557)."""
     r = cfg.rope_dims
@@ -56,12 +104,18 @@ class Decoder:
     block bytes (np.uint8) of a quantized matrix, an np.float32 array for a
     norm scale or bias, or an already registered mimg.Weight. procs is the
     GOMAXPROCS of the reference run to reproduce (its swiglu results depend
-    on it).
+    on it). kquant_block is the activation block of the Q4_K/Q6_K products
+    with 8-bit activations (256: dequant_matmul_a8.v2, 32: .v1).
     """
 
-    def __init__(self, config, tensors, a8=True, cache_f16=False, max_rows=64, slots=1, procs=16):
+    def __init__(self, config, tensors, a8=True, cache_f16=False, max_rows=64, slots=1, procs=16, kquant_block=256):
         c = self.c = config if isinstance(config, Config) else Config(**config)
         self.a8, self.f16, self.slots = bool(a8), bool(cache_f16), int(slots)
+        # activation blocks for Q4_K/Q6_K weights: 256 is dequant_matmul_a8.v2
+        # as the importer writes it (importer/llama.go:264-280), 32 is .v1
+        if kquant_block not in (32, 256):
+            raise ValueError(f"kquant_block {kquant_block}: 32 or 256")
+        self.kquant_block = kquant_block
         # the reference's GOMAXPROCS: swiglu's results follow its piece split
         self.procs = int(procs)
         self.R = int(max_rows)
@@ -109,7 +163,7 @@ class Decoder:
     # ---- the graph's ops ---------------------------------------------------
 
     def _block(self, w):
-        return 256 if w.dt in (mimg.Q4_K, mimg.Q6_K) else 32
+        return self.kquant_block if w.dt in (mimg.Q4_K, mimg.Q6_K) else 32
 
     def _linears(self, names, x, rows, ys, biases=None):
         """ys[i] = x . W_i^T (+ bias_i) for weights sharing the input x."""

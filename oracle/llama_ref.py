@@ -94,8 +94,9 @@ def swiglu(g, u, procs=16):
 class Decoder:
     """The forward pass with a key-value cache, on the CPU."""
 
-    def __init__(self, model, a8=True, cache_f16=False, threads=8, procs=16):
+    def __init__(self, model, a8=True, cache_f16=False, threads=8, procs=16, kquant_block=256):
         self.m, self.a8, self.f16, self.threads, self.procs = model, a8, cache_f16, threads, procs
+        self.kquant_block = kquant_block
         c = model.c
         C = c["context"]
         cdt = np.float16 if cache_f16 else np.float32
@@ -109,7 +110,7 @@ class Decoder:
             y = (x @ w.T).astype(np.float32)
             return y if bias is None else (y + bias).astype(np.float32)
         if self.a8:
-            block = 256 if dt in (Q4_K, Q6_K) else 32
+            block = self.kquant_block if dt in (Q4_K, Q6_K) else 32
             return mimref.linear_a8(x, w, dt, n, k, bias=bias, block=block, threads=self.threads)
         return mimref.linear_f32(x, w, dt, n, k, bias=bias, threads=self.threads)
 

@@ -20,6 +20,10 @@ Fixtures (data only: inputs and expected outputs):
                            metadata and the reference's expected outputs
                            (testdata/*/expected.json: prompt ids, greedy ids,
                            float64-oracle logits, llama.cpp's deviation).
+  {llama,qwen2}-tiny-q4km.gguf  the reference's GGUF fixtures
+                           (testdata/{llama,qwen2}/tiny-q4km.gguf, written by
+                           llama.cpp), copied byte for byte, for the
+                           product's own GGUF reader.
   tiny-llama.mim, tiny-llama.expected.json
                            the reference's compatibility fixture
                            (testdata/compat/0.2-0.1/): a container written by
@@ -164,6 +168,12 @@ def main(ref):
     print("wrote", len(names), "tensors:", ", ".join(names))
     for fx in ("llama", "qwen2"):
         write_model(ref, fx)
+    for fx in ("llama", "qwen2"):
+        with open(os.path.join(ref, f"testdata/{fx}/tiny-q4km.gguf"), "rb") as f:
+            data = f.read()
+        with open(os.path.join(HERE, f"{fx}-tiny-q4km.gguf"), "wb") as f:
+            f.write(data)
+        print("copied", fx, "gguf", len(data), "bytes")
     for name in ("tiny-llama.mim", "tiny-llama.expected.json"):
         with open(os.path.join(ref, "testdata/compat/0.2-0.1", name), "rb") as f:
             data = f.read()

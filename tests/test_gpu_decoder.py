@@ -494,3 +494,77 @@ def test_container_upload_runs_match_the_go_executor(gpu):
             t[2].release()
     sec.free()
     f.close()
+
+
+def _gguf_decoder(fx, **kw):
+    import os
+
+    import decoder
+    import gguf
+    from conftest import GOLDEN
+
+    g = gguf.GGUFFile(os.path.join(GOLDEN, f"{fx}-tiny-q4km.gguf"))
+    sec, tensors = g.upload()
+    dec = decoder.Decoder(decoder.config_from_metadata(g.metadata), tensors, max_rows=16, **kw)
+    return g, sec, tensors, dec
+
+
+def _release(g, sec, tensors, gpu):
+    for t in tensors.values():
+        if isinstance(t[2], gpu.Weight):
+            t[2].release()
+    sec.free()
+    g.close()
+
+
+@pytest.mark.parametrize("name", fm.FIXTURES)
+def test_gguf_model_end_to_end(gpu, name):
+    """8(f)(4): the reference's GGUF fixture read by the product's GGUF
+    reader, its tensor data uploaded in one transfer (views per matrix),
+    the configuration from its metadata (LlamaConfigOf), and the reference's
+    generate checks: f32 path within 2e-5 with the oracle's greedy ids; a8
+    (dequant_matmul_a8.v2, f16 cache) within llama.cpp's deviation x1.1."""
+    _, _, e = fm.load(name)
+    P = len(e["prompt_ids"])
+    for a8 in (False, True):
+        g, sec, tensors, dec = _gguf_decoder(name, a8=a8, cache_f16=a8)
+        steps = [dec.forward(e["prompt_ids"], np.arange(P))]
+        for i, tok in enumerate(e["greedy"][:-1]):
+            steps.append(dec.forward([tok], [P + i]))
+        worst = fm.max_diff(steps[0], fm.f32b64(e["prompt_logits"]))
+        for i, lg in enumerate(steps):
+            last = lg[-1]
+            want = fm.f32b64(e["greedy_logits"][i])
+            worst = max(worst, fm.max_diff(last, want))
+            if not a8:
+                ok, w, allowed = fm.near(last, want, 2e-5)
+                assert ok and int(np.argmax(last)) == e["greedy"][i], (i, w, allowed)
+        if a8:
+            assert worst <= 1.1 * e["llama_cpp_max_diff"], worst
+        del dec
+        _release(g, sec, tensors, gpu)
+
+
+@pytest.mark.parametrize("name", fm.FIXTURES)
+def test_block32_a8_graph_matches_the_restatement(gpu, name):
+    """8(f)(4): dequant_matmul_a8.v1 (activation blocks of 32) for the Q4_K
+    and Q6_K matrices of the fixture model, the lane order of
+    dotQ4KQ8AVX2/dotQ6KQ8AVX2: the GPU decoder's logits and greedy ids
+    equal the CPU restatement's with the same block."""
+    cfg, tensors_np, e = fm.load(name)
+    g, sec, tensors, dec = _gguf_decoder(name, a8=True, kquant_block=32)
+    ref = llama_ref.Decoder(llama_ref.Model(cfg, tensors_np), a8=True, kquant_block=32, threads=4)
+    P = len(e["prompt_ids"])
+    a = dec.forward(e["prompt_ids"], np.arange(P))
+    b = ref.forward(e["prompt_ids"], np.arange(P))
+    assert np.max(np.abs(a - b)) <= 1e-5 * np.max(np.abs(b))
+    ids_g, ids_r = [], []
+    lg_g, lg_r = a[-1], b[-1]
+    for i in range(8):
+        ids_g.append(int(np.argmax(lg_g)))
+        ids_r.append(llama_ref.argmax(lg_r))
+        lg_g = dec.forward([ids_g[-1]], [P + i])[0]
+        lg_r = ref.forward([ids_r[-1]], [P + i])[0]
+    assert ids_g == ids_r
+    del dec
+    _release(g, sec, tensors, gpu)
