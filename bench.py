@@ -147,7 +147,37 @@ def cpu_baseline(host_bytes, xs, seconds, log):
     }
 
 
-def decode_bench(name, log, graph=True):
+def decode_cpu_check(cfg, tensors, prompt, gpu_ids, n, log):
+    """The CPU restatement of the decoder (oracle/llama_ref.py, the linears
+    through the C oracle on this host's cores) on the same weight bytes and
+    prompt: its first n greedy ids, compared with the GPU's, and its decode
+    rate (tokens/s after the prompt)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import llama_ref
+    import synthetic
+
+    threads = min(16, os.cpu_count() or 1)
+    ref = llama_ref.Decoder(llama_ref.Model(cfg, synthetic.host_bytes(tensors)), a8=True, cache_f16=True,
+                            threads=threads)
+    P = len(prompt)
+    t0 = time.time()
+    lg = ref.forward(prompt, np.arange(P))[-1]
+    t_prompt = time.time() - t0
+    ids = []
+    t0 = time.time()
+    for i in range(n):
+        ids.append(llama_ref.argmax(lg))
+        if i + 1 < n:
+            lg = ref.forward([ids[-1]], [P + i])[0]
+    t_dec = time.time() - t0
+    match = ids == [int(v) for v in gpu_ids[:n]]
+    log(f"  cpu restatement: {n} ids {'==' if match else '!='} GPU; {(n - 1) / t_dec:.2f} tok/s decode, "
+        f"{P / t_prompt:.1f} tok/s prompt ({threads} threads)")
+    return {"ids_equal_gpu": match, "tokens_checked": n, "decode_tok_per_s": round((n - 1) / t_dec, 3),
+            "prompt_tok_per_s": round(P / t_prompt, 2), "cores": threads, "kind": "port"}
+
+
+def decode_bench(name, log, graph=True, cpu=False):
     """Greedy generation on the GPU decoder with a random model of the
     named shape (module docstring)."""
     import decoder
@@ -183,6 +213,8 @@ def decode_bench(name, log, graph=True):
             "first_ids": ids[0, :8].tolist(),
             "graphs": graph,
         }
+        if cpu and batch == 1 and name == "llama1b":
+            out[key]["cpu_restatement"] = decode_cpu_check(cfg, tensors, prompts[0], ids[0], 8, log)
         log(f"  {key}: {out[key]}")
     del dec
     tensors.clear()
@@ -411,7 +443,7 @@ def main():
     layers.clear()
     decode_res = {}
     for name in [d for d in args.decode.split(",") if d]:
-        decode_res.update(decode_bench(name, log, graph=not args.eager))
+        decode_res.update(decode_bench(name, log, graph=not args.eager, cpu=not args.no_cpu))
     if decode_res:
         result["decode"] = decode_res
     if not args.no_cpu:
