@@ -17,15 +17,17 @@
 // Mapping: a 256-thread workgroup owns R weight rows. Its 32 groups of 8
 // lanes take the R*nb (row, block) pairs, U pairs at a time with all their
 // weight loads issued before any compute, so that many 128-bit loads per
-// lane are in flight (the GEMV is bound by HBM latency x bandwidth). For a
-// pair, lane l of the group loads 16 bytes of the block's quants, forms its
-// part of S with v_dot4_i32_i8 against the activation quants (read through
-// L1, they are shared by all rows), and the group sums the parts with three
-// DPP steps (integer, so exact in any order). The exact (S, M) and the two
-// f32 scale products of every pair go to LDS; then one lane per (row,
-// activation row) runs the serial float chain over the blocks in order.
-// (A tiled kernel walking each row's blocks in order, and a persistent
-// software-pipelined variant, measured slower on MI355X at these shapes.)
+// lane are in flight (the GEMV is bound by HBM latency x bandwidth). The U
+// pairs of a group are U rows of one block, so the group reads that block's
+// activation quants once (through L1: they are shared by all rows), before
+// its weight loads. For a pair, lane l of the group loads 16 bytes of the
+// block's quants, forms its part of S with v_dot4_i32_i8, and the group sums
+// the parts with three DPP steps (integer, so exact in any order). The exact
+// (S, M) and the two f32 scale products of every pair go to LDS; then one
+// lane per (row, activation row) runs the serial float chain over the blocks
+// in order. (A tiled kernel walking each row's blocks in order, and a
+// persistent software-pipelined variant, measured slower on MI355X at these
+// shapes.)
 //
 // Rows of x the quantizer refused and rows of w with a non-finite block scale
 // take the float32 path (reference linearA8, interp/fast.go:323-377), in the
@@ -73,20 +75,79 @@ struct KQ {
     static constexpr int S16PB = DT == DT_Q4_K ? 8 : 16;  // s16 entries per block
 };
 
-// Activation staging: with one activation row and K <= STAGE_MAXK the
-// workgroup copies the row's quants, block sums and scales into LDS behind
-// the pair table before computing, so the compute phase reads no global
-// memory (global reads issued after the weight loads would wait for all of
-// them, the load counter being in order).
-constexpr int STAGE_MAXK = 16384;
+// Pairs per group and iteration (all their weight loads in flight at once).
+#ifndef MIMG_PAIRS_U
+#define MIMG_PAIRS_U 4
+#endif
 
-template <uint32_t DT, int M, int R, bool STAGE>
+// One group's share of the activation for one block: Q4_K ya/yh = the 16
+// quants of each of its two runs, xs the sum of its sub-block; Q6_K ya/yh
+// and the two runs' sums ysL/ysH. dx is the block's activation scale.
+struct ActLane {
+    u32x4 ya, yh;
+    int sa, sb;
+    float dx;
+};
+
+template <uint32_t DT>
+__device__ __forceinline__ ActLane act_lane(const int8_t* q, const int16_t* s16, const float* d32, int64_t K, int m,
+                                           int b, int l) {
+    const int64_t R32 = K / 32, R16 = K / 16;
+    const int8_t* yb = q + m * K + (uint32_t)(b * 256);
+    ActLane a;
+    if constexpr (DT == DT_Q4_K) {
+        const int yoff = 64 * (l >> 1) + 16 * (l & 1);
+        a.ya = *(const u32x4*)(yb + yoff);
+        a.yh = *(const u32x4*)(yb + yoff + 32);
+        a.sa = s16[m * R32 + 8 * b + l];
+        a.sb = 0;
+    } else {
+        const int eL = 128 * (l >> 2) + 32 * ((l & 3) >> 1) + 16 * (l & 1);
+        a.ya = *(const u32x4*)(yb + eL);
+        a.yh = *(const u32x4*)(yb + eL + 64);
+        const int16_t* ys = s16 + m * R16 + 16 * b;
+        a.sa = ys[eL >> 4];
+        a.sb = ys[(eL + 64) >> 4];
+    }
+    a.dx = d32[m * R32 + 8 * b];
+    return a;
+}
+
+// The exact (S, M) of one (row, block) pair for one activation row and the
+// two f32 scale products, as the pair table holds them.
+template <uint32_t DT>
+__device__ __forceinline__ i32x4 pair_part(const u32x4& hdr, const u32x4& qv, const Q6KRaw& raw, const ActLane& a,
+                                           int l) {
+    i32x4 v;
+    if constexpr (DT == DT_Q4_K) {
+        const Q4KLane w = q4k_lane(hdr, qv, l);
+        v.x = group8_sum(q4k_part(w, a.ya, a.yh));
+        v.y = group8_sum(w.mm * a.sa);
+        v.z = __float_as_int(w.d * a.dx);
+        v.w = __float_as_int(w.dmin * a.dx);
+    } else {
+        const Q6KLane w = q6k_lane(raw, l);
+        v.x = group8_sum(q6k_part(w, a.ya, a.yh, a.sa, a.sb));
+        v.y = 0;
+        v.z = __float_as_int(w.d * a.dx);
+        v.w = 0;
+    }
+    return v;
+}
+
+// Pairs are numbered block-major (p = b*R + r), and group g of an iteration
+// takes pairs p0 + U*g + [0, U): with U dividing R these are U rows of one
+// block, so the group's activation for the iteration is one block's. Its
+// loads (for one activation row) and the row flags are issued before the
+// weights: the load counter being in order, anything issued after the
+// weights would wait for all of them. Every load is unconditional (clamped
+// in bounds) in straight-line code, and every loaded pair is consumed.
+template <uint32_t DT, int M, int R>
 __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
-    i32x4* part = (i32x4*)smem;  // [R][nb][M]: S, M term, bits(d*dx), bits(dmin*dx)
-    constexpr int U = 4;
-    constexpr int S16PB = KQ<DT>::S16PB;
-    static_assert(!STAGE || M == 1, "staging holds one activation row");
+    constexpr int U = MIMG_PAIRS_U;
+    constexpr bool SHARED = R % U == 0;  // a group's U pairs share one block
+    constexpr bool PRE = M == 1;         // activation loaded before the weights
     // This workgroup's matrix of the launch.
     int mi = 0;
     if (A.nmat > 1 && (int)blockIdx.x >= A.mat[1].tile0) mi = 1;
@@ -100,144 +161,86 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
     A.y_stride = P.N;
     const int g = threadIdx.x >> 3, l = threadIdx.x & 7, t = threadIdx.x;
     const int nb = A.nb, row0 = ((int)blockIdx.x - P.tile0) * R, npairs = R * nb;
-    const int64_t K = A.K, R32 = K / 32, R16 = K / 16;
+    // The tile's R rows: a 4-byte-aligned base (Q6_K rows are 2-byte
+    // aligned) and 32-bit offsets from it.
+    const int64_t tbyte = (int64_t)row0 * A.rb;
+    const uint8_t* Wt = A.W + (tbyte & ~(int64_t)3);
+    const uint32_t tadj = (uint32_t)(tbyte & 3), rb32 = (uint32_t)A.rb;
+    const int rlast = min(R, A.N - row0) - 1;        // last row of the tile in the matrix
+    i32x4* part = (i32x4*)smem;                                 // [R][nb][M]: S, M term, bits(d*dx), bits(dmin*dx)
+    int* refused = (int*)(smem + (size_t)R * nb * M * 16);      // [R*M]: the pair takes the float32 path
 
-    // Staged row: q [K] int8, s16 [nb*S16PB] int16, dx [nb] f32.
-    int8_t* sq = (int8_t*)(smem + (size_t)R * nb * M * 16);
-    int16_t* ss = (int16_t*)(sq + K);
-    float* sdx = (float*)(ss + nb * S16PB);
-    const int nq = (int)(K / 16), ns = nb * S16PB / 8;
-    if constexpr (STAGE) {
-        // Straight into LDS (global_load_lds: lane i of a wave writes
-        // bytes [16i, 16i+16) after the wave's base), no registers held.
-        const int wave = t >> 6;
+    // Lane t < R*M owns (weight row t/M, activation row t%M) at the end.
+    // Every lane loads the flags and bias of a clamped (row, activation row)
+    // first and looks at them last (a branch or a scalar load here would
+    // wait for them before the weights are requested).
+    int fm = min(t, R * M - 1) % M;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(fm) : "v"(fm));  // a vector index: ok[] through the vector cache
+    const int frow = min(row0 + min(t, R * M - 1) / M, A.N - 1);
+    const int wr = A.wref[frow], okm = A.ok[fm];
+    const float bias = A.bias ? A.bias[frow] : 0.f;
+    __builtin_amdgcn_sched_barrier(0);
+
+    for (int p0 = 0; p0 < npairs; p0 += 32 * U) {
+        ActLane pre[SHARED ? 1 : U];
+        if constexpr (PRE) {
 #pragma unroll
-        for (int j = 0; j < STAGE_MAXK / 16 / 256; j++)
-            if (t + 256 * j < nq)
-                __builtin_amdgcn_global_load_lds((const u32x4*)A.q + t + 256 * j,
-                                                 (__attribute__((address_space(3))) void*)(sq + 1024 * wave + 4096 * j),
-                                                 16, 0, 0);
-        if (t < ns)
-            __builtin_amdgcn_global_load_lds((const u32x4*)A.s16 + t,
-                                             (__attribute__((address_space(3))) void*)((uint8_t*)ss + 1024 * wave), 16, 0, 0);
-        if (t < nb)
-            __builtin_amdgcn_global_load_lds(A.d32 + 8 * t, (__attribute__((address_space(3))) void*)(sdx + 64 * wave),
-                                             4, 0, 0);
-    }
-
-    // With staging the loop's trip count is the same for every group (the
-    // staging barrier sits in its first iteration).
-    const int pstart = STAGE ? 0 : g, poff = STAGE ? g : 0;
-    for (int p0 = pstart; p0 < npairs; p0 += 32 * U) {
-        // The weights of this group's next U pairs, all in flight.
+            for (int u = 0; u < (SHARED ? 1 : U); u++) {
+                const int p = SHARED ? min(p0 + U * g, npairs - U) : min(p0 + U * g + u, npairs - 1);
+                pre[u] = act_lane<DT>(A.q, A.s16, A.d32, A.K, 0, p / R, l);
+            }
+        }
+        // Keep the issue order: activation, then all weights, then compute.
+        __builtin_amdgcn_sched_barrier(0);
         u32x4 hdr[U], qv[U];
         Q6KRaw raw[U];
-        // Unconditional (clamped) loads in straight-line code: a load in a
-        // conditional block makes the compiler wait for every earlier load
-        // before it (the blocks reuse registers), which would put the U
-        // pairs' HBM round trips in series.
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int p = min(p0 + poff + 32 * u, npairs - 1);
-            const int r = p / nb, b = p - r * nb;
-            const int row = min(row0 + r, A.N - 1);
-            const uint8_t* blk = A.W + (int64_t)row * A.rb + (int64_t)b * KQ<DT>::BYTES;
-            if constexpr (DT == DT_Q4_K) {
-                hdr[u] = *(const u32x4*)blk;
-                qv[u] = *(const u32x4*)(blk + 16 + 16 * l);
+            int b, r;
+            if constexpr (SHARED) {
+                const int pb = min(p0 + U * g, npairs - U);  // a multiple of U: rows r0..r0+U-1 of block b
+                b = pb / R;
+                r = min(pb - b * R + u, rlast);
             } else {
-                raw[u] = q6k_load(blk, l);
+                const int p = min(p0 + U * g + u, npairs - 1);
+                b = p / R;
+                r = min(p - b * R, rlast);
+            }
+            const uint32_t off = tadj + (uint32_t)r * rb32 + (uint32_t)b * KQ<DT>::BYTES;
+            if constexpr (DT == DT_Q4_K) {
+                hdr[u] = *(const u32x4*)(Wt + off);
+                qv[u] = *(const u32x4*)(Wt + (off + 16 * l + 16));
+            } else {
+                raw[u] = q6k_load_at(Wt, off, l);
             }
         }
-        if constexpr (STAGE) {
-            if (p0 == 0) {
-                // The staged row and this wave's first weights have landed.
-                __builtin_amdgcn_s_waitcnt(0);
-                __syncthreads();
-            }
-        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            // Every loaded pair is consumed (a clamped duplicate past the end
-            // is computed and not stored), so no load is left pending across
-            // the loop's back edge, which would again cost a full wait.
-            const int pu = p0 + poff + 32 * u;
+            const int pu = p0 + U * g + u;
             const bool store = pu < npairs;
             const int p = min(pu, npairs - 1);
-            const int r = p / nb, b = p - r * nb;
-            if constexpr (DT == DT_Q4_K) {
-                const Q4KLane w = q4k_lane(hdr[u], qv[u], l);
+            const int b = p / R, r = p - b * R;
 #pragma unroll
-                for (int m = 0; m < M; m++) {
-                    u32x4 ya, yh;
-                    int xs;
-                    float dx;
-                    if constexpr (STAGE) {
-                        const int8_t* yb = sq + 256 * b + w.yoff;
-                        ya = *(const u32x4*)yb;
-                        yh = *(const u32x4*)(yb + 32);
-                        xs = ss[8 * b + l];
-                        dx = sdx[b];
-                    } else {
-                        const int8_t* yb = A.q + m * K + (int64_t)b * 256 + w.yoff;
-                        ya = *(const u32x4*)yb;
-                        yh = *(const u32x4*)(yb + 32);
-                        xs = A.s16[m * R32 + 8 * b + l];
-                        dx = A.d32[m * R32 + 8 * b];
-                    }
-                    const int S = group8_sum(q4k_part(w, ya, yh));
-                    const int Mt = group8_sum(w.mm * xs);
-                    if (l == 0 && store) {
-                        i32x4 v;
-                        v.x = S;
-                        v.y = Mt;
-                        v.z = __float_as_int(w.d * dx);
-                        v.w = __float_as_int(w.dmin * dx);
-                        part[(r * nb + b) * M + m] = v;
-                    }
-                }
-            } else {
-                const Q6KLane w = q6k_lane(raw[u], l);
-#pragma unroll
-                for (int m = 0; m < M; m++) {
-                    u32x4 ya, yh;
-                    int ysL, ysH;
-                    float dx;
-                    if constexpr (STAGE) {
-                        const int8_t* yb = sq + 256 * b;
-                        ya = *(const u32x4*)(yb + w.eL);
-                        yh = *(const u32x4*)(yb + w.eL + 64);
-                        ysL = ss[16 * b + (w.eL >> 4)];
-                        ysH = ss[16 * b + ((w.eL + 64) >> 4)];
-                        dx = sdx[b];
-                    } else {
-                        const int8_t* yb = A.q + m * K + (int64_t)b * 256;
-                        ya = *(const u32x4*)(yb + w.eL);
-                        yh = *(const u32x4*)(yb + w.eL + 64);
-                        const int16_t* ys = A.s16 + m * R16 + 16 * b;
-                        ysL = ys[w.eL >> 4];
-                        ysH = ys[(w.eL + 64) >> 4];
-                        dx = A.d32[m * R32 + 8 * b];
-                    }
-                    const int S = group8_sum(q6k_part(w, ya, yh, ysL, ysH));
-                    if (l == 0 && store) {
-                        i32x4 v;
-                        v.x = S;
-                        v.y = 0;
-                        v.z = __float_as_int(w.d * dx);
-                        v.w = 0;
-                        part[(r * nb + b) * M + m] = v;
-                    }
-                }
+            for (int m = 0; m < M; m++) {
+                // Without PRE the activation is read here, after the weights
+                // (once per iteration and activation row when SHARED).
+                ActLane a;
+                if constexpr (PRE) a = pre[SHARED ? 0 : u];
+                else a = act_lane<DT>(A.q, A.s16, A.d32, A.K, m, b, l);
+                const i32x4 v = pair_part<DT>(hdr[u], qv[u], raw[u], a, l);
+                if (l == 0 && store) part[(r * nb + b) * M + m] = v;
             }
         }
     }
+    const int flag = (wr != 0) | (okm == 0);
+    if (t < R * M) refused[t] = flag;
     __syncthreads();
 
     // The serial float chain, one lane per (weight row, activation row).
     if (t < R * M) {
         const int r = t / M, m = t - r * M, row = row0 + r;
-        if (row < A.N && A.wref[row] == 0 && A.ok[m]) {
+        if (row < A.N && !flag) {
             float tot = 0.f, off = 0.f;
             for (int b = 0; b < nb; b++) {
                 const i32x4 v = part[(r * nb + b) * M + m];
@@ -245,15 +248,15 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
                 if (DT == DT_Q4_K) off = __builtin_fmaf((float)v.y, __int_as_float(v.w), off);
             }
             float res = DT == DT_Q4_K ? tot - off : tot;
-            if (A.bias) res += A.bias[row];
+            if (A.bias) res += bias;
             A.y[(int64_t)m * A.y_stride + row] = res;
         }
     }
     // The float32 path for refused pairs, one group of eight lanes per pair.
     for (int qq = g; qq < R * M; qq += 32) {
         const int r = qq / M, m = qq - r * M, row = row0 + r;
-        if (row < A.N && (A.wref[row] != 0 || !A.ok[m])) {
-            float res = f32dot_g8<DT>(A.W + (int64_t)row * A.rb, A.x + (int64_t)m * K, K, A.fused != 0);
+        if (row < A.N && refused[qq]) {
+            float res = f32dot_g8<DT>(A.W + (int64_t)row * A.rb, A.x + (int64_t)m * A.K, A.K, A.fused != 0);
             if (A.bias) res += A.bias[row];
             if (l == 0) A.y[(int64_t)m * A.y_stride + row] = res;
         }
@@ -267,16 +270,8 @@ static hipError_t launch_pairs_r(GemvArgs A, hipStream_t stream) {
         A.mat[i].tile0 = tiles;
         tiles += (A.mat[i].N + R - 1) / R;
     }
-    size_t lds = (size_t)R * A.nb * M * 16;
-    if constexpr (M == 1) {
-        if (A.K <= STAGE_MAXK) {
-            lds += (size_t)A.K + (size_t)A.nb * KQ<DT>::S16PB * 2 + (size_t)A.nb * 4;
-            hipLaunchKernelGGL((gemv_a8k_pairs_kernel<DT, M, R, true>), dim3((unsigned)tiles), dim3(256), lds,
-                               stream, A);
-            return hipGetLastError();
-        }
-    }
-    hipLaunchKernelGGL((gemv_a8k_pairs_kernel<DT, M, R, false>), dim3((unsigned)tiles), dim3(256), lds, stream, A);
+    const size_t lds = (size_t)R * A.nb * M * 16 + (size_t)R * M * 4;
+    hipLaunchKernelGGL((gemv_a8k_pairs_kernel<DT, M, R>), dim3((unsigned)tiles), dim3(256), lds, stream, A);
     return hipGetLastError();
 }
 

@@ -81,6 +81,24 @@ __device__ __forceinline__ Q6KRaw q6k_load(const uint8_t* blk, int l) {
     return r;
 }
 
+// The same seven loads from base + off, with base 4-byte aligned and off a
+// 32-bit offset (the compiler addresses them as an SGPR base plus one VGPR
+// offset each, with the constant parts as immediates).
+__device__ __forceinline__ Q6KRaw q6k_load_at(const uint8_t* base, uint32_t off, int l) {
+    const uint32_t h = (uint32_t)l >> 2, p = (uint32_t)l & 3, idx = 2 * (p >> 1) + (p & 1);
+    Q6KRaw r;
+    const uint32_t oa = (off + 64 * h + 16 * p) & ~3u, oc = (off + 128 + 32 * h + 16 * (p & 1)) & ~3u;
+    const u32x4a4 av = *(const u32x4a4*)(base + oa), cv = *(const u32x4a4*)(base + oc);
+    r.ql[0] = av.x, r.ql[1] = av.y, r.ql[2] = av.z, r.ql[3] = av.w, r.ql[4] = *(const uint32_t*)(base + oa + 16);
+    r.qh[0] = cv.x, r.qh[1] = cv.y, r.qh[2] = cv.z, r.qh[3] = cv.w, r.qh[4] = *(const uint32_t*)(base + oc + 16);
+    r.shift = off & 3;
+    const uint32_t os = off + 8 * h + idx;
+    r.scl = (int)*(const int8_t*)(base + os + 192);
+    r.sch = (int)*(const int8_t*)(base + os + 196);
+    r.dbits = *(const uint16_t*)(base + off + 208);
+    return r;
+}
+
 struct Q6KLane {
     uint32_t vl[4], vh[4];
     int scl, sch, eL;
