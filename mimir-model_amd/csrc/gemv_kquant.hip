@@ -215,21 +215,42 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
             }
         }
         __builtin_amdgcn_sched_barrier(0);
+        // Table slots of the group's pairs: (r*nb + b)*M + m.
+        int slot0 = 0, pb = 0;
+        if constexpr (SHARED) {
+            pb = p0 + U * g;
+            const int b = min(pb, npairs - U) / R;
+            slot0 = ((min(pb, npairs - U) - b * R) * nb + b) * M;
+        }
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int pu = p0 + U * g + u;
-            const bool store = pu < npairs;
-            const int p = min(pu, npairs - 1);
-            const int b = p / R, r = p - b * R;
+            bool store;
+            int slot;
+            if constexpr (SHARED) {
+                store = pb < npairs;  // all U pairs of the group, or none
+                slot = slot0 + u * nb * M;
+            } else {
+                const int pu = p0 + U * g + u;
+                store = pu < npairs;
+                const int p = min(pu, npairs - 1);
+                const int b = p / R, r = p - b * R;
+                slot = (r * nb + b) * M;
+            }
 #pragma unroll
             for (int m = 0; m < M; m++) {
                 // Without PRE the activation is read here, after the weights
                 // (once per iteration and activation row when SHARED).
                 ActLane a;
-                if constexpr (PRE) a = pre[SHARED ? 0 : u];
-                else a = act_lane<DT>(A.q, A.s16, A.d32, A.K, m, b, l);
+                if constexpr (PRE) {
+                    a = pre[SHARED ? 0 : u];
+                } else {
+                    // (Written per pair: read once for all U pairs, the M
+                    // rows' activations would all stay in registers.)
+                    const int p = min(p0 + U * g + u, npairs - 1);
+                    a = act_lane<DT>(A.q, A.s16, A.d32, A.K, m, p / R, l);
+                }
                 const i32x4 v = pair_part<DT>(hdr[u], qv[u], raw[u], a, l);
-                if (l == 0 && store) part[(r * nb + b) * M + m] = v;
+                if (l == 0 && store) part[slot + m] = v;
             }
         }
     }
@@ -278,6 +299,9 @@ static hipError_t launch_pairs_r(GemvArgs A, hipStream_t stream) {
 // Rows per workgroup: enough (row, block) pairs to keep 32 groups busy, as
 // many workgroups as possible, and the pair table within 48 KB of LDS.
 static int pairs_rows(int N, int nb, int M) {
+#ifdef MIMG_PAIRS_R
+    if ((size_t)MIMG_PAIRS_R * nb * M * 16 <= 48 * 1024) return MIMG_PAIRS_R;  // a tuning build
+#endif
     int R = 8;
     while (R > 1 && ((N + R - 1) / R < 1024 || (size_t)R * nb * M * 16 > 48 * 1024)) R >>= 1;
     return R;

@@ -47,7 +47,9 @@ __device__ __forceinline__ int q4k_part(const Q4KLane& w, const u32x4& ya, const
     dh = sdot4(w.hi[1], yh.y, dh);
     dh = sdot4(w.hi[2], yh.z, dh);
     dh = sdot4(w.hi[3], yh.w, dh);
-    return w.scl * dl + w.sch * dh;
+    // |dl|, |dh| <= 16*15*128 and the scales are 6-bit: 24-bit multiplies
+    // (full rate) are exact.
+    return __mul24(w.scl, dl) + __mul24(w.sch, dh);
 }
 
 // Raw loads of one lane's share of a Q6_K block (2-byte aligned blocks):
@@ -138,7 +140,9 @@ __device__ __forceinline__ int q6k_part(const Q6KLane& w, const u32x4& ya, const
     dh = sdot4(w.vh[1], yh.y, dh);
     dh = sdot4(w.vh[2], yh.z, dh);
     dh = sdot4(w.vh[3], yh.w, dh);
-    return w.scl * (dl - 32 * ysL) + w.sch * (dh - 32 * ysH);
+    // |dl - 32*ysL| <= 16*63*128 + 32*16*128 < 2^23 and the scales are int8:
+    // 24-bit multiplies (full rate) are exact.
+    return __mul24(w.scl, dl - 32 * ysL) + __mul24(w.sch, dh - 32 * ysH);
 }
 
 }  // namespace mimg

@@ -83,10 +83,12 @@ __device__ __forceinline__ int dpp_i(int v, int ctrl) {
 
 // Sum of an int32 over each aligned group of 8 lanes, left in all 8 lanes.
 // Integer addition is associative, so the result is exact in any order.
+// (Every lane of these permutes has a source, so bound_ctrl changes nothing;
+// with it set the compiler folds each move into the add, v_add_u32_dpp.)
 __device__ __forceinline__ int group8_sum(int v) {
-    v += __builtin_amdgcn_mov_dpp(v, DPP_QUAD_1032, 0xF, 0xF, false);
-    v += __builtin_amdgcn_mov_dpp(v, DPP_QUAD_2301, 0xF, 0xF, false);
-    v += __builtin_amdgcn_mov_dpp(v, DPP_HALF_MIRROR, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, DPP_QUAD_1032, 0xF, 0xF, true);
+    v += __builtin_amdgcn_update_dpp(0, v, DPP_QUAD_2301, 0xF, 0xF, true);
+    v += __builtin_amdgcn_update_dpp(0, v, DPP_HALF_MIRROR, 0xF, 0xF, true);
     return v;
 }
 
