@@ -48,6 +48,7 @@ import mimg  # noqa: E402
 METRIC = "Q4_K GEMV GB/s (% of HBM peak); decode tok/s at 8B Q4_K_M; prefill TFLOP/s"
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
 Q4_K, Q6_K = mimg.Q4_K, mimg.Q6_K
 
 # (name, N, K, dtype, weight seed, input index)
@@ -340,7 +341,11 @@ def main():
     # at M activation rows on the int8 MFMA GEMM, activations quantized
     # beforehand; a graph of --rotate launches over the rotation copies.
     # Ops = 2*M*N*K; the fraction is of MI355X's dense int8 peak.
-    def prefill(name, rows):
+    # With f32 (BASELINE.json north_star's f32-activation prefill,
+    # dequant_matmul.v1): the same products with float32 activations on the
+    # fp32 matrix cores (mimg_linear_f32_mfma_dev), fraction of the dense
+    # fp32 matrix peak.
+    def prefill(name, rows, f32=False):
         _, n, k, dt, _, _ = next(c for c in CFG1 if c[0] == name)
         xp = hiprt.DeviceBuffer.from_array(np.random.default_rng(200 + rows).standard_normal((rows, k), dtype=np.float32))
         wsb = mimg.a8_workspace_bytes(rows, k)
@@ -350,8 +355,11 @@ def main():
 
         def launches():
             for l in range(args.rotate):
-                mimg.matmul_a8_quantized_dev(layers[l][name], xp.ptr, rows, None, 256, yp.ptr, wsp.ptr, wsb,
-                                             stream.handle)
+                if f32:
+                    mimg.linear_f32_mfma_dev(layers[l][name], xp.ptr, rows, None, yp.ptr, stream.handle)
+                else:
+                    mimg.matmul_a8_quantized_dev(layers[l][name], xp.ptr, rows, None, 256, yp.ptr, wsp.ptr, wsb,
+                                                 stream.handle)
 
         g = hiprt.Graph(stream, launches)
         g.launch(stream)
@@ -364,14 +372,19 @@ def main():
         for buf in (xp, wsp, yp):
             buf.free()
         tops = 2.0 * rows * n * k / (us * 1e-6) / 1e12
+        if f32:
+            return {"us_per_launch": round(us, 2), "TFLOP_per_s": round(tops, 1),
+                    "frac_fp32_peak": round(tops / FP32_PEAK_TFLOPS, 4)}
         return {"us_per_launch": round(us, 2), "TOP_per_s": round(tops, 1),
                 "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
 
-    prefill_res = {}
+    prefill_res, prefill_f32 = {}, {}
     for rows in [int(r) for r in args.prefill_rows.split(",") if r]:
         for name in ("gate", "down"):
             prefill_res[f"{name}_M{rows}"] = prefill(name, rows)
             log(f"  prefill {name} M={rows}: {prefill_res[f'{name}_M{rows}']}")
+            prefill_f32[f"{name}_M{rows}"] = prefill(name, rows, f32=True)
+            log(f"  prefill f32 {name} M={rows}: {prefill_f32[f'{name}_M{rows}']}")
 
     # The host-memory entry point a cgo caller uses (x copied in, y copied
     # back, the call returns when y is in host memory): PCIe- and
@@ -432,6 +445,11 @@ def main():
             "workload": "cfg2: gate 14336x4096 Q4_K and down 4096x14336 Q6_K, dequant_matmul_a8.v2 block=256, "
                         "int8 MFMA GEMM (bit-identical to the GEMV), activations quantized beforehand",
             "results": prefill_res,
+        },
+        "prefill_f32": {
+            "workload": "the same gate/down products with float32 activations (dequant_matmul.v1) on the fp32 "
+                        "matrix cores, within the spec bound (K+1)u sum|xw|",
+            "results": prefill_f32,
         },
         "host_api": {
             "entry": "mimg_dequant_matmul_a8 (gate, host x and y)",

@@ -210,6 +210,17 @@ int mimg_rope_kv_dev(float *q, const float *k, const float *v, const int64_t *po
 int mimg_linear_f32_dev(uint64_t w, const float *x, int64_t rows, const float *bias, float *y,
                         void *stream);
 
+/* dequant_matmul.v1 for many rows (prefill) on the fp32 matrix cores
+ * (reference linearF32/linearCols, interp/fast.go:161-183). Each weight is
+ * decoded as mim.Dequantize does, bit for bit; the products are summed in
+ * float32 in another order than the reference's, within the bound the spec
+ * sets for dequant_matmul.v1 (spec/stdlib.md:230-246):
+ * |y - exact| <= (K+1) * 2^-24 * sum_k |x_k w_k|, then bias is added. K must
+ * be a multiple of 32 (of 256 for Q4_K and Q6_K); rows <= 65535*128. The
+ * rows of W the 8-bit path refuses need no special case here. */
+int mimg_linear_f32_mfma_dev(uint64_t w, const float *x, int64_t rows, const float *bias, float *y,
+                             void *stream);
+
 /* mimg_dequantize on device buffers. */
 int mimg_dequantize_dev(uint32_t dtype, const void *src, uint64_t len, float *dst, int64_t n,
                         void *stream);

@@ -641,6 +641,19 @@ int mimg_linear_f32_dev(uint64_t wh, const float* x, int64_t rows, const float* 
     return MIMG_OK;
 }
 
+int mimg_linear_f32_mfma_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, float* y, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    Weight* w;
+    if ((rc = lookup(wh, &w))) return rc;
+    if (rows < 0 || rows > INT32_MAX) return fail(MIMG_ERR_ARG, "rows = %lld", (long long)rows);
+    if (rows == 0) return MIMG_OK;
+    if (!x || !y) return fail(MIMG_ERR_ARG, "null pointer");
+    if ((rows + 127) / 128 > 65535) return fail(MIMG_ERR_ARG, "rows = %lld: more than 65535 tiles of 128", (long long)rows);
+    HIP_TRY(launch_linear_f32_mfma(w->dw, x, rows, bias, y, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
 int mimg_matmul_a8_quantized_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, int block, float* y,
                                  const void* ws, uint64_t ws_bytes, void* stream) {
     int rc = ensure_device();

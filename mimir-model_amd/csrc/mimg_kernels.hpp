@@ -97,6 +97,10 @@ hipError_t launch_gemv_kq_a8_b32(const DevWeight& w, const ActPtrs& a, int64_t r
 
 hipError_t launch_linear_f32(const DevWeight& w, const float* x, int64_t rows, const float* bias,
                              float* y, hipStream_t stream);
+// The same product on the fp32 matrix cores, within the spec's bound for
+// dequant_matmul.v1 (gemm_f32.hip).
+hipError_t launch_linear_f32_mfma(const DevWeight& w, const float* x, int64_t rows, const float* bias, float* y,
+                                  hipStream_t stream);
 
 // Decoder-step ops (decoder_ops.hip).
 hipError_t launch_embed_rows(uint32_t dt, const uint8_t* table, int64_t row_bytes, const int32_t* ids, int T, int V,

@@ -106,9 +106,14 @@ class Decoder:
     GOMAXPROCS of the reference run to reproduce (its swiglu results depend
     on it). kquant_block is the activation block of the Q4_K/Q6_K products
     with 8-bit activations (256: dequant_matmul_a8.v2, 32: .v1).
+    f32_tile_rows (float32 activations only): products of at least this many
+    rows run on the fp32 matrix cores (mimg_linear_f32_mfma_dev), within the
+    spec's bound for dequant_matmul.v1 but not in the reference's float
+    order; 0 keeps the reference's order everywhere.
     """
 
-    def __init__(self, config, tensors, a8=True, cache_f16=False, max_rows=64, slots=1, procs=16, kquant_block=256):
+    def __init__(self, config, tensors, a8=True, cache_f16=False, max_rows=64, slots=1, procs=16, kquant_block=256,
+                 f32_tile_rows=0):
         c = self.c = config if isinstance(config, Config) else Config(**config)
         self.a8, self.f16, self.slots = bool(a8), bool(cache_f16), int(slots)
         # activation blocks for Q4_K/Q6_K weights: 256 is dequant_matmul_a8.v2
@@ -116,6 +121,7 @@ class Decoder:
         if kquant_block not in (32, 256):
             raise ValueError(f"kquant_block {kquant_block}: 32 or 256")
         self.kquant_block = kquant_block
+        self.f32_tile_rows = int(f32_tile_rows)
         # the reference's GOMAXPROCS: swiglu's results follow its piece split
         self.procs = int(procs)
         self.R = int(max_rows)
@@ -171,8 +177,9 @@ class Decoder:
         bs = [None if b is None or b not in self.vec else self.vec[b].ptr for b in (biases or [None] * len(names))]
         s = self.stream.handle
         if not self.a8:
+            tiles = 0 < self.f32_tile_rows <= rows
             for w, b, y in zip(ws, bs, ys):
-                mimg.linear_f32_dev(w, x, rows, b, y, s)
+                (mimg.linear_f32_mfma_dev if tiles else mimg.linear_f32_dev)(w, x, rows, b, y, s)
             return
         blocks = {self._block(w) for w in ws}
         if len(ws) > 1 and len(blocks) == 1:
@@ -253,6 +260,8 @@ class Decoder:
             xh, yh = self.h.ptr + src * E * 4, self.logits.ptr + dst * V * 4
             if self.a8:
                 mimg.linear_a8_dev(self.head, xh, n, None, self._block(self.head), yh, self.ws.ptr, self.ws_bytes, s)
+            elif 0 < self.f32_tile_rows <= n:
+                mimg.linear_f32_mfma_dev(self.head, xh, n, None, yh, s)
             else:
                 mimg.linear_f32_dev(self.head, xh, n, None, yh, s)
 

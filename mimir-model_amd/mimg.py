@@ -47,6 +47,7 @@ SIGNATURES = {
                                       ctypes.POINTER(_P), _P, _U64, _P]),
     "mimg_matmul_a8_quantized_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P, _U64, _P]),
     "mimg_linear_f32_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
+    "mimg_linear_f32_mfma_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
     "mimg_dequantize_dev": (_I, [_U32, _P, _U64, _P, _I64, _P]),
     "mimg_quantize_dev": (_I, [_U32, _P, _I64, _P, _U64, _P]),
     "mimg_synthetic_normal_dev": (_I, [_U64, ctypes.c_float, _P, _I64, _P]),
@@ -274,6 +275,14 @@ def rope_kv_dev(q_ptr, k_ptr, v_ptr, pos_ptr, cidx_ptr, inv_freq_ptr, T, heads, 
 def linear_f32_dev(w, x_ptr, rows, bias_ptr, y_ptr, stream):
     _check(load().mimg_linear_f32_dev(w.handle, _P(x_ptr), rows, _P(bias_ptr) if bias_ptr else None,
                                       _P(y_ptr), _P(stream)))
+
+
+def linear_f32_mfma_dev(w, x_ptr, rows, bias_ptr, y_ptr, stream):
+    """dequant_matmul.v1 on the fp32 matrix cores (mimg_linear_f32_mfma_dev):
+    within (K+1)*2^-24*sum|x w| of the exact product, not the reference's
+    float order."""
+    _check(load().mimg_linear_f32_mfma_dev(w.handle, _P(x_ptr), rows, _P(bias_ptr) if bias_ptr else None,
+                                           _P(y_ptr), _P(stream)))
 
 
 def dequantize_dev(dt, src_ptr, nbytes, dst_ptr, n, stream):

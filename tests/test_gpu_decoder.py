@@ -236,6 +236,29 @@ def test_fixture_generate_f32(gpu, name):
     assert got[0].tolist() == e["greedy"]
 
 
+@pytest.mark.parametrize("name", fm.FIXTURES)
+def test_fixture_generate_f32_matrix_cores(gpu, name):
+    """The float32 path with every product on the fp32 matrix cores
+    (f32_tile_rows=1: dequant_matmul.v1 within the spec's bound, another
+    summation order): every logit still within 2e-5 of the largest of the
+    Go executor's, and its greedy ids."""
+    import decoder
+
+    cfg, tensors, e = fm.load(name)
+    dec = decoder.Decoder(cfg, tensors, a8=False, max_rows=16, f32_tile_rows=1)
+    P = len(e["prompt_ids"])
+    prompt = dec.forward(e["prompt_ids"], np.arange(P))
+    ok, worst, allowed = fm.near(prompt, fm.f32b64(e["prompt_logits"]), 2e-5)
+    assert ok, f"prompt logits: {worst} > {allowed}"
+    lg = prompt[-1]
+    for i, tok in enumerate(e["greedy"]):
+        ok, worst, allowed = fm.near(lg, fm.f32b64(e["greedy_logits"][i]), 2e-5)
+        assert ok, f"step {i}: {worst} > {allowed}"
+        assert int(np.argmax(lg)) == tok, f"step {i}"
+        if i + 1 < len(e["greedy"]):
+            lg = dec.forward([tok], [P + i])[0]
+
+
 @pytest.mark.parametrize("cache_f16", [False, True], ids=["f32cache", "f16cache"])
 @pytest.mark.parametrize("name", fm.FIXTURES)
 def test_fixture_generate_a8(gpu, name, cache_f16):
