@@ -14,12 +14,13 @@
 // the float32 normal range may be flushed by the matrix cores; the bound is
 // not claimed for a sum made of such products only.
 //
-// Tiling: a 256-thread workgroup computes 128 weight rows x 128 activation
-// rows, K in stages of 32. Per stage every thread decodes 16 weights of one
+// Tiling: a 256-thread workgroup computes 128 weight rows x BM activation
+// rows (BM = 128, or 64 when the 128-row tiles would leave CUs idle), K in
+// stages of 32. Per stage every thread decodes 16 weights of one
 // row and loads 16 activations of one row, both into LDS ([row][k], row
 // stride 34 floats: the MFMA operand reads of a half-wave, 16 rows x 2 k,
-// fall in 32 distinct banks); the four waves then run 16 MFMAs per 4 k each
-// on their 64 x 64 quarter. LDS is double-buffered: the global loads of
+// fall in 32 distinct banks); the four waves then run 4*BM/32 MFMAs per 4 k
+// each on their 64 x BM/2 quarter. LDS is double-buffered: the global loads of
 // stage s+1 are issued before the MFMAs of stage s and decoded into the
 // other buffer after them, one barrier per stage.
 #include "f32path.hpp"
@@ -30,8 +31,7 @@ namespace mimg {
 
 namespace {
 
-constexpr int GF_BN = 128, GF_BM = 128, GF_BK = 32, GF_S = GF_BK + 2;
-constexpr int GF_TILE = GF_BN * GF_S;  // floats of one operand tile
+constexpr int GF_BN = 128, GF_BK = 32, GF_S = GF_BK + 2;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -122,34 +122,40 @@ __device__ __forceinline__ void decode_w(const WRaw& r, int64_t k0, float* out) 
 
 }  // namespace
 
-template <uint32_t DT>
+template <uint32_t DT, int BM>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const uint8_t* __restrict__ W, int64_t rb, int N, int64_t K,
                                                        const float* __restrict__ x, int M,
                                                        const float* __restrict__ bias, float* __restrict__ y) {
-    __shared__ __align__(16) float lds[2][2][GF_TILE];  // [buffer][weights, activations]
+    constexpr int TB = BM / 32;  // activation tiles of 16 per wave
+    __shared__ __align__(16) float lw[2][GF_BN * GF_S];  // [buffer] weights [n][k]
+    __shared__ __align__(16) float lx[2][BM * GF_S];     // [buffer] activations [m][k]
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int n0 = blockIdx.x * GF_BN, m0 = blockIdx.y * GF_BM;
-    const int wn = (wave & 1) * 64, wm = (wave >> 1) * 64;
-    // This thread's loads: row t/2 of each tile, k half t%2.
+    const int n0 = blockIdx.x * GF_BN, m0 = blockIdx.y * BM;
+    const int wn = (wave & 1) * 64, wm = (wave >> 1) * (BM / 2);
+    // This thread's loads: row t/2 of each tile, k half t%2 (activations:
+    // the threads of the first BM rows).
     const int lr = t >> 1, h = t & 1;
+    const bool xload = lr < BM;
     const uint8_t* wrow = W + (int64_t)min(n0 + lr, N - 1) * rb;
-    const float* xrow = x + (int64_t)min(m0 + lr, M - 1) * K + 16 * h;
+    const float* xrow = x + (int64_t)min(m0 + min(lr, BM - 1), M - 1) * K + 16 * h;
 
-    f32x4 acc[4][4];
+    f32x4 acc[4][TB];
 #pragma unroll
     for (int a = 0; a < 4; a++)
 #pragma unroll
-        for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < TB; b++) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     auto stage_store = [&](int buf, const WRaw& wr, const f32x4* xv, int64_t k0) {
         float wv[16];
         decode_w<DT>(wr, k0, wv);
-        float* ws = &lds[buf][0][lr * GF_S + 16 * h];
-        float* xs = &lds[buf][1][lr * GF_S + 16 * h];
+        float* ws = &lw[buf][lr * GF_S + 16 * h];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            *(float2*)(ws + 2 * i) = float2{wv[2 * i], wv[2 * i + 1]};
-            *(float2*)(xs + 2 * i) = float2{xv[i >> 1][2 * (i & 1)], xv[i >> 1][2 * (i & 1) + 1]};
+        for (int i = 0; i < 8; i++) *(float2*)(ws + 2 * i) = float2{wv[2 * i], wv[2 * i + 1]};
+        if (xload) {
+            float* xs = &lx[buf][lr * GF_S + 16 * h];
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                *(float2*)(xs + 2 * i) = float2{xv[i >> 1][2 * (i & 1)], xv[i >> 1][2 * (i & 1) + 1]};
         }
     };
 
@@ -171,19 +177,19 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const uint8_t* __restrict
 #pragma unroll
             for (int i = 0; i < 4; i++) xv[i] = *(const f32x4*)(xrow + k1 + 4 * i);
         }
-        const float* ws = &lds[buf][0][0];
-        const float* xs = &lds[buf][1][0];
+        const float* ws = &lw[buf][0];
+        const float* xs = &lx[buf][0];
 #pragma unroll
         for (int k4 = 0; k4 < GF_BK / 4; k4++) {
-            float av[4], bv[4];
+            float av[4], bv[TB];
 #pragma unroll
             for (int a = 0; a < 4; a++) av[a] = ws[(wn + 16 * a + r16) * GF_S + 4 * k4 + kq];
 #pragma unroll
-            for (int b = 0; b < 4; b++) bv[b] = xs[(wm + 16 * b + r16) * GF_S + 4 * k4 + kq];
+            for (int b = 0; b < TB; b++) bv[b] = xs[(wm + 16 * b + r16) * GF_S + 4 * k4 + kq];
 #pragma unroll
             for (int a = 0; a < 4; a++)
 #pragma unroll
-                for (int b = 0; b < 4; b++)
+                for (int b = 0; b < TB; b++)
                     acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[a], bv[b], acc[a][b], 0, 0, 0);
         }
         if (more) stage_store(buf ^ 1, wr, xv, k1);
@@ -193,7 +199,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const uint8_t* __restrict
     // acc[a][b] lane l holds rows n = 16a + 4(l/16) + j (j = 0..3) of
     // activation row m = 16b + l%16, of this wave's quarter.
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
+    for (int b = 0; b < TB; b++) {
         const int m = m0 + wm + 16 * b + r16;
         if (m >= M) continue;
 #pragma unroll
@@ -212,28 +218,37 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const uint8_t* __restrict
     }
 }
 
-hipError_t launch_linear_f32_mfma(const DevWeight& w, const float* x, int64_t rows, const float* bias, float* y,
-                                  hipStream_t stream) {
-    if (rows <= 0 || w.n <= 0) return hipSuccess;
-    if (w.k % GF_BK || rows > INT32_MAX || w.n > INT32_MAX) return hipErrorInvalidValue;
-    dim3 grid((unsigned)((w.n + GF_BN - 1) / GF_BN), (unsigned)((rows + GF_BM - 1) / GF_BM)), blk(256);
+template <int BM>
+static hipError_t launch_gf(const DevWeight& w, const float* x, int64_t rows, const float* bias, float* y,
+                            hipStream_t stream) {
+    dim3 grid((unsigned)((w.n + GF_BN - 1) / GF_BN), (unsigned)((rows + BM - 1) / BM)), blk(256);
     if (grid.y > 65535) return hipErrorInvalidValue;
     switch (w.dt) {
     case DT_Q4_K:
-        hipLaunchKernelGGL(gemm_f32_kernel<DT_Q4_K>, grid, blk, 0, stream, w.data, w.row_bytes, (int)w.n, w.k, x,
+        hipLaunchKernelGGL((gemm_f32_kernel<DT_Q4_K, BM>), grid, blk, 0, stream, w.data, w.row_bytes, (int)w.n, w.k, x,
                            (int)rows, bias, y);
         break;
     case DT_Q6_K:
-        hipLaunchKernelGGL(gemm_f32_kernel<DT_Q6_K>, grid, blk, 0, stream, w.data, w.row_bytes, (int)w.n, w.k, x,
+        hipLaunchKernelGGL((gemm_f32_kernel<DT_Q6_K, BM>), grid, blk, 0, stream, w.data, w.row_bytes, (int)w.n, w.k, x,
                            (int)rows, bias, y);
         break;
     case DT_Q8_0:
-        hipLaunchKernelGGL(gemm_f32_kernel<DT_Q8_0>, grid, blk, 0, stream, w.data, w.row_bytes, (int)w.n, w.k, x,
+        hipLaunchKernelGGL((gemm_f32_kernel<DT_Q8_0, BM>), grid, blk, 0, stream, w.data, w.row_bytes, (int)w.n, w.k, x,
                            (int)rows, bias, y);
         break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_linear_f32_mfma(const DevWeight& w, const float* x, int64_t rows, const float* bias, float* y,
+                                  hipStream_t stream) {
+    if (rows <= 0 || w.n <= 0) return hipSuccess;
+    if (w.k % GF_BK || rows > INT32_MAX || w.n > INT32_MAX) return hipErrorInvalidValue;
+    // 64-row tiles when 128-row tiles would not give every CU one.
+    const int64_t tiles128 = (w.n + GF_BN - 1) / GF_BN * ((rows + 127) / 128);
+    if (tiles128 < 256) return launch_gf<64>(w, x, rows, bias, y, stream);
+    return launch_gf<128>(w, x, rows, bias, y, stream);
 }
 
 }  // namespace mimg

@@ -45,7 +45,8 @@ def _bound_check(oracle, dt, wb, x, n, k, got, bias=None):
 
 @pytest.mark.parametrize("dt", [Q4_K, Q6_K])
 @pytest.mark.parametrize("rows,n,k", [(1, 5, 256), (7, 130, 512), (64, 128, 256), (130, 257, 1024),
-                                      (257, 64, 4096), (300, 129, 2048)])
+                                      (257, 64, 4096), (300, 129, 2048),
+                                      (250, 16384, 256)])  # 256 tiles of 128 rows: the 128-row tiling
 def test_f32_mfma_within_spec_bound(gpu, oracle, dt, rows, n, k):
     wb = oracle.synthetic_weight(dt, n, k, seed=rows + n)
     x = oracle.synthetic_acts(rows, k, seed=k)
