@@ -178,14 +178,14 @@ def decode_cpu_check(cfg, tensors, prompt, gpu_ids, n, log):
             "prompt_tok_per_s": round(P / t_prompt, 2), "cores": threads, "kind": "port"}
 
 
-def decode_bench(name, log, graph=True, cpu=False):
+def decode_bench(name, log, graph=True, cpu=False, batches=(1, 8)):
     """Greedy generation on the GPU decoder with a random model of the
-    named shape (module docstring)."""
+    named shape (module docstring); batches selects the 8B runs."""
     import decoder
     import synthetic
 
     cfg = dict(synthetic.LLAMA_1B if name == "llama1b" else synthetic.LLAMA_8B)
-    runs = [(32, 128, 1)] if name == "llama1b" else [(512, 256, 1), (512, 256, 8)]
+    runs = [(32, 128, 1)] if name == "llama1b" else [(512, 256, b) for b in batches]
     cfg["context"] = max(p + n for p, n, _ in runs)
     t0 = time.time()
     tensors = synthetic.build(cfg, seed=1, log=log)
@@ -234,6 +234,7 @@ def main():
     ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
     ap.add_argument("--prefill-rows", default="512,2048",
                     help="activation rows of the prefill GEMM measurements (comma list; empty to skip)")
+    ap.add_argument("--decode-batches", default="1,8", help="batch sizes of the llama8b decode runs")
     ap.add_argument("--decode", default="llama1b,llama8b",
                     help="whole-model decode runs (comma list of llama1b, llama8b; empty to skip)")
     ap.add_argument("--roofline-replays", type=int, default=8,
@@ -461,7 +462,8 @@ def main():
     layers.clear()
     decode_res = {}
     for name in [d for d in args.decode.split(",") if d]:
-        decode_res.update(decode_bench(name, log, graph=not args.eager, cpu=not args.no_cpu))
+        decode_res.update(decode_bench(name, log, graph=not args.eager, cpu=not args.no_cpu,
+                                       batches=[int(b) for b in args.decode_batches.split(",") if b]))
     if decode_res:
         result["decode"] = decode_res
     if not args.no_cpu:

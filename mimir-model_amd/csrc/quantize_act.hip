@@ -9,9 +9,11 @@
 // ys16 = sum of each run of 16 (used by the Q6_K kernels for the bias of
 // 32); dbs = d*f32(xs).
 //
-// One workgroup per row, up to 16 waves; each wave takes one chunk of 256
-// elements at a time (one block of 256, or eight blocks of 32), four
-// elements per lane, float4 loads.
+// Work split: a wave takes one chunk of 256 elements at a time (one block of
+// 256, or eight blocks of 32), four elements per lane, float4 loads. rms_norm
+// (which needs the whole row's sum of squares first) runs one workgroup per
+// row of up to 16 waves; the plain quantizer and swiglu run eight chunks per
+// workgroup, many workgroups per row.
 #include "decoder_math.hpp"
 #include "mimg_device.hpp"
 #include "mimg_kernels.hpp"
@@ -34,6 +36,64 @@ namespace mimg {
 // The produced row must fit in one round of loads (K <= 16*CPW*256).
 enum { QA_PLAIN = 0, QA_NORM = 1, QA_SWIGLU = 2 };
 
+// Quantizes one chunk of 256 elements of row `row` (four per lane, lane's
+// first element e0; all 64 lanes of the wave call it) and returns whether a
+// lane's elements refuse the row (NaN or |x| > 2^60). The chunk's outputs
+// depend on its own elements only.
+template <int BLOCK>
+__device__ __forceinline__ bool qa_chunk(const float4 v, int64_t row, int64_t e0, int64_t K, const ActPtrs& a,
+                                         int lane) {
+    const int64_t R32 = K / 32;
+    // blocks of 32: K is a multiple of 32, so each group of eight lanes is
+    // wholly inside or outside the row (the DPP steps stay in-group)
+    if (BLOCK == 32 && e0 >= K) return false;
+    float av[4] = {fabsf(v.x), fabsf(v.y), fabsf(v.z), fabsf(v.w)};
+    bool lbad = false;
+    float m = 0.f;
+    for (int k = 0; k < 4; k++) {
+        lbad |= !(av[k] <= 0x1p60f);
+        m = fmaxf(m, av[k]);
+    }
+    float amax;
+    bool bbad;
+    if (BLOCK == 256) {
+        // max over the wave; fmaxf of non-negative finite values is exact
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_QUAD_1032, 0xF, 0xF, false)));
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_QUAD_2301, 0xF, 0xF, false)));
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_HALF_MIRROR, 0xF, 0xF, false)));
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_ROW_MIRROR, 0xF, 0xF, false)));
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        amax = m;
+        bbad = __any(lbad);
+    } else {
+        amax = group8_max(m);  // eight lanes hold one block of 32
+        bbad = lbad;
+    }
+    const float xv[4] = {v.x, v.y, v.z, v.w};
+    int qv[4];
+    const bool quant = !bbad && amax > 0.f;
+    const float inv = quant ? 1.0f / amax : 0.f;
+    for (int k = 0; k < 4; k++) qv[k] = quant ? quant_rne(xv[k], amax, inv) : 0;
+    uint32_t packed = (uint32_t)(qv[0] & 0xFF) | ((uint32_t)(qv[1] & 0xFF) << 8) |
+                      ((uint32_t)(qv[2] & 0xFF) << 16) | ((uint32_t)(qv[3] & 0xFF) << 24);
+    *(uint32_t*)(a.q + row * K + e0) = packed;
+    int s4 = qv[0] + qv[1] + qv[2] + qv[3];
+    // run of 16 = 4 lanes, run of 32 = 8 lanes
+    int s16 = s4 + __builtin_amdgcn_mov_dpp(s4, DPP_QUAD_1032, 0xF, 0xF, false);
+    s16 += __builtin_amdgcn_mov_dpp(s16, DPP_QUAD_2301, 0xF, 0xF, false);
+    int s32 = s16 + __builtin_amdgcn_mov_dpp(s16, DPP_HALF_MIRROR, 0xF, 0xF, false);
+    const float d = amax / 127.0f;
+    const int64_t run = e0 / 32;
+    if ((lane & 3) == 0) a.ys16[row * (K / 16) + e0 / 16] = (int16_t)s16;
+    if ((lane & 7) == 0) {
+        a.xs[row * R32 + run] = (int16_t)s32;
+        a.d32[row * R32 + run] = d;
+        a.dbs[row * R32 + run] = d * (float)(int16_t)s32;
+    }
+    return bbad;
+}
+
 template <int BLOCK, int CPW, int MODE>
 __global__ __launch_bounds__(1024) void quantize_act_kernel(const float* __restrict__ x, int64_t K,
                                                             ActPtrs a, QaSource src) {
@@ -42,7 +102,7 @@ __global__ __launch_bounds__(1024) void quantize_act_kernel(const float* __restr
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int nwaves = blockDim.x >> 6;
     const float* xr = x + (int64_t)row * K;
-    const int64_t R32 = K / 32, nch = (K + 255) / 256;
+    const int64_t nch = (K + 255) / 256;
     bool bad = false;
     for (int64_t c0 = wave; c0 < nch; c0 += (int64_t)nwaves * CPW) {
     float4 vv[CPW];
@@ -111,59 +171,79 @@ __global__ __launch_bounds__(1024) void quantize_act_kernel(const float* __restr
     for (int i = 0; i < CPW; i++) {
         const int64_t c = c0 + nwaves * i;
         if (c >= nch) break;  // uniform within the wave
-        const int64_t e0 = c * 256 + 4 * lane;
-        // blocks of 32: K is a multiple of 32, so each group of eight lanes
-        // is wholly inside or outside the row (the DPP steps stay in-group)
-        if (BLOCK == 32 && e0 >= K) continue;
-        const float4 v = vv[i];
-        float av[4] = {fabsf(v.x), fabsf(v.y), fabsf(v.z), fabsf(v.w)};
-        bool lbad = false;
-        float m = 0.f;
-        for (int k = 0; k < 4; k++) {
-            lbad |= !(av[k] <= 0x1p60f);
-            m = fmaxf(m, av[k]);
-        }
-        float amax;
-        bool bbad;
-        if (BLOCK == 256) {
-            // max over the wave; fmaxf of non-negative finite values is exact
-            m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_QUAD_1032, 0xF, 0xF, false)));
-            m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_QUAD_2301, 0xF, 0xF, false)));
-            m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_HALF_MIRROR, 0xF, 0xF, false)));
-            m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_ROW_MIRROR, 0xF, 0xF, false)));
-            m = fmaxf(m, __shfl_xor(m, 16));
-            m = fmaxf(m, __shfl_xor(m, 32));
-            amax = m;
-            bbad = __any(lbad);
-        } else {
-            amax = group8_max(m);  // eight lanes hold one block of 32
-            bbad = lbad;
-        }
-        bad |= bbad;
-        const float xv[4] = {v.x, v.y, v.z, v.w};
-        int qv[4];
-        const bool quant = !bbad && amax > 0.f;
-        const float inv = quant ? 1.0f / amax : 0.f;
-        for (int k = 0; k < 4; k++) qv[k] = quant ? quant_rne(xv[k], amax, inv) : 0;
-        uint32_t packed = (uint32_t)(qv[0] & 0xFF) | ((uint32_t)(qv[1] & 0xFF) << 8) |
-                          ((uint32_t)(qv[2] & 0xFF) << 16) | ((uint32_t)(qv[3] & 0xFF) << 24);
-        *(uint32_t*)(a.q + (int64_t)row * K + e0) = packed;
-        int s4 = qv[0] + qv[1] + qv[2] + qv[3];
-        // run of 16 = 4 lanes, run of 32 = 8 lanes
-        int s16 = s4 + __builtin_amdgcn_mov_dpp(s4, DPP_QUAD_1032, 0xF, 0xF, false);
-        s16 += __builtin_amdgcn_mov_dpp(s16, DPP_QUAD_2301, 0xF, 0xF, false);
-        int s32 = s16 + __builtin_amdgcn_mov_dpp(s16, DPP_HALF_MIRROR, 0xF, 0xF, false);
-        const float d = amax / 127.0f;
-        const int64_t run = e0 / 32;
-        if ((lane & 3) == 0) a.ys16[(int64_t)row * (K / 16) + e0 / 16] = (int16_t)s16;
-        if ((lane & 7) == 0) {
-            a.xs[row * R32 + run] = (int16_t)s32;
-            a.d32[row * R32 + run] = d;
-            a.dbs[row * R32 + run] = d * (float)(int16_t)s32;
-        }
+        bad |= qa_chunk<BLOCK>(vv[i], row, c * 256 + 4 * lane, K, a, lane);
     }
     }
     int any_bad = __syncthreads_or(bad ? 1 : 0);
+    if (threadIdx.x == 0) a.ok[row] = any_bad ? 0 : 1;
+}
+
+// Many workgroups per row (QA_PLAIN, QA_SWIGLU): workgroup 1+gi of a row
+// quantizes chunks 8gi..8gi+7, one per wave. The row's refusal flag depends
+// on the whole row, so workgroup 0 of each row only scans it, all its loads
+// in one round for K <= 16384: QA_PLAIN tests every x; QA_SWIGLU screens g
+// and u, and computes y exactly (swiglu_at, as written) only where the
+// screen does not pass. Screen: g and u finite with |g|, |u| <= 2^29. Then
+// |silu(g)| <= |g| in both of the reference's formulas (the vector one
+// divides (g*h)*h or g, h = exp(-|g|/2) <= 1, by h*h + 1 >= 1; the scalar one
+// divides by 1 + exp(-g) >= 1), so |y| <= 2^58 < 2^60 and y is not NaN: such
+// elements never refuse a row.
+constexpr int QA_MW_WAVES = 8;  // chunks of 256 per workgroup, one per wave
+
+template <int BLOCK, int MODE>
+__global__ __launch_bounds__(64 * QA_MW_WAVES) void quantize_act_mw_kernel(const float* __restrict__ x, int64_t K,
+                                                                           ActPtrs a, QaSource src) {
+    static_assert(MODE == QA_PLAIN || MODE == QA_SWIGLU, "rms_norm needs the whole row first");
+    const int row = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t nch = (K + 255) / 256;
+    const float* xr = x + (int64_t)row * K;
+    const float* ur = MODE == QA_SWIGLU ? src.aux + (int64_t)row * K : nullptr;
+    if (blockIdx.x > 0) {
+        const int64_t c = (int64_t)(blockIdx.x - 1) * QA_MW_WAVES + wave;
+        if (c >= nch) return;  // uniform within the wave
+        const int64_t e0 = c * 256 + 4 * lane, el = min(e0, K - 4);
+        float4 v = *(const float4*)(xr + el);
+        if constexpr (MODE == QA_SWIGLU) {
+            const float4 uu = *(const float4*)(ur + el);
+            const int64_t gi = (int64_t)row * K + el;
+            v = swiglu4(v, uu, gi, src.total, src.chunk);
+            if (e0 < K) *(float4*)(src.y + gi) = v;
+        }
+        qa_chunk<BLOCK>(v, row, e0, K, a, lane);
+        return;
+    }
+    // SCAN float4 loads of x (and of u) per thread in flight, clamped and
+    // checked where inside the row, in straight-line code (registers).
+    constexpr int SCAN = 8, STEP = 4 * 64 * QA_MW_WAVES;
+    bool bad = false;
+    for (int64_t e0 = 4 * (int64_t)threadIdx.x; e0 < K; e0 += (int64_t)STEP * SCAN) {
+        float4 v[SCAN], w[MODE == QA_SWIGLU ? SCAN : 1];
+#pragma unroll
+        for (int j = 0; j < SCAN; j++) {
+            const int64_t e = min(e0 + (int64_t)STEP * j, K - 4);
+            v[j] = *(const float4*)(xr + e);
+            if constexpr (MODE == QA_SWIGLU) w[j] = *(const float4*)(ur + e);
+        }
+#pragma unroll
+        for (int j = 0; j < SCAN; j++) {
+            const int64_t e = e0 + (int64_t)STEP * j;
+            if (e >= K) continue;
+            const float xv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+            if constexpr (MODE == QA_PLAIN) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) bad |= !(fabsf(xv[k]) <= 0x1p60f);
+            } else {
+                const float uv[4] = {w[j].x, w[j].y, w[j].z, w[j].w};
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    if (fabsf(xv[k]) <= 0x1p29f && fabsf(uv[k]) <= 0x1p29f) continue;
+                    const float y = swiglu_at(xv[k], uv[k], (int64_t)row * K + e + k, src.total, src.chunk);
+                    bad |= !(fabsf(y) <= 0x1p60f);
+                }
+            }
+        }
+    }
+    const int any_bad = __syncthreads_or(bad ? 1 : 0);
     if (threadIdx.x == 0) a.ok[row] = any_bad ? 0 : 1;
 }
 
@@ -172,6 +252,16 @@ static hipError_t launch_qa(const float* x, int64_t rows, int64_t K, int block, 
                             hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
     const int64_t chunks = (K + 255) / 256;
+    if (MODE != QA_NORM && rows <= 65535) {
+        dim3 grid((unsigned)(1 + (chunks + QA_MW_WAVES - 1) / QA_MW_WAVES), (unsigned)rows), blk(64 * QA_MW_WAVES);
+        if (block == 256)
+            hipLaunchKernelGGL((quantize_act_mw_kernel<256, MODE == QA_NORM ? QA_PLAIN : MODE>), grid, blk, 0, stream,
+                               x, K, a, src);
+        else
+            hipLaunchKernelGGL((quantize_act_mw_kernel<32, MODE == QA_NORM ? QA_PLAIN : MODE>), grid, blk, 0, stream,
+                               x, K, a, src);
+        return hipGetLastError();
+    }
     const int waves = (int)(chunks < 16 ? chunks : 16);
     const int64_t cpw = (chunks + waves - 1) / waves;  // rounds of 8 beyond K = 32768
     if (MODE != QA_PLAIN && cpw > 8) return hipErrorInvalidValue;

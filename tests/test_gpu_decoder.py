@@ -399,6 +399,43 @@ def test_swiglu_quant_equals_two_launches(gpu, rt, rows, n, block, procs):
     assert outs[0][1] == outs[1][1]
 
 
+@pytest.mark.parametrize("block", [256, 32])
+def test_swiglu_quant_refusals_match_oracle(gpu, oracle, rt, block):
+    """The fused swiglu quantizer's row flags and blocks against the
+    restatement (SiluMulF32 then the quantizer), with elements outside the
+    quantizer's cheap screen: a huge g times a tiny u (kept), huge times huge
+    (refused, |y| > 2^60), NaN (refused), in chunks past the first
+    workgroup's."""
+    rows, n, procs = 5, 4096, 16
+    rng = np.random.default_rng(11)
+    g = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+    u = rng.standard_normal((rows, n)).astype(np.float32)
+    g[0, 3000], u[0, 3000] = 1e10, 1e-20
+    g[1, 3500], u[1, 3500] = 2.0 ** 40, 2.0 ** 30
+    g[2, 4000] = np.nan
+    g[3, 2100], u[3, 2100] = -1e30, 5.0
+    s = rt.Stream()
+    wsb = gpu.a8_workspace_bytes(rows, n)
+    dg, du, do, ws = dev(rt, g), dev(rt, u), rt.DeviceBuffer(g.nbytes), rt.DeviceBuffer(wsb)
+    ws.zero()
+    gpu.swiglu_quant_dev(dg.ptr, du.ptr, do.ptr, rows, n, procs, block, ws.ptr, wsb, s.handle)
+    s.sync()
+    y = oracle.silu_mul(g.ravel(), u.ravel(), procs).reshape(rows, n)
+    got_y = do.download(np.float32).reshape(rows, n)
+    assert np.array_equal(got_y.view(np.uint32), y.view(np.uint32))
+    q, d, xs, _, dbs, ok = _ws_bytes(gpu, ws, rows, n)
+    ok = np.frombuffer(ok, np.int32)
+    q = np.frombuffer(q, np.int8).reshape(rows, n)
+    d = np.frombuffer(d, np.float32).reshape(rows, -1)
+    for i in range(rows):
+        a = oracle.Act(y[i], block)
+        assert bool(ok[i]) == a.ok, i
+        if a.ok:
+            assert np.array_equal(q[i], a.q), i
+            assert np.array_equal(d[i].view(np.uint32), np.asarray(a.d, np.float32).view(np.uint32)), i
+    assert ok.tolist() == [1, 0, 0, 1, 1]
+
+
 @pytest.mark.parametrize("f16", [False, True])
 @pytest.mark.parametrize("T,H,Hkv,D,rot,inter", [(1, 32, 8, 128, 128, True), (5, 4, 2, 64, 32, False),
                                                  (3, 8, 8, 64, 64, False), (2, 4, 1, 80, 48, True)])

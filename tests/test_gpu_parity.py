@@ -99,7 +99,7 @@ def test_encoder_gpu_equals_oracle(gpu, oracle, dt):
 def test_quantize_act_bitexact(gpu, oracle, block):
     import hiprt
 
-    rows, k = 7, 2048
+    rows, k = 10, 2048
     rng = np.random.default_rng(block)
     x = rng.standard_normal((rows, k)).astype(np.float32)
     x[1] *= np.float32(1e-30)
@@ -107,6 +107,10 @@ def test_quantize_act_bitexact(gpu, oracle, block):
     x[3, :256] = 0
     x[4, 100] = np.nan
     x[5, 1000] = np.float32(2.0 ** 61)
+    # refusals in the row's last chunks (another workgroup than the first)
+    x[7, 2000] = np.nan
+    x[8, 1500] = -np.inf
+    x[9, 2047] = np.float32(2.0 ** 60)  # at the limit: not refused
     amax = np.abs(x[6, :block]).max()
     x[6, 1:5] = np.float32([0.5, 1.5, 2.5, -3.5]) * amax / np.float32(127)
     ws_bytes = gpu.a8_workspace_bytes(rows, k)
