@@ -4,11 +4,12 @@
 // decoder layer; gate and up) in one launch.
 //
 // Each 256-thread workgroup owns R rows of one matrix. It first issues the
-// weight loads of its (row, block) pairs, then quantizes x into LDS while
-// they are in flight (every workgroup quantizes the same row the same way,
-// so no second launch and no global workspace), then forms the exact int32
-// block sums of its pairs (as gemv_kquant.hip) and runs the serial float
-// chain of each row in block order.
+// loads of x, of its rows' flags and of the weights of its (row, block)
+// pairs, then quantizes x into LDS while they are in flight (every
+// workgroup quantizes the same row the same way, so no second launch and no
+// global workspace), then forms the exact int32 block sums of its pairs (as
+// gemv_kquant.hip, block-major pairs) and runs the serial float chain of
+// each row in block order.
 //
 // Quantization (reference Q8.QuantizeBlocks, internal/kernels/q8.go:50-97):
 // per block of 256, amax = max|x| (the row is refused if any |x| is NaN or
@@ -109,12 +110,39 @@ struct FusedRaw<DT_Q6_K> {
     Q6KRaw raw;
 };
 
-template <uint32_t DT, int U>
+// A group's activation for block b, from the row quantized into LDS.
+template <uint32_t DT>
+__device__ __forceinline__ ActLane act_lane_lds(const QuantLds& Q, int b, int l) {
+    ActLane a;
+    const int8_t* yb = Q.q + 256 * b;
+    if constexpr (DT == DT_Q4_K) {
+        const int yoff = 64 * (l >> 1) + 16 * (l & 1);
+        a.ya = *(const u32x4*)(yb + yoff);
+        a.yh = *(const u32x4*)(yb + yoff + 32);
+        a.sa = Q.xs[8 * b + l];
+        a.sb = 0;
+    } else {
+        const int eL = 128 * (l >> 2) + 32 * ((l & 3) >> 1) + 16 * (l & 1);
+        a.ya = *(const u32x4*)(yb + eL);
+        a.yh = *(const u32x4*)(yb + eL + 64);
+        a.sa = Q.ys16[16 * b + (eL >> 4)];
+        a.sb = Q.ys16[16 * b + ((eL + 64) >> 4)];
+    }
+    a.dx = Q.dx[b];
+    return a;
+}
+
+// The pairs are numbered block-major (p = b*R + r) and group g of an
+// iteration takes pairs p0 + U*g + [0, U); with U dividing R (SHARED) these
+// are U rows of one block, whose activation is read from LDS once. Weights
+// are addressed as 32-bit offsets from the tile's base; the row flags and
+// bias are loaded first and looked at last.
+template <uint32_t DT, int U, bool SHARED>
 __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F, int tile, uint8_t* smem) {
     constexpr int BYTES = DT == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     const int nb = A.nb, R = F.R, np = R * nb;
     const int64_t K = A.K;
-    const int g = threadIdx.x >> 3, l = threadIdx.x & 7;
+    const int g = threadIdx.x >> 3, l = threadIdx.x & 7, t = threadIdx.x;
     const int row0 = tile * R;
     QuantLds Q;
     Q.q = (int8_t*)smem;
@@ -122,31 +150,47 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     Q.xs = (int16_t*)(Q.dx + nb);
     Q.ys16 = (int16_t*)(Q.xs + K / 32);
     i32x4* part = (i32x4*)(smem + ((K + nb * 4 + (K / 32) * 2 + (K / 16) * 2 + 15) & ~(int64_t)15));
+    int* refl = (int*)(part + (size_t)R * nb);  // [R]: the row's weight is refused
+    const int64_t tbyte = (int64_t)row0 * F.rb;
+    const uint8_t* Wt = F.W + (tbyte & ~(int64_t)3);
+    const uint32_t tadj = (uint32_t)(tbyte & 3), rb32 = (uint32_t)F.rb;
+    const int rlast = min(R, F.N - row0) - 1;
 
-    // 1. The first U pairs' weights, unconditionally (clamped), in flight.
+    // 1. x (the first 16 blocks), the row flags and bias, then the first U
+    // pairs' weights, all in flight; the load counter retires in order, so
+    // the quantizer waits for x alone.
+    const int j = t & 15, bq = t >> 4;
+    float4 xv[4];
+    load_x16(A.x, min(bq, nb - 1), j, xv);
+    const int frow = min(row0 + min(t, R - 1), F.N - 1);
+    const int wr = F.wref[frow];
+    const float bias = F.bias ? F.bias[frow] : 0.f;
+    __builtin_amdgcn_sched_barrier(0);
     FusedRaw<DT> raw[U];
     auto load = [&](int p0) {
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int p = min(p0 + 32 * u, np - 1);
-            const int r = p / nb, b = p - r * nb;
-            const int row = min(row0 + r, F.N - 1);
-            const uint8_t* blk = F.W + (int64_t)row * F.rb + (int64_t)b * BYTES;
-            if constexpr (DT == DT_Q4_K) {
-                raw[u].hdr = *(const u32x4*)blk;
-                raw[u].qv = *(const u32x4*)(blk + 16 + 16 * l);
+            int b, r;
+            if constexpr (SHARED) {
+                const int pb = min(p0 + U * g, np - U);
+                b = pb / R;
+                r = min(pb - b * R + u, rlast);
             } else {
-                raw[u].raw = q6k_load(blk, l);
+                const int p = min(p0 + U * g + u, np - 1);
+                b = p / R;
+                r = min(p - b * R, rlast);
+            }
+            const uint32_t off = tadj + (uint32_t)r * rb32 + (uint32_t)b * BYTES;
+            if constexpr (DT == DT_Q4_K) {
+                raw[u].hdr = *(const u32x4*)(Wt + off);
+                raw[u].qv = *(const u32x4*)(Wt + (off + 16 * l + 16));
+            } else {
+                raw[u].raw = q6k_load_at(Wt, off, l);
             }
         }
     };
-    // The first 16 blocks of x are loaded before the weights: the load
-    // counter retires in order, so the quantizer, which needs only x, then
-    // waits for x alone while the weights are still in flight.
-    const int t = threadIdx.x, j = t & 15, bq = t >> 4;
-    float4 xv[4];
-    load_x16(A.x, min(bq, nb - 1), j, xv);
-    load(g);
+    load(0);
+    __builtin_amdgcn_sched_barrier(0);
 
     // 2. Quantize x into LDS while the weights arrive.
     bool bad = bq < nb ? quantize_block_lds(xv, bq, j, Q) : false;
@@ -157,40 +201,36 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     const bool row_refused = __syncthreads_or(bad ? 1 : 0) != 0;
 
     // 3. Exact block sums of this workgroup's pairs.
-    for (int p0 = g; p0 < np; p0 += 32 * U) {
-        if (p0 != g) load(p0);
+    for (int p0 = 0; p0 < np; p0 += 32 * U) {
+        if (p0 != 0) load(p0);
+        const int pb = p0 + U * g;
+        ActLane a0;
+        if constexpr (SHARED) a0 = act_lane_lds<DT>(Q, min(pb, np - U) / R, l);
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int p = p0 + 32 * u;
-            if (p >= np) break;  // uniform within the group
-            const int r = p / nb, b = p - r * nb;
-            i32x4 v;
+            const int p = SHARED ? min(pb, np - U) + u : min(pb + u, np - 1);
+            const bool store = SHARED ? pb < np : pb + u < np;
+            const int b = p / R, r = p - b * R;
+            const ActLane a = SHARED ? a0 : act_lane_lds<DT>(Q, b, l);
+            u32x4 hdr = {0, 0, 0, 0}, qv = {0, 0, 0, 0};
+            Q6KRaw q6{};
             if constexpr (DT == DT_Q4_K) {
-                const Q4KLane w = q4k_lane(raw[u].hdr, raw[u].qv, l);
-                const int8_t* yb = Q.q + 256 * b + w.yoff;
-                v.x = group8_sum(q4k_part(w, *(const u32x4*)yb, *(const u32x4*)(yb + 32)));
-                v.y = group8_sum(w.mm * (int)Q.xs[8 * b + l]);
-                const float dx = Q.dx[b];
-                v.z = __float_as_int(w.d * dx);
-                v.w = __float_as_int(w.dmin * dx);
+                hdr = raw[u].hdr;
+                qv = raw[u].qv;
             } else {
-                const Q6KLane w = q6k_lane(raw[u].raw, l);
-                const int8_t* yb = Q.q + 256 * b;
-                v.x = group8_sum(q6k_part(w, *(const u32x4*)(yb + w.eL), *(const u32x4*)(yb + w.eL + 64),
-                                          Q.ys16[16 * b + (w.eL >> 4)], Q.ys16[16 * b + ((w.eL + 64) >> 4)]));
-                v.y = 0;
-                v.z = __float_as_int(w.d * Q.dx[b]);
-                v.w = 0;
+                q6 = raw[u].raw;
             }
-            if (l == 0) part[r * nb + b] = v;
+            const i32x4 v = pair_part<DT>(hdr, qv, q6, a, l);
+            if (l == 0 && store) part[r * nb + b] = v;
         }
     }
+    if (t < R) refl[t] = wr;
     __syncthreads();
 
     // 4. The serial float chain of each row, in block order.
     if (t < R) {
         const int row = row0 + t;
-        if (row < F.N && F.wref[row] == 0 && !row_refused) {
+        if (row < F.N && wr == 0 && !row_refused) {
             float tot = 0.f, off = 0.f;
             for (int b = 0; b < nb; b++) {
                 const i32x4 v = part[t * nb + b];
@@ -198,14 +238,14 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
                 if (DT == DT_Q4_K) off = __builtin_fmaf((float)v.y, __int_as_float(v.w), off);
             }
             float res = DT == DT_Q4_K ? tot - off : tot;
-            if (F.bias) res += F.bias[row];
+            if (F.bias) res += bias;
             F.y[row] = res;
         }
     }
     // 5. The float32 path for refused rows (fused order: one activation row).
     for (int r = g; r < R; r += 32) {
         const int row = row0 + r;
-        if (row < F.N && (F.wref[row] != 0 || row_refused)) {
+        if (row < F.N && (refl[r] != 0 || row_refused)) {
             float res = f32dot_g8<DT>(F.W + (int64_t)row * F.rb, A.x, K, true);
             if (F.bias) res += F.bias[row];
             if (l == 0) F.y[row] = res;
@@ -213,7 +253,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     }
 }
 
-template <int U>
+template <int U, bool SHARED>
 __global__ __launch_bounds__(256) void gemv_a8k_fused_kernel(FusedArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
     int mi = 0;
@@ -221,13 +261,13 @@ __global__ __launch_bounds__(256) void gemv_a8k_fused_kernel(FusedArgs A) {
     if (A.nmat > 2 && (int)blockIdx.x >= A.mat[2].tile0) mi = 2;
     const FusedMat F = mi == 0 ? A.mat[0] : mi == 1 ? A.mat[1] : A.mat[2];
     const int tile = (int)blockIdx.x - F.tile0;
-    if (F.dt == DT_Q4_K) fused_body<DT_Q4_K, U>(A, F, tile, smem);
-    else fused_body<DT_Q6_K, U>(A, F, tile, smem);
+    if (F.dt == DT_Q4_K) fused_body<DT_Q4_K, U, SHARED>(A, F, tile, smem);
+    else fused_body<DT_Q6_K, U, SHARED>(A, F, tile, smem);
 }
 
 static size_t fused_lds_bytes(int64_t K, int nb, int maxR) {
     size_t q = ((size_t)K + nb * 4 + (K / 32) * 2 + (K / 16) * 2 + 15) & ~(size_t)15;
-    return q + (size_t)maxR * nb * 16;
+    return q + (size_t)maxR * nb * 16 + (size_t)maxR * 4;
 }
 
 // Rows per workgroup for a matrix: pairs per workgroup at most 32*U*2 (two
@@ -275,7 +315,11 @@ hipError_t launch_gemv_a8k_fused(const DevWeight* const* ws, int nmat, const flo
         }
     }
     const size_t lds = fused_lds_bytes(A.K, A.nb, maxR);
-    hipLaunchKernelGGL(gemv_a8k_fused_kernel<4>, dim3(tiles), dim3(256), lds, stream, A);
+    // every matrix has the same R (it depends on K only)
+    if (A.mat[0].R % 4 == 0)
+        hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, true>), dim3(tiles), dim3(256), lds, stream, A);
+    else
+        hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, false>), dim3(tiles), dim3(256), lds, stream, A);
     return hipGetLastError();
 }
 

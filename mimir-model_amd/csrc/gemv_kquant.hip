@@ -80,61 +80,6 @@ struct KQ {
 #define MIMG_PAIRS_U 4
 #endif
 
-// One group's share of the activation for one block: Q4_K ya/yh = the 16
-// quants of each of its two runs, xs the sum of its sub-block; Q6_K ya/yh
-// and the two runs' sums ysL/ysH. dx is the block's activation scale.
-struct ActLane {
-    u32x4 ya, yh;
-    int sa, sb;
-    float dx;
-};
-
-template <uint32_t DT>
-__device__ __forceinline__ ActLane act_lane(const int8_t* q, const int16_t* s16, const float* d32, int64_t K, int m,
-                                           int b, int l) {
-    const int64_t R32 = K / 32, R16 = K / 16;
-    const int8_t* yb = q + m * K + (uint32_t)(b * 256);
-    ActLane a;
-    if constexpr (DT == DT_Q4_K) {
-        const int yoff = 64 * (l >> 1) + 16 * (l & 1);
-        a.ya = *(const u32x4*)(yb + yoff);
-        a.yh = *(const u32x4*)(yb + yoff + 32);
-        a.sa = s16[m * R32 + 8 * b + l];
-        a.sb = 0;
-    } else {
-        const int eL = 128 * (l >> 2) + 32 * ((l & 3) >> 1) + 16 * (l & 1);
-        a.ya = *(const u32x4*)(yb + eL);
-        a.yh = *(const u32x4*)(yb + eL + 64);
-        const int16_t* ys = s16 + m * R16 + 16 * b;
-        a.sa = ys[eL >> 4];
-        a.sb = ys[(eL + 64) >> 4];
-    }
-    a.dx = d32[m * R32 + 8 * b];
-    return a;
-}
-
-// The exact (S, M) of one (row, block) pair for one activation row and the
-// two f32 scale products, as the pair table holds them.
-template <uint32_t DT>
-__device__ __forceinline__ i32x4 pair_part(const u32x4& hdr, const u32x4& qv, const Q6KRaw& raw, const ActLane& a,
-                                           int l) {
-    i32x4 v;
-    if constexpr (DT == DT_Q4_K) {
-        const Q4KLane w = q4k_lane(hdr, qv, l);
-        v.x = group8_sum(q4k_part(w, a.ya, a.yh));
-        v.y = group8_sum(w.mm * a.sa);
-        v.z = __float_as_int(w.d * a.dx);
-        v.w = __float_as_int(w.dmin * a.dx);
-    } else {
-        const Q6KLane w = q6k_lane(raw, l);
-        v.x = group8_sum(q6k_part(w, a.ya, a.yh, a.sa, a.sb));
-        v.y = 0;
-        v.z = __float_as_int(w.d * a.dx);
-        v.w = 0;
-    }
-    return v;
-}
-
 // Pairs are numbered block-major (p = b*R + r), and group g of an iteration
 // takes pairs p0 + U*g + [0, U): with U dividing R these are U rows of one
 // block, so the group's activation for the iteration is one block's. Its
