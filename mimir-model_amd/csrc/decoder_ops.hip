@@ -628,31 +628,52 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
             __syncthreads();
         }
         if (tid < DS) {
-            // the chain in key order, four keys per LDS read of each operand
+            // the chain in key order, 16 keys per batch of LDS reads (four
+            // keys per read of each operand); the next batch's reads are
+            // issued before this batch's multiply-adds, so the chain waits
+            // on LDS only once
             const float* e = sc + c0;
             const VT* vd = vb + tid * vstride;
-            int64_t j = 0;
-            for (; j + 16 <= rows; j += 16) {
-                float4 ev[4], vv[4];
+            using VR = typename std::conditional<F16, uint2, float4>::type;
+            auto fetch = [&](int64_t j, float4 (&ev)[4], VR (&vr)[4]) {
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
                     ev[u] = *(const float4*)(e + j + 4 * u);
-                    if constexpr (F16) {
-                        const uint2 h = *(const uint2*)(vd + j + 4 * u);
-                        vv[u] = make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(h.x & 0xFFFF)),
-                                            (float)__builtin_bit_cast(_Float16, (uint16_t)(h.x >> 16)),
-                                            (float)__builtin_bit_cast(_Float16, (uint16_t)(h.y & 0xFFFF)),
-                                            (float)__builtin_bit_cast(_Float16, (uint16_t)(h.y >> 16)));
-                    } else {
-                        vv[u] = *(const float4*)(vd + j + 4 * u);
-                    }
+                    vr[u] = *(const VR*)(vd + j + 4 * u);
                 }
+            };
+            auto chain16 = [&](const float4 (&ev)[4], const VR (&vr)[4]) {
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
-                    acc = __builtin_fmaf(ev[u].x, vv[u].x, acc);
-                    acc = __builtin_fmaf(ev[u].y, vv[u].y, acc);
-                    acc = __builtin_fmaf(ev[u].z, vv[u].z, acc);
-                    acc = __builtin_fmaf(ev[u].w, vv[u].w, acc);
+                    float4 vv;
+                    if constexpr (F16) {
+                        vv = make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(vr[u].x & 0xFFFF)),
+                                         (float)__builtin_bit_cast(_Float16, (uint16_t)(vr[u].x >> 16)),
+                                         (float)__builtin_bit_cast(_Float16, (uint16_t)(vr[u].y & 0xFFFF)),
+                                         (float)__builtin_bit_cast(_Float16, (uint16_t)(vr[u].y >> 16)));
+                    } else {
+                        vv = vr[u];
+                    }
+                    acc = __builtin_fmaf(ev[u].x, vv.x, acc);
+                    acc = __builtin_fmaf(ev[u].y, vv.y, acc);
+                    acc = __builtin_fmaf(ev[u].z, vv.z, acc);
+                    acc = __builtin_fmaf(ev[u].w, vv.w, acc);
+                }
+            };
+            int64_t j = 0;
+            if (rows >= 16) {
+                float4 eA[4], eB[4];
+                VR vA[4], vB[4];
+                fetch(0, eA, vA);
+                for (; j + 32 <= rows; j += 32) {
+                    fetch(j + 16, eB, vB);
+                    chain16(eA, vA);
+                    if (j + 48 <= rows) fetch(j + 32, eA, vA);
+                    chain16(eB, vB);
+                }
+                if (j + 16 <= rows) {  // the batch already in eA/vA
+                    chain16(eA, vA);
+                    j += 16;
                 }
             }
             for (; j < rows; j++) acc = __builtin_fmaf(e[j], (float)vd[j], acc);

@@ -57,11 +57,20 @@ __device__ __forceinline__ bool quantize_block_lds(const float4 (&v)[4], int b, 
     const float amax = row16_max(m);
     const bool quant = amax > 0.f && amax <= 0x1p60f;
     const float inv = quant ? 1.0f / amax : 0.f;
+    // the fast rounding for all 16 (branch-free), the exact one where it
+    // cannot decide (about one element in 2^11)
+    int qs[16];
+    bool fast[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) fast[i] = quant_rne_fast(xv[i], amax, inv, qs[i]);
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        if (quant && !fast[i]) qs[i] = quant_rne(xv[i], amax, inv);
     uint32_t w[4] = {0, 0, 0, 0};
     int s16 = 0;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-        const int q = quant ? quant_rne(xv[i], amax, inv) : 0;
+        const int q = quant ? qs[i] : 0;
         s16 += q;
         w[i >> 2] |= (uint32_t)(q & 0xFF) << (8 * (i & 3));
     }

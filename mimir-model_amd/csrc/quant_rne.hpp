@@ -49,4 +49,17 @@ MIMG_HD inline int quant_rne(float x, float amax, float inv) {
     return (int)q;
 }
 
+// The fast path of quant_rne alone, branch-free: q = rint(f32(127x)*inv),
+// and whether that is the rounding of q* (false: call quant_rne). Same
+// expressions as quant_rne's fast path, so the two agree wherever this one
+// answers.
+MIMG_HD inline bool quant_rne_fast(float x, float amax, float inv, int& q) {
+    const float rf = (127.0f * x) * inv;
+    const float nf = __builtin_rintf(rf);
+    const float df = rf - nf;  // exact (Sterbenz)
+    const bool ok = amax >= 0x1p-120f && __builtin_fabsf(df) <= 0.5f - 0x1p-12f;
+    q = ok ? (int)nf : 0;  // |nf| <= 127 when ok
+    return ok;
+}
+
 }  // namespace mimg

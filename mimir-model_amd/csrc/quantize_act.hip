@@ -74,7 +74,11 @@ __device__ __forceinline__ bool qa_chunk(const float4 v, int64_t row, int64_t e0
     int qv[4];
     const bool quant = !bbad && amax > 0.f;
     const float inv = quant ? 1.0f / amax : 0.f;
-    for (int k = 0; k < 4; k++) qv[k] = quant ? quant_rne(xv[k], amax, inv) : 0;
+    bool fast[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) fast[k] = quant_rne_fast(xv[k], amax, inv, qv[k]);
+#pragma unroll
+    for (int k = 0; k < 4; k++) qv[k] = !quant ? 0 : fast[k] ? qv[k] : quant_rne(xv[k], amax, inv);
     uint32_t packed = (uint32_t)(qv[0] & 0xFF) | ((uint32_t)(qv[1] & 0xFF) << 8) |
                       ((uint32_t)(qv[2] & 0xFF) << 16) | ((uint32_t)(qv[3] & 0xFF) << 24);
     *(uint32_t*)(a.q + row * K + e0) = packed;

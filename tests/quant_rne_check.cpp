@@ -40,6 +40,11 @@ int main(int argc, char** argv) {
         if (!(std::fabs(x) <= amax) || !(amax > 0)) return;
         const float inv = 1.0f / amax;
         const int got = mimg::quant_rne(x, amax, inv), want = exact_rne(x, amax);
+        int fq;
+        if (mimg::quant_rne_fast(x, amax, inv, fq) && fq != want) {
+            if (bad < 10) printf("fast path: x=%a amax=%a got %d want %d\n", x, amax, fq, want);
+            bad++;
+        }
         checked++;
         if (got != want) {
             if (bad < 10) printf("x=%a amax=%a got %d want %d\n", x, amax, got, want);
