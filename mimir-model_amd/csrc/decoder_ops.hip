@@ -365,6 +365,237 @@ __global__ __launch_bounds__(256) void att_scores_kernel(const float* __restrict
     }
 }
 
+// One query's attention in one launch (decode): a workgroup per (DG dims,
+// head, query) computes all of the query's scores itself (the workgroups of
+// one head repeat them, each score in the same order), then the softmax and
+// the ordered weighted sum of its dims. The steps and their float order are
+// those of att_scores_kernel and att_wsum_kernel:
+//   score j: lane c of a group of eight runs l_c = fma(q[8m+c], k_j[8m+c],
+//     l_c) over m, the group adds the eight as att_reduce8 does (here with
+//     DPP moves; only lane 0's sum is used, and its partners are the same),
+//     times 1/sqrt(D);
+//   max, NaN check, Cephes exp for the first n&~7 keys and the f64 exp for
+//   the rest, eight stride-8 lane sums + HSUM + the tail in order;
+//   per dim acc = fma(e_j, v_j[d], acc) in key order, then acc / sum.
+// Keys are read with one load per lane and element, two keys per group in
+// flight while the previous two are summed; the values of the workgroup's
+// dims are staged dim-major in LDS; the lane sums (wave 1) run beside the
+// chain (wave 0).
+// Lane i of a row of 16 reads lane (i - n) mod 16 under row_ror:n, so
+// row_ror:12 gives lane i lane i+4 (lanes 0..3 of each group of eight read
+// lanes 4..7 of the same group).
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_ROR4 = 0x12C;
+
+__device__ __forceinline__ float dpp_f(float v, int ctrl) {
+    const int x = __float_as_int(v);
+    switch (ctrl) {
+    case DPP_XOR1: return __int_as_float(__builtin_amdgcn_update_dpp(0, x, DPP_XOR1, 0xF, 0xF, true));
+    case DPP_XOR2: return __int_as_float(__builtin_amdgcn_update_dpp(0, x, DPP_XOR2, 0xF, 0xF, true));
+    default: return __int_as_float(__builtin_amdgcn_update_dpp(0, x, DPP_ROR4, 0xF, 0xF, true));
+    }
+}
+
+// att_reduce8's sum at lane 0 of each group of eight: with four,
+// ((l0+l1)+(l2+l3))+((l4+l5)+(l6+l7)); otherwise ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)).
+// (The row rotation gives lanes 0..3 their partners c+4, all lane 0 needs.)
+__device__ __forceinline__ float reduce8_lane0(float l, bool four) {
+    float a = l + (four ? dpp_f(l, DPP_XOR1) : dpp_f(l, DPP_ROR4));
+    float b = a + (four ? dpp_f(a, DPP_XOR2) : dpp_f(a, DPP_XOR1));
+    return b + (four ? dpp_f(b, DPP_ROR4) : dpp_f(b, DPP_XOR2));
+}
+
+template <bool F16, int D, int DG>
+__global__ __launch_bounds__(256) void att_decode_kernel(const float* __restrict__ q, const void* kc, const void* vc,
+                                                         const int64_t* __restrict__ kend,
+                                                         const int64_t* __restrict__ kstart, int H, int Hkv, int64_t C,
+                                                         int64_t maxk, float* __restrict__ out) {
+    extern __shared__ float att_lds[];
+    __shared__ float red[4];
+    __shared__ float lane_sum[8];
+    __shared__ int nan_any;
+    using VT = typename std::conditional<F16, _Float16, float>::type;
+    constexpr int DM = D / 8;
+    constexpr int PER_KEY = DG * (int)sizeof(VT) / 16;  // 16-byte pieces of a key's DG values
+    constexpr int VPAD = F16 ? 8 : 4;
+    const int d0 = blockIdx.x * DG, h = blockIdx.y, t = blockIdx.z, tid = threadIdx.x, w = tid >> 6;
+    const int lane = tid & 63, c = lane & 7, grp = tid >> 3;
+    const AttRange r = att_range(kend, kstart, t, C, maxk);
+    const int64_t n = r.n;
+    float* orow = out + ((int64_t)t * H + h) * D + d0;
+    if (n <= 0) {
+        if (tid < DG) orow[tid] = 0.f;
+        return;
+    }
+    const int hk = h / (H / Hkv);
+    const int64_t base = (int64_t)hk * C + r.k0;  // first visible cache row
+    const int64_t mk = (maxk + 3) & ~(int64_t)3, vstride = mk + VPAD;
+    float* sc = att_lds;            // [mk]: scores, then exponentials
+    VT* vb = (VT*)(att_lds + mk);   // [DG][vstride]: values, dim-major
+    if (tid == 0) nan_any = 0;
+
+    // 1. Scores: group grp takes keys grp, grp+32, ..., two at a time, the
+    // next two's loads issued before the current two are summed.
+    const float scale = (float)(1.0 / sqrt((double)D));
+    const float* qr = q + ((int64_t)t * H + h) * D;
+    float qv[DM];
+#pragma unroll
+    for (int m = 0; m < DM; m++) qv[m] = qr[8 * m + c];
+    const int64_t n4 = n - n % 4;
+    float mx = -INFINITY;
+    int isnan_local = 0;
+    auto kload = [&](int64_t j, float (&kv)[DM]) {
+        const int64_t a = base + (j < n ? j : n - 1);  // past the end: the last key, unstored
+#pragma unroll
+        for (int m = 0; m < DM; m++) kv[m] = kv_load<F16>(kc, a * D + 8 * m + c);
+    };
+    auto score = [&](int64_t j, const float (&kv)[DM]) {
+        float l = 0.f;
+#pragma unroll
+        for (int m = 0; m < DM; m++) l = __builtin_fmaf(qv[m], kv[m], l);
+        const float p = reduce8_lane0(l, j < n4) * scale;
+        if (c == 0 && j < n) {
+            sc[j] = p;
+            isnan_local |= p != p;
+            mx = fmaxf(mx, p);
+        }
+    };
+    {
+        float ka[DM], kb[DM], kc2[DM], kd[DM];
+        int64_t j = grp;
+        kload(j, ka);
+        kload(j + 32, kb);
+        for (; j < n; j += 64) {
+            kload(j + 64, kc2);
+            kload(j + 96, kd);
+            score(j, ka);
+            score(j + 32, kb);
+#pragma unroll
+            for (int m = 0; m < DM; m++) {
+                ka[m] = kc2[m];
+                kb[m] = kd[m];
+            }
+        }
+    }
+
+    // 2. The values of this workgroup's dims, dim-major into LDS.
+    const int64_t vbase = base * D + d0;
+    for (int64_t i = tid; i < n * PER_KEY; i += 256) {
+        const int64_t row = i / PER_KEY, piece = i % PER_KEY;
+        if constexpr (F16) {
+            const uint4 raw = *(const uint4*)((const _Float16*)vc + vbase + row * D + piece * 8);
+            const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
+            VT* dst = vb + piece * 8 * vstride + row;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                dst[(2 * e) * vstride] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
+                dst[(2 * e + 1) * vstride] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
+            }
+        } else {
+            const float4 v4 = *(const float4*)((const float*)vc + vbase + row * D + piece * 4);
+            VT* dst = vb + piece * 4 * vstride + row;
+            dst[0] = v4.x;
+            dst[vstride] = v4.y;
+            dst[2 * vstride] = v4.z;
+            dst[3 * vstride] = v4.w;
+        }
+    }
+
+    // 3. Max and NaN over the scores, then the exponentials.
+    mx = wave_max_f32(mx);
+    __syncthreads();  // scores in LDS; nan_any cleared
+    if (lane == 0) red[w] = mx;
+    if (isnan_local) nan_any = 1;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    if (nan_any || __builtin_isinf(mx)) {
+        if (tid < DG) orow[tid] = __builtin_nanf("");
+        return;
+    }
+    const int64_t nv = n >= 8 ? (n & ~(int64_t)7) : 0;
+    for (int64_t j = tid; j < n; j += 256) {
+        const float x = sc[j] - mx;
+        sc[j] = j < nv ? cephes_exp(x) : (float)exp((double)x);
+    }
+    __syncthreads();
+
+    // 4. Wave 1: the eight stride-8 lane sums; wave 0: the chain of its dims.
+    float acc = 0.f;
+    if (w == 1 && lane < 8) {
+        float sl = 0.f;
+        int64_t j = lane;
+        for (; j + 120 < nv; j += 128) {
+            float e[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) e[u] = sc[j + 8 * u];
+#pragma unroll
+            for (int u = 0; u < 16; u++) sl = sl + e[u];
+        }
+        for (; j < nv; j += 8) sl = sl + sc[j];
+        lane_sum[lane] = sl;
+    } else if (w == 0 && lane < DG) {
+        const VT* vd = vb + lane * vstride;
+        using VR = typename std::conditional<F16, uint2, float4>::type;
+        auto fetch = [&](int64_t j, float4 (&ev)[4], VR (&vr)[4]) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                ev[u] = *(const float4*)(sc + j + 4 * u);
+                vr[u] = *(const VR*)(vd + j + 4 * u);
+            }
+        };
+        auto chain16 = [&](const float4 (&ev)[4], const VR (&vr)[4]) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                float4 vv;
+                if constexpr (F16) {
+                    vv = make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(vr[u].x & 0xFFFF)),
+                                     (float)__builtin_bit_cast(_Float16, (uint16_t)(vr[u].x >> 16)),
+                                     (float)__builtin_bit_cast(_Float16, (uint16_t)(vr[u].y & 0xFFFF)),
+                                     (float)__builtin_bit_cast(_Float16, (uint16_t)(vr[u].y >> 16)));
+                } else {
+                    vv = vr[u];
+                }
+                acc = __builtin_fmaf(ev[u].x, vv.x, acc);
+                acc = __builtin_fmaf(ev[u].y, vv.y, acc);
+                acc = __builtin_fmaf(ev[u].z, vv.z, acc);
+                acc = __builtin_fmaf(ev[u].w, vv.w, acc);
+            }
+        };
+        int64_t j = 0;
+        if (n >= 16) {
+            float4 eA[4], eB[4];
+            VR vA[4], vB[4];
+            fetch(0, eA, vA);
+            for (; j + 32 <= n; j += 32) {
+                fetch(j + 16, eB, vB);
+                chain16(eA, vA);
+                if (j + 48 <= n) fetch(j + 32, eA, vA);
+                chain16(eB, vB);
+            }
+            if (j + 16 <= n) {
+                chain16(eA, vA);
+                j += 16;
+            }
+        }
+        for (; j < n; j++) acc = __builtin_fmaf(sc[j], (float)vd[j], acc);
+    }
+    __syncthreads();
+    if (w == 0 && lane < DG) {
+        float sum = ((lane_sum[0] + lane_sum[4]) + (lane_sum[1] + lane_sum[5])) +
+                    ((lane_sum[2] + lane_sum[6]) + (lane_sum[3] + lane_sum[7]));
+        for (int64_t j = nv; j < n; j++) sum = sum + sc[j];
+        orow[lane] = acc / sum;
+    }
+}
+
+constexpr int64_t ATT_DEC_MAXK = 256;
+
+template <bool F16, int D>
+static size_t att_decode_lds(int64_t maxk) {
+    constexpr int DG = 32, VPAD = F16 ? 8 : 4, ESZ = F16 ? 2 : 4;
+    const int64_t mk = (maxk + 3) & ~(int64_t)3;
+    return (size_t)(mk * 4 + (int64_t)DG * (mk + VPAD) * ESZ);
+}
+
 // Many queries (prefill): a workgroup per (64 dims, head, four queries),
 // wave w for query 4z + w, lane for one dim. The waves share each staged
 // chunk of values when their queries share the first visible cache entry;
@@ -877,6 +1108,27 @@ hipError_t launch_attention(const float* q, const void* kc, const void* vc, cons
             hipLaunchKernelGGL(att_wsum_q4_kernel<false>, g2, dim3(256), lds, s, vc, kend, kstart, T, H, Hkv, D, C, maxk,
                                ws, out);
         return hipGetLastError();
+    }
+    // few queries, D = 64 or 128, at most ATT_DEC_MAXK keys: one launch per
+    // query (att_decode_kernel). Its workgroups compute all of a query's
+    // scores each, which beats the two-kernel path (scores spread over
+    // tiles of 64 keys) only for short contexts (measured on MI355X at
+    // D = 128: 4.7 against 7.5 us at 64 keys, 17.9 against 13.6 at 640).
+    if ((D == 64 || D == 128) && T <= 65535 && maxk <= ATT_DEC_MAXK) {
+        constexpr size_t LDS_MAX = 160 * 1024 - 64;
+        const dim3 g((unsigned)(D / 32), (unsigned)H, (unsigned)T);
+#define ATT_DEC(F, DD)                                                                                           \
+    const size_t lds = att_decode_lds<F, DD>(maxk);                                                              \
+    if (lds <= LDS_MAX) {                                                                                        \
+        hipLaunchKernelGGL((att_decode_kernel<F, DD, 32>), g, dim3(256), lds, s, q, kc, vc, kend, kstart, H, Hkv, \
+                           C, maxk, out);                                                                        \
+        return hipGetLastError();                                                                                \
+    }
+        if (f16 && D == 128) { ATT_DEC(true, 128) }
+        else if (f16) { ATT_DEC(true, 64) }
+        else if (D == 128) { ATT_DEC(false, 128) }
+        else { ATT_DEC(false, 64) }
+#undef ATT_DEC
     }
     const dim3 grid(tiles, (unsigned)H, (unsigned)T);
     if (f16) launch_att_scores<true, 1>(grid, q, kc, kend, kstart, T, H, Hkv, D, C, maxk, ws, s);

@@ -138,7 +138,7 @@ def test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, slo
 
 
 @pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
-@pytest.mark.parametrize("C,D", [(700, 128), (1100, 64), (300, 8)])
+@pytest.mark.parametrize("C,D", [(700, 128), (1100, 64), (300, 8), (250, 128), (256, 64)])
 def test_attention_long_context_bitexact(gpu, oracle, rt, f16, C, D):
     """Long visible ranges: many score tiles and several value chunks."""
     test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, 3, 4, 2, D, 1, C=C)
