@@ -813,10 +813,11 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
         }
     }
     __syncthreads();
-    // eight stride-8 lane sums in key order, then HSUM and the tail
-    if (tid < 8) {
+    // eight stride-8 lane sums in key order (wave 1, beside the chain of
+    // wave 0); HSUM and the tail at the end
+    if (tid >= 64 && tid < 72) {
         float s = 0.f;
-        int64_t j = tid;
+        int64_t j = tid - 64;
         for (; j + 120 < nv; j += 128) {
             float e[16];
 #pragma unroll
@@ -825,12 +826,8 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
             for (int u = 0; u < 16; u++) s = s + e[u];
         }
         for (; j < nv; j += 8) s = s + sc[j];
-        lane_sum[tid] = s;
+        lane_sum[tid - 64] = s;
     }
-    __syncthreads();
-    float sum = ((lane_sum[0] + lane_sum[4]) + (lane_sum[1] + lane_sum[5])) +
-                ((lane_sum[2] + lane_sum[6]) + (lane_sum[3] + lane_sum[7]));
-    for (int64_t j = nv; j < n; j++) sum = sum + sc[j];
     float acc = 0.f;
     for (int64_t c0 = 0; c0 < n; c0 += vch) {
         const int64_t rows = n - c0 < vch ? n - c0 : vch;
@@ -910,7 +907,13 @@ __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int
             for (; j < rows; j++) acc = __builtin_fmaf(e[j], (float)vd[j], acc);
         }
     }
-    if (tid < DS) orow[tid] = acc / sum;
+    __syncthreads();
+    if (tid < DS) {
+        float sum = ((lane_sum[0] + lane_sum[4]) + (lane_sum[1] + lane_sum[5])) +
+                    ((lane_sum[2] + lane_sum[6]) + (lane_sum[3] + lane_sum[7]));
+        for (int64_t j = nv; j < n; j++) sum = sum + sc[j];
+        orow[tid] = acc / sum;
+    }
 }
 
 // swiglu.v1 (reference interp/fast.go:487-498): the reference splits the n
