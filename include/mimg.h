@@ -166,6 +166,22 @@ int mimg_linear_a8_group_dev(const uint64_t *w, int count, const float *x, int64
                              const float *const *bias, int block, float *const *y, void *ws,
                              uint64_t ws_bytes, void *stream);
 
+/* rms_norm.v1 in front of mimg_linear_a8_group_dev at one activation row,
+ * blocks of 256, in one launch: x_out = x + resid (x copied when resid is
+ * NULL), h = rms_norm(x_out) * scale (reference interp/fast.go:434-485), and
+ * y[i] = h . W_i^T (+ bias[i]) as dequant_matmul_a8 computes it
+ * (interp/builtins.go dequant_matmul_a8.v2, q8.go:50-97). Bit for bit
+ * mimg_rms_norm_dev followed by mimg_linear_a8_group_dev. x_out must not
+ * overlap x or resid (every workgroup reads them). Returns MIMG_NOT_HANDLED
+ * (nothing launched) unless K is a multiple of 1024 up to 4096, every
+ * weight is Q4_K or Q6_K and the group's rows fit one launch: the caller
+ * then makes the two calls. No reference counterpart beyond the two ops it
+ * equals (importer/llama.go:423-534 writes the norm and the q, k, v
+ * products as separate graph nodes). */
+int mimg_rms_norm_linear_a8_group_dev(const uint64_t *w, int count, const float *x, const float *resid,
+                                      const float *scale, float eps, float *x_out, const float *const *bias,
+                                      float *const *y, void *stream);
+
 /* The product alone, for activations already quantized into ws by
  * mimg_quantize_act_dev with the same rows, K and block. */
 int mimg_matmul_a8_quantized_dev(uint64_t w, const float *x, int64_t rows, const float *bias, int block,

@@ -16,6 +16,7 @@
 // above 2^60); q = RoundToEven(127 x / amax) of the exact quotient
 // (quant_rne.hpp); d = amax/127 (correctly rounded f32 division); per-16 and
 // per-32 sums of q.
+#include "decoder_math.hpp"
 #include "f32path.hpp"
 #include "kquant_lane.hpp"
 #include "mimg_device.hpp"
@@ -106,7 +107,128 @@ struct FusedArgs {
     const float* x;
     int64_t K;
     int nb;
+    // rms_norm in front (NORM kernels): y = rms_norm(x + resid) * scale is
+    // quantized; x + resid goes to x_out (tile 0 of matrix 0 writes it)
+    const float* resid;
+    const float* scale;
+    float eps;
+    float* x_out;
 };
+
+// rms_norm.v1 of the row (rms_norm_kernel's order: thread t sums the float4s
+// t + 256k of x + resid, then the wave and workgroup sums), and the
+// quantization of y straight from that layout: float4 t + 256k is lane t%64
+// of chunk 4k + t/64, one block of 256 per wave (quantize_act.hip's
+// layout). y also goes to LDS (yl) for the float32 path of refused rows.
+// Returns this thread's refusal flag. K % 1024 == 0, K <= 4096.
+constexpr int NORM_R = 4;  // float4s per thread of the normed row, K <= 4096
+
+// The row's loads, issued before the weights (the load counter retires in
+// order): x, resid, scale as float4s t + 256k (clamped; used where inside).
+struct NormRegs {
+    float4 x[NORM_R], r[NORM_R], s[NORM_R];
+};
+__device__ __forceinline__ void norm_load(const FusedArgs& A, NormRegs& N) {
+    const int n4 = (int)(A.K / 4);
+#pragma unroll
+    for (int k = 0; k < NORM_R; k++) {
+        const int i = min((int)threadIdx.x + 256 * k, n4 - 1);
+        N.x[k] = ((const float4*)A.x)[i];
+        if (A.resid) N.r[k] = ((const float4*)A.resid)[i];
+        if (A.scale) N.s[k] = ((const float4*)A.scale)[i];
+    }
+}
+
+// A barrier for LDS only: it waits for this wave's LDS operations, not for
+// its outstanding global loads (the weights).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ bool norm_quantize_lds(const FusedArgs& A, const NormRegs& N, bool write_x, float* yl,
+                                                  double* part, const QuantLds& Q) {
+    constexpr int NR = NORM_R;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int n4 = (int)(A.K / 4);
+    float4 v[NR];
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < NR; k++) {
+        const int i = t + 256 * k;
+        v[k] = N.x[k];
+        if (i < n4) {
+            if (A.resid) {
+                v[k].x = v[k].x + N.r[k].x;
+                v[k].y = v[k].y + N.r[k].y;
+                v[k].z = v[k].z + N.r[k].z;
+                v[k].w = v[k].w + N.r[k].w;
+            }
+            if (write_x) ((float4*)A.x_out)[i] = v[k];
+            ss += (double)v[k].x * (double)v[k].x + (double)v[k].y * (double)v[k].y +
+                  (double)v[k].z * (double)v[k].z + (double)v[k].w * (double)v[k].w;
+        }
+    }
+    ss = wave_sum_f64(ss);
+    if (lane == 0) part[w] = ss;
+    lds_barrier();
+    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
+    const float inv = (float)(1.0 / sqrt((double)(float)(tot / (double)A.K) + (double)A.eps));
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < NR; k++) {
+        const int i = t + 256 * k;
+        if (i >= n4) continue;  // uniform within the wave (K % 1024 == 0)
+        float4 o = {v[k].x * inv, v[k].y * inv, v[k].z * inv, v[k].w * inv};
+        if (A.scale) {
+            const float4 s4 = N.s[k];
+            o.x = o.x * s4.x;
+            o.y = o.y * s4.y;
+            o.z = o.z * s4.z;
+            o.w = o.w * s4.w;
+        }
+        ((float4*)yl)[i] = o;
+        // block b = i / 64 of 256: this wave's, lane's four at 4*lane
+        const int b = i >> 6;
+        const float xv[4] = {o.x, o.y, o.z, o.w};
+        float av[4] = {fabsf(o.x), fabsf(o.y), fabsf(o.z), fabsf(o.w)};
+        bool lbad = false;
+        float m = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            lbad |= !(av[e] <= 0x1p60f);
+            m = fmaxf(m, av[e]);
+        }
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_QUAD_1032, 0xF, 0xF, false)));
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_QUAD_2301, 0xF, 0xF, false)));
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_HALF_MIRROR, 0xF, 0xF, false)));
+        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_ROW_MIRROR, 0xF, 0xF, false)));
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        const float amax = m;
+        const bool bbad = __any(lbad);
+        bad |= lbad;
+        const bool quant = !bbad && amax > 0.f;
+        const float qinv = quant ? 1.0f / amax : 0.f;
+        int qv[4];
+        bool fast[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) fast[e] = quant_rne_fast(xv[e], amax, qinv, qv[e]);
+#pragma unroll
+        for (int e = 0; e < 4; e++) qv[e] = !quant ? 0 : fast[e] ? qv[e] : quant_rne(xv[e], amax, qinv);
+        *(uint32_t*)(Q.q + 4 * i) = (uint32_t)(qv[0] & 0xFF) | ((uint32_t)(qv[1] & 0xFF) << 8) |
+                                    ((uint32_t)(qv[2] & 0xFF) << 16) | ((uint32_t)(qv[3] & 0xFF) << 24);
+        const int s4 = qv[0] + qv[1] + qv[2] + qv[3];
+        int s16 = s4 + __builtin_amdgcn_mov_dpp(s4, DPP_QUAD_1032, 0xF, 0xF, false);
+        s16 += __builtin_amdgcn_mov_dpp(s16, DPP_QUAD_2301, 0xF, 0xF, false);
+        const int s32 = s16 + __builtin_amdgcn_mov_dpp(s16, DPP_HALF_MIRROR, 0xF, 0xF, false);
+        if ((lane & 3) == 0) Q.ys16[i >> 2] = (int16_t)s16;
+        if ((lane & 7) == 0) Q.xs[i >> 3] = (int16_t)s32;
+        if (lane == 0) Q.dx[b] = amax / 127.0f;
+    }
+    return bad;
+}
 
 template <uint32_t DT>
 struct FusedRaw;
@@ -146,8 +268,9 @@ __device__ __forceinline__ ActLane act_lane_lds(const QuantLds& Q, int b, int l)
 // are U rows of one block, whose activation is read from LDS once. Weights
 // are addressed as 32-bit offsets from the tile's base; the row flags and
 // bias are loaded first and looked at last.
-template <uint32_t DT, int U, bool SHARED>
-__device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F, int tile, uint8_t* smem) {
+template <uint32_t DT, int U, bool SHARED, bool NORM>
+__device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F, int tile, uint8_t* smem,
+                                           double* npart) {
     constexpr int BYTES = DT == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     const int nb = A.nb, R = F.R, np = R * nb;
     const int64_t K = A.K;
@@ -160,6 +283,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     Q.ys16 = (int16_t*)(Q.xs + K / 32);
     i32x4* part = (i32x4*)(smem + ((K + nb * 4 + (K / 32) * 2 + (K / 16) * 2 + 15) & ~(int64_t)15));
     int* refl = (int*)(part + (size_t)R * nb);  // [R]: the row's weight is refused
+    float* yl = (float*)(smem + (((size_t)((uint8_t*)(refl + R) - smem) + 15) & ~(size_t)15));  // NORM: [K] y
     const int64_t tbyte = (int64_t)row0 * F.rb;
     const uint8_t* Wt = F.W + (tbyte & ~(int64_t)3);
     const uint32_t tadj = (uint32_t)(tbyte & 3), rb32 = (uint32_t)F.rb;
@@ -170,7 +294,9 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     // the quantizer waits for x alone.
     const int j = t & 15, bq = t >> 4;
     float4 xv[4];
-    load_x16(A.x, min(bq, nb - 1), j, xv);
+    NormRegs N;
+    if constexpr (NORM) norm_load(A, N);
+    else load_x16(A.x, min(bq, nb - 1), j, xv);
     const int frow = min(row0 + min(t, R - 1), F.N - 1);
     const int wr = F.wref[frow];
     const float bias = F.bias ? F.bias[frow] : 0.f;
@@ -201,11 +327,17 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     load(0);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. Quantize x into LDS while the weights arrive.
-    bool bad = bq < nb ? quantize_block_lds(xv, bq, j, Q) : false;
-    for (int b = bq + 16; b < nb; b += 16) {  // rows longer than 4096
-        load_x16(A.x, b, j, xv);
-        bad |= quantize_block_lds(xv, b, j, Q);
+    // 2. Quantize x (NORM: rms_norm(x + resid) * scale) into LDS while the
+    // weights arrive.
+    bool bad;
+    if constexpr (NORM) {
+        bad = norm_quantize_lds(A, N, blockIdx.x == 0, yl, npart, Q);
+    } else {
+        bad = bq < nb ? quantize_block_lds(xv, bq, j, Q) : false;
+        for (int b = bq + 16; b < nb; b += 16) {  // rows longer than 4096
+            load_x16(A.x, b, j, xv);
+            bad |= quantize_block_lds(xv, b, j, Q);
+        }
     }
     const bool row_refused = __syncthreads_or(bad ? 1 : 0) != 0;
 
@@ -255,28 +387,30 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     for (int r = g; r < R; r += 32) {
         const int row = row0 + r;
         if (row < F.N && (refl[r] != 0 || row_refused)) {
-            float res = f32dot_g8<DT>(F.W + (int64_t)row * F.rb, A.x, K, true);
+            float res = f32dot_g8<DT>(F.W + (int64_t)row * F.rb, NORM ? (const float*)yl : A.x, K, true);
             if (F.bias) res += F.bias[row];
             if (l == 0) F.y[row] = res;
         }
     }
 }
 
-template <int U, bool SHARED>
+template <int U, bool SHARED, bool NORM>
 __global__ __launch_bounds__(256) void gemv_a8k_fused_kernel(FusedArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ double npart[4];
     int mi = 0;
     if (A.nmat > 1 && (int)blockIdx.x >= A.mat[1].tile0) mi = 1;
     if (A.nmat > 2 && (int)blockIdx.x >= A.mat[2].tile0) mi = 2;
     const FusedMat F = mi == 0 ? A.mat[0] : mi == 1 ? A.mat[1] : A.mat[2];
     const int tile = (int)blockIdx.x - F.tile0;
-    if (F.dt == DT_Q4_K) fused_body<DT_Q4_K, U, SHARED>(A, F, tile, smem);
-    else fused_body<DT_Q6_K, U, SHARED>(A, F, tile, smem);
+    if (F.dt == DT_Q4_K) fused_body<DT_Q4_K, U, SHARED, NORM>(A, F, tile, smem, npart);
+    else fused_body<DT_Q6_K, U, SHARED, NORM>(A, F, tile, smem, npart);
 }
 
-static size_t fused_lds_bytes(int64_t K, int nb, int maxR) {
+static size_t fused_lds_bytes(int64_t K, int nb, int maxR, bool norm = false) {
     size_t q = ((size_t)K + nb * 4 + (K / 32) * 2 + (K / 16) * 2 + 15) & ~(size_t)15;
-    return q + (size_t)maxR * nb * 16 + (size_t)maxR * 4;
+    const size_t base = q + (size_t)maxR * nb * 16 + (size_t)maxR * 4;
+    return norm ? ((base + 15) & ~(size_t)15) + (size_t)K * 4 : base;
 }
 
 // Rows per workgroup for a matrix: pairs per workgroup at most 32*U*2 (two
@@ -297,12 +431,17 @@ bool fused_gemv_ok(const DevWeight* const* ws, int nmat) {
     return fused_lds_bytes(K, (int)(K / 256), fused_rows((int)(K / 256), K)) <= 48 * 1024;
 }
 
-hipError_t launch_gemv_a8k_fused(const DevWeight* const* ws, int nmat, const float* x,
-                                 const float* const* bias, float* const* y, hipStream_t stream) {
+static hipError_t launch_fused(const DevWeight* const* ws, int nmat, const float* x, const float* resid,
+                               const float* scale, float eps, float* x_out, bool norm, const float* const* bias,
+                               float* const* y, hipStream_t stream) {
     if (!fused_gemv_ok(ws, nmat)) return hipErrorInvalidValue;
     FusedArgs A;
     A.nmat = nmat;
     A.x = x;
+    A.resid = resid;
+    A.scale = scale;
+    A.eps = eps;
+    A.x_out = x_out;
     A.K = ws[0]->k;
     A.nb = (int)(A.K / 256);
     int tiles = 0, maxR = 1;
@@ -323,13 +462,36 @@ hipError_t launch_gemv_a8k_fused(const DevWeight* const* ws, int nmat, const flo
             maxR = max(maxR, F.R);
         }
     }
-    const size_t lds = fused_lds_bytes(A.K, A.nb, maxR);
+    const size_t lds = fused_lds_bytes(A.K, A.nb, maxR, norm);
     // every matrix has the same R (it depends on K only)
-    if (A.mat[0].R % 4 == 0)
-        hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, true>), dim3(tiles), dim3(256), lds, stream, A);
+    const bool shared = A.mat[0].R % 4 == 0;
+    if (norm && shared)
+        hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, true, true>), dim3(tiles), dim3(256), lds, stream, A);
+    else if (norm)
+        hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, false, true>), dim3(tiles), dim3(256), lds, stream, A);
+    else if (shared)
+        hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, true, false>), dim3(tiles), dim3(256), lds, stream, A);
     else
-        hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, false>), dim3(tiles), dim3(256), lds, stream, A);
+        hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, false, false>), dim3(tiles), dim3(256), lds, stream, A);
     return hipGetLastError();
+}
+
+hipError_t launch_gemv_a8k_fused(const DevWeight* const* ws, int nmat, const float* x,
+                                 const float* const* bias, float* const* y, hipStream_t stream) {
+    return launch_fused(ws, nmat, x, nullptr, nullptr, 0.f, nullptr, false, bias, y, stream);
+}
+
+bool fused_norm_ok(const DevWeight* const* ws, int nmat) {
+    const int64_t K = ws[0]->k;
+    return fused_gemv_ok(ws, nmat) && K % 1024 == 0 && K <= 256 * 4 * NORM_R &&
+           fused_lds_bytes(K, (int)(K / 256), fused_rows((int)(K / 256), K), true) <= 64 * 1024;
+}
+
+hipError_t launch_gemv_a8k_fused_norm(const DevWeight* const* ws, int nmat, const float* x, const float* resid,
+                                      const float* scale, float eps, float* x_out, const float* const* bias,
+                                      float* const* y, hipStream_t stream) {
+    if (!fused_norm_ok(ws, nmat) || !x_out) return hipErrorInvalidValue;
+    return launch_fused(ws, nmat, x, resid, scale, eps, x_out, true, bias, y, stream);
 }
 
 }  // namespace mimg

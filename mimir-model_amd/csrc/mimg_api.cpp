@@ -753,6 +753,46 @@ int mimg_linear_a8_dev(uint64_t wh, const float* x, int64_t rows, const float* b
     return mimg_linear_a8_group_dev(&wh, 1, x, rows, bs, block, ys, ws, ws_bytes, stream);
 }
 
+int mimg_rms_norm_linear_a8_group_dev(const uint64_t* whs, int count, const float* x, const float* resid,
+                                      const float* scale, float eps, float* x_out, const float* const* bias,
+                                      float* const* y, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!whs || !y || count < 1 || count > 3) return fail(MIMG_ERR_ARG, "a group holds 1 to 3 weights, got %d", count);
+    if (!x || !x_out || !aligned(x, 16) || !aligned(x_out, 16) || (resid && !aligned(resid, 16)) ||
+        (scale && !aligned(scale, 16)))
+        return fail(MIMG_ERR_ARG, "x, x_out, resid and scale must be non-null (resid, scale may be null) and 16-byte aligned");
+    Weight* w[3];
+    const DevWeight* dw[3];
+    int64_t total_n = 0;
+    for (int i = 0; i < count; i++) {
+        if ((rc = lookup(whs[i], &w[i]))) return rc;
+        if (w[i]->dw.k != w[0]->dw.k) return fail(MIMG_ERR_ARG, "the weights of a group must share K");
+        bool use_f32;
+        if ((rc = a8_checks(w[i], 1, 256, &use_f32))) return rc;
+        if (use_f32) return fail(MIMG_NOT_HANDLED, "%s has no 8-bit kernel for blocks of 256", dt_name(w[i]->dw.dt));
+        dw[i] = &w[i]->dw;
+        total_n += w[i]->dw.n;
+    }
+    const int64_t K = w[0]->dw.k;
+    const uint64_t xb = (uint64_t)K * 4;
+    auto overlap = [xb](const void* a, const void* b) {
+        return b && (uintptr_t)a < (uintptr_t)b + xb && (uintptr_t)b < (uintptr_t)a + xb;
+    };
+    if (overlap(x_out, x) || overlap(x_out, resid))
+        return fail(MIMG_ERR_ARG, "x_out must not overlap x or resid (every workgroup reads them)");
+    if (total_n > fused_max_n() || !fused_norm_ok(dw, count))
+        return fail(MIMG_NOT_HANDLED, "no fused norm GEMV for K %lld, %lld rows", (long long)K, (long long)total_n);
+    float* ys[3];
+    const float* bs[3];
+    for (int i = 0; i < count; i++) {
+        ys[i] = y[i];
+        bs[i] = bias ? bias[i] : nullptr;
+    }
+    HIP_TRY(launch_gemv_a8k_fused_norm(dw, count, x, resid, scale, eps, x_out, bs, ys, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
 int mimg_dequantize_dev(uint32_t dtype, const void* src, uint64_t len, float* dst, int64_t n, void* stream) {
     int rc = ensure_device();
     if (rc) return rc;

@@ -84,6 +84,13 @@ hipError_t launch_gemm_a8k(const DevWeight& w, const ActPtrs& a, int64_t rows, i
 bool fused_gemv_ok(const DevWeight* const* ws, int nmat);
 hipError_t launch_gemv_a8k_fused(const DevWeight* const* ws, int nmat, const float* x,
                                  const float* const* bias, float* const* y, hipStream_t stream);
+// The same with rms_norm.v1 in front: y = rms_norm(x + resid) * scale is
+// quantized and multiplied; x + resid is written to x_out (not in place: the
+// workgroups all read x). One activation row, K a multiple of 1024, <= 4096.
+bool fused_norm_ok(const DevWeight* const* ws, int nmat);
+hipError_t launch_gemv_a8k_fused_norm(const DevWeight* const* ws, int nmat, const float* x, const float* resid,
+                                      const float* scale, float eps, float* x_out, const float* const* bias,
+                                      float* const* y, hipStream_t stream);
 
 hipError_t launch_gemv_q8_0_a8(const DevWeight& w, const ActPtrs& a, int64_t rows,
                                int64_t total_rows, const float* x, const float* bias, float* y,

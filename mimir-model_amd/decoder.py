@@ -151,6 +151,10 @@ class Decoder:
             buf.zero()
         self.invf = B.from_array(inv_freq(c))
         self.x, self.h, self.ao = B(R * E * 4), B(R * E * 4), B(R * E * 4)
+        # the fused norm + q/k/v GEMV writes x + resid to the other buffer
+        self.x_pair = (self.x, B(E * 4))
+        self.x_alt = self.x_pair[1]
+        self.norm_fused = {}  # names -> whether the fused norm GEMV takes them
         self.q, self.o = B(R * H * D * 4), B(R * H * D * 4)
         self.k, self.v = B(R * Hkv * D * 4), B(R * Hkv * D * 4)
         self.g, self.u = B(R * F * 4), B(R * F * 4)
@@ -194,11 +198,26 @@ class Decoder:
         With 8-bit activations and one block size for the group, the norm
         and the quantization of h are one launch and the products take the
         quantized h (bit for bit the separate ops); at one row, q/k/v
-        (single_fused) instead use the GEMV that quantizes inside."""
+        (single_fused) take one launch for the norm and the products (x +
+        resid lands in the other x buffer), or where that kernel does not
+        take the shape, the GEMV that quantizes inside."""
         c, s = self.c, self.stream.handle
         E = c.embed
         ws = [self.w[n] for n in names]
         blocks = {self._block(w) for w in ws}
+        key = tuple(names)
+        if self.a8 and single_fused and T == 1 and self.norm_fused.get(key, True):
+            # one launch: x + resid into the other x buffer, the norm and the
+            # q/k/v products (NotHandled: launched nothing, shape not taken)
+            bs = [None if b is None or b not in self.vec else self.vec[b].ptr for b in (biases or [None] * len(names))]
+            try:
+                mimg.rms_norm_linear_a8_group_dev(ws, self.x.ptr, resid, self.vec[norm].ptr, c.norm_eps,
+                                                  self.x_alt.ptr, bs if any(bs) else None, ys, s)
+                self.norm_fused[key] = True
+                self.x, self.x_alt = self.x_alt, self.x
+                return
+            except mimg.NotHandled:
+                self.norm_fused[key] = False
         if self.a8 and len(blocks) == 1 and not (single_fused and T == 1) and E <= 32768:
             block = blocks.pop()
             mimg.rms_norm_quant_dev(self.x.ptr, resid, self.vec[norm].ptr, c.norm_eps, T, E, self.h.ptr, block,
@@ -222,6 +241,7 @@ class Decoder:
         pos = pos or self.pos.ptr
         cidx = cidx or self.cidx.ptr
         kstart = (kstart or self.kstart.ptr) if self.slots > 1 else None
+        self.x, self.x_alt = self.x_pair  # every forward the same buffers (graphs replay them)
         mimg.embedding_dev(self.w["token_embd.weight"], ids, T, self.x.ptr, s)
         resid = None  # the previous sublayer's output, added to x by the next norm
         for l in range(c.layers):

@@ -45,6 +45,8 @@ SIGNATURES = {
     "mimg_linear_a8_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P, _U64, _P]),
     "mimg_linear_a8_group_dev": (_I, [ctypes.POINTER(_U64), _I, _P, _I64, ctypes.POINTER(_P), _I,
                                       ctypes.POINTER(_P), _P, _U64, _P]),
+    "mimg_rms_norm_linear_a8_group_dev": (_I, [ctypes.POINTER(_U64), _I, _P, _P, _P, ctypes.c_float, _P,
+                                               ctypes.POINTER(_P), ctypes.POINTER(_P), _P]),
     "mimg_matmul_a8_quantized_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P, _U64, _P]),
     "mimg_linear_f32_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
     "mimg_linear_f32_mfma_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
@@ -239,6 +241,18 @@ def linear_a8_group_dev(weights, x_ptr, rows, bias_ptrs, block, y_ptrs, ws_ptr, 
     bs = None if bias_ptrs is None else (_P * n)(*[_P(p) if p else None for p in bias_ptrs])
     _check(load().mimg_linear_a8_group_dev(hs, n, _P(x_ptr), rows, bs, block, ys,
                                            _P(ws_ptr) if ws_ptr else None, ws_bytes, _P(stream)))
+
+
+def rms_norm_linear_a8_group_dev(weights, x_ptr, resid_ptr, scale_ptr, eps, x_out_ptr, bias_ptrs, y_ptrs, stream):
+    """One row: x_out = x + resid, h = rms_norm(x_out) * scale, y_ptrs[i] =
+    h . W_i^T (+ bias) in one launch; raises NotHandled where the fused
+    kernel does not apply (then call rms_norm_dev and linear_a8_group_dev)."""
+    n = len(weights)
+    hs = (_U64 * n)(*[w.handle for w in weights])
+    ys = (_P * n)(*[_P(p) for p in y_ptrs])
+    bs = None if bias_ptrs is None else (_P * n)(*[_P(p) if p else None for p in bias_ptrs])
+    _check(load().mimg_rms_norm_linear_a8_group_dev(hs, n, _P(x_ptr), _o(resid_ptr), _o(scale_ptr), eps,
+                                                    _P(x_out_ptr), bs, ys, _P(stream)))
 
 
 def matmul_a8_quantized_dev(w, x_ptr, rows, bias_ptr, block, y_ptr, ws_ptr, ws_bytes, stream):

@@ -377,6 +377,95 @@ def test_rms_norm_quant_equals_two_launches(gpu, rt, rows, n, block, resid):
     assert q0 == q1
 
 
+_NORM_GROUPS = {
+    # K, [(dtype, rows)], resid, case
+    "llama8b_qkv": (4096, [(Q4_K, 512), (Q4_K, 128), (Q6_K, 128)], True, None),
+    "llama1b_qkv": (2048, [(Q4_K, 2048), (Q4_K, 512), (Q6_K, 512)], False, None),
+    "refused_row": (1024, [(Q6_K, 300)], True, "huge"),
+    "refused_weight": (3072, [(Q4_K, 96), (Q6_K, 64)], True, "inf_scale"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(_NORM_GROUPS))
+def test_rms_norm_linear_group_equals_two_calls(gpu, oracle, rt, name):
+    """The norm fused in front of the one-row q/k/v GEMV: x_out = x + resid
+    exactly, and y bit for bit rms_norm_dev then linear_a8_group_dev (and the
+    reference product of that normed row), with refused activation rows
+    (an element of h above 2^60) and refused weight rows (a non-finite
+    block scale) on the float32 path."""
+    K, specs, resid, case = _NORM_GROUPS[name]
+    rng = np.random.default_rng(K + len(specs))
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    r = rng.standard_normal((1, K)).astype(np.float32) if resid else None
+    sc = rng.standard_normal(K).astype(np.float32)
+    if case == "huge":
+        sc[777] = np.float32(1e30)  # |h[777]| far above 2^60: the row is refused
+    wbs = []
+    for i, (dt, n) in enumerate(specs):
+        wb = oracle.synthetic_weight(dt, n, K, seed=40 + i)
+        if case == "inf_scale" and i == 0:
+            wb = bytearray(wb.tobytes())
+            o = len(wb) // n * 17 + 144
+            wb[o:o + 2] = b"\x00\x7c"  # row 17, block 1: d = +inf
+            wb = np.frombuffer(bytes(wb), np.uint8)
+        wbs.append(wb)
+    W = [gpu.Weight(wb, dt, n, K) for wb, (dt, n) in zip(wbs, specs)]
+    if case == "inf_scale":
+        assert W[0].info()[1] == 1
+    bias = [rng.standard_normal(n).astype(np.float32) if i != 1 else None for i, (_, n) in enumerate(specs)]
+    s = rt.Stream()
+    dx, dsc = dev(rt, x), dev(rt, sc)
+    dr = dev(rt, r) if resid else None
+    dbs = [dev(rt, b) if b is not None else None for b in bias]
+    bptrs = [b.ptr if b else 0 for b in dbs]
+
+    xo = rt.DeviceBuffer(x.nbytes)
+    ys = [rt.DeviceBuffer(n * 4) for _, n in specs]
+    gpu.rms_norm_linear_a8_group_dev(W, dx.ptr, dr.ptr if dr else None, dsc.ptr, 1e-5, xo.ptr, bptrs,
+                                     [y.ptr for y in ys], s.handle)
+    s.sync()
+    got_x = xo.download(np.float32)
+    got = [y.download(np.float32) for y in ys]
+
+    dx2, dh = dev(rt, x), rt.DeviceBuffer(x.nbytes)
+    ys2 = [rt.DeviceBuffer(n * 4) for _, n in specs]
+    gpu.rms_norm_dev(dx2.ptr, dr.ptr if dr else None, dsc.ptr, 1e-5, 1, K, dh.ptr, s.handle)
+    gpu.linear_a8_group_dev(W, dh.ptr, 1, bptrs, 256, [y.ptr for y in ys2], None, 0, s.handle)
+    s.sync()
+    want_x = dx2.download(np.float32)
+    h = dh.download(np.float32).reshape(1, K)
+    want = [y.download(np.float32) for y in ys2]
+    assert np.array_equal(got_x.view(np.uint32), want_x.view(np.uint32))
+    assert np.array_equal(got_x, (x + r if resid else x).ravel())
+    if case == "huge":
+        assert np.abs(h).max() > 2.0 ** 60
+    for i, ((dt, n), wb) in enumerate(zip(specs, wbs)):
+        assert np.array_equal(got[i].view(np.uint32), want[i].view(np.uint32)), (i, np.flatnonzero(got[i] != want[i])[:5])
+        ref = oracle.linear_a8(h, wb, dt, n, K, bias=bias[i], block=256).ravel()
+        assert np.array_equal(got[i].view(np.uint32), ref.view(np.uint32)), i
+    for w in W:
+        w.release()
+
+
+def test_rms_norm_linear_group_not_handled(gpu, oracle, rt):
+    """Shapes the fused norm GEMV does not take are refused before any launch
+    (NotHandled: the caller makes the two calls), and an x_out that overlaps
+    x is an argument error."""
+    s = rt.Stream()
+    for dt, K in ((Q4_K, 1280), (Q8_0, 1024), (Q4_K, 5120)):
+        w = gpu.Weight(oracle.synthetic_weight(dt, 8, K, seed=3), dt, 8, K)
+        dx, xo, y = rt.DeviceBuffer(K * 4), rt.DeviceBuffer(K * 4), rt.DeviceBuffer(8 * 4)
+        with pytest.raises(gpu.NotHandled):
+            gpu.rms_norm_linear_a8_group_dev([w], dx.ptr, None, None, 1e-5, xo.ptr, None, [y.ptr], s.handle)
+        w.release()
+    w = gpu.Weight(oracle.synthetic_weight(Q4_K, 8, 1024, seed=3), Q4_K, 8, 1024)
+    dx, y = rt.DeviceBuffer(2 * 1024 * 4), rt.DeviceBuffer(8 * 4)
+    with pytest.raises(gpu.MimgError) as e:
+        gpu.rms_norm_linear_a8_group_dev([w], dx.ptr, None, None, 1e-5, dx.ptr + 2048, None, [y.ptr], s.handle)
+    assert not isinstance(e.value, gpu.NotHandled)
+    w.release()
+
+
 @pytest.mark.parametrize("rows,n,block,procs", [(1, 14336, 256, 16), (4, 8192, 256, 7), (3, 1792, 32, 16)])
 def test_swiglu_quant_equals_two_launches(gpu, rt, rows, n, block, procs):
     rng = np.random.default_rng(rows + n)
