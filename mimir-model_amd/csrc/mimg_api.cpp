@@ -284,6 +284,14 @@ static int64_t gemm_min_rows() {
     return v;
 }
 
+// Activation rows (of a chunk of at most eight) from which the GEMV runs
+// on the matrix cores (measured: at 6 and 8 rows it beats the pair kernel,
+// at 4 it does not). MIMG_MFMA_MIN_ROWS overrides, for tuning (9: never).
+static int64_t mfma_min_rows() {
+    static const int64_t v = env_or("MIMG_MFMA_MIN_ROWS", 5);
+    return v;
+}
+
 int matmul_quantized(const Weight* const* w, int count, const float* x, int64_t rows, const float* const* bias,
                      int block, float* const* y, const ActPtrs& a, hipStream_t s) {
     const int64_t K = w[0]->dw.k, R32 = K / 32, R16 = K / 16;
@@ -326,6 +334,8 @@ int matmul_quantized(const Weight* const* w, int count, const float* x, int64_t 
                 }
                 if (mr == 1 && tiles_wpc() > 0 && gemv_tiles_ok(*dws[0], 1))
                     e = launch_gemv_a8k_tiles(dws, n, c, rows, x + r0 * K, bs, ys, (int)tiles_wpc(), s);
+                else if (mr >= mfma_min_rows() && gemv_mfma_ok(dws, n, mr))
+                    e = launch_gemv_a8k_mfma(dws, n, c, mr, rows, x + r0 * K, bs, ys, s);
                 else
                     e = launch_gemv_a8k(dws, n, c, mr, rows, x + r0 * K, bs, ys, s);
             } else {

@@ -61,6 +61,12 @@ hipError_t launch_weight_refusals(uint32_t dt, const uint8_t* w, int64_t n, int6
 // y_i[r*N_i+j] for act rows r in [0, rows) of up to three matrices of one
 // dtype and K (rows <= 8 per launch; `total_rows` is the row count of the
 // whole call, which selects the float32 fallback's order).
+// The decode GEMV for 2..8 activation rows on the int8 matrix cores
+// (gemv_mfma.hip): same arguments and results as launch_gemv_a8k.
+bool gemv_mfma_ok(const DevWeight* const* ws, int nmat, int64_t rows);
+hipError_t launch_gemv_a8k_mfma(const DevWeight* const* ws, int nmat, const ActPtrs& a, int64_t rows,
+                                int64_t total_rows, const float* x, const float* const* bias, float* const* y,
+                                hipStream_t stream);
 hipError_t launch_gemv_a8k(const DevWeight* const* ws, int nmat, const ActPtrs& a, int64_t rows,
                            int64_t total_rows, const float* x, const float* const* bias, float* const* y,
                            hipStream_t stream);

@@ -284,7 +284,7 @@ def _dev_linear(gpu, weights, x, biases=None, group=True, prequant=False):
     return [y.download(np.float32).reshape(rows, w.n) for y, w in zip(ys, weights)]
 
 
-@pytest.mark.parametrize("rows", [1, 3])
+@pytest.mark.parametrize("rows", [1, 3, 8])
 def test_group_qkv_bitexact(gpu, oracle, rows):
     """q, k (Q4_K) and v (Q6_K) sharing one input in one grouped call (a single
     fused launch at one row) equal the separate reference products."""
@@ -311,6 +311,23 @@ def test_pairs_kernel_one_row_bitexact(gpu, oracle, dt, n, k):
     x = oracle.synthetic_acts(1, k, seed=32)
     got = _dev_linear(gpu, [W], x, prequant=True)[0]
     want = oracle.linear_a8(x, wb, dt, n, k, block=256)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K])
+@pytest.mark.parametrize("n,k", [(300, 14336), (4100, 4096), (7, 256), (33, 768)])
+@pytest.mark.parametrize("rows", [5, 8])
+def test_mfma_gemv_bitexact(gpu, oracle, dt, n, k, rows):
+    """5..8 activation rows run on the int8 matrix-core GEMV: ragged last
+    tile of 16 rows, K from one block to 56 (four waves splitting them
+    unevenly), odd block counts (Q6_K rows 2-byte aligned); the same bits
+    as the reference's per-row products."""
+    wb = _weights(oracle, dt, n, k, seed=n + rows)
+    W = gpu.Weight(wb, dt, n, k)
+    x = oracle.synthetic_acts(rows, k, seed=rows + 7)
+    got = _dev_linear(gpu, [W], x, prequant=True)[0]
+    want = oracle.linear_a8(x, wb, dt, n, k, block=256, threads=8)
     W.release()
     assert bits_equal(got, want), first_diff(got, want)
 
