@@ -301,10 +301,12 @@ def main():
     value = step_bytes(M) / (ms_per_step * 1e-3) / 1e9
     log(f"  timed: {args.steps} steps, {ms_per_step * 1e3:.2f} us/step (events), wall {wall * 1e6 / args.steps:.2f} us/step, {value:.1f} GB/s")
 
-    # Roofline of the dominant kernel: the Q4_K GEMV at the gate/up shape
-    # (14336 x 4096, 33 MB), per-launch HIP events on the launch stream,
-    # over distinct rotation copies so every launch reads from HBM.
-    def per_launch(name):
+    # Roofline of the dominant kernel of the step: the Q4_K GEMV launch that
+    # computes gate and up together (2 x 14336 x 4096, 66 MB; the step's
+    # grouped call), per-launch HIP events on the launch stream, over
+    # distinct rotation copies so every launch reads from HBM. The same
+    # kernel on gate alone and the Q6_K down launch are reported beside it.
+    def per_launch(names):
         """The GEMV kernel alone on one matrix: activations quantized once
         beforehand, then a HIP graph of `rotate` back-to-back launches of the
         pair kernel (one per rotation copy, so every launch reads its
@@ -312,13 +314,15 @@ def main():
         events on the launch stream. Returns the average time per launch
         (graph time / launches, so the small gaps between kernels are
         included), the algorithmic bytes per launch and their rate."""
-        _, n, k, dt, _, inp = next(c for c in CFG1 if c[0] == name)
+        cs = [next(c for c in CFG1 if c[0] == name) for name in names]
+        _, n, k, dt, _, inp = cs[0]
         mimg.quantize_act_dev(xd[inp].ptr, M, k, 256, ws[inp].ptr, ws_bytes[inp], stream.handle)
 
         def launches():
             for l in range(args.rotate):
-                mimg.matmul_a8_quantized_dev(layers[l][name], xd[inp].ptr, M, None, 256,
-                                             yd[name].ptr, ws[inp].ptr, ws_bytes[inp], stream.handle)
+                mimg.matmul_a8_quantized_group_dev([layers[l][name] for name in names], xd[inp].ptr, M, None, 256,
+                                                   [yd[name].ptr for name in names], ws[inp].ptr, ws_bytes[inp],
+                                                   stream.handle)
 
         g = hiprt.Graph(stream, launches)
         for _ in range(2):
@@ -330,13 +334,16 @@ def main():
         b.record(stream)
         b.sync()
         us = a.elapsed_ms(b) * 1e3 / (args.roofline_replays * args.rotate)
-        nbytes = launch_bytes(n, k, dt, M)
+        # the activation row is read once per launch; weights and outputs per matrix
+        nbytes = sum(launch_bytes(c[1], c[2], c[3], M) for c in cs) - (len(cs) - 1) * (launch_bytes(0, k, dt, M))
         return us, nbytes, nbytes / (us * 1e-6) / 1e9
 
-    g_us, g_bytes, g_gbs = per_launch("gate")
-    d_us, d_bytes, d_gbs = per_launch("down")
-    log(f"  gate GEMV (Q4_K 14336x4096): {g_us:.2f} us/launch, {g_gbs:.0f} GB/s; "
-        f"down GEMV (Q6_K 4096x14336): {d_us:.2f} us/launch, {d_gbs:.0f} GB/s")
+    r_us, r_bytes, r_gbs = per_launch(["gate", "up"])
+    g_us, g_bytes, g_gbs = per_launch(["gate"])
+    d_us, d_bytes, d_gbs = per_launch(["down"])
+    log(f"  gate+up GEMV (Q4_K 2x14336x4096, one launch): {r_us:.2f} us/launch, {r_gbs:.0f} GB/s; "
+        f"gate alone: {g_us:.2f} us, {g_gbs:.0f} GB/s; down GEMV (Q6_K 4096x14336): {d_us:.2f} us/launch, "
+        f"{d_gbs:.0f} GB/s")
 
     # Prefill: the gate (Q4_K) and down (Q6_K) products
     # at M activation rows on the int8 MFMA GEMM, activations quantized
@@ -401,12 +408,13 @@ def main():
     # HBM bytes per launch of the same kernel at the same shape, from the
     # rocprofv3 FETCH_SIZE / WRITE_SIZE passes summarised in profiles/ (the
     # counters cannot be read from inside this process).
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"gemv_pairs_q4k_gate_m{M}_traffic.md")
-    if os.path.exists(tpath):
-        for line in open(tpath):
-            if line.startswith("bytes_per_launch:"):
-                traffic = int(line.split(":", 1)[1].strip())
+    def traffic_of(which):
+        tpath = os.path.join(ROOT, "profiles", f"gemv_pairs_q4k_{which}_m{M}_traffic.md")
+        if os.path.exists(tpath):
+            for line in open(tpath):
+                if line.startswith("bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+        return None
 
     result = {
         "metric": METRIC,
@@ -432,14 +440,17 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(g_gbs, 1),
+            "achieved": round(r_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(g_gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "kernel": f"gemv_a8k_pairs_kernel<Q4_K,M={M}> at 14336x4096 (gate/up), pre-quantized activations",
-            "launch_bytes": g_bytes,
-            "avg_launch_us": round(g_us, 3),
+            "frac": round(r_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic_of("gateup"),
+            "kernel": f"{'gemv_a8k_mfma_kernel<Q4_K>' if M >= 5 else f'gemv_a8k_pairs_kernel<Q4_K,M={M}>'}: gate and up "
+                      "(2 x 14336x4096) in one launch as the step groups them, pre-quantized activations",
+            "launch_bytes": r_bytes,
+            "avg_launch_us": round(r_us, 3),
+            "gate_alone": {"avg_launch_us": round(g_us, 3), "launch_bytes": g_bytes, "achieved": round(g_gbs, 1),
+                           "traffic": traffic_of("gate")},
             "q6k_down": {"avg_launch_us": round(d_us, 3), "launch_bytes": d_bytes, "achieved": round(d_gbs, 1)},
         },
         "prefill": {
