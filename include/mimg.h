@@ -172,7 +172,7 @@ int mimg_linear_a8_group_dev(const uint64_t *w, int count, const float *x, int64
  * y[i] = h . W_i^T (+ bias[i]) as dequant_matmul_a8 computes it
  * (interp/builtins.go dequant_matmul_a8.v2, q8.go:50-97). Bit for bit
  * mimg_rms_norm_dev followed by mimg_linear_a8_group_dev. x_out must not
- * overlap x or resid (every workgroup reads them). Returns MIMG_NOT_HANDLED
+ * overlap x, resid or scale (every workgroup reads them). Returns MIMG_NOT_HANDLED
  * (nothing launched) unless K is a multiple of 1024 up to 4096, every
  * weight is Q4_K or Q6_K and the group's rows fit one launch: the caller
  * then makes the two calls. No reference counterpart beyond the two ops it

@@ -789,8 +789,8 @@ int mimg_rms_norm_linear_a8_group_dev(const uint64_t* whs, int count, const floa
     auto overlap = [xb](const void* a, const void* b) {
         return b && (uintptr_t)a < (uintptr_t)b + xb && (uintptr_t)b < (uintptr_t)a + xb;
     };
-    if (overlap(x_out, x) || overlap(x_out, resid))
-        return fail(MIMG_ERR_ARG, "x_out must not overlap x or resid (every workgroup reads them)");
+    if (overlap(x_out, x) || overlap(x_out, resid) || overlap(x_out, scale))
+        return fail(MIMG_ERR_ARG, "x_out must not overlap x, resid or scale (every workgroup reads them)");
     if (total_n > fused_max_n() || !fused_norm_ok(dw, count))
         return fail(MIMG_NOT_HANDLED, "no fused norm GEMV for K %lld, %lld rows", (long long)K, (long long)total_n);
     float* ys[3];
