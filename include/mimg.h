@@ -209,7 +209,9 @@ int mimg_rms_norm_quant_dev(float *x, const float *resid, const float *scale, fl
 /* swiglu.v1 over g, u [rows, n] (as mimg_swiglu_dev over rows*n elements
  * with GOMAXPROCS = procs) and the 8-bit quantizer on its output, in one
  * launch: out is written and quantized into ws. Bit for bit the two calls.
- * 16-byte aligned; n a multiple of block, at most 32768. */
+ * 16-byte aligned; n a multiple of block, at most 32768; out must not
+ * overlap g or u (MIMG_ERR_ARG): the row's refusal flag is screened from g
+ * and u while out is written. */
 int mimg_swiglu_quant_dev(const float *g, const float *u, float *out, int64_t rows, int64_t n, int procs, int block,
                           void *ws, uint64_t ws_bytes, void *stream);
 

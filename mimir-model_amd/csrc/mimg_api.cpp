@@ -585,6 +585,14 @@ int mimg_swiglu_quant_dev(const float* g, const float* u, float* out, int64_t ro
     if ((rc = qa_checks(rows, n, block, ws, ws_bytes, &l)) || rows == 0) return rc;
     if (!g || !u || !out || !aligned(g, 16) || !aligned(u, 16) || !aligned(out, 16))
         return fail(MIMG_ERR_ARG, "g, u and out must be 16-byte aligned");
+    // One workgroup per row screens the whole of g and u for the refusal
+    // flag while the others write out: out must be a buffer of its own.
+    const uint64_t nbytes = (uint64_t)rows * (uint64_t)n * 4;
+    auto overlap = [nbytes](const void* a, const void* b) {
+        return (uintptr_t)a < (uintptr_t)b + nbytes && (uintptr_t)b < (uintptr_t)a + nbytes;
+    };
+    if (overlap(out, g) || overlap(out, u))
+        return fail(MIMG_ERR_ARG, "swiglu_quant: out must not overlap g or u");
     const int64_t total = rows * n, w = procs < total ? procs : total;
     int64_t chunk = total;
     if (w > 1) chunk = total / (w * 8) > 1 ? total / (w * 8) : 1;

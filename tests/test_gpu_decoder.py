@@ -466,6 +466,20 @@ def test_rms_norm_linear_group_not_handled(gpu, oracle, rt):
     w.release()
 
 
+def test_swiglu_quant_out_must_be_its_own_buffer(gpu, rt):
+    """swiglu_quant screens g and u for the refusal flag while it writes
+    out, so an out that overlaps g or u is refused before any launch."""
+    rows, n = 1, 1024
+    dg, du = rt.DeviceBuffer(rows * n * 4), rt.DeviceBuffer(rows * n * 4)
+    wsb = gpu.a8_workspace_bytes(rows, n)
+    ws = rt.DeviceBuffer(wsb)
+    s = rt.Stream()
+    for out in (dg.ptr, du.ptr, dg.ptr + 2048):
+        with pytest.raises(gpu.MimgError) as e:
+            gpu.swiglu_quant_dev(dg.ptr, du.ptr, out, rows, n, 16, 256, ws.ptr, wsb, s.handle)
+        assert not isinstance(e.value, gpu.NotHandled)
+
+
 @pytest.mark.parametrize("rows,n,block,procs", [(1, 14336, 256, 16), (4, 8192, 256, 7), (3, 1792, 32, 16)])
 def test_swiglu_quant_equals_two_launches(gpu, rt, rows, n, block, procs):
     rng = np.random.default_rng(rows + n)
