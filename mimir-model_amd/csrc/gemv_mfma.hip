@@ -1,8 +1,9 @@
-// Decode GEMV for 2..8 activation rows (dequant_matmul_a8.v2, block = 256)
-// on the int8 matrix cores. At these row counts the pair kernel's integer
-// dot products (eight lanes per (row, block, activation row)) cost more VALU
-// time than the weights take to stream; one v_mfma_i32_16x16x64_i8 instead
-// computes 16 weight rows x 16 activation rows x 64 k.
+// Decode GEMV for 4..8 activation rows (dequant_matmul_a8.v2, block = 256;
+// correct for 2..8) on the int8 matrix cores. At these row counts the pair
+// kernel's integer dot products (eight lanes per (row, block, activation
+// row)) cost more VALU time than the weights take to stream; one
+// v_mfma_i32_16x16x64_i8 instead computes 16 weight rows x 16 activation
+// rows x 64 k.
 //
 // Numerics: the same exact int32 block sums as the pair kernel and the GEMM
 // (reference internal/kernels/q8k.go dotQ8KRef, q8k_test.go:38-102; the

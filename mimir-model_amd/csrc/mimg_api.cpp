@@ -285,10 +285,11 @@ static int64_t gemm_min_rows() {
 }
 
 // Activation rows (of a chunk of at most eight) from which the GEMV runs
-// on the matrix cores (measured: at 6 and 8 rows it beats the pair kernel,
-// at 4 it does not). MIMG_MFMA_MIN_ROWS overrides, for tuning (9: never).
+// on the matrix cores (measured, cfg1 layer set: 100 against 105 us per
+// step at 4 rows, 99 against 95 at 3). MIMG_MFMA_MIN_ROWS overrides, for
+// tuning (9: never).
 static int64_t mfma_min_rows() {
-    static const int64_t v = env_or("MIMG_MFMA_MIN_ROWS", 5);
+    static const int64_t v = env_or("MIMG_MFMA_MIN_ROWS", 4);
     return v;
 }
 

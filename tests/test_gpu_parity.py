@@ -317,9 +317,9 @@ def test_pairs_kernel_one_row_bitexact(gpu, oracle, dt, n, k):
 
 @pytest.mark.parametrize("dt", [Q4_K, Q6_K])
 @pytest.mark.parametrize("n,k", [(300, 14336), (4100, 4096), (7, 256), (33, 768)])
-@pytest.mark.parametrize("rows", [5, 8])
+@pytest.mark.parametrize("rows", [4, 5, 8])
 def test_mfma_gemv_bitexact(gpu, oracle, dt, n, k, rows):
-    """5..8 activation rows run on the int8 matrix-core GEMV: ragged last
+    """4..8 activation rows run on the int8 matrix-core GEMV: ragged last
     tile of 16 rows, K from one block to 56 (four waves splitting them
     unevenly), odd block counts (Q6_K rows 2-byte aligned); the same bits
     as the reference's per-row products."""
