@@ -284,6 +284,17 @@ static int64_t gemm_min_rows() {
     return v;
 }
 
+// Every workgroup of a product reads all of x (the float32 path of refused
+// rows included) while others write y: y[i] must not overlap x.
+static int check_outputs(const float* x, int64_t rows, int64_t K, const int64_t* N, float* const* y, int count) {
+    const uintptr_t xa = (uintptr_t)x, xe = xa + (uint64_t)rows * (uint64_t)K * 4;
+    for (int i = 0; i < count; i++) {
+        const uintptr_t ya = (uintptr_t)y[i], ye = ya + (uint64_t)rows * (uint64_t)N[i] * 4;
+        if (y[i] && ya < xe && xa < ye) return fail(MIMG_ERR_ARG, "output %d overlaps the input x", i);
+    }
+    return MIMG_OK;
+}
+
 // Activation rows (of a chunk of at most eight) from which the GEMV runs
 // on the matrix cores (measured, cfg1 layer set: 100 against 105 us per
 // step at 4 rows, 99 against 95 at 3). MIMG_MFMA_MIN_ROWS overrides, for
@@ -641,10 +652,13 @@ int mimg_matmul_a8_quantized_group_dev(const uint64_t* whs, int count, const flo
         return fail(MIMG_ERR_WORKSPACE, "workspace %llu < %llu bytes", (unsigned long long)ws_bytes, (unsigned long long)l.total);
     const float* bs[3];
     float* ys[3];
+    int64_t ns[3];
     for (int i = 0; i < count; i++) {
         bs[i] = bias ? bias[i] : nullptr;
         ys[i] = y[i];
+        ns[i] = w[i]->dw.n;
     }
+    if ((rc = check_outputs(x, rows, w[0]->dw.k, ns, ys, count))) return rc;
     return matmul_quantized(w, count, x, rows, bs, block, ys, act_ptrs((void*)ws, l), (hipStream_t)stream);
 }
 
@@ -686,6 +700,7 @@ int mimg_matmul_a8_quantized_dev(uint64_t wh, const float* x, int64_t rows, cons
     if (!x || !y || !ws || !aligned(ws, 256)) return fail(MIMG_ERR_ARG, "null or misaligned pointer");
     ActLayout l = act_layout(rows, w->dw.k);
     if (ws_bytes < l.total) return fail(MIMG_ERR_WORKSPACE, "workspace %llu < %llu bytes", (unsigned long long)ws_bytes, (unsigned long long)l.total);
+    if ((rc = check_outputs(x, rows, w->dw.k, &w->dw.n, &y, 1))) return rc;
     const Weight* ws1[1] = {w};
     const float* bs1[1] = {bias};
     float* ys1[1] = {y};
@@ -726,8 +741,9 @@ int mimg_linear_a8_group_dev(const uint64_t* whs, int count, const float* x, int
     if (rows == 0) return MIMG_OK;
     if (!x || !aligned(x, 16)) return fail(MIMG_ERR_ARG, "x must be 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
-    int64_t total_n = 0;
-    for (int i = 0; i < count; i++) total_n += w[i]->dw.n;
+    int64_t total_n = 0, ns[3];
+    for (int i = 0; i < count; i++) total_n += (ns[i] = w[i]->dw.n);
+    if ((rc = check_outputs(x, rows, w[0]->dw.k, ns, y, count))) return rc;
     if (!any_f32 && rows == 1 && block == 256 && w[0]->dw.k <= fused_max_k() && total_n <= fused_max_n() &&
         fused_gemv_ok(dw, count)) {
         float* ys[3];

@@ -332,6 +332,29 @@ def test_mfma_gemv_bitexact(gpu, oracle, dt, n, k, rows):
     assert bits_equal(got, want), first_diff(got, want)
 
 
+def test_output_overlapping_input_refused(gpu, oracle):
+    """Every workgroup reads all of x while others write y, so an output
+    that overlaps the input is an argument error (before any launch), for
+    the one-row fused launch, the pre-quantized products and the groups."""
+    import hiprt
+
+    k, n = 1024, 64
+    W = gpu.Weight(_weights(oracle, Q4_K, n, k, seed=5), Q4_K, n, k)
+    buf = hiprt.DeviceBuffer(8 * k * 4)
+    wsb = gpu.a8_workspace_bytes(8, k)
+    ws = hiprt.DeviceBuffer(wsb)
+    s = hiprt.Stream()
+    for rows in (1, 8):
+        with pytest.raises(gpu.MimgError) as e:
+            gpu.linear_a8_group_dev([W], buf.ptr, rows, None, 256, [buf.ptr + 256], ws.ptr, wsb, s.handle)
+        assert not isinstance(e.value, gpu.NotHandled)
+        with pytest.raises(gpu.MimgError):
+            gpu.matmul_a8_quantized_dev(W, buf.ptr, rows, None, 256, buf.ptr, ws.ptr, wsb, s.handle)
+        with pytest.raises(gpu.MimgError):
+            gpu.matmul_a8_quantized_group_dev([W], buf.ptr, rows, None, 256, [buf.ptr], ws.ptr, wsb, s.handle)
+    W.release()
+
+
 @pytest.mark.parametrize("dt", [Q4_K, Q6_K])
 def test_fused_refusals_large_k(gpu, oracle, dt):
     """The fused one-row kernel at K = 14336 with a refused weight row, then
