@@ -151,7 +151,8 @@ int mimg_quantize_act_dev(const float *x, int64_t rows, int64_t k, int block, vo
                           uint64_t ws_bytes, void *stream);
 
 /* mimg_dequant_matmul_a8 on device buffers: quantizes x into ws, then runs
- * the product. y is [rows, N] row-major. */
+ * the product. y is [rows, N] row-major and must not overlap x (here and in
+ * the other product entry points on device buffers: MIMG_ERR_ARG). */
 int mimg_linear_a8_dev(uint64_t w, const float *x, int64_t rows, const float *bias, int block, float *y,
                        void *ws, uint64_t ws_bytes, void *stream);
 
