@@ -17,8 +17,9 @@ To measure HBM rather than the 256 MB MALL, the weights are copied into
 and step s uses layer s mod rotate. Each layer's step is captured in a HIP
 graph. Timed region: exactly --steps steps between two synchronisations.
 
-value = bytes per step / time per step, bytes by BASELINE.md's formula
-(sum of N*(K/QK)*block_bytes + K*4 + N*4 over the seven matrices).
+value = bytes per step / time per step, bytes = the sum of
+N*(K/QK)*block_bytes + K*4 + N*4 over the seven matrices (the benchmark's
+published formula for this metric).
 
 The "decode" section runs whole greedy generation on the GPU decoder
 (mimir-model_amd/decoder.py) with random Q4_K_M weights of two model shapes
