@@ -21,6 +21,12 @@ value = bytes per step / time per step, bytes = the sum of
 N*(K/QK)*block_bytes + K*4 + N*4 over the seven matrices (the benchmark's
 published formula for this metric).
 
+roofline: the step's longest launch, the Q4_K GEMV computing gate and up
+together, timed alone (graphs of --rotate launches over the rotation copies,
+HIP events on the launch stream), its algorithmic bytes over that time
+against 8 TB/s; traffic from the committed rocprofv3 FETCH/WRITE summary.
+The same kernel on gate alone and the Q6_K down launch are reported beside it.
+
 The "decode" section runs whole greedy generation on the GPU decoder
 (mimir-model_amd/decoder.py) with random Q4_K_M weights of two model shapes
 (BASELINE.json configs[3] and [4]): a Llama-3.2-1B shape with a 32-token
