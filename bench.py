@@ -223,7 +223,21 @@ def decode_bench(name, log, graph=True, cpu=False, batches=(1, 8)):
         }
         if cpu and batch == 1 and name == "llama1b":
             out[key]["cpu_restatement"] = decode_cpu_check(cfg, tensors, prompts[0], ids[0], 8, log)
+        if batch == 1:
+            b1_ids = ids[0]
+        elif P == runs[0][0] and runs[0][2] == 1:
+            # slot 0 holds the batch-1 run's prompt: the same ids
+            out[key]["slot0_ids_equal_batch1"] = bool(np.array_equal(ids[0], b1_ids))
         log(f"  {key}: {out[key]}")
+    if cpu and name == "llama8b":
+        # The 512-token prompt is too long for the CPU restatement within the
+        # bench's budget: a 32-token prompt (seed 7) and 8 greedy ids on both.
+        short = np.random.default_rng(7).integers(0, cfg["vocab"], (1, 32)).astype(np.int32)
+        dec.reset()
+        gids = dec.generate(short, 8, graph=graph)
+        dec.reset()
+        out["llama8b_P32_N8_B1_cpu_check"] = {"cpu_restatement": decode_cpu_check(cfg, tensors, short[0], gids[0], 8,
+                                                                                   log)}
     del dec
     tensors.clear()
     return out
@@ -239,7 +253,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
-    ap.add_argument("--prefill-rows", default="512,2048",
+    ap.add_argument("--prefill-rows", default="64,512,2048",
                     help="activation rows of the prefill GEMM measurements (comma list; empty to skip)")
     ap.add_argument("--decode-batches", default="1,8", help="batch sizes of the llama8b decode runs")
     ap.add_argument("--decode", default="llama1b,llama8b",
@@ -348,6 +362,66 @@ def main():
     r_us, r_bytes, r_gbs = per_launch(["gate", "up"])
     g_us, g_bytes, g_gbs = per_launch(["gate"])
     d_us, d_bytes, d_gbs = per_launch(["down"])
+
+    # The read ceiling of the roofline launch, measured here: a plain
+    # streaming read (mimg_stream_read_dev: 16-byte nontemporal loads, every
+    # load of a thread in flight at once, nothing computed) of the same
+    # gate and up bytes in one launch, timed the same way over the rotation
+    # copies; the best of three workgroup sizes.
+    sink = hiprt.DeviceBuffer(4096)
+
+    def read_ceiling(names, per):
+        def launches():
+            for l in range(args.rotate):
+                mimg.stream_read_dev([(layers[l][name].info()[0], weight_bytes(*next((c[1], c[2], c[3])
+                                                                               for c in CFG1 if c[0] == name)))
+                                      for name in names], per, sink.ptr, stream.handle)
+
+        g = hiprt.Graph(stream, launches)
+        for _ in range(2):
+            g.launch(stream)
+        a, b = hiprt.Event(), hiprt.Event()
+        a.record(stream)
+        for _ in range(args.roofline_replays):
+            g.launch(stream)
+        b.record(stream)
+        b.sync()
+        g.destroy()
+        return a.elapsed_ms(b) * 1e3 / (args.roofline_replays * args.rotate)
+
+    gu_weight_bytes = sum(weight_bytes(c[1], c[2], c[3]) for c in CFG1 if c[0] in ("gate", "up"))
+    ceil = {per: read_ceiling(["gate", "up"], per) for per in (4, 8, 16)}
+    c_per = min(ceil, key=ceil.get)
+    c_us = ceil[c_per]
+    c_gbs = gu_weight_bytes / (c_us * 1e-6) / 1e9
+    log(f"  read ceiling (gate+up weight bytes, one launch): {c_us:.2f} us, {c_gbs:.0f} GB/s "
+        f"({', '.join(f'{p}x16B: {u:.2f} us' for p, u in ceil.items())})")
+
+    # the single 4096 x 4096 Q4_K product (the q matrix,
+    # weight seed 0) of one activation row (seed 1), as the reference calls
+    # it: dequant_matmul_a8.v2, x quantized inside the one-row launch; a
+    # graph of --rotate calls over the rotation copies.
+    x0 = hiprt.DeviceBuffer.from_array(np.random.default_rng(1).standard_normal((1, 4096), dtype=np.float32))
+    y0 = hiprt.DeviceBuffer(4096 * 4)
+
+    def cfg0_launches():
+        for l in range(args.rotate):
+            mimg.linear_a8_group_dev([layers[l]["q"]], x0.ptr, 1, None, 256, [y0.ptr], ws[0].ptr, ws_bytes[0],
+                                     stream.handle)
+
+    g0 = hiprt.Graph(stream, cfg0_launches)
+    g0.launch(stream)
+    a0, b0 = hiprt.Event(), hiprt.Event()
+    a0.record(stream)
+    for _ in range(args.roofline_replays):
+        g0.launch(stream)
+    b0.record(stream)
+    b0.sync()
+    g0.destroy()
+    cfg0_us = a0.elapsed_ms(b0) * 1e3 / (args.roofline_replays * args.rotate)
+    cfg0_bytes = weight_bytes(4096, 4096, Q4_K) + 4096 * 4 + 4096 * 4
+    cfg0_gbs = cfg0_bytes / (cfg0_us * 1e-6) / 1e9
+    log(f"  cfg0 (Q4_K 4096x4096, M=1, a8 block 256, one call): {cfg0_us:.2f} us, {cfg0_gbs:.0f} GB/s")
     log(f"  gate+up GEMV (Q4_K 2x14336x4096, one launch): {r_us:.2f} us/launch, {r_gbs:.0f} GB/s; "
         f"gate alone: {g_us:.2f} us, {g_gbs:.0f} GB/s; down GEMV (Q6_K 4096x14336): {d_us:.2f} us/launch, "
         f"{d_gbs:.0f} GB/s")
@@ -459,6 +533,19 @@ def main():
             "gate_alone": {"avg_launch_us": round(g_us, 3), "launch_bytes": g_bytes, "achieved": round(g_gbs, 1),
                            "traffic": traffic_of("gate")},
             "q6k_down": {"avg_launch_us": round(d_us, 3), "launch_bytes": d_bytes, "achieved": round(d_gbs, 1)},
+            "read_ceiling": {"kernel": "stream_read_kernel (mimg_stream_read_dev): the gate and up weight bytes "
+                                       "read in one launch, 16-byte nontemporal loads, nothing computed",
+                             "bytes": gu_weight_bytes, "avg_launch_us": round(c_us, 3), "achieved": round(c_gbs, 1),
+                             "frac": round(c_gbs / HBM_PEAK_GBS, 4), "loads_per_thread": c_per,
+                             "kernel_over_ceiling": round(r_gbs / c_gbs, 4)},
+        },
+        "cfg0": {
+            "workload": "cfg0: one 4096x4096 Q4_K product (weight seed 0) of one activation row (seed 1), "
+                        "dequant_matmul_a8.v2 block 256, quantized inside the launch",
+            "bytes": cfg0_bytes,
+            "us_per_call": round(cfg0_us, 3),
+            "GB_per_s": round(cfg0_gbs, 1),
+            "hbm_fraction": round(cfg0_gbs / HBM_PEAK_GBS, 4),
         },
         "prefill": {
             "workload": "cfg2: gate 14336x4096 Q4_K and down 4096x14336 Q6_K, dequant_matmul_a8.v2 block=256, "

@@ -58,7 +58,11 @@ extern "C" {
  * lifetime (interp.Load, interp/interp.go:101-122) brackets init/shutdown. */
 int mimg_init(int device);
 
-/* Frees every registered weight and the per-thread buffers. */
+/* Waits for the device, frees every registered weight (a view's bytes with
+ * its section), every uploaded weights section and the calling thread's
+ * stream and buffers (other threads' go when those threads exit), and
+ * forgets the device, so mimg_init may be called again. No call may be in
+ * flight on another thread. */
 void mimg_shutdown(void);
 
 /* Text of the last error of the calling thread ("" if none). */
@@ -103,7 +107,11 @@ int mimg_register_weight_view(const void *dev, uint64_t len, uint32_t dtype, int
                               uint64_t *handle);
 
 /* Drops one reference of a registration; the last frees the device buffer
- * (a view's flags only). */
+ * (a view's flags only). A call that looked the handle up before the last
+ * release keeps the weight alive until it returns, so sessions on several
+ * threads may share weights (reference interp/pool.go:30-40,
+ * interp/interp.go:409-523 run sessions concurrently); the handle itself
+ * is unknown to calls that start after the last release. */
 int mimg_release_weight(uint64_t handle);
 
 /* Device address of a weight's bytes and the number of its rows that the
@@ -173,7 +181,8 @@ int mimg_linear_a8_group_dev(const uint64_t *w, int count, const float *x, int64
  * y[i] = h . W_i^T (+ bias[i]) as dequant_matmul_a8 computes it
  * (interp/builtins.go dequant_matmul_a8.v2, q8.go:50-97). Bit for bit
  * mimg_rms_norm_dev followed by mimg_linear_a8_group_dev. x_out must not
- * overlap x, resid or scale (every workgroup reads them). Returns MIMG_NOT_HANDLED
+ * overlap x, resid or scale, and no y[i] may overlap x, resid, scale or
+ * x_out (every workgroup reads them; MIMG_ERR_ARG). Returns MIMG_NOT_HANDLED
  * (nothing launched) unless K is a multiple of 1024 up to 4096, every
  * weight is Q4_K or Q6_K and the group's rows fit one launch: the caller
  * then makes the two calls. No reference counterpart beyond the two ops it
@@ -225,7 +234,7 @@ int mimg_rope_kv_dev(float *q, const float *k, const float *v, const int64_t *po
                      const double *inv_freq, int64_t T, int heads, int kv_heads, int d, int rotary, int interleaved,
                      int64_t context, void *kcache, void *vcache, int f16, void *stream);
 
-/* mimg_dequant_matmul on device buffers. */
+/* mimg_dequant_matmul on device buffers; y must not overlap x. */
 int mimg_linear_f32_dev(uint64_t w, const float *x, int64_t rows, const float *bias, float *y,
                         void *stream);
 
@@ -236,7 +245,8 @@ int mimg_linear_f32_dev(uint64_t w, const float *x, int64_t rows, const float *b
  * sets for dequant_matmul.v1 (spec/stdlib.md:230-246):
  * |y - exact| <= (K+1) * 2^-24 * sum_k |x_k w_k|, then bias is added. K must
  * be a multiple of 32 (of 256 for Q4_K and Q6_K); rows <= 65535*128. The
- * rows of W the 8-bit path refuses need no special case here. */
+ * rows of W the 8-bit path refuses need no special case here. y must not
+ * overlap x. */
 int mimg_linear_f32_mfma_dev(uint64_t w, const float *x, int64_t rows, const float *bias, float *y,
                              void *stream);
 
@@ -252,6 +262,16 @@ int mimg_dequantize_dev(uint32_t dtype, const void *src, uint64_t len, float *ds
 int mimg_quantize_dev(uint32_t dtype, const float *src, int64_t n, void *dst, uint64_t dst_len,
                       void *stream);
 
+/* A plain streaming read of `count` (1..3) device byte ranges (16-byte
+ * aligned, lengths non-zero multiples of 16) in one launch: one workgroup of
+ * 256 threads per per_thread*4 KB (per_thread 16-byte nontemporal loads
+ * each, 2, 4, 8 or 16). sink: 1024 uint32 of device memory, written only
+ * for one XOR pattern of the data. No reference counterpart: it measures
+ * the read rate a launch of that size reaches on this GPU, the ceiling the
+ * HBM-bound products are compared with. */
+int mimg_stream_read_dev(const void *const *src, const uint64_t *len, int count, int per_thread, uint32_t *sink,
+                         void *stream);
+
 /* n values ~ N(0, stdv^2) into dst (device), a function of (seed, index)
  * only. No reference counterpart: it builds the random weights of the
  * benchmark models (N(0, 0.02^2) before encoding) on the device. */
@@ -266,7 +286,8 @@ int mimg_synthetic_normal_dev(uint64_t seed, float stdv, float *dst, int64_t n, 
  * tolerances, not bit for bit. */
 
 /* embedding.v1 (reference interp/fast.go:818-842): out[t] = the decoded row
- * ids[t] of a registered table [V, E] (Q4_K, Q6_K, Q8_0 or F32). */
+ * ids[t] of a registered table [V, E] (Q4_K, Q6_K, Q8_0 or F32); a row of
+ * zeros for an id outside 0..V-1, as the reference leaves it. */
 int mimg_embedding_dev(uint64_t table, const int32_t *ids, int64_t T, float *out, void *stream);
 
 /* rms_norm.v1 (reference interp/fast.go:434-485), with the graph's residual

@@ -33,12 +33,19 @@ template <uint32_t DT>
 __global__ void embed_rows_kernel(const uint8_t* __restrict__ table, int64_t row_bytes, const int32_t* __restrict__ ids,
                                   int V, int64_t E, float* __restrict__ out) {
     const int t = blockIdx.y;
-    int id = ids[t];
-    id = id < 0 ? 0 : (id >= V ? V - 1 : id);
-    const uint8_t* row = table + (int64_t)id * row_bytes;
-    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < E; e += (int64_t)gridDim.x * blockDim.x)
-        if constexpr (DT == DT_F32) out[(int64_t)t * E + e] = ((const float*)row)[e];
-        else out[(int64_t)t * E + e] = decode_weight<DT>(row, e);
+    const int id = ids[t];
+    // Out-of-range ids give a zero row, as the reference's gather leaves
+    // them (interp/fast.go:834-838); no table byte is read for them.
+    const bool valid = id >= 0 && id < V;
+    const uint8_t* row = table + (int64_t)(valid ? id : 0) * row_bytes;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < E; e += (int64_t)gridDim.x * blockDim.x) {
+        float v = 0.0f;
+        if (valid) {
+            if constexpr (DT == DT_F32) v = ((const float*)row)[e];
+            else v = decode_weight<DT>(row, e);
+        }
+        out[(int64_t)t * E + e] = v;
+    }
 }
 
 // One 256-thread workgroup per row: x += resid (if given, written back to

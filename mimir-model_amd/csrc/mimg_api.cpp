@@ -51,6 +51,8 @@ struct Weight {
     std::tuple<uintptr_t, uint64_t, uint32_t, int64_t, int64_t> key;
     uint64_t fp = 0;    // sampled fingerprint of the host bytes (has_key)
     int64_t refs = 1;   // registrations not yet released
+    int64_t inflight = 0;  // calls between their lookup and their return
+    bool dead = false;     // released while calls were in flight: the last one frees it
     uint8_t* view_of = nullptr;  // a view into this uploaded weights section (data not owned)
 };
 
@@ -132,13 +134,51 @@ int thread_buf(int i, size_t bytes, void** out) {
     return MIMG_OK;
 }
 
-int lookup(uint64_t h, Weight** out) {
-    std::lock_guard<std::mutex> lk(g_mu);
-    auto it = g_weights.find(h);
-    if (it == g_weights.end()) return fail(MIMG_ERR_HANDLE, "unknown weight handle %llu", (unsigned long long)h);
-    *out = it->second;
-    return MIMG_OK;
+// Frees a weight that is out of the maps and used by no call (g_mu held).
+// Kernels enqueued on it by earlier calls may still run: wait for them.
+void destroy_locked(Weight* w) {
+    (void)hipDeviceSynchronize();
+    if (w->view_of) {
+        auto it = g_uploads.find((uintptr_t)w->view_of);
+        if (it != g_uploads.end()) it->second.views--;
+    } else {
+        (void)hipFree(w->data);
+    }
+    (void)hipFree(w->wref);
+    delete w;
 }
+
+// A weight held by one call from its lookup to its return. While any call
+// holds it, mimg_release_weight only unlinks it (no new call can find it)
+// and the last holder frees it, so a weight shared by concurrent sessions
+// is never freed under a call that is still enqueuing work on it.
+class Held {
+  public:
+    Held() = default;
+    Held(const Held&) = delete;
+    Held& operator=(const Held&) = delete;
+    ~Held() { reset(); }
+    int acquire(uint64_t h) {
+        reset();
+        std::lock_guard<std::mutex> lk(g_mu);
+        auto it = g_weights.find(h);
+        if (it == g_weights.end()) return fail(MIMG_ERR_HANDLE, "unknown weight handle %llu", (unsigned long long)h);
+        w_ = it->second;
+        w_->inflight++;
+        return MIMG_OK;
+    }
+    void reset() {
+        if (!w_) return;
+        std::lock_guard<std::mutex> lk(g_mu);
+        if (--w_->inflight == 0 && w_->dead) destroy_locked(w_);
+        w_ = nullptr;
+    }
+    Weight* get() const { return w_; }
+    Weight* operator->() const { return w_; }
+
+  private:
+    Weight* w_ = nullptr;
+};
 
 int check_shape(uint32_t dtype, uint64_t len, int64_t n, int64_t k) {
     int64_t be = block_elems(dtype);
@@ -408,14 +448,28 @@ int mimg_init(int device) {
 
 void mimg_shutdown(void) {
     std::lock_guard<std::mutex> lk(g_mu);
-    if (g_device >= 0) (void)hipSetDevice(g_device);
+    if (g_device < 0) return;
+    (void)hipSetDevice(g_device);
+    (void)hipDeviceSynchronize();
     for (auto& kv : g_weights) {
-        (void)hipFree(kv.second->data);
-        (void)hipFree(kv.second->wref);
-        delete kv.second;
+        Weight* w = kv.second;
+        if (!w->view_of) (void)hipFree(w->data);  // a view's bytes belong to its section
+        (void)hipFree(w->wref);
+        delete w;
     }
     g_weights.clear();
     g_keys.clear();
+    for (auto& kv : g_uploads) (void)hipFree((void*)kv.first);
+    g_uploads.clear();
+    // the calling thread's stream and buffers; other threads' go at their exit
+    for (int i = 0; i < 4; i++) {
+        if (t_ctx.buf[i]) (void)hipFree(t_ctx.buf[i]);
+        t_ctx.buf[i] = nullptr;
+        t_ctx.cap[i] = 0;
+    }
+    if (t_ctx.stream) (void)hipStreamDestroy(t_ctx.stream);
+    t_ctx.stream = nullptr;
+    g_device = -1;
 }
 
 int mimg_register_weight(const void* host, uint64_t len, uint32_t dtype, int64_t n, int64_t k, uint64_t* handle) {
@@ -437,11 +491,8 @@ int mimg_release_weight(uint64_t handle) {
     if (--w->refs > 0) return MIMG_OK;
     if (w->has_key) g_keys.erase(w->key);
     g_weights.erase(it);
-    HIP_TRY(hipDeviceSynchronize());
-    if (w->view_of) g_uploads[(uintptr_t)w->view_of].views--;
-    else (void)hipFree(w->data);
-    (void)hipFree(w->wref);
-    delete w;
+    if (w->inflight > 0) w->dead = true;  // the last call holding it frees it
+    else destroy_locked(w);
     return MIMG_OK;
 }
 
@@ -526,8 +577,8 @@ int mimg_register_weight_view(const void* dev, uint64_t len, uint32_t dtype, int
 }
 
 int mimg_weight_info(uint64_t handle, const void** dev_ptr, int64_t* n_refused) {
-    Weight* w;
-    int rc = lookup(handle, &w);
+    Held w;
+    int rc = w.acquire(handle);
     if (rc) return rc;
     if (dev_ptr) *dev_ptr = w->data;
     if (n_refused) *n_refused = w->dw.n_refused;
@@ -635,10 +686,11 @@ int mimg_matmul_a8_quantized_group_dev(const uint64_t* whs, int count, const flo
     int rc = ensure_device();
     if (rc) return rc;
     if (!whs || !y || count < 1 || count > 3) return fail(MIMG_ERR_ARG, "a group holds 1 to 3 weights, got %d", count);
+    Held held[3];
     const Weight* w[3];
     for (int i = 0; i < count; i++) {
-        Weight* wi;
-        if ((rc = lookup(whs[i], &wi))) return rc;
+        if ((rc = held[i].acquire(whs[i]))) return rc;
+        Weight* wi = held[i].get();
         bool use_f32;
         if ((rc = a8_checks(wi, rows, block, &use_f32))) return rc;
         if (use_f32) return fail(MIMG_ERR_ARG, "%s has no 8-bit kernel for blocks of %d", dt_name(wi->dw.dt), block);
@@ -665,11 +717,12 @@ int mimg_matmul_a8_quantized_group_dev(const uint64_t* whs, int count, const flo
 int mimg_linear_f32_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, float* y, void* stream) {
     int rc = ensure_device();
     if (rc) return rc;
-    Weight* w;
-    if ((rc = lookup(wh, &w))) return rc;
+    Held w;
+    if ((rc = w.acquire(wh))) return rc;
     if (rows < 0) return fail(MIMG_ERR_ARG, "rows = %lld", (long long)rows);
     if (rows == 0) return MIMG_OK;
     if (!x || !y) return fail(MIMG_ERR_ARG, "null pointer");
+    if ((rc = check_outputs(x, rows, w->dw.k, &w->dw.n, &y, 1))) return rc;
     HIP_TRY(launch_linear_f32(w->dw, x, rows, bias, y, (hipStream_t)stream));
     return MIMG_OK;
 }
@@ -677,11 +730,12 @@ int mimg_linear_f32_dev(uint64_t wh, const float* x, int64_t rows, const float* 
 int mimg_linear_f32_mfma_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, float* y, void* stream) {
     int rc = ensure_device();
     if (rc) return rc;
-    Weight* w;
-    if ((rc = lookup(wh, &w))) return rc;
+    Held w;
+    if ((rc = w.acquire(wh))) return rc;
     if (rows < 0 || rows > INT32_MAX) return fail(MIMG_ERR_ARG, "rows = %lld", (long long)rows);
     if (rows == 0) return MIMG_OK;
     if (!x || !y) return fail(MIMG_ERR_ARG, "null pointer");
+    if ((rc = check_outputs(x, rows, w->dw.k, &w->dw.n, &y, 1))) return rc;
     if ((rows + 127) / 128 > 65535) return fail(MIMG_ERR_ARG, "rows = %lld: more than 65535 tiles of 128", (long long)rows);
     HIP_TRY(launch_linear_f32_mfma(w->dw, x, rows, bias, y, (hipStream_t)stream));
     return MIMG_OK;
@@ -691,17 +745,17 @@ int mimg_matmul_a8_quantized_dev(uint64_t wh, const float* x, int64_t rows, cons
                                  const void* ws, uint64_t ws_bytes, void* stream) {
     int rc = ensure_device();
     if (rc) return rc;
-    Weight* w;
-    if ((rc = lookup(wh, &w))) return rc;
+    Held w;
+    if ((rc = w.acquire(wh))) return rc;
     bool use_f32;
-    if ((rc = a8_checks(w, rows, block, &use_f32))) return rc;
+    if ((rc = a8_checks(w.get(), rows, block, &use_f32))) return rc;
     if (use_f32) return fail(MIMG_ERR_ARG, "%s has no 8-bit kernel for blocks of %d", dt_name(w->dw.dt), block);
     if (rows == 0) return MIMG_OK;
     if (!x || !y || !ws || !aligned(ws, 256)) return fail(MIMG_ERR_ARG, "null or misaligned pointer");
     ActLayout l = act_layout(rows, w->dw.k);
     if (ws_bytes < l.total) return fail(MIMG_ERR_WORKSPACE, "workspace %llu < %llu bytes", (unsigned long long)ws_bytes, (unsigned long long)l.total);
     if ((rc = check_outputs(x, rows, w->dw.k, &w->dw.n, &y, 1))) return rc;
-    const Weight* ws1[1] = {w};
+    const Weight* ws1[1] = {w.get()};
     const float* bs1[1] = {bias};
     float* ys1[1] = {y};
     return matmul_quantized(ws1, 1, x, rows, bs1, block, ys1, act_ptrs((void*)ws, l), (hipStream_t)stream);
@@ -726,11 +780,13 @@ int mimg_linear_a8_group_dev(const uint64_t* whs, int count, const float* x, int
     int rc = ensure_device();
     if (rc) return rc;
     if (!whs || !y || count < 1 || count > 3) return fail(MIMG_ERR_ARG, "a group holds 1 to 3 weights, got %d", count);
+    Held held[3];
     Weight* w[3];
     const DevWeight* dw[3];
     bool all_f32 = true, any_f32 = false;
     for (int i = 0; i < count; i++) {
-        if ((rc = lookup(whs[i], &w[i]))) return rc;
+        if ((rc = held[i].acquire(whs[i]))) return rc;
+        w[i] = held[i].get();
         if (w[i]->dw.k != w[0]->dw.k) return fail(MIMG_ERR_ARG, "the weights of a group must share K");
         bool use_f32;
         if ((rc = a8_checks(w[i], rows, block, &use_f32))) return rc;
@@ -797,11 +853,13 @@ int mimg_rms_norm_linear_a8_group_dev(const uint64_t* whs, int count, const floa
     if (!x || !x_out || !aligned(x, 16) || !aligned(x_out, 16) || (resid && !aligned(resid, 16)) ||
         (scale && !aligned(scale, 16)))
         return fail(MIMG_ERR_ARG, "x, x_out, resid and scale must be non-null (resid, scale may be null) and 16-byte aligned");
+    Held held[3];
     Weight* w[3];
     const DevWeight* dw[3];
     int64_t total_n = 0;
     for (int i = 0; i < count; i++) {
-        if ((rc = lookup(whs[i], &w[i]))) return rc;
+        if ((rc = held[i].acquire(whs[i]))) return rc;
+        w[i] = held[i].get();
         if (w[i]->dw.k != w[0]->dw.k) return fail(MIMG_ERR_ARG, "the weights of a group must share K");
         bool use_f32;
         if ((rc = a8_checks(w[i], 1, 256, &use_f32))) return rc;
@@ -816,6 +874,17 @@ int mimg_rms_norm_linear_a8_group_dev(const uint64_t* whs, int count, const floa
     };
     if (overlap(x_out, x) || overlap(x_out, resid) || overlap(x_out, scale))
         return fail(MIMG_ERR_ARG, "x_out must not overlap x, resid or scale (every workgroup reads them)");
+    // Every workgroup reads x, resid and scale and writes its share of x_out
+    // and y: an output y[i] must overlap none of those four buffers.
+    for (int i = 0; i < count; i++) {
+        const uintptr_t ya = (uintptr_t)y[i], ye = ya + (uint64_t)w[i]->dw.n * 4;
+        auto hits = [&](const void* b) {
+            return b && ya < (uintptr_t)b + xb && (uintptr_t)b < ye;
+        };
+        if (!y[i]) return fail(MIMG_ERR_ARG, "output %d is null", i);
+        if (hits(x) || hits(resid) || hits(scale) || hits(x_out))
+            return fail(MIMG_ERR_ARG, "output %d overlaps x, resid, scale or x_out", i);
+    }
     if (total_n > fused_max_n() || !fused_norm_ok(dw, count))
         return fail(MIMG_NOT_HANDLED, "no fused norm GEMV for K %lld, %lld rows", (long long)K, (long long)total_n);
     float* ys[3];
@@ -847,8 +916,8 @@ int mimg_dequantize_dev(uint32_t dtype, const void* src, uint64_t len, float* ds
 int mimg_embedding_dev(uint64_t table, const int32_t* ids, int64_t T, float* out, void* stream) {
     int rc = ensure_device();
     if (rc) return rc;
-    Weight* w;
-    if ((rc = lookup(table, &w))) return rc;
+    Held w;
+    if ((rc = w.acquire(table))) return rc;
     if (T < 0 || T > (1 << 30)) return fail(MIMG_ERR_ARG, "T = %lld", (long long)T);
     if (T == 0) return MIMG_OK;
     if (!ids || !out) return fail(MIMG_ERR_ARG, "null pointer");
@@ -975,6 +1044,26 @@ int mimg_quantize_dev(uint32_t dtype, const float* src, int64_t n, void* dst, ui
     return MIMG_OK;
 }
 
+int mimg_stream_read_dev(const void* const* src, const uint64_t* len, int count, int per_thread, uint32_t* sink,
+                         void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!src || !len || !sink || count < 1 || count > 3)
+        return fail(MIMG_ERR_ARG, "stream read: 1 to 3 ranges and a sink");
+    if (per_thread != 2 && per_thread != 4 && per_thread != 8 && per_thread != 16)
+        return fail(MIMG_ERR_ARG, "stream read: %d loads per thread (2, 4, 8 or 16)", per_thread);
+    ReadRanges r{};
+    r.count = count;
+    for (int i = 0; i < count; i++) {
+        if (!src[i] || len[i] == 0 || len[i] % 16 || !aligned(src[i], 16))
+            return fail(MIMG_ERR_ARG, "stream read: range %d must be 16-byte aligned, a non-zero multiple of 16", i);
+        r.src[i] = (const uint8_t*)src[i];
+        r.len[i] = (int64_t)len[i];
+    }
+    HIP_TRY(launch_stream_read(r, per_thread, sink, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
 int mimg_dequantize(uint32_t dtype, const void* src, uint64_t len, float* dst, int64_t n) {
     int rc = ensure_device();
     if (rc) return rc;
@@ -998,11 +1087,11 @@ int mimg_dequantize(uint32_t dtype, const void* src, uint64_t len, float* dst, i
 static int host_call(uint64_t wh, const float* x, int64_t rows, const float* bias, int block, float* y, bool a8) {
     int rc = ensure_device();
     if (rc) return rc;
-    Weight* w;
-    if ((rc = lookup(wh, &w))) return rc;
+    Held w;
+    if ((rc = w.acquire(wh))) return rc;
     if (rows < 0) return fail(MIMG_ERR_ARG, "rows = %lld", (long long)rows);
     bool use_f32 = !a8;
-    if (a8 && (rc = a8_checks(w, rows, block, &use_f32))) return rc;
+    if (a8 && (rc = a8_checks(w.get(), rows, block, &use_f32))) return rc;
     if (rows == 0) return MIMG_OK;
     if (!x || !y) return fail(MIMG_ERR_ARG, "null pointer");
     if ((rc = ensure_thread_stream())) return rc;

@@ -136,6 +136,17 @@ hipError_t launch_dequantize(uint32_t dt, const uint8_t* src, int64_t n_elems, f
                              hipStream_t stream);
 
 hipError_t launch_encode(uint32_t dt, const float* x, int64_t n, uint8_t* dst, hipStream_t stream);
+
+// A plain streaming read of up to three byte ranges (misc_kernels.hip), the
+// measured ceiling of the HBM-bound kernels; per = 16-byte loads per thread
+// (2, 4, 8 or 16), one workgroup of 256 threads per per*4 KB.
+struct ReadRanges {
+    const uint8_t* src[3];
+    int64_t len[3];  // multiples of 16
+    int64_t wgs[3];  // workgroups per range (set by the launcher)
+    int count;
+};
+hipError_t launch_stream_read(const ReadRanges& r, int per, uint32_t* sink, hipStream_t s);
 hipError_t launch_normal_fill(uint64_t seed, float stdv, float* dst, int64_t n, hipStream_t stream);
 
 }  // namespace mimg

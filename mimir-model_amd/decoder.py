@@ -331,9 +331,12 @@ class Decoder:
 
     def _ensure_out(self, cap, n):
         if self.out is None or self.out_cap < cap or self.out.nbytes < cap * n * 4:
+            self.stream.sync()
+            for g in self.graphs.values():  # captured with the old buffer
+                g.destroy()
+            self.graphs = {}
             self.out = hiprt.DeviceBuffer(cap * n * 4)
             self.out_cap = cap
-            self.graphs = {}  # captured with the old buffer
 
     def generate(self, prompts, n_new, slots=None, graph=True, timing=None):
         """Greedy continuation of each prompt (one per slot, all of the same

@@ -113,6 +113,17 @@ class Stream:
     def sync(self):
         check(rt().hipStreamSynchronize(ctypes.c_void_p(self.handle)), "hipStreamSynchronize")
 
+    def destroy(self):
+        if self.handle:
+            check(rt().hipStreamDestroy(ctypes.c_void_p(self.handle)), "hipStreamDestroy")
+            self.handle = 0
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
 
 class Event:
     def __init__(self):
@@ -130,6 +141,17 @@ class Event:
         ms = ctypes.c_float()
         check(rt().hipEventElapsedTime(ctypes.byref(ms), ctypes.c_void_p(self.handle), ctypes.c_void_p(end.handle)), "hipEventElapsedTime")
         return ms.value
+
+    def destroy(self):
+        if self.handle:
+            check(rt().hipEventDestroy(ctypes.c_void_p(self.handle)), "hipEventDestroy")
+            self.handle = 0
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
 
 
 class Graph:
@@ -150,6 +172,22 @@ class Graph:
 
     def launch(self, stream):
         check(rt().hipGraphLaunch(ctypes.c_void_p(self.exec), ctypes.c_void_p(stream.handle)), "hipGraphLaunch")
+
+    def destroy(self):
+        """Frees the executable graph and the graph (a replay still in flight
+        finishes first: hipGraphExecDestroy waits for it)."""
+        if getattr(self, "exec", 0):
+            check(rt().hipGraphExecDestroy(ctypes.c_void_p(self.exec)), "hipGraphExecDestroy")
+            self.exec = 0
+        if getattr(self, "graph", 0):
+            check(rt().hipGraphDestroy(ctypes.c_void_p(self.graph)), "hipGraphDestroy")
+            self.graph = 0
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
 
 
 def device_sync():

@@ -70,6 +70,7 @@ SIGNATURES = {
     "mimg_greedy_advance_dev": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _P]),
     "mimg_swiglu_dev": (_I, [_P, _P, _P, _I64, _I, _P]),
     "mimg_argmax_dev": (_I, [_P, _I64, _I64, _P, _P]),
+    "mimg_stream_read_dev": (_I, [ctypes.POINTER(_P), ctypes.POINTER(_U64), _I, _I, _P, _P]),
 }
 
 
@@ -365,3 +366,12 @@ def argmax_dev(x_ptr, rows, n, out_ptr, stream):
 
 def row_bytes(dt, k):
     return k // BLOCK_ELEMS[dt] * BLOCK_BYTES[dt]
+
+
+def stream_read_dev(ranges, per_thread, sink_ptr, stream):
+    """A plain streaming read of up to three (device pointer, bytes) ranges
+    in one launch (mimg_stream_read_dev): the HBM read ceiling."""
+    n = len(ranges)
+    ps = (_P * n)(*[_P(p) for p, _ in ranges])
+    ls = (_U64 * n)(*[b for _, b in ranges])
+    _check(load().mimg_stream_read_dev(ps, ls, n, per_thread, _P(sink_ptr), _P(stream)))

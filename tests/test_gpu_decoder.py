@@ -44,15 +44,21 @@ def test_embedding_rows_exact(gpu, oracle, rt, dt):
     V, E = 37, 512
     raw = oracle.synthetic_weight(dt, V, E, seed=3)
     w = gpu.Weight(raw, dt, V, E)
-    ids = np.array([0, 5, 36, 5, 17], np.int32)
+    # ids outside 0..V-1 give zero rows, as the reference leaves them
+    # (interp/fast.go:834-838)
+    ids = np.array([0, 5, 36, -1, 5, V, 17], np.int32)
     s = rt.Stream()
     d_ids, out = dev(rt, ids), rt.DeviceBuffer(ids.size * E * 4)
+    out.upload(np.full(ids.size * E, np.nan, np.float32))
     gpu.embedding_dev(w, d_ids.ptr, ids.size, out.ptr, s.handle)
     s.sync()
     got = out.download(np.float32).reshape(ids.size, E)
     rb = len(raw) // V
     for i, t in enumerate(ids):
-        want = oracle.dequantize(dt, raw[rb * t: rb * (t + 1)], E)
+        if 0 <= t < V:
+            want = oracle.dequantize(dt, raw[rb * t: rb * (t + 1)], E)
+        else:
+            want = np.zeros(E, np.float32)
         assert np.array_equal(got[i].view(np.uint32), want.view(np.uint32)), f"row {i} (token {t})"
     w.release()
 
@@ -312,32 +318,98 @@ def test_graph_replay_equals_eager(gpu):
     assert a.tolist() == b.tolist()
 
 
+def _oracle_greedy(ref, prompt, n_new):
+    """Greedy ids of the CPU restatement (reference cmd/mim-run/main.go
+    generate, 184-257): the prompt's last logits, then one token a step."""
+    P = len(prompt)
+    lg = ref.forward(prompt, np.arange(P))[-1]
+    want = []
+    for i in range(n_new):
+        want.append(llama_ref.argmax(lg))
+        if i + 1 < n_new:
+            lg = ref.forward([want[-1]], [P + i])[0]
+    return want
+
+
 @pytest.mark.parametrize("cache_f16", [False, True], ids=["f32cache", "f16cache"])
 def test_llama1b_shape_greedy_matches_oracle(gpu, cache_f16):
-    """BASELINE config 3's model shape (16 layers, d 2048, FFN 8192, 32/8
-    heads, vocab 128256) with random Q4_K_M weights built on the device: a
-    32-token prompt (uniform ids, seed 7) and 16 greedy tokens; the GPU
-    decoder and the CPU restatement, on the same weight bytes, pick the same
-    ids."""
+    """the Llama-3.2-1B model shape (16 layers, d 2048,
+    FFN 8192, 32/8 heads, vocab 128256) with random Q4_K_M weights built on
+    the device, a 32-token prompt (uniform ids, seed 7) and all 128 greedy
+    tokens of the config; the GPU decoder and the CPU restatement, on the
+    same weight bytes, pick the same ids."""
     import decoder
     import synthetic
 
-    cfg = dict(synthetic.LLAMA_1B, context=64)
+    cfg = dict(synthetic.LLAMA_1B, context=192)
     tensors = synthetic.build(cfg, seed=1)
     prompt = np.random.default_rng(7).integers(0, cfg["vocab"], 32).astype(np.int32)
-    n_new = 16
+    n_new = 128
     dec = decoder.Decoder(cfg, tensors, a8=True, cache_f16=cache_f16, max_rows=32)
     got = dec.generate([prompt], n_new)[0].tolist()
     del dec
     ref = llama_ref.Decoder(llama_ref.Model(cfg, synthetic.host_bytes(tensors)), a8=True, cache_f16=cache_f16,
                             threads=16)
-    lg = ref.forward(prompt, np.arange(32))[-1]
-    want = []
-    for i in range(n_new):
-        want.append(llama_ref.argmax(lg))
-        if i + 1 < n_new:
-            lg = ref.forward([want[-1]], [32 + i])[0]
-    assert got == want
+    want = _oracle_greedy(ref, prompt, n_new)
+    assert got == want, next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)
+
+
+@pytest.fixture(scope="module")
+def llama8b(gpu):
+    """BASELINE config 4's model: the Llama-3-8B shape (32 layers, d 4096,
+    FFN 14336, 32/8 heads, vocab 128256) with random Q4_K_M weights drawn
+    and encoded on the device (4.9 GB)."""
+    import synthetic
+
+    cfg = dict(synthetic.LLAMA_8B, context=64)
+    tensors = synthetic.build(cfg, seed=3)
+    yield cfg, tensors
+    for _, _, w in tensors.values():
+        if isinstance(w, gpu.Weight):
+            w.release()
+
+
+def test_llama8b_shape_greedy_matches_oracle(gpu, llama8b):
+    """Config 4's model at batch 1: a 32-token prompt (uniform ids, seed 7)
+    and 16 greedy tokens, f16 cache (the importer's default, -kv f16); the
+    GPU decoder and the CPU restatement pick the same ids on the same
+    weight bytes."""
+    import decoder
+    import synthetic
+
+    cfg, tensors = llama8b
+    prompt = np.random.default_rng(7).integers(0, cfg["vocab"], 32).astype(np.int32)
+    n_new = 16
+    dec = decoder.Decoder(cfg, tensors, a8=True, cache_f16=True, max_rows=32)
+    got = dec.generate([prompt], n_new)[0].tolist()
+    del dec
+    print("llama8b GPU ids", got, flush=True)
+    ref = llama_ref.Decoder(llama_ref.Model(cfg, synthetic.host_bytes(tensors)), a8=True, cache_f16=True,
+                            threads=16)
+    want = _oracle_greedy(ref, prompt, n_new)
+    assert got == want, next(i for i, (a, b) in enumerate(zip(got, want)) if a != b)
+
+
+def test_llama8b_shape_eight_slots_match_single_sequences(gpu, llama8b):
+    """Config 4's batch of 8: eight distinct prompts in eight slots of one
+    cache (the reference's "slots", importer/llama.go:378-395), decoded as
+    one batch of rows on the matrix-core GEMV, give each prompt the ids of
+    its own single-sequence run; slot 0's prompt is the batch-1 test's, whose
+    ids equal the CPU restatement's."""
+    import decoder
+
+    cfg, tensors = llama8b
+    rng = np.random.default_rng(7)
+    prompts = np.stack([rng.integers(0, cfg["vocab"], 32) for _ in range(8)]).astype(np.int32)
+    n_new = 16
+    batch = decoder.Decoder(cfg, tensors, a8=True, cache_f16=True, max_rows=256, slots=8)
+    got = batch.generate(prompts, n_new)
+    del batch
+    single = decoder.Decoder(cfg, tensors, a8=True, cache_f16=True, max_rows=32, slots=1)
+    for i in range(8):
+        single.reset()
+        want = single.generate(prompts[i:i + 1], n_new)[0].tolist()
+        assert got[i].tolist() == want, f"slot {i}"
 
 
 # ------------------------------------------------------ fused launches

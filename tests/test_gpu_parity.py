@@ -352,6 +352,20 @@ def test_output_overlapping_input_refused(gpu, oracle):
             gpu.matmul_a8_quantized_dev(W, buf.ptr, rows, None, 256, buf.ptr, ws.ptr, wsb, s.handle)
         with pytest.raises(gpu.MimgError):
             gpu.matmul_a8_quantized_group_dev([W], buf.ptr, rows, None, 256, [buf.ptr], ws.ptr, wsb, s.handle)
+        with pytest.raises(gpu.MimgError):
+            gpu.linear_f32_dev(W, buf.ptr, rows, None, buf.ptr + 1024, s.handle)
+        with pytest.raises(gpu.MimgError):
+            gpu.linear_f32_mfma_dev(W, buf.ptr, rows, None, buf.ptr, s.handle)
+    # the fused norm GEMV: y[i] against x, resid, scale and x_out
+    other = hiprt.DeviceBuffer(4 * k * 4)
+    x, resid, scale, x_out = (other.ptr + i * k * 4 for i in range(4))
+    for y in (x, resid, scale, x_out, x + 64):
+        with pytest.raises(gpu.MimgError) as e:
+            gpu.rms_norm_linear_a8_group_dev([W], x, resid, scale, 1e-5, x_out, None, [y], s.handle)
+        assert not isinstance(e.value, gpu.NotHandled)
+    own = hiprt.DeviceBuffer(n * 4)
+    gpu.rms_norm_linear_a8_group_dev([W], x, resid, scale, 1e-5, x_out, None, [own.ptr], s.handle)
+    s.sync()
     W.release()
 
 
