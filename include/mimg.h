@@ -175,6 +175,20 @@ int mimg_linear_a8_group_dev(const uint64_t *w, int count, const float *x, int64
                              const float *const *bias, int block, float *const *y, void *ws,
                              uint64_t ws_bytes, void *stream);
 
+/* mimg_linear_a8_dev without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc): the quantized activations go to a scratch array
+ * of mimg_noalloc_scratch_bytes() (4 MiB) in the library's device memory,
+ * one per GPU, kept until the process ends. The call allocates nothing.
+ * Rows x K whose workspace (mimg_a8_workspace_bytes) exceeds the scratch
+ * return MIMG_ERR_WORKSPACE (e.g. at most ~800 rows at K = 4096, ~230 at
+ * K = 14336). Every call on one GPU shares its scratch: calls that overlap
+ * in time on that GPU (other streams or threads) race and must be
+ * serialised by the caller. No counterpart in the reference. */
+int mimg_linear_a8_noalloc_dev(uint64_t w, const float *x, int64_t rows, const float *bias, int block, float *y,
+                               void *stream);
+uint64_t mimg_noalloc_scratch_bytes(void);
+
 /* rms_norm.v1 in front of mimg_linear_a8_group_dev at one activation row,
  * blocks of 256, in one launch: x_out = x + resid (x copied when resid is
  * NULL), h = rms_norm(x_out) * scale (reference interp/fast.go:434-485), and

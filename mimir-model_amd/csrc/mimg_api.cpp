@@ -65,6 +65,17 @@ std::map<uintptr_t, Upload> g_uploads;
 
 std::mutex g_mu;
 int g_device = -1;
+
+// Scratch of mimg_linear_a8_noalloc_dev: the quantized activations
+// (act_layout) in a file-scope device array, so that the call allocates
+// nothing. Each GPU the library runs on holds its own copy until the
+// process ends. In host code `scratch` is only a stand-in for the symbol:
+// its device address is taken once per device with hipGetSymbolAddress at
+// mimg_init and kept in g_scratch; kernels receive that address.
+constexpr uint64_t SCRATCH_BYTES = 4ull << 20;
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+constexpr int MAX_DEVICES = 64;
+void* g_scratch[MAX_DEVICES] = {};
 uint64_t g_next = 1;
 std::unordered_map<uint64_t, Weight*> g_weights;
 std::map<std::tuple<uintptr_t, uint64_t, uint32_t, int64_t, int64_t>, uint64_t> g_keys;
@@ -442,6 +453,14 @@ int mimg_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(MIMG_ERR_DEVICE, "device %d is %s; libmimg is built for gfx950", device, prop.gcnArchName);
     HIP_TRY(hipSetDevice(device));
+    if (device >= MAX_DEVICES) return fail(MIMG_ERR_DEVICE, "device %d: at most %d devices", device, MAX_DEVICES);
+    if (!g_scratch[device]) {
+        void* p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(MIMG_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+        g_scratch[device] = p;
+    }
     g_device = device;
     return MIMG_OK;
 }
@@ -843,6 +862,30 @@ int mimg_linear_a8_dev(uint64_t wh, const float* x, int64_t rows, const float* b
     float* ys[1] = {y};
     return mimg_linear_a8_group_dev(&wh, 1, x, rows, bs, block, ys, ws, ws_bytes, stream);
 }
+
+int mimg_linear_a8_noalloc_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, int block, float* y,
+                               void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    void* ws = g_scratch[g_device];
+    if (!ws) return fail(MIMG_ERR_NOT_INIT, "no scratch address for device %d", g_device);
+    int64_t K;
+    {
+        Held w;
+        if ((rc = w.acquire(wh))) return rc;
+        K = w->dw.k;
+    }
+    if (rows < 0) return fail(MIMG_ERR_ARG, "rows = %lld", (long long)rows);
+    const uint64_t need = act_layout(rows, K).total;
+    if (need > SCRATCH_BYTES)
+        return fail(MIMG_ERR_WORKSPACE,
+                    "%lld rows x K = %lld need %llu bytes of scratch; the library's static scratch holds %llu "
+                    "(call mimg_linear_a8_dev with a workspace instead)",
+                    (long long)rows, (long long)K, (unsigned long long)need, (unsigned long long)SCRATCH_BYTES);
+    return mimg_linear_a8_dev(wh, x, rows, bias, block, y, ws, SCRATCH_BYTES, stream);
+}
+
+uint64_t mimg_noalloc_scratch_bytes(void) { return SCRATCH_BYTES; }
 
 int mimg_rms_norm_linear_a8_group_dev(const uint64_t* whs, int count, const float* x, const float* resid,
                                       const float* scale, float eps, float* x_out, const float* const* bias,

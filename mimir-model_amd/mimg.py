@@ -71,6 +71,8 @@ SIGNATURES = {
     "mimg_swiglu_dev": (_I, [_P, _P, _P, _I64, _I, _P]),
     "mimg_argmax_dev": (_I, [_P, _I64, _I64, _P, _P]),
     "mimg_stream_read_dev": (_I, [ctypes.POINTER(_P), ctypes.POINTER(_U64), _I, _I, _P, _P]),
+    "mimg_linear_a8_noalloc_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P]),
+    "mimg_noalloc_scratch_bytes": (_U64, []),
 }
 
 
@@ -232,6 +234,13 @@ def quantize_act_dev(x_ptr, rows, k, block, ws_ptr, ws_bytes, stream):
 def linear_a8_dev(w, x_ptr, rows, bias_ptr, block, y_ptr, ws_ptr, ws_bytes, stream):
     _check(load().mimg_linear_a8_dev(w.handle, _P(x_ptr), rows, _P(bias_ptr) if bias_ptr else None, block,
                                      _P(y_ptr), _P(ws_ptr), ws_bytes, _P(stream)))
+
+
+def linear_a8_noalloc_dev(w, x_ptr, rows, bias_ptr, block, y_ptr, stream):
+    """mimg_linear_a8_dev with the library's static scratch (no workspace,
+    no allocation)."""
+    _check(load().mimg_linear_a8_noalloc_dev(w.handle, _P(x_ptr), rows, _P(bias_ptr) if bias_ptr else None, block,
+                                             _P(y_ptr), _P(stream)))
 
 
 def linear_a8_group_dev(weights, x_ptr, rows, bias_ptrs, block, y_ptrs, ws_ptr, ws_bytes, stream):
