@@ -1,6 +1,6 @@
 // Prefill GEMM, Q4_K / Q6_K weights x 8-bit activations in blocks of 256
 // (dequant_matmul_a8.v2, block = 256) for many activation rows, on the int8
-// matrix cores (v_mfma_i32_16x16x64_i8). The result equals the decode GEMV's
+// matrix cores (v_mfma_i32_32x32x32_i8). The result equals the decode GEMV's
 // bit for bit, as the reference's AMX/VNNI tile kernels equal its one-row
 // kernel (reference internal/kernels/amx.go:194-316, amx_test.go:41-141):
 // per (weight row n, activation row m) and block b the exact int32
@@ -13,23 +13,28 @@
 // fit int8 (Q4_K up to 945, Q6_K -4096..4064), so it is split in two planes.
 // Q4_K: sc = 8*sh + sl (sh, sl <= 7), planes sh*q and sl*q (each <= 105),
 // S = 8*sum(sh*q*y) + sum(sl*q*y); the planes are the packed nibbles times
-// a constant. Q6_K: w = 128*hi + lo with lo in [0,127], hi in [-32,31],
-// S = 128*sum(hi*y) + sum(lo*y). Each MFMA sum is exact in int32 (|sum| <
-// 2^31 for 256-element blocks). Q4_K's M term is a third MFMA plane with
-// A = m_s(k).
+// a constant. Q6_K: w = 256*hi + lo with lo the low byte of w as a signed
+// value (-128..127) and hi in [-16, 16], S = 256*sum(hi*y) + sum(lo*y):
+// with u = w + 128 in a 16-bit lane, hi is u's high byte and lo its low
+// byte with the top bit flipped. Each MFMA sum is exact in int32 (|sum| <
+// 2^31 for 256-element blocks). Q4_K's M term is a third MFMA plane whose
+// operand is m_s for the 32 k of sub-block s.
 //
-// Tiling: a 256-thread workgroup owns 64 weight rows x 128 activation rows;
-// wave w takes weight rows 16w..16w+15 (the A operand: lane l holds row
-// l%16 and the 16 k of group l/16) against all 8 activation tiles of 16 (the
-// B operand, same k mapping); C lane l holds rows 4(l/16)+r, column l%16.
-// Per block of 256, the raw weight blocks (as in the file), the int8
+// Operands: the activation rows are the MFMA's row operand and the weight
+// rows its column operand, so a lane of the 32 x 32 result holds one weight
+// row (lane l: row l % 32) and 16 activation rows (8j + 4(l/32) + r), and
+// needs one block scale d (and dmin) per block. A k step of 32 is one
+// sub-block; lane l supplies k 16(l/32)..+15 of it for both operands.
+//
+// Tiling: a workgroup of NW x WM waves owns 32 NW weight rows x 64 WM
+// activation rows; a wave takes 32 weight rows (its column tile, unpacked
+// in registers from the raw blocks) against two row tiles of 32 activation
+// rows. Per block of 256 the raw weight blocks (as in the file), the int8
 // activation rows and their scales are copied into LDS with
 // global_load_lds, double-buffered: block b+1 loads while block b computes.
-// Each wave unpacks its A planes in registers (nibbles or 6-bit values times
-// the sub-block scale, split into hi/lo) and reuses them for 8 MFMA columns.
 // Activation rows sit in LDS with their 16-byte chunks XOR-swizzled by row
-// (chunk c of row m at c ^ (m & 15)) so the B reads are free of bank
-// conflicts.
+// (chunk c of row m at c ^ (m & 15)): the 32 lanes of a row-operand read,
+// one chunk of 32 consecutive rows, touch every bank once per 16 rows.
 //
 // Rows of x the quantizer refused and weight rows with a non-finite block
 // scale take the float32 path (reference interp/fast.go:323-377) at the end.
@@ -40,39 +45,27 @@
 namespace mimg {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
-#ifndef MIMG_GEMM_BM
-#define MIMG_GEMM_BM 128
-#endif
-#ifndef MIMG_GEMM_THREADS
-#define MIMG_GEMM_THREADS 512
-#endif
-#ifndef MIMG_GEMM_NW
-#define MIMG_GEMM_NW 4
-#endif
-constexpr int GM_T = MIMG_GEMM_THREADS;   // threads per workgroup (256: one wave per SIMD, 512: two)
-constexpr int GM_NW = MIMG_GEMM_NW;       // waves along the weight rows (16 rows each)
-constexpr int GM_BN = 16 * GM_NW;         // weight rows per workgroup
-constexpr int GM_BM = MIMG_GEMM_BM;       // activation rows per workgroup
-constexpr int GM_WM = GM_T / 64 / GM_NW;  // waves along the activation rows
-constexpr int GM_TM = GM_BM / 16 / GM_WM; // activation tiles of 16 per wave
-static_assert(GM_WM * GM_NW * 64 == GM_T && GM_TM * GM_WM * 16 == GM_BM && GM_T >= GM_BN && GM_T >= GM_BM,
-              "GEMM tile shape");
-constexpr int GM_ACH = GM_BM * 16 / GM_T; // activation copy instructions per thread per block
-
-template <uint32_t DT>
+// Workgroup shape: NW waves along the weight rows (32 each), WM along the
+// activation rows (64 each: two MFMA row tiles).
+template <uint32_t DT, int NW, int WM>
 struct GemmLayout {
-    // LDS bytes per weight row slot: Q4_K blocks are 16-byte aligned and
-    // copied as 9 chunks; Q6_K blocks (2-byte aligned) are copied as the 54
-    // aligned dwords that cover them.
-    static constexpr int WSLOT = DT == DT_Q4_K ? 144 : 216;
-    static constexpr int WDMA = DT == DT_Q4_K ? (GM_BN * 9 + GM_T - 1) / GM_T   // copy instructions per
-                                             : (GM_BN * 54 + GM_T - 1) / GM_T;  // thread per block
-    static constexpr int WBYTES = WDMA * GM_T * (DT == DT_Q4_K ? 16 : 4);  // incl. slack for unconditional copies
-    static constexpr int ABYTES = GM_BM * 256;
-    static constexpr int DXBYTES = GM_T * 4;
-    static constexpr int BUF = WBYTES + ABYTES + DXBYTES;
-    static constexpr int NDMA = WDMA + GM_ACH + 1;
+    static constexpr int T = 64 * NW * WM;   // threads
+    static constexpr int BN = 32 * NW;       // weight rows per workgroup
+    static constexpr int BM = 64 * WM;       // activation rows per workgroup
+    // LDS per weight row: a Q4_K block (16-byte aligned) as its 9 chunks of
+    // 16 bytes; a Q6_K block (2-byte aligned) as the 14 aligned chunks that
+    // cover it, the block starting (address & 15) bytes into its slot.
+    static constexpr int WCH = DT == DT_Q4_K ? 9 : 14;
+    static constexpr int WSLOT = 16 * WCH;
+    static constexpr int WDMA = (BN * WCH + T - 1) / T;  // copies per thread per block
+    static constexpr int WBYTES = WDMA * T * 16;         // incl. slack for unconditional copies
+    static constexpr int ADMA = BM * 16 / T;
+    static constexpr int ABYTES = BM * 256;
+    static constexpr int BUF = WBYTES + ABYTES;
+    static constexpr int DXBYTES = T * 4;                // one dword copy per thread (BM used)
+    static_assert(ADMA * T == BM * 16 && T >= BM && WM == 2, "GEMM tile shape");
 };
 
 struct GemmArgs {
@@ -88,6 +81,7 @@ struct GemmArgs {
     const int32_t* ok;     // [M]
     const float* x;        // [M][K] f32 (fallback)
     int fused;             // float32 fallback order (rows of the whole call <= 8)
+    int tiles_m;           // row tiles of BM activation rows
 };
 
 // Global -> LDS copies (global_load_lds: lane i of the wave writes its 16
@@ -123,57 +117,78 @@ __device__ __forceinline__ void gm_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// Byte offset of block b of weight row n inside its LDS slot (Q6_K blocks
+// are copied from the 16-byte boundary below them).
+__device__ __forceinline__ uint32_t q6k_slot_off(const GemmArgs& A, int n, int b) {
+    return (uint32_t)(((uint64_t)n * (uint64_t)A.rb + (uint64_t)b * Q6K_BYTES) & 15u);
+}
+
 // Issues the copies of block b into LDS buffer `buf` (every thread issues
 // exactly NDMA instructions, so the wait counts are the same in each wave).
-template <uint32_t DT>
-__device__ __forceinline__ void gemm_issue_block(const GemmArgs& A, int n0, int m0, int b, uint8_t* buf) {
-    using L = GemmLayout<DT>;
-    const int t = threadIdx.x, wave = t >> 6;  // wave of the workgroup (0 .. GM_T/64-1)
+template <uint32_t DT, int NW, int WM>
+__device__ __forceinline__ void gemm_issue_block(const GemmArgs& A, int n0, int m0, int b, uint8_t* buf, uint8_t* dl) {
+    using L = GemmLayout<DT, NW, WM>;
+    const int t = threadIdx.x, wave = t >> 6;
     uint8_t* wl = buf;
     uint8_t* al = buf + L::WBYTES;
-    uint8_t* dl = al + L::ABYTES;
-    if constexpr (DT == DT_Q4_K) {
 #pragma unroll
-        for (int i = 0; i < L::WDMA; i++) {
-            const int c = min(GM_T * i + t, GM_BN * 9 - 1);  // chunk of 16 bytes
-            const int r = c / 9, j = c - 9 * r;
-            const int n = min(n0 + r, A.N - 1);
-            lds_copy16(A.W + (int64_t)n * A.rb + (int64_t)b * Q4K_BYTES + 16 * j, wl + 16 * (GM_T * i + 64 * wave));
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < L::WDMA; i++) {
-            const int c = min(GM_T * i + t, GM_BN * 54 - 1);  // dword
-            const int r = c / 54, j = c - 54 * r;
-            const int n = min(n0 + r, A.N - 1);
-            const uint8_t* blk = A.W + (int64_t)n * A.rb + (int64_t)b * Q6K_BYTES;
-            const uint8_t* base = (const uint8_t*)__builtin_align_down(blk, 4);
-            lds_copy4(base + 4 * j, wl + 4 * (GM_T * i + 64 * wave));
-        }
+    for (int i = 0; i < L::WDMA; i++) {
+        const int c = min(L::T * i + t, L::BN * L::WCH - 1);  // chunk of 16 bytes
+        const int r = c / L::WCH, j = c - L::WCH * r;
+        const int n = min(n0 + r, A.N - 1);
+        const uint8_t* blk = A.W + (int64_t)n * A.rb + (int64_t)b * (DT == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES);
+        const uint8_t* base = DT == DT_Q4_K ? blk : (const uint8_t*)__builtin_align_down(blk, 16);
+        lds_copy16(base + 16 * j, wl + 16 * (L::T * i + 64 * wave));
     }
 #pragma unroll
-    for (int i = 0; i < GM_ACH; i++) {
-        const int c = GM_T * i + t;              // LDS chunk: row c/16, slot c%16
+    for (int i = 0; i < L::ADMA; i++) {
+        const int c = L::T * i + t;  // LDS chunk: row c/16, slot c%16
         const int r = c >> 4, s = c & 15;
         const int m = min(m0 + r, A.M - 1);
-        lds_copy16(A.q + (int64_t)m * A.K + 256 * b + 16 * (s ^ (r & 15)), al + 16 * (GM_T * i + 64 * wave));
+        lds_copy16(A.q + (int64_t)m * A.K + 256 * b + 16 * (s ^ (r & 15)), al + 16 * (L::T * i + 64 * wave));
     }
     {
-        const int m = min(m0 + min(t, GM_BM - 1), A.M - 1);
-        lds_copy4(A.d32 + (int64_t)m * (A.K / 32) + 8 * b, dl + 4 * (64 * wave));  // slots t >= GM_BM are slack
+        const int m = min(m0 + min(t, L::BM - 1), A.M - 1);
+        lds_copy4(A.d32 + (int64_t)m * (A.K / 32) + 8 * b, dl + 4 * (64 * wave));  // slots t >= BM are slack
     }
 }
 
-template <uint32_t DT>
-__global__ __launch_bounds__(GM_T) void gemm_a8k_kernel(GemmArgs A) {
-    using L = GemmLayout<DT>;
+// 16 bytes at an LDS address that is 2-byte aligned: five aligned dwords
+// and a byte realignment.
+__device__ __forceinline__ u32x4 lds_read16_a2(const uint8_t* p) {
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 3);
+    const uint32_t* w = (const uint32_t*)__builtin_align_down(p, 4);
+    const uint32_t w0 = w[0], w1 = w[1], w2 = w[2], w3 = w[3], w4 = w[4];
+    return u32x4{__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh),
+                 __builtin_amdgcn_alignbyte(w3, w2, sh), __builtin_amdgcn_alignbyte(w4, w3, sh)};
+}
+
+template <uint32_t DT, int NW, int WM>
+__global__ __launch_bounds__(64 * NW * WM) void gemm_a8k_kernel(GemmArgs A) {
+    using L = GemmLayout<DT, NW, WM>;
     __shared__ __align__(16) uint8_t smem[2 * L::BUF];
-    __shared__ int flags[2];
-    const int t = threadIdx.x, l = t & 63;
-    const int wn = (t >> 6) % GM_NW, wm = (t >> 6) / GM_NW;  // this wave's weight rows 16wn.., activation tiles wm*GM_TM..
-    const int ar = l & 15, G = l >> 4;
-    const int n0 = blockIdx.x * GM_BN, m0 = blockIdx.y * GM_BM;
+    __shared__ __align__(16) uint8_t dxs[3 * L::DXBYTES];
+    __shared__ int flags[1];
+    const int t = threadIdx.x, l = t & 63, wave = t >> 6;
+    const int wn = wave % NW, wm = wave / NW;
+    const int a = l & 31, g = l >> 5;
+    // Workgroups are dealt to the XCDs in turn; consecutive row tiles of
+    // one weight tile go to the same XCD (and its L2) where possible.
+    const int ntn = (A.N + L::BN - 1) / L::BN;
+    const int nwg = ntn * A.tiles_m;
+    int wg = blockIdx.x;
+    if (nwg % 8 == 0) wg = (wg % 8) * (nwg / 8) + wg / 8;
+    const int tile_n = wg / A.tiles_m, tile_m = wg % A.tiles_m;
+    const int n0 = tile_n * L::BN, m0 = tile_m * L::BM;
     const int nb = A.nb;
+    const int nrow = min(n0 + 32 * wn + a, A.N - 1);  // this lane's weight row (clamped)
+    // The two waves on a SIMD run half a block apart: while one issues block
+    // b's MFMAs the other runs block b-1's float chain, and they swap at each
+    // barrier, so the matrix core and the vector unit of the SIMD work at the
+    // same time. Waves w and w ^ 4 share a SIMD when waves are dealt to the
+    // SIMDs in turn, w and w ^ 1 when dealt in pairs: this split puts a
+    // leader and a trailer on each SIMD either way.
+    const bool leader = ((wave ^ (wave >> 2)) & 1) == 0;
 
     // Refusals of this tile: any weight row with a non-finite block scale,
     // any refused activation row.
@@ -181,188 +196,189 @@ __global__ __launch_bounds__(GM_T) void gemm_a8k_kernel(GemmArgs A) {
     __syncthreads();
     {
         int f = 0;
-        if (t < GM_BN && n0 + t < A.N) f |= A.wref[n0 + t] != 0;
-        if (t < GM_BM && m0 + t < A.M) f |= A.ok[m0 + t] == 0;
+        if (t < L::BN && n0 + t < A.N) f |= A.wref[n0 + t] != 0;
+        if (t < L::BM && m0 + t < A.M) f |= A.ok[m0 + t] == 0;
         if (f) flags[0] = 1;
     }
 
-    v4i accH[GM_TM], accL[GM_TM], accM[GM_TM];
-    float tot[GM_TM][4], off[GM_TM][4];
+    float tot[2][16], off[2][16];
 #pragma unroll
-    for (int mt = 0; mt < GM_TM; mt++) {
-        accH[mt] = v4i{0, 0, 0, 0};
-        accL[mt] = v4i{0, 0, 0, 0};
-        accM[mt] = v4i{0, 0, 0, 0};
-#pragma unroll
-        for (int r = 0; r < 4; r++) tot[mt][r] = off[mt][r] = 0.f;
-    }
+    for (int i = 0; i < 16; i++) tot[0][i] = tot[1][i] = off[0][i] = off[1][i] = 0.f;
+    v16i accH[2], accL[2], accM[2];
+    float dN = 0.f, dminN = 0.f;
 
-    gemm_issue_block<DT>(A, n0, m0, 0, smem);
-    for (int b = 0; b < nb; b++) {
-        uint8_t* buf = smem + (b & 1) * L::BUF;
-        if (b + 1 < nb) {
-            gemm_issue_block<DT>(A, n0, m0, b + 1, smem + ((b + 1) & 1) * L::BUF);
-            GM_WAIT_VMCNT(L::NDMA);  // block b's copies (issued earlier) have landed
-        } else {
-            GM_WAIT_VMCNT(0);
-        }
-        gm_barrier();
+    // Block b's integer sums (the MFMAs) from LDS buffer b & 1.
+    auto block_sums = [&](int b) {
+        const uint8_t* buf = smem + (b & 1) * L::BUF;
         const uint8_t* wl = buf;
         const uint8_t* al = buf + L::WBYTES;
-        const float* dl = (const float*)(al + L::ABYTES);
-
-        // A operand row (weights): wave rows 16*wave + ar.
-        float dC[4], dminC[4];
+        // row operands of k step ks: 16 bytes of two activation rows
+        auto arow = [&](int ks, int tt) -> v4i {
+            const int row = 64 * wm + 32 * tt + a;
+            return *(const v4i*)(al + row * 256 + 16 * ((2 * ks + g) ^ (row & 15)));
+        };
         if constexpr (DT == DT_Q4_K) {
-            const uint8_t* wr = wl + (16 * wn + ar) * L::WSLOT;
+            const uint8_t* wr = wl + (32 * wn + a) * L::WSLOT;
+            const uint32_t dd = *(const uint32_t*)wr;
+            dN = f16_to_f32(dd & 0xFFFFu);
+            dminN = f16_to_f32(dd >> 16);
             const uint32_t* sw = (const uint32_t*)(wr + 4);
             const Q4KScales s = q4k_scales(sw[0], sw[1], sw[2]);
+            u32x4 qv[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const uint32_t dd = *(const uint32_t*)(wl + (16 * wn + 4 * G + r) * L::WSLOT);
-                dC[r] = f16_to_f32(dd & 0xFFFFu);
-                dminC[r] = f16_to_f32(dd >> 16);
-            }
+            for (int c = 0; c < 4; c++) qv[c] = *(const u32x4*)(wr + 16 + 32 * c + 16 * g);
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                // All B operands of this k step first: their LDS latency then
-                // hides under the unpacking of the A planes.
-                v4i bvs[GM_TM];
-#pragma unroll
-                for (int mt = 0; mt < GM_TM; mt++) {
-                    const int row = 16 * (wm * GM_TM + mt) + ar;
-                    bvs[mt] = *(const v4i*)(al + row * 256 + 16 * ((4 * ks + G) ^ (row & 15)));
-                }
-                const int sub = 2 * ks + (G >> 1);
-                const uint32_t sc = byte_of(s.sc, sub), mm = byte_of(s.m, sub);
-                const u32x4 qraw = *(const u32x4*)(wr + 16 + 32 * ks + 16 * (G & 1));
-                const uint32_t qd[4] = {qraw.x, qraw.y, qraw.z, qraw.w};
+            for (int ks = 0; ks < 8; ks++) {
+                const v4i a0 = arow(ks, 0), a1 = arow(ks, 1);
+                const uint32_t sc = byte_of(s.sc, ks), mm = byte_of(s.m, ks);
                 // sc = 8*sh + sl with sh, sl <= 7: sh*q and sl*q (q <= 15) are at
                 // most 105, so each plane is the packed nibbles times a small
                 // constant (16-bit lanes, no carry between the bytes).
                 const short sh = (short)(sc >> 3), sl = (short)(sc & 7);
                 const s16x2 shp = {sh, sh}, slp = {sl, sl};
-                const int shift = 4 * (G >> 1);  // low nibbles for G < 2, high for G >= 2
-                v4i aH, aL, aM;
+                const int shift = 4 * (ks & 1);  // sub-block 2c: low nibbles, 2c+1: high
+                const u32x4 qd = qv[ks >> 1];
+                v4i bH, bL, bM;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const s16x2 nib = as_s16x2((qd[k] >> shift) & 0x0F0F0F0Fu);
-                    aH[k] = (int)as_u32(nib * shp);
-                    aL[k] = (int)as_u32(nib * slp);
-                    aM[k] = (int)(mm * 0x01010101u);
+                    bH[k] = (int)as_u32(nib * shp);
+                    bL[k] = (int)as_u32(nib * slp);
+                    bM[k] = (int)__builtin_amdgcn_perm(0u, mm, 0x00000000u);
                 }
-#pragma unroll
-                for (int mt = 0; mt < GM_TM; mt++) {
-                    accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bvs[mt], accH[mt], 0, 0, 0);
-                    accL[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, bvs[mt], accL[mt], 0, 0, 0);
-                    accM[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aM, bvs[mt], accM[mt], 0, 0, 0);
-                }
+                const v16i z = {};
+                accH[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bH, ks ? accH[0] : z, 0, 0, 0);
+                accH[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bH, ks ? accH[1] : z, 0, 0, 0);
+                accL[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bL, ks ? accL[0] : z, 0, 0, 0);
+                accL[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bL, ks ? accL[1] : z, 0, 0, 0);
+                accM[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bM, ks ? accM[0] : z, 0, 0, 0);
+                accM[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bM, ks ? accM[1] : z, 0, 0, 0);
             }
         } else {
-            // Q6_K: the row's block starts sh bytes into its slot.
-            auto wbyte_addr = [&](int row) -> const uint8_t* {
-                const int n = min(n0 + row, A.N - 1);
-                const uint8_t* blk = A.W + (int64_t)n * A.rb + (int64_t)b * Q6K_BYTES;
-                return wl + row * L::WSLOT + ((uintptr_t)blk & 3);
-            };
-            const uint8_t* wr = wbyte_addr(16 * wn + ar);
-            const uint32_t rsh = (uint32_t)((uintptr_t)wr & 3);
-            const uint32_t* wra = (const uint32_t*)(wr - rsh);
-            auto rd16 = [&](int off) -> u32x4 {  // 16 bytes at wr + off (off % 4 == 0)
-                const uint32_t* p = wra + off / 4;
-                return u32x4{__builtin_amdgcn_alignbyte(p[1], p[0], rsh), __builtin_amdgcn_alignbyte(p[2], p[1], rsh),
-                             __builtin_amdgcn_alignbyte(p[3], p[2], rsh), __builtin_amdgcn_alignbyte(p[4], p[3], rsh)};
-            };
+            const uint8_t* wr = wl + (32 * wn + a) * L::WSLOT + q6k_slot_off(A, nrow, b);
+            u32x4 qlv[4], qhv[2];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const uint8_t* wc = wbyte_addr(16 * wn + 4 * G + r);
-                dC[r] = f16_to_f32((uint32_t)wc[208] | ((uint32_t)wc[209] << 8));
-                dminC[r] = 0.f;
+            for (int i = 0; i < 4; i++) qlv[i] = lds_read16_a2(wr + 64 * (i >> 1) + 32 * (i & 1) + 16 * g);
+#pragma unroll
+            for (int h = 0; h < 2; h++) qhv[h] = lds_read16_a2(wr + 128 + 32 * h + 16 * g);
+            const u32x4 scv = lds_read16_a2(wr + 192);
+            {
+                const uint32_t* dw = (const uint32_t*)__builtin_align_down(wr + 208, 4);
+                const uint32_t sh = (uint32_t)((uintptr_t)(wr + 208) & 3);
+                dN = f16_to_f32(__builtin_amdgcn_alignbyte(dw[1], dw[0], sh) & 0xFFFFu);
             }
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                // All B operands of this k step first: their LDS latency then
-                // hides under the unpacking of the A planes.
-                v4i bvs[GM_TM];
-#pragma unroll
-                for (int mt = 0; mt < GM_TM; mt++) {
-                    const int row = 16 * (wm * GM_TM + mt) + ar;
-                    bvs[mt] = *(const v4i*)(al + row * 256 + 16 * ((4 * ks + G) ^ (row & 15)));
-                }
-                const int h = ks >> 1, p = 2 * (ks & 1) + (G >> 1);
-                const u32x4 ql = rd16(64 * h + 32 * (p & 1) + 16 * (G & 1));
-                const u32x4 qh = rd16(128 + 32 * h + 16 * (G & 1));
-                const int sc = (int)(int8_t)wr[192 + 8 * h + (G & 1) + 2 * p];
-                const s16x2 sc2 = {(short)sc, (short)sc};
-                const uint32_t qld[4] = {ql.x, ql.y, ql.z, ql.w}, qhd[4] = {qh.x, qh.y, qh.z, qh.w};
-                v4i aH, aL;
+            for (int ks = 0; ks < 8; ks++) {
+                const v4i a0 = arow(ks, 0), a1 = arow(ks, 1);
+                const int h = ks >> 2, p = ks & 3;
+                const u32x4 ql = qlv[2 * h + (p & 1)], qh = qhv[h];
+                const int si = 8 * h + g + 2 * p;  // scale of this lane's 16 elements
+                const int sc = (int)(int8_t)(uint8_t)(scv[si >> 2] >> (8 * (si & 3)));
+                // u = sc*q - 32*sc + 128 = w + 128 in 16-bit lanes (packed
+                // integer multiply-add, exact: |u| <= 4224)
+                const short cu = (short)(128 - 32 * sc);
+                const s16x2 sc2 = {(short)sc, (short)sc}, c2 = {cu, cu};
+                v4i bH, bL;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    const uint32_t q6 = (((p >> 1) ? (qld[k] >> 4) : qld[k]) & 0x0F0F0F0Fu) |
-                                        (((qhd[k] >> (2 * p)) & 0x03030303u) << 4);
-                    // 16-bit lanes of sc*(q - 32): packed integer ops, exact (|w| <= 4096)
-                    const s16x2 we = (as_s16x2(q6 & 0x00FF00FFu) - (s16x2){32, 32}) * sc2;
-                    const s16x2 wo = (as_s16x2((q6 >> 8) & 0x00FF00FFu) - (s16x2){32, 32}) * sc2;
-                    uint32_t lo, hi;
-                    split4(as_u32(we), as_u32(wo), as_u32(we >> (s16x2){7, 7}), as_u32(wo >> (s16x2){7, 7}), lo, hi);
-                    aL[k] = (int)lo;
-                    aH[k] = (int)hi;
+                    const uint32_t q6 = (((p >> 1) ? (ql[k] >> 4) : ql[k]) & 0x0F0F0F0Fu) |
+                                        (((qh[k] >> (2 * p)) & 0x03030303u) << 4);
+                    const uint32_t ue = as_u32(as_s16x2(__builtin_amdgcn_perm(0u, q6, 0x0C020C00u)) * sc2 + c2);
+                    const uint32_t uo = as_u32(as_s16x2(__builtin_amdgcn_perm(0u, q6, 0x0C030C01u)) * sc2 + c2);
+                    // v_perm selector [src1.bX, src0.bX, src1.bY, src0.bY]: the
+                    // high bytes of the lanes (hi) and the low bytes (lo + 128)
+                    bH[k] = (int)__builtin_amdgcn_perm(uo, ue, 0x07030501u);
+                    bL[k] = (int)(__builtin_amdgcn_perm(uo, ue, 0x06020400u) ^ 0x80808080u);
                 }
+                const v16i z = {};
+                accH[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bH, ks ? accH[0] : z, 0, 0, 0);
+                accH[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bH, ks ? accH[1] : z, 0, 0, 0);
+                accL[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bL, ks ? accL[0] : z, 0, 0, 0);
+                accL[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bL, ks ? accL[1] : z, 0, 0, 0);
+            }
+        }
+    };
+    // Block b's float step, per output in block order: lane l holds
+    // activation rows 8j + 4g + r of each row tile against its weight row.
+    auto block_chain = [&](int b) {
+        const float* dl = (const float*)(dxs + (b % 3) * L::DXBYTES);
 #pragma unroll
-                for (int mt = 0; mt < GM_TM; mt++) {
-                    accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bvs[mt], accH[mt], 0, 0, 0);
-                    accL[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, bvs[mt], accL[mt], 0, 0, 0);
+        for (int tt = 0; tt < 2; tt++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float4 dx4 = *(const float4*)(dl + 64 * wm + 32 * tt + 8 * j + 4 * g);
+                const float dxr[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int i = 4 * j + r;
+                    const int S = (accH[tt][i] << (DT == DT_Q4_K ? 3 : 8)) + accL[tt][i];
+                    tot[tt][i] = __builtin_fmaf((float)S, dN * dxr[r], tot[tt][i]);
+                    if constexpr (DT == DT_Q4_K)
+                        off[tt][i] = __builtin_fmaf((float)accM[tt][i], dminN * dxr[r], off[tt][i]);
                 }
             }
         }
+    };
 
-        // The block's float step, per output in block order.
-#pragma unroll
-        for (int mt = 0; mt < GM_TM; mt++) {
-            const float dx = dl[16 * (wm * GM_TM + mt) + ar];
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int S = (accH[mt][r] << (DT == DT_Q4_K ? 3 : 7)) + accL[mt][r];
-                tot[mt][r] = __builtin_fmaf((float)S, dC[r] * dx, tot[mt][r]);
-                if (DT == DT_Q4_K) off[mt][r] = __builtin_fmaf((float)accM[mt][r], dminC[r] * dx, off[mt][r]);
-            }
-            accH[mt] = v4i{0, 0, 0, 0};
-            accL[mt] = v4i{0, 0, 0, 0};
-            accM[mt] = v4i{0, 0, 0, 0};
+    // Block b's copies (weights and activations into buffer b & 1, the
+    // activation scales into dx stage b % 3) are issued at the start of the
+    // first half of block b-1 and waited for at the end of its second half.
+    // Buffer (b+1) & 1 was last read by the trailing waves' sums of block
+    // b-1, before the barrier that starts block b's first half; dx stage
+    // (b+1) % 3 by the chain of block b-2.
+    gemm_issue_block<DT, NW, WM>(A, n0, m0, 0, smem, dxs);
+    GM_WAIT_VMCNT(0);
+    gm_barrier();
+    for (int b = 0; b <= nb; b++) {
+        // first half: the leaders' sums of block b, the trailers' chain of b-1
+        if (b + 1 < nb)
+            gemm_issue_block<DT, NW, WM>(A, n0, m0, b + 1, smem + ((b + 1) & 1) * L::BUF,
+                                         dxs + ((b + 1) % 3) * L::DXBYTES);
+        if (leader) {
+            if (b < nb) block_sums(b);
+        } else if (b > 0) {
+            block_chain(b - 1);
         }
         GM_WAIT_LGKM0();
-        gm_barrier();  // buffer b&1 is reloaded in the next iteration
+        gm_barrier();
+        if (b == nb) break;
+        // second half: the leaders' chain of block b, the trailers' sums of b
+        if (leader) block_chain(b);
+        else block_sums(b);
+        GM_WAIT_VMCNT(0);  // block b+1's copies have landed
+        GM_WAIT_LGKM0();
+        gm_barrier();
     }
 
-    // Outputs: lane holds rows n = n0 + 16*wave + 4G + r of column m.
-    const int nbase = n0 + 16 * wn + 4 * G;
+    // Outputs: lane l holds weight row n against activation rows m.
+    const int n = n0 + 32 * wn + a;
     const int refused = flags[0];
+    if (n < A.N && !(refused && A.wref[n] != 0)) {
+        const float bn = A.bias ? A.bias[n] : 0.f;
 #pragma unroll
-    for (int mt = 0; mt < GM_TM; mt++) {
-        const int m = m0 + 16 * (wm * GM_TM + mt) + ar;
-        if (m >= A.M) continue;
-        if (refused && A.ok[m] == 0) continue;
+        for (int tt = 0; tt < 2; tt++) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int n = nbase + r;
-            if (n >= A.N) continue;
-            if (refused && A.wref[n] != 0) continue;
-            float res = DT == DT_Q4_K ? tot[mt][r] - off[mt][r] : tot[mt][r];
-            if (A.bias) res += A.bias[n];
-            A.y[(int64_t)m * A.N + n] = res;
+            for (int i = 0; i < 16; i++) {
+                const int m = m0 + 64 * wm + 32 * tt + 8 * (i >> 2) + 4 * g + (i & 3);
+                if (m >= A.M) continue;
+                if (refused && A.ok[m] == 0) continue;
+                float res = DT == DT_Q4_K ? tot[tt][i] - off[tt][i] : tot[tt][i];
+                if (A.bias) res += bn;
+                A.y[(int64_t)m * A.N + n] = res;
+            }
         }
     }
     if (!refused) return;
     // Refused pairs of the tile: the float32 path, one group of eight lanes
     // per (row, activation row).
-    const int g = t >> 3;
-    for (int pidx = g; pidx < GM_BN * GM_BM; pidx += GM_T / 8) {
-        const int n = n0 + pidx % GM_BN, m = m0 + pidx / GM_BN;
-        if (n >= A.N || m >= A.M) continue;
-        if (A.wref[n] == 0 && A.ok[m] != 0) continue;
-        float res = f32dot_g8<DT>(A.W + (int64_t)n * A.rb, A.x + (int64_t)m * A.K, A.K, A.fused != 0);
-        if (A.bias) res += A.bias[n];
-        if ((t & 7) == 0) A.y[(int64_t)m * A.N + n] = res;
+    const int grp = t >> 3;
+    for (int pidx = grp; pidx < L::BN * L::BM; pidx += L::T / 8) {
+        const int nn = n0 + pidx % L::BN, m = m0 + pidx / L::BN;
+        if (nn >= A.N || m >= A.M) continue;
+        if (A.wref[nn] == 0 && A.ok[m] != 0) continue;
+        float res = f32dot_g8<DT>(A.W + (int64_t)nn * A.rb, A.x + (int64_t)m * A.K, A.K, A.fused != 0);
+        if (A.bias) res += A.bias[nn];
+        if ((t & 7) == 0) A.y[(int64_t)m * A.N + nn] = res;
     }
 }
 
@@ -388,11 +404,19 @@ hipError_t launch_gemm_a8k(const DevWeight& w, const ActPtrs& a, int64_t rows, i
     A.ok = a.ok;
     A.x = x;
     A.fused = total_rows <= 8;
-    dim3 grid((unsigned)((w.n + GM_BN - 1) / GM_BN), (unsigned)((rows + GM_BM - 1) / GM_BM));
-    if (w.dt == DT_Q4_K)
-        hipLaunchKernelGGL(gemm_a8k_kernel<DT_Q4_K>, grid, dim3(GM_T), 0, stream, A);
-    else
-        hipLaunchKernelGGL(gemm_a8k_kernel<DT_Q6_K>, grid, dim3(GM_T), 0, stream, A);
+    // 128 weight rows x 128 activation rows per workgroup of eight waves;
+    // where that leaves CUs without a workgroup (few weight or activation
+    // rows: down at 512 rows, 64 prompt rows) the 16 x 16 x 64 kernel with
+    // 64-row tiles runs instead (measured on MI355X: gate/down at 64 rows
+    // 41/155 against 57/218 us, down at 512 rows 176 against 222 us).
+    constexpr int BN = 128, BM = 128;
+    A.tiles_m = (int)((rows + BM - 1) / BM);
+    const int64_t nwg = (w.n + BN - 1) / BN * A.tiles_m;
+    if (nwg < 256) return launch_gemm_a8k_16(w, a, rows, total_rows, x, bias, y, stream);
+    if (nwg > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)nwg), block(512);
+    if (w.dt == DT_Q4_K) hipLaunchKernelGGL((gemm_a8k_kernel<DT_Q4_K, 4, 2>), grid, block, 0, stream, A);
+    else hipLaunchKernelGGL((gemm_a8k_kernel<DT_Q6_K, 4, 2>), grid, block, 0, stream, A);
     return hipGetLastError();
 }
 

@@ -1,0 +1,389 @@
+// Prefill GEMM for small grids: Q4_K / Q6_K weights x 8-bit activations in
+// blocks of 256 on v_mfma_i32_16x16x64_i8, 64 weight rows x 128 activation
+// rows per workgroup of eight waves. gemm_kquant.hip's 32 x 32 x 32 kernel
+// takes 128 x 128 tiles; where that gives fewer workgroups than the GPU has
+// CUs (few weight rows or few activation rows, e.g. 64 prompt rows) this one
+// runs instead. Same result, bit for bit (both equal the decode GEMV):
+// per (weight row n, activation row m) and block b the exact int32
+//   Q4_K  S = sum_k sc_s(k) q_k y_k,   M = sum_k m_s(k) y_k (= sum_s m_s xs_s)
+//   Q6_K  S = sum_k sc_s(k) (q_k - 32) y_k
+// then serially in block order tot = fma(f32(S), d*dx_b, tot) (and off for
+// Q4_K), result tot - off (+ bias), as dotQ8KRef (reference
+// internal/kernels/q8k_test.go:38-102; tiles as amx.go:194-316).
+//
+// Exact products on int8 MFMA: Q4_K sc = 8*sh + sl (sh, sl <= 7), planes
+// sh*q and sl*q (each <= 105), S = 8*H + L; Q6_K w = 128*hi + lo, lo in
+// [0,127], hi in [-32,31]; Q4_K's M term is a third plane with A = m_s.
+//
+// Tiling: wave w takes weight rows 16w..16w+15 (A operand: lane l holds row
+// l%16 and the 16 k of group l/16) against activation tiles of 16 (B, same k
+// mapping); C lane l holds rows 4(l/16)+r, column l%16. Per block of 256 the
+// raw weight blocks, the int8 activation rows and their scales are copied
+// into LDS with global_load_lds, double-buffered. Activation rows sit in LDS
+// with their 16-byte chunks XOR-swizzled by row (chunk c of row m at
+// c ^ (m & 15)). Refused rows take the float32 path at the end.
+#include "f32path.hpp"
+#include "mimg_device.hpp"
+#include "mimg_kernels.hpp"
+
+namespace mimg {
+namespace g16 {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+#ifndef MIMG_GEMM_BM
+#define MIMG_GEMM_BM 128
+#endif
+#ifndef MIMG_GEMM_THREADS
+#define MIMG_GEMM_THREADS 512
+#endif
+#ifndef MIMG_GEMM_NW
+#define MIMG_GEMM_NW 4
+#endif
+constexpr int GM_T = MIMG_GEMM_THREADS;   // threads per workgroup (256: one wave per SIMD, 512: two)
+constexpr int GM_NW = MIMG_GEMM_NW;       // waves along the weight rows (16 rows each)
+constexpr int GM_BN = 16 * GM_NW;         // weight rows per workgroup
+constexpr int GM_BM = MIMG_GEMM_BM;       // activation rows per workgroup
+constexpr int GM_WM = GM_T / 64 / GM_NW;  // waves along the activation rows
+constexpr int GM_TM = GM_BM / 16 / GM_WM; // activation tiles of 16 per wave
+static_assert(GM_WM * GM_NW * 64 == GM_T && GM_TM * GM_WM * 16 == GM_BM && GM_T >= GM_BN && GM_T >= GM_BM,
+              "GEMM tile shape");
+constexpr int GM_ACH = GM_BM * 16 / GM_T; // activation copy instructions per thread per block
+
+template <uint32_t DT>
+struct GemmLayout {
+    // LDS bytes per weight row slot: Q4_K blocks are 16-byte aligned and
+    // copied as 9 chunks; Q6_K blocks (2-byte aligned) are copied as the 54
+    // aligned dwords that cover them.
+    static constexpr int WSLOT = DT == DT_Q4_K ? 144 : 216;
+    static constexpr int WDMA = DT == DT_Q4_K ? (GM_BN * 9 + GM_T - 1) / GM_T   // copy instructions per
+                                             : (GM_BN * 54 + GM_T - 1) / GM_T;  // thread per block
+    static constexpr int WBYTES = WDMA * GM_T * (DT == DT_Q4_K ? 16 : 4);  // incl. slack for unconditional copies
+    static constexpr int ABYTES = GM_BM * 256;
+    static constexpr int DXBYTES = GM_T * 4;
+    static constexpr int BUF = WBYTES + ABYTES + DXBYTES;
+    static constexpr int NDMA = WDMA + GM_ACH + 1;
+};
+
+struct GemmArgs {
+    const uint8_t* W;
+    const uint8_t* wref;   // [N]
+    const float* bias;     // [N] or null
+    float* y;              // [M][N]
+    int64_t rb;            // bytes per weight row
+    int N, M, nb;
+    int64_t K;
+    const int8_t* q;       // [M][K]
+    const float* d32;      // [M][K/32]
+    const int32_t* ok;     // [M]
+    const float* x;        // [M][K] f32 (fallback)
+    int fused;             // float32 fallback order (rows of the whole call <= 8)
+};
+
+// Global -> LDS copies (global_load_lds: lane i of the wave writes its 16
+// or 4 bytes at the wave's LDS base + 16i or 4i). Written as inline
+// assembly so that the compiler does not track them: it would otherwise wait
+// for every copy in flight (vmcnt(0)) before the first LDS read of a block,
+// including the next block's prefetch. The waits are explicit instead
+// (GM_WAIT_VMCNT), and the compiler's own waits can only be stronger, the
+// counter retiring in order.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
+}
+__device__ __forceinline__ void lds_copy16(const void* g, uint8_t* lds_wave_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr(lds_wave_base))
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void lds_copy4(const void* g, uint8_t* lds_wave_base) {
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_addr(lds_wave_base))
+                 : "memory", "m0");
+}
+
+// s_waitcnt with vmcnt <= n (n < 64) and the other counters unconstrained.
+#define GM_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+// s_waitcnt lgkmcnt(0) (LDS reads of this wave done).
+#define GM_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)
+
+// A workgroup barrier without the memory fence of __syncthreads, whose
+// vmcnt(0) would also wait for the next block's copies in flight; the
+// waits it needs are written out before it.
+__device__ __forceinline__ void gm_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Issues the copies of block b into LDS buffer `buf` (every thread issues
+// exactly NDMA instructions, so the wait counts are the same in each wave).
+template <uint32_t DT>
+__device__ __forceinline__ void gemm_issue_block(const GemmArgs& A, int n0, int m0, int b, uint8_t* buf) {
+    using L = GemmLayout<DT>;
+    const int t = threadIdx.x, wave = t >> 6;  // wave of the workgroup (0 .. GM_T/64-1)
+    uint8_t* wl = buf;
+    uint8_t* al = buf + L::WBYTES;
+    uint8_t* dl = al + L::ABYTES;
+    if constexpr (DT == DT_Q4_K) {
+#pragma unroll
+        for (int i = 0; i < L::WDMA; i++) {
+            const int c = min(GM_T * i + t, GM_BN * 9 - 1);  // chunk of 16 bytes
+            const int r = c / 9, j = c - 9 * r;
+            const int n = min(n0 + r, A.N - 1);
+            lds_copy16(A.W + (int64_t)n * A.rb + (int64_t)b * Q4K_BYTES + 16 * j, wl + 16 * (GM_T * i + 64 * wave));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < L::WDMA; i++) {
+            const int c = min(GM_T * i + t, GM_BN * 54 - 1);  // dword
+            const int r = c / 54, j = c - 54 * r;
+            const int n = min(n0 + r, A.N - 1);
+            const uint8_t* blk = A.W + (int64_t)n * A.rb + (int64_t)b * Q6K_BYTES;
+            const uint8_t* base = (const uint8_t*)__builtin_align_down(blk, 4);
+            lds_copy4(base + 4 * j, wl + 4 * (GM_T * i + 64 * wave));
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < GM_ACH; i++) {
+        const int c = GM_T * i + t;              // LDS chunk: row c/16, slot c%16
+        const int r = c >> 4, s = c & 15;
+        const int m = min(m0 + r, A.M - 1);
+        lds_copy16(A.q + (int64_t)m * A.K + 256 * b + 16 * (s ^ (r & 15)), al + 16 * (GM_T * i + 64 * wave));
+    }
+    {
+        const int m = min(m0 + min(t, GM_BM - 1), A.M - 1);
+        lds_copy4(A.d32 + (int64_t)m * (A.K / 32) + 8 * b, dl + 4 * (64 * wave));  // slots t >= GM_BM are slack
+    }
+}
+
+template <uint32_t DT>
+__global__ __launch_bounds__(GM_T) void gemm_a8k_kernel(GemmArgs A) {
+    using L = GemmLayout<DT>;
+    __shared__ __align__(16) uint8_t smem[2 * L::BUF];
+    __shared__ int flags[2];
+    const int t = threadIdx.x, l = t & 63;
+    const int wn = (t >> 6) % GM_NW, wm = (t >> 6) / GM_NW;  // this wave's weight rows 16wn.., activation tiles wm*GM_TM..
+    const int ar = l & 15, G = l >> 4;
+    const int n0 = blockIdx.x * GM_BN, m0 = blockIdx.y * GM_BM;
+    const int nb = A.nb;
+
+    // Refusals of this tile: any weight row with a non-finite block scale,
+    // any refused activation row.
+    if (t == 0) flags[0] = 0;
+    __syncthreads();
+    {
+        int f = 0;
+        if (t < GM_BN && n0 + t < A.N) f |= A.wref[n0 + t] != 0;
+        if (t < GM_BM && m0 + t < A.M) f |= A.ok[m0 + t] == 0;
+        if (f) flags[0] = 1;
+    }
+
+    v4i accH[GM_TM], accL[GM_TM], accM[GM_TM];
+    float tot[GM_TM][4], off[GM_TM][4];
+#pragma unroll
+    for (int mt = 0; mt < GM_TM; mt++) {
+        accH[mt] = v4i{0, 0, 0, 0};
+        accL[mt] = v4i{0, 0, 0, 0};
+        accM[mt] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int r = 0; r < 4; r++) tot[mt][r] = off[mt][r] = 0.f;
+    }
+
+    gemm_issue_block<DT>(A, n0, m0, 0, smem);
+    for (int b = 0; b < nb; b++) {
+        uint8_t* buf = smem + (b & 1) * L::BUF;
+        if (b + 1 < nb) {
+            gemm_issue_block<DT>(A, n0, m0, b + 1, smem + ((b + 1) & 1) * L::BUF);
+            GM_WAIT_VMCNT(L::NDMA);  // block b's copies (issued earlier) have landed
+        } else {
+            GM_WAIT_VMCNT(0);
+        }
+        gm_barrier();
+        const uint8_t* wl = buf;
+        const uint8_t* al = buf + L::WBYTES;
+        const float* dl = (const float*)(al + L::ABYTES);
+
+        // A operand row (weights): wave rows 16*wave + ar.
+        float dC[4], dminC[4];
+        if constexpr (DT == DT_Q4_K) {
+            const uint8_t* wr = wl + (16 * wn + ar) * L::WSLOT;
+            const uint32_t* sw = (const uint32_t*)(wr + 4);
+            const Q4KScales s = q4k_scales(sw[0], sw[1], sw[2]);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t dd = *(const uint32_t*)(wl + (16 * wn + 4 * G + r) * L::WSLOT);
+                dC[r] = f16_to_f32(dd & 0xFFFFu);
+                dminC[r] = f16_to_f32(dd >> 16);
+            }
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                // All B operands of this k step first: their LDS latency then
+                // hides under the unpacking of the A planes.
+                v4i bvs[GM_TM];
+#pragma unroll
+                for (int mt = 0; mt < GM_TM; mt++) {
+                    const int row = 16 * (wm * GM_TM + mt) + ar;
+                    bvs[mt] = *(const v4i*)(al + row * 256 + 16 * ((4 * ks + G) ^ (row & 15)));
+                }
+                const int sub = 2 * ks + (G >> 1);
+                const uint32_t sc = byte_of(s.sc, sub), mm = byte_of(s.m, sub);
+                const u32x4 qraw = *(const u32x4*)(wr + 16 + 32 * ks + 16 * (G & 1));
+                const uint32_t qd[4] = {qraw.x, qraw.y, qraw.z, qraw.w};
+                // sc = 8*sh + sl with sh, sl <= 7: sh*q and sl*q (q <= 15) are at
+                // most 105, so each plane is the packed nibbles times a small
+                // constant (16-bit lanes, no carry between the bytes).
+                const short sh = (short)(sc >> 3), sl = (short)(sc & 7);
+                const s16x2 shp = {sh, sh}, slp = {sl, sl};
+                const int shift = 4 * (G >> 1);  // low nibbles for G < 2, high for G >= 2
+                v4i aH, aL, aM;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const s16x2 nib = as_s16x2((qd[k] >> shift) & 0x0F0F0F0Fu);
+                    aH[k] = (int)as_u32(nib * shp);
+                    aL[k] = (int)as_u32(nib * slp);
+                    aM[k] = (int)(mm * 0x01010101u);
+                }
+#pragma unroll
+                for (int mt = 0; mt < GM_TM; mt++) {
+                    accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bvs[mt], accH[mt], 0, 0, 0);
+                    accL[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, bvs[mt], accL[mt], 0, 0, 0);
+                    accM[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aM, bvs[mt], accM[mt], 0, 0, 0);
+                }
+            }
+        } else {
+            // Q6_K: the row's block starts sh bytes into its slot.
+            auto wbyte_addr = [&](int row) -> const uint8_t* {
+                const int n = min(n0 + row, A.N - 1);
+                const uint8_t* blk = A.W + (int64_t)n * A.rb + (int64_t)b * Q6K_BYTES;
+                return wl + row * L::WSLOT + ((uintptr_t)blk & 3);
+            };
+            const uint8_t* wr = wbyte_addr(16 * wn + ar);
+            const uint32_t rsh = (uint32_t)((uintptr_t)wr & 3);
+            const uint32_t* wra = (const uint32_t*)(wr - rsh);
+            auto rd16 = [&](int off) -> u32x4 {  // 16 bytes at wr + off (off % 4 == 0)
+                const uint32_t* p = wra + off / 4;
+                return u32x4{__builtin_amdgcn_alignbyte(p[1], p[0], rsh), __builtin_amdgcn_alignbyte(p[2], p[1], rsh),
+                             __builtin_amdgcn_alignbyte(p[3], p[2], rsh), __builtin_amdgcn_alignbyte(p[4], p[3], rsh)};
+            };
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint8_t* wc = wbyte_addr(16 * wn + 4 * G + r);
+                dC[r] = f16_to_f32((uint32_t)wc[208] | ((uint32_t)wc[209] << 8));
+                dminC[r] = 0.f;
+            }
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                // All B operands of this k step first: their LDS latency then
+                // hides under the unpacking of the A planes.
+                v4i bvs[GM_TM];
+#pragma unroll
+                for (int mt = 0; mt < GM_TM; mt++) {
+                    const int row = 16 * (wm * GM_TM + mt) + ar;
+                    bvs[mt] = *(const v4i*)(al + row * 256 + 16 * ((4 * ks + G) ^ (row & 15)));
+                }
+                const int h = ks >> 1, p = 2 * (ks & 1) + (G >> 1);
+                const u32x4 ql = rd16(64 * h + 32 * (p & 1) + 16 * (G & 1));
+                const u32x4 qh = rd16(128 + 32 * h + 16 * (G & 1));
+                const int sc = (int)(int8_t)wr[192 + 8 * h + (G & 1) + 2 * p];
+                const s16x2 sc2 = {(short)sc, (short)sc};
+                const uint32_t qld[4] = {ql.x, ql.y, ql.z, ql.w}, qhd[4] = {qh.x, qh.y, qh.z, qh.w};
+                v4i aH, aL;
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint32_t q6 = (((p >> 1) ? (qld[k] >> 4) : qld[k]) & 0x0F0F0F0Fu) |
+                                        (((qhd[k] >> (2 * p)) & 0x03030303u) << 4);
+                    // 16-bit lanes of sc*(q - 32): packed integer ops, exact (|w| <= 4096)
+                    const s16x2 we = (as_s16x2(q6 & 0x00FF00FFu) - (s16x2){32, 32}) * sc2;
+                    const s16x2 wo = (as_s16x2((q6 >> 8) & 0x00FF00FFu) - (s16x2){32, 32}) * sc2;
+                    uint32_t lo, hi;
+                    split4(as_u32(we), as_u32(wo), as_u32(we >> (s16x2){7, 7}), as_u32(wo >> (s16x2){7, 7}), lo, hi);
+                    aL[k] = (int)lo;
+                    aH[k] = (int)hi;
+                }
+#pragma unroll
+                for (int mt = 0; mt < GM_TM; mt++) {
+                    accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bvs[mt], accH[mt], 0, 0, 0);
+                    accL[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, bvs[mt], accL[mt], 0, 0, 0);
+                }
+            }
+        }
+
+        // The block's float step, per output in block order.
+#pragma unroll
+        for (int mt = 0; mt < GM_TM; mt++) {
+            const float dx = dl[16 * (wm * GM_TM + mt) + ar];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int S = (accH[mt][r] << (DT == DT_Q4_K ? 3 : 7)) + accL[mt][r];
+                tot[mt][r] = __builtin_fmaf((float)S, dC[r] * dx, tot[mt][r]);
+                if (DT == DT_Q4_K) off[mt][r] = __builtin_fmaf((float)accM[mt][r], dminC[r] * dx, off[mt][r]);
+            }
+            accH[mt] = v4i{0, 0, 0, 0};
+            accL[mt] = v4i{0, 0, 0, 0};
+            accM[mt] = v4i{0, 0, 0, 0};
+        }
+        GM_WAIT_LGKM0();
+        gm_barrier();  // buffer b&1 is reloaded in the next iteration
+    }
+
+    // Outputs: lane holds rows n = n0 + 16*wave + 4G + r of column m.
+    const int nbase = n0 + 16 * wn + 4 * G;
+    const int refused = flags[0];
+#pragma unroll
+    for (int mt = 0; mt < GM_TM; mt++) {
+        const int m = m0 + 16 * (wm * GM_TM + mt) + ar;
+        if (m >= A.M) continue;
+        if (refused && A.ok[m] == 0) continue;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int n = nbase + r;
+            if (n >= A.N) continue;
+            if (refused && A.wref[n] != 0) continue;
+            float res = DT == DT_Q4_K ? tot[mt][r] - off[mt][r] : tot[mt][r];
+            if (A.bias) res += A.bias[n];
+            A.y[(int64_t)m * A.N + n] = res;
+        }
+    }
+    if (!refused) return;
+    // Refused pairs of the tile: the float32 path, one group of eight lanes
+    // per (row, activation row).
+    const int g = t >> 3;
+    for (int pidx = g; pidx < GM_BN * GM_BM; pidx += GM_T / 8) {
+        const int n = n0 + pidx % GM_BN, m = m0 + pidx / GM_BN;
+        if (n >= A.N || m >= A.M) continue;
+        if (A.wref[n] == 0 && A.ok[m] != 0) continue;
+        float res = f32dot_g8<DT>(A.W + (int64_t)n * A.rb, A.x + (int64_t)m * A.K, A.K, A.fused != 0);
+        if (A.bias) res += A.bias[n];
+        if ((t & 7) == 0) A.y[(int64_t)m * A.N + n] = res;
+    }
+}
+
+}  // namespace g16
+
+// The 16 x 16 x 64 form of the prefill GEMM (see the top of this file).
+hipError_t launch_gemm_a8k_16(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows, const float* x,
+                           const float* bias, float* y, hipStream_t stream) {
+    using namespace g16;
+    if (!gemm_a8k_ok(w) || rows <= 0 || rows > (1 << 30) || w.n > (1 << 30)) return hipErrorInvalidValue;
+    GemmArgs A;
+    A.W = w.data;
+    A.wref = w.wref;
+    A.bias = bias;
+    A.y = y;
+    A.rb = w.row_bytes;
+    A.N = (int)w.n;
+    A.M = (int)rows;
+    A.nb = (int)(w.k / 256);
+    A.K = w.k;
+    A.q = a.q;
+    A.d32 = a.d32;
+    A.ok = a.ok;
+    A.x = x;
+    A.fused = total_rows <= 8;
+    dim3 grid((unsigned)((w.n + GM_BN - 1) / GM_BN), (unsigned)((rows + GM_BM - 1) / GM_BM));
+    if (w.dt == DT_Q4_K)
+        hipLaunchKernelGGL(gemm_a8k_kernel<DT_Q4_K>, grid, dim3(GM_T), 0, stream, A);
+    else
+        hipLaunchKernelGGL(gemm_a8k_kernel<DT_Q6_K>, grid, dim3(GM_T), 0, stream, A);
+    return hipGetLastError();
+}
+
+}  // namespace mimg

@@ -82,6 +82,10 @@ hipError_t launch_gemv_a8k_tiles(const DevWeight* const* ws, int nmat, const Act
 // Many activation rows (already quantized) against one Q4_K/Q6_K matrix,
 // on the int8 matrix cores (gemm_kquant.hip); bit-identical to the GEMV.
 bool gemm_a8k_ok(const DevWeight& w);
+// The 16 x 16 x 64 form for small grids (gemm_kquant16.hip); launch_gemm_a8k
+// picks it by grid size.
+hipError_t launch_gemm_a8k_16(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows, const float* x,
+                              const float* bias, float* y, hipStream_t stream);
 hipError_t launch_gemm_a8k(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows, const float* x,
                            const float* bias, float* y, hipStream_t stream);
 

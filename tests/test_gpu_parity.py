@@ -216,6 +216,46 @@ def test_gemm_a8k_bitexact(gpu, oracle, dt, rows, n, k):
     assert bits_equal(got, want), first_diff(got, want)
 
 
+@pytest.mark.parametrize("dt,rows,n,k", [(Q4_K, 1100, 4100, 256), (Q6_K, 1000, 4160, 1024), (Q4_K, 2050, 2070, 2048),
+                                         (Q6_K, 1290, 3000, 768), (Q6_K, 1030, 4096, 2304)])
+def test_gemm_a8k_wide_tiles_bitexact(gpu, oracle, dt, rows, n, k):
+    """Grids of at least 256 tiles of 128 x 128 run on the 32x32x32 kernel
+    (ping-pong waves): ragged last weight and activation tiles, K from one
+    block up, Q6_K rows whose blocks sit at every offset mod 16; bit for bit
+    the reference."""
+    wb = _weights(oracle, dt, n, k, seed=rows + n + k)
+    x = oracle.synthetic_acts(rows, k, seed=rows + 2)
+    W = gpu.Weight(wb, dt, n, k)
+    got = gpu.dequant_matmul_a8(W, x, block=256)
+    want = oracle.linear_a8(x, wb, dt, n, k, block=256, threads=16)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K])
+def test_gemm_a8k_wide_tiles_refusals_and_bias(gpu, oracle, dt):
+    """The 32x32x32 kernel's refused pairs (a NaN activation row, a row
+    above 2^60, weight rows with an infinite or NaN block scale) take the
+    float32 path, and bias is added as s + bias[j]."""
+    n, k, rows = 4100, 512, 1040
+    wb = bytearray(_weights(oracle, dt, n, k, seed=18).tobytes())
+    rb = len(wb) // n
+    f = 208 if dt == Q6_K else 2
+    for j, blk in ((5, 0), (3000, 1)):
+        o = rb * j + blk * (210 if dt == Q6_K else 144) + f
+        wb[o:o + 2] = b"\x00\x7c" if j == 5 else b"\x01\x7e"
+    wb = np.frombuffer(bytes(wb), np.uint8)
+    x = oracle.synthetic_acts(rows, k, seed=19)
+    x[7, 3] = np.nan
+    x[900, 100] = np.float32(1e30)
+    bias = np.random.default_rng(20).standard_normal(n).astype(np.float32)
+    W = gpu.Weight(wb, dt, n, k)
+    got = gpu.dequant_matmul_a8(W, x, bias=bias, block=256)
+    want = oracle.linear_a8(x, wb, dt, n, k, bias=bias, block=256, threads=16)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+
+
 @pytest.mark.parametrize("dt", [Q4_K, Q6_K])
 @pytest.mark.parametrize("rows", [1, 3, 12, 40])
 def test_linear_a8k_refusals_and_bias(gpu, oracle, dt, rows):
