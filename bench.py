@@ -111,6 +111,31 @@ def make_weights(stream, rotate, log):
     return layers, host_bytes
 
 
+def make_q8_0_weights(stream, rotate, log):
+    """BASELINE configs[2]'s Q8_0 variant of gate (= up's shape) and down:
+    the same f32 weights (seeds 4 and 6) encoded as Q8_0 (the reference's
+    encoder, mim.Quantize), `rotate` device copies each."""
+    layers = [dict() for _ in range(rotate)]
+    for name, n, k, _, seed, _ in CFG1:
+        if name not in ("gate", "down"):
+            continue
+        t0 = time.time()
+        w32 = np.random.default_rng(seed).standard_normal((n, k), dtype=np.float32)
+        w32 *= np.float32(0.02)
+        xd = hiprt.DeviceBuffer.from_array(w32)
+        del w32
+        nb = n * (k // 32) * 34
+        enc = hiprt.DeviceBuffer(nb)
+        mimg.quantize_dev(mimg.Q8_0, xd.ptr, n * k, enc.ptr, nb, stream.handle)
+        stream.sync()
+        xd.free()
+        for l in range(rotate):
+            layers[l][name] = mimg.Weight((enc.ptr, nb), mimg.Q8_0, n, k, device=True)
+        enc.free()
+        log(f"  {name} Q8_0: {n}x{k} {nb / 1e6:.1f} MB x {rotate} ({time.time() - t0:.1f} s)")
+    return layers
+
+
 def cpu_baseline(host_bytes, xs, seconds, log):
     """The oracle's linear_a8 (C restatement of the reference numerics) over
     the seven matrices of one layer, on this host's cores."""
@@ -434,20 +459,22 @@ def main():
     # dequant_matmul.v1): the same products with float32 activations on the
     # fp32 matrix cores (mimg_linear_f32_mfma_dev), fraction of the dense
     # fp32 matrix peak.
-    def prefill(name, rows, f32=False):
+    def prefill(name, rows, f32=False, q8_layers=None):
         _, n, k, dt, _, _ = next(c for c in CFG1 if c[0] == name)
+        block = 32 if q8_layers else 256
         xp = hiprt.DeviceBuffer.from_array(np.random.default_rng(200 + rows).standard_normal((rows, k), dtype=np.float32))
         wsb = mimg.a8_workspace_bytes(rows, k)
         wsp = hiprt.DeviceBuffer(wsb)
         yp = hiprt.DeviceBuffer(rows * n * 4)
-        mimg.quantize_act_dev(xp.ptr, rows, k, 256, wsp.ptr, wsb, stream.handle)
+        mimg.quantize_act_dev(xp.ptr, rows, k, block, wsp.ptr, wsb, stream.handle)
+        src = q8_layers or layers
 
         def launches():
             for l in range(args.rotate):
                 if f32:
-                    mimg.linear_f32_mfma_dev(layers[l][name], xp.ptr, rows, None, yp.ptr, stream.handle)
+                    mimg.linear_f32_mfma_dev(src[l][name], xp.ptr, rows, None, yp.ptr, stream.handle)
                 else:
-                    mimg.matmul_a8_quantized_dev(layers[l][name], xp.ptr, rows, None, 256, yp.ptr, wsp.ptr, wsb,
+                    mimg.matmul_a8_quantized_dev(src[l][name], xp.ptr, rows, None, block, yp.ptr, wsp.ptr, wsb,
                                                  stream.handle)
 
         g = hiprt.Graph(stream, launches)
@@ -457,6 +484,7 @@ def main():
         g.launch(stream)
         b.record(stream)
         b.sync()
+        g.destroy()
         us = a.elapsed_ms(b) * 1e3 / args.rotate
         for buf in (xp, wsp, yp):
             buf.free()
@@ -467,13 +495,19 @@ def main():
         return {"us_per_launch": round(us, 2), "TOP_per_s": round(tops, 1),
                 "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
 
-    prefill_res, prefill_f32 = {}, {}
-    for rows in [int(r) for r in args.prefill_rows.split(",") if r]:
+    prefill_res, prefill_f32, prefill_q8 = {}, {}, {}
+    prefill_rows = [int(r) for r in args.prefill_rows.split(",") if r]
+    q8_layers = make_q8_0_weights(stream, args.rotate, log) if prefill_rows else None
+    for rows in prefill_rows:
         for name in ("gate", "down"):
             prefill_res[f"{name}_M{rows}"] = prefill(name, rows)
             log(f"  prefill {name} M={rows}: {prefill_res[f'{name}_M{rows}']}")
+            prefill_q8[f"{name}_M{rows}"] = prefill(name, rows, q8_layers=q8_layers)
+            log(f"  prefill Q8_0 {name} M={rows}: {prefill_q8[f'{name}_M{rows}']}")
             prefill_f32[f"{name}_M{rows}"] = prefill(name, rows, f32=True)
             log(f"  prefill f32 {name} M={rows}: {prefill_f32[f'{name}_M{rows}']}")
+    if q8_layers:
+        q8_layers.clear()
 
     # The host-memory entry point a cgo caller uses (x copied in, y copied
     # back, the call returns when y is in host memory): PCIe- and
@@ -551,6 +585,12 @@ def main():
             "workload": "cfg2: gate 14336x4096 Q4_K and down 4096x14336 Q6_K, dequant_matmul_a8.v2 block=256, "
                         "int8 MFMA GEMM (bit-identical to the GEMV), activations quantized beforehand",
             "results": prefill_res,
+        },
+        "prefill_q8_0": {
+            "workload": "cfg2's Q8_0 variant: gate 14336x4096 and down 4096x14336 Q8_0 (62 MB each), "
+                        "dequant_matmul_a8.v1 (activation blocks of 32) on the int8 MFMA GEMM, one float chain of "
+                        "exact block sums (within the spec's a8 tolerance), activations quantized beforehand",
+            "results": prefill_q8,
         },
         "prefill_f32": {
             "workload": "the same gate/down products with float32 activations (dequant_matmul.v1) on the fp32 "

@@ -128,7 +128,12 @@ int mimg_weight_info(uint64_t handle, const void **dev_ptr, int64_t *n_refused);
  * for `block` runs the float32 path, as the reference does (fast.go:256-259).
  * Rows of x with a NaN or |x| > 2^60, and rows of W with a non-finite block
  * scale, use the float32 path (fast.go:323-377). bias may be NULL. Returns
- * MIMG_ERR_ARG for block not in {32, 256} (the reference's error). */
+ * MIMG_ERR_ARG for block not in {32, 256} (the reference's error).
+ * Order: blocks of 256 are bit for bit the reference (dotQ8KRef); blocks of
+ * 32 follow the AVX2 lane order of dotQ8_0Q8AVX2 / dotQ4KQ8AVX2 /
+ * dotQ6KQ8AVX2 up to 15 rows, and from 16 rows Q8_0 (K a multiple of 256)
+ * runs on the matrix cores with exact block sums and one float chain,
+ * within the spec's tolerance (spec/stdlib.md:260-275). */
 int mimg_dequant_matmul_a8(uint64_t w, const float *x, int64_t rows, const float *bias, int block,
                            float *y);
 

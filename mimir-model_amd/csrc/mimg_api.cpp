@@ -369,6 +369,19 @@ int matmul_quantized(const Weight* const* w, int count, const float* x, int64_t 
             return MIMG_OK;
         }
     }
+    if (block == 32 && rows >= gemm_min_rows()) {
+        // Q8_0 with blocks of 32 on the int8 MFMA GEMM (one chain of exact
+        // block sums, within the spec's tolerance; see gemm_q8_0.hip)
+        bool all = true;
+        for (int i = 0; i < count; i++) all = all && gemm_q8_0_ok(w[i]->dw);
+        if (all) {
+            for (int i = 0; i < count; i++) {
+                hipError_t e = launch_gemm_q8_0(w[i]->dw, a, rows, rows, x, bias ? bias[i] : nullptr, y[i], s);
+                if (e != hipSuccess) return fail(MIMG_ERR_HIP, "Q8_0 GEMM launch: %s", hipGetErrorString(e));
+            }
+            return MIMG_OK;
+        }
+    }
     for (int64_t r0 = 0; r0 < rows; r0 += 8) {
         const int64_t mr = rows - r0 < 8 ? rows - r0 : 8;
         ActPtrs c;

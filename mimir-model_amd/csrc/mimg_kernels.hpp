@@ -102,6 +102,13 @@ hipError_t launch_gemv_a8k_fused_norm(const DevWeight* const* ws, int nmat, cons
                                       const float* scale, float eps, float* x_out, const float* const* bias,
                                       float* const* y, hipStream_t stream);
 
+// Many activation rows (quantized in blocks of 32) against one Q8_0 matrix
+// with K a multiple of 256, on the int8 matrix cores (gemm_q8_0.hip): exact
+// block sums, one float chain in block order (within the spec's tolerance).
+bool gemm_q8_0_ok(const DevWeight& w);
+hipError_t launch_gemm_q8_0(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows, const float* x,
+                            const float* bias, float* y, hipStream_t stream);
+
 hipError_t launch_gemv_q8_0_a8(const DevWeight& w, const ActPtrs& a, int64_t rows,
                                int64_t total_rows, const float* x, const float* bias, float* y,
                                int64_t y_stride, hipStream_t stream);
