@@ -12,16 +12,24 @@
 // tot = fma(f32(S_b), d_b*dx_b, tot) (and off for Q4_K's mins) in block
 // order: bit for bit the one-row kernel.
 //
-// Work split: a 256-thread workgroup owns 16 weight rows of one matrix. Its
-// four waves take blocks w, w+4, w+8, ... (measured against two, eight and
-// sixteen waves: four is fastest); per block a wave loads its A
-// operand straight from the weights in their file layout (lane l: row l%16,
-// the 16 k of group l/16 in each 64-k step), the B operand from the
-// quantized activations (lane l: activation row l%16, rows past M clamped,
-// their columns never read), runs 12 (Q4_K) or 8 (Q6_K) MFMAs and writes
-// the block's exact (S, M) per (row, activation row) to an LDS table (Q6_K:
-// with the next block's loads in flight). Then one lane per (row,
-// activation row) runs the float chain over the table in block order.
+// Work split: a 256-thread workgroup owns 16 weight rows of one matrix; its
+// four waves take blocks w, w+4, w+8, ... A wave's MFMA operand is 16 rows
+// x 16 bytes per lane, and loads in that layout touch 16 rows 2-3 KB apart
+// in every instruction (measured on MI355X: 31 us for the 66 MB of gate+up
+// at 8 rows, against 17-18 us for the same bytes loaded 64 consecutive
+// chunks per instruction, whether the runs are 144 bytes or whole rows).
+// So a wave loads its block's 16 x 144 (Q4_K) or 16 x 224 (Q6_K, from the
+// 16-byte boundary below each row's block) bytes as consecutive 16-byte
+// chunks, two blocks ahead, writes them to its own LDS region (rows an odd
+// number of chunks apart, so the 16 rows start in different banks) and
+// reads its operand back in MFMA layout: no barrier, the wave's LDS
+// accesses run in order. (A workgroup-wide staging of four blocks with a
+// barrier per stage measured slower: 32 us without any arithmetic.) The
+// activations (lane l: activation row l%16, rows past M clamped, their
+// columns never read) come straight from global memory (L2-resident).
+// Per block a wave runs 12 (Q4_K) or 8 (Q6_K) MFMAs and writes the block's
+// exact (S, M) per (row, activation row) to an LDS table; then one lane per
+// (row, activation row) runs the float chain over the table in block order.
 // Rows of x the quantizer refused and weight rows with a non-finite block
 // scale take the float32 path (reference interp/fast.go:323-377).
 #include "f32path.hpp"
@@ -33,11 +41,10 @@ namespace mimg {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int MF_ROWS = 16;  // weight rows per workgroup (the MFMA's A rows)
-#ifndef MIMG_MF_WAVES
-#define MIMG_MF_WAVES 4
-#endif
-constexpr int MF_WAVES = MIMG_MF_WAVES;  // waves per workgroup; they split the blocks
-constexpr int MF_T = 64 * MF_WAVES;
+// Blocks a wave loads ahead: Q4_K one (fewer registers, more waves;
+// measured 22.7 against 25.7 us for gate+up at 8 rows), Q6_K two.
+template <uint32_t DT>
+constexpr int mf_sets() { return DT == DT_Q4_K ? 1 : 2; }
 
 struct MfmaMat {
     const uint8_t* W;
@@ -80,38 +87,92 @@ struct MfRaw<DT_Q6_K> {
     float dx;
 };
 
+// A wave's staging of one block: CPR 16-byte chunks per row (Q6_K blocks
+// start 2-byte aligned: 14 chunks from the boundary below cover 210 bytes),
+// stored RST chunks apart in the wave's LDS region.
 template <uint32_t DT>
-__device__ __forceinline__ void mf_load(const uint8_t* Wt, uint32_t roff, int b, const int8_t* ya,
-                                        const float* dxr, int G, MfRaw<DT>& r) {
-    if constexpr (DT == DT_Q4_K) {
-        const uint32_t off = roff + (uint32_t)b * Q4K_BYTES;  // 16-byte aligned
-        r.hdr = *(const u32x4*)(Wt + off);
+struct MfWave {
+    static constexpr int BYTES = DT == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    static constexpr int CPR = DT == DT_Q4_K ? 9 : 14;
+    static constexpr int RST = CPR | 1;
+    static constexpr int CH = MF_ROWS * CPR;       // chunks per block
+    static constexpr int NLD = (CH + 63) / 64;     // loads per lane and block
+    static constexpr int LBYTES = MF_ROWS * RST * 16;
+};
+
+// A lane's part of every block's loads: chunk q = 64i + lane (clamped to
+// the last) of row r = q / CPR (rows past N read the last), stored at LDS
+// byte 16 (RST r + j), j = q % CPR. Computed once per workgroup.
+template <uint32_t DT>
+struct MfLanes {
+    const uint8_t* row[MfWave<DT>::NLD];  // the row's first byte (+16j for Q4_K)
+    uint32_t j16[MfWave<DT>::NLD];        // 16j (Q6_K)
+    uint32_t lds[MfWave<DT>::NLD];
+    __device__ MfLanes(const uint8_t* W, int64_t rb, int row0, int N) {
+        using S = MfWave<DT>;
+        const int l = threadIdx.x & 63;
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) r.qs[ks] = *(const u32x4*)(Wt + (off + 16 + 32 * ks + 16 * (G & 1)));
+        for (int i = 0; i < S::NLD; i++) {
+            const int q = min(64 * i + l, S::CH - 1);
+            const int r = q / S::CPR, j = q - S::CPR * r;
+            row[i] = W + (int64_t)min(row0 + r, N - 1) * rb + (DT == DT_Q4_K ? 16 * j : 0);
+            j16[i] = 16 * j;
+            lds[i] = 16 * (S::RST * r + j);
+        }
+    }
+};
+
+// Issues the loads of block b: Q4_K blocks are 16-byte aligned (rows and
+// weight views are); Q6_K chunks count from the 16-byte boundary at or
+// below the row's block and end at most 14 bytes past it (inside the next
+// block, or WEIGHT_PAD past the matrix).
+template <uint32_t DT>
+__device__ __forceinline__ void mf_load_w(const MfLanes<DT>& L, int b, u32x4* v) {
+    using S = MfWave<DT>;
+#pragma unroll
+    for (int i = 0; i < S::NLD; i++) {
+        const uint8_t* p = L.row[i] + (int64_t)b * S::BYTES;
+        if constexpr (DT == DT_Q6_K) p = (const uint8_t*)__builtin_align_down(p, 16) + L.j16[i];
+        v[i] = *(const u32x4*)p;
+    }
+}
+
+// Writes a block's chunks to the wave's LDS region (lanes past the last
+// chunk write it again, the same bytes).
+template <uint32_t DT>
+__device__ __forceinline__ void mf_stage_w(const MfLanes<DT>& L, uint8_t* wl, const u32x4* v) {
+#pragma unroll
+    for (int i = 0; i < MfWave<DT>::NLD; i++) *(u32x4*)(wl + L.lds[i]) = v[i];
+}
+
+// A lane's weight operand for one block from the wave's LDS region; p is
+// the block's first byte (Q4_K: 16-byte aligned; Q6_K: 2-byte aligned, read as
+// aligned dwords and realigned in mf_block).
+template <uint32_t DT>
+__device__ __forceinline__ void mf_lds_w(const uint8_t* p, int G, MfRaw<DT>& r) {
+    if constexpr (DT == DT_Q4_K) {
+        r.hdr = *(const u32x4*)p;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) r.qs[ks] = *(const u32x4*)(p + 16 + 32 * ks + 16 * (G & 1));
     } else {
-        const uint32_t off = roff + (uint32_t)b * Q6K_BYTES;  // 2-byte aligned
-        r.shift = off & 3;
+        r.shift = (uint32_t)(uintptr_t)p & 3;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const uint32_t oa = (off + 64 * h + 16 * G) & ~3u;
-            const uint32_t oc = (off + 128 + 32 * h + 16 * (G & 1)) & ~3u;
-            const u32x4a4 av = *(const u32x4a4*)(Wt + oa), cv = *(const u32x4a4*)(Wt + oc);
-            r.ql[h][0] = av.x, r.ql[h][1] = av.y, r.ql[h][2] = av.z, r.ql[h][3] = av.w;
-            r.ql[h][4] = *(const uint32_t*)(Wt + oa + 16);
-            r.qh[h][0] = cv.x, r.qh[h][1] = cv.y, r.qh[h][2] = cv.z, r.qh[h][3] = cv.w;
-            r.qh[h][4] = *(const uint32_t*)(Wt + oc + 16);
+            const uint32_t* qa = (const uint32_t*)__builtin_align_down(p + 64 * h + 16 * G, 4);
+            const uint32_t* qc = (const uint32_t*)__builtin_align_down(p + 128 + 32 * h + 16 * (G & 1), 4);
+#pragma unroll
+            for (int k = 0; k < 5; k++) {
+                r.ql[h][k] = qa[k];
+                r.qh[h][k] = qc[k];
+            }
         }
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            const int h = ks >> 1, p = 2 * (ks & 1) + (G >> 1);
-            r.sc[ks] = (int)*(const int8_t*)(Wt + (off + 192 + 8 * h + (G & 1) + 2 * p));
+            const int h = ks >> 1, q = 2 * (ks & 1) + (G >> 1);
+            r.sc[ks] = (int)*(const int8_t*)(p + 192 + 8 * h + (G & 1) + 2 * q);
         }
-        r.dbits = *(const uint16_t*)(Wt + (off + 208));
+        r.dbits = *(const uint16_t*)(p + 208);
     }
-    const int8_t* yb = ya + (uint32_t)b * 256;
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++) r.act[ks] = *(const v4i*)(yb + 64 * ks + 16 * G);
-    r.dx = dxr[8 * b];
 }
 
 // The block's exact sums: lane l holds, for weight rows 4(l/16) + i (i <
@@ -182,17 +243,21 @@ __device__ __forceinline__ void mf_block(const MfRaw<DT>& r, int G, v4i& s, v4i&
     }
 }
 
-// LDS: the (S, M) table [nb][16][M] (int2; Q6_K int), the block scales'
+// LDS: the waves' staging regions, the (S, M) table [nb][16][M] (int2; Q6_K int), the block scales'
 // f16 bits per (block, row), dx per (block, activation row) and the
 // refusal flag per (row, activation row).
 template <uint32_t DT>
-__host__ __device__ constexpr size_t mf_lds_bytes(int nb, int M) {
-    return (size_t)nb * MF_ROWS * M * (DT == DT_Q4_K ? 8 : 4) + (size_t)nb * MF_ROWS * 4 + (size_t)nb * M * 4 +
+__host__ __device__ constexpr size_t mf_lds_bytes(int nb, int M, int nw) {
+    return nw * (size_t)MfWave<DT>::LBYTES + (size_t)nb * MF_ROWS * M * (DT == DT_Q4_K ? 8 : 4) + (size_t)nb * MF_ROWS * 4 + (size_t)nb * M * 4 +
            (size_t)MF_ROWS * M * 4;
 }
 
-template <uint32_t DT>
-__global__ __launch_bounds__(MF_T) void gemv_a8k_mfma_kernel(MfmaArgs A) {
+// Q4_K fits 5 waves per SIMD (at most 102 registers) with one block ahead.
+template <uint32_t DT, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K ? 5 : 1)))
+void gemv_a8k_mfma_kernel(MfmaArgs A) {
+    using S = MfWave<DT>;
+    constexpr int MF_T = 64 * NW, MF_SETS = mf_sets<DT>();
     extern __shared__ __align__(16) uint8_t smem[];
     int mi = 0;
     if (A.nmat > 1 && (int)blockIdx.x >= A.mat[1].tile0) mi = 1;
@@ -203,30 +268,27 @@ __global__ __launch_bounds__(MF_T) void gemv_a8k_mfma_kernel(MfmaArgs A) {
     const int nb = A.nb, M = A.M, N = P.N;
     const int row0 = ((int)blockIdx.x - P.tile0) * MF_ROWS;
     constexpr int TW = DT == DT_Q4_K ? 2 : 1;  // table words per entry
-    int* tab = (int*)smem;                                        // [nb][16][M][TW]
+    uint8_t* wl = smem + w * S::LBYTES;                               // this wave's staging
+    int* tab = (int*)(smem + NW * S::LBYTES);                         // [nb][16][M][TW]
     uint32_t* dd = (uint32_t*)(tab + (size_t)nb * MF_ROWS * M * TW);  // [nb][16]
     float* dxs = (float*)(dd + (size_t)nb * MF_ROWS);                 // [nb][M]
     int* refl = (int*)(dxs + (size_t)nb * M);                         // [16][M]
 
-    // The tile's rows from a 4-byte-aligned base (Q6_K rows may be 2-byte
-    // aligned) with 32-bit offsets; rows past N read the last row.
-    const int64_t tbyte = (int64_t)row0 * A.rb;
-    const uint8_t* Wt = P.W + (tbyte & ~(int64_t)3);
-    const uint32_t roff = (uint32_t)(tbyte & 3) + (uint32_t)min(ar, N - 1 - row0) * (uint32_t)A.rb;
+    // This lane's weight row (A operand; rows past N read the last row) and
+    // activation row (B operand).
+    const uint8_t* rowp = P.W + (int64_t)min(row0 + ar, N - 1) * A.rb;
     const int am = min(ar, M - 1);
     const int8_t* ya = A.q + (int64_t)am * A.K;
     const float* dxr = A.d32 + (int64_t)am * (A.K / 32);
 
     // Lane t < 16*M owns (row t/M, activation row t%M) at the end. Its
-    // flags and bias are loaded first and looked at last (loaded after the
-    // weights, they would wait for all of them).
+    // flags and bias are loaded first and looked at last.
     const int ft = min(t, MF_ROWS * M - 1), fr = ft / M;
     int fm = ft - fr * M;
     asm volatile("v_mov_b32 %0, %1" : "=v"(fm) : "v"(fm));  // a vector index: ok[] through the vector cache
     const int frow = min(row0 + fr, N - 1);
     const int wr = P.wref[frow], okm = A.ok[fm];
     const float bias = P.bias ? P.bias[frow] : 0.f;
-    __builtin_amdgcn_sched_barrier(0);
 
     // Block b's table entries, scale bits and dx.
     auto step = [&](const MfRaw<DT>& r, int b) {
@@ -246,35 +308,52 @@ __global__ __launch_bounds__(MF_T) void gemv_a8k_mfma_kernel(MfmaArgs A) {
         }
         if (G == 1 && ar < M) dxs[b * M + ar] = r.dx;
     };
-    // Everything block b needs is loaded with it (the load counter retires
-    // in order: a load issued after the next block's would make this block
-    // wait for all of them), and sched_barrier keeps the scheduler from
-    // sinking the next block's loads below this block's arithmetic.
-    if constexpr (DT == DT_Q4_K) {
-        // One block in flight per wave: 88 registers against 128, so more
-        // waves (measured: 19.1 against 21.7 us for gate at 8 rows).
-        for (int b = w; b < nb; b += MF_WAVES) {
-            MfRaw<DT> r1;
-            mf_load<DT>(Wt, roff, b, ya, dxr, G, r1);
-            __builtin_amdgcn_sched_barrier(0);
-            step(r1, b);
+    // The activation operand and scale of block b.
+    auto load_a = [&](int b, v4i* act, float& dx) {
+        const int8_t* yb = ya + (int64_t)b * 256;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) act[ks] = *(const v4i*)(yb + 64 * ks + 16 * G);
+        dx = dxr[8 * b];
+    };
+    // Block b from load set (v, act, dx): stage it, load block
+    // b + MF_SETS*NW into the freed weight registers, read the operand
+    // back, compute, then load that block's activations. MF_SETS blocks'
+    // weights are in flight while one computes. Every load is issued unconditionally (past the last
+    // block: the last block again), so the compiler's waits before the
+    // staging count exactly the loads issued after the set's.
+    const MfLanes<DT> L(P.W, A.rb, row0, N);
+    auto body = [&](int b, u32x4* v, v4i* act, float& dx) {
+        mf_stage_w<DT>(L, wl, v);
+        const int bn = min(b + MF_SETS * NW, nb - 1);
+        mf_load_w<DT>(L, bn, v);
+        if (b < nb) {
+            MfRaw<DT> r;
+            mf_lds_w<DT>(wl + ar * (S::RST * 16) + ((uint32_t)(uintptr_t)(rowp + (int64_t)b * S::BYTES) & 15), G, r);
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) r.act[ks] = act[ks];
+            r.dx = dx;
+            step(r, b);
+        }
+        load_a(bn, act, dx);
+    };
+    u32x4 v0[S::NLD], v1[S::NLD];
+    v4i a0[4], a1[4];
+    float d0, d1;
+    const int b0 = min(w, nb - 1);
+    mf_load_w<DT>(L, b0, v0);
+    load_a(b0, a0, d0);
+    __builtin_amdgcn_sched_barrier(0);  // the sets in order: the loop's waits are counted from them
+    if constexpr (MF_SETS == 2) {  // two sets in turn
+        const int b1 = min(w + NW, nb - 1);
+        mf_load_w<DT>(L, b1, v1);
+        load_a(b1, a1, d1);
+        __builtin_amdgcn_sched_barrier(0);
+        for (int b = w; b < nb; b += 2 * NW) {
+            body(b, v0, a0, d0);
+            body(b + NW, v1, a1, d1);
         }
     } else {
-        // Q6_K (seven loads per 16 bytes of weights): two sets of registers
-        // in turn, block b computing while block b + MF_WAVES loads (a copy
-        // from one set to the other would wait for its loads); measured
-        // 24.3 against 26.2 us for down at 8 rows.
-        MfRaw<DT> ra, rb;
-        mf_load<DT>(Wt, roff, min(w, nb - 1), ya, dxr, G, ra);
-        for (int b = w; b < nb; b += 2 * MF_WAVES) {
-            mf_load<DT>(Wt, roff, min(b + MF_WAVES, nb - 1), ya, dxr, G, rb);
-            __builtin_amdgcn_sched_barrier(0);
-            step(ra, b);
-            if (b + MF_WAVES >= nb) break;  // uniform within the wave
-            mf_load<DT>(Wt, roff, min(b + 2 * MF_WAVES, nb - 1), ya, dxr, G, ra);
-            __builtin_amdgcn_sched_barrier(0);
-            step(rb, b + MF_WAVES);
-        }
+        for (int b = w; b < nb; b += NW) body(b, v0, a0, d0);
     }
     const int flag = (wr != 0) | (okm == 0);
     if (t < MF_ROWS * M) refl[t] = flag;
@@ -309,15 +388,30 @@ __global__ __launch_bounds__(MF_T) void gemv_a8k_mfma_kernel(MfmaArgs A) {
     }
 }
 
+// Waves per workgroup: 4, or for Q6_K 8 while the grid holds fewer than
+// 4096 waves (16 per CU; down at 8 rows: 19.4 against 20.9 us). Measured at
+// the llama-8B shapes, Q4_K is fastest at 4 whatever the grid (gate+up
+// 22.5 us at 4, 28.6 at 8, 39 at 16), and Q6_K at 16 would not fit its two
+// sets in flight in the 128 registers of a 1024-thread workgroup.
+static int mf_waves(uint32_t dt, int64_t tiles, int nb) {
+    return dt == DT_Q6_K && tiles * 4 < 4096 && nb >= 8 ? 8 : 4;
+}
+
+static size_t mf_lds(uint32_t dt, int nb, int M, int nw) {
+    return dt == DT_Q4_K ? mf_lds_bytes<DT_Q4_K>(nb, M, nw) : mf_lds_bytes<DT_Q6_K>(nb, M, nw);
+}
+
 bool gemv_mfma_ok(const DevWeight* const* ws, int nmat, int64_t rows) {
     if (rows < 2 || rows > 8 || nmat < 1 || nmat > 3) return false;
     const DevWeight& w = *ws[0];
     if ((w.dt != DT_Q4_K && w.dt != DT_Q6_K) || w.k % 256 || w.k <= 0) return false;
-    for (int i = 0; i < nmat; i++)
+    int64_t tiles = 0;
+    for (int i = 0; i < nmat; i++) {
         if (ws[i]->dt != w.dt || ws[i]->k != w.k || ws[i]->n <= 0) return false;
+        tiles += (ws[i]->n + MF_ROWS - 1) / MF_ROWS;
+    }
     const int nb = (int)(w.k / 256);
-    const size_t lds = w.dt == DT_Q4_K ? mf_lds_bytes<DT_Q4_K>(nb, (int)rows) : mf_lds_bytes<DT_Q6_K>(nb, (int)rows);
-    return lds <= 64 * 1024;
+    return mf_lds(w.dt, nb, (int)rows, mf_waves(w.dt, tiles, nb)) <= 96 * 1024;
 }
 
 hipError_t launch_gemv_a8k_mfma(const DevWeight* const* ws, int nmat, const ActPtrs& a, int64_t rows,
@@ -347,12 +441,15 @@ hipError_t launch_gemv_a8k_mfma(const DevWeight* const* ws, int nmat, const ActP
         A.mat[i].tile0 = tiles;
         if (i < nmat) tiles += (int)((wi.n + MF_ROWS - 1) / MF_ROWS);
     }
-    if (w.dt == DT_Q4_K)
-        hipLaunchKernelGGL(gemv_a8k_mfma_kernel<DT_Q4_K>, dim3((unsigned)tiles), dim3(MF_T),
-                           mf_lds_bytes<DT_Q4_K>(A.nb, A.M), stream, A);
-    else
-        hipLaunchKernelGGL(gemv_a8k_mfma_kernel<DT_Q6_K>, dim3((unsigned)tiles), dim3(MF_T),
-                           mf_lds_bytes<DT_Q6_K>(A.nb, A.M), stream, A);
+    const int nw = mf_waves(w.dt, tiles, A.nb);
+    const size_t lds = mf_lds(w.dt, A.nb, A.M, nw);
+    const dim3 grid((unsigned)tiles), block((unsigned)(64 * nw));
+    if (w.dt == DT_Q4_K) {
+        hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q4_K, 4>), grid, block, lds, stream, A);
+    } else {
+        if (nw == 4) hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 4>), grid, block, lds, stream, A);
+        else hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 8>), grid, block, lds, stream, A);
+    }
     return hipGetLastError();
 }
 

@@ -257,12 +257,13 @@ def test_gemm_a8k_wide_tiles_refusals_and_bias(gpu, oracle, dt):
 
 
 @pytest.mark.parametrize("dt", [Q4_K, Q6_K])
-@pytest.mark.parametrize("rows", [1, 3, 12, 40])
-def test_linear_a8k_refusals_and_bias(gpu, oracle, dt, rows):
+@pytest.mark.parametrize("rows,k", [(1, 1024), (3, 1024), (12, 1024), (40, 1024), (6, 1024), (8, 4096), (7, 14336)])
+def test_linear_a8k_refusals_and_bias(gpu, oracle, dt, rows, k):
     """Rows of x with NaN/Inf/huge values and rows of w with a non-finite
     block scale take the float32 path (reference interp/fast.go:323-377);
-    bias is added as s + bias[j]."""
-    n, k = 40, 1024
+    bias is added as s + bias[j]. 6..8 rows run on the matrix-core GEMV,
+    with 4 waves per workgroup (K = 1024) and 16 (three workgroups)."""
+    n = 40
     wb = bytearray(_weights(oracle, dt, n, k, seed=8).tobytes())
     rb = len(wb) // n
     f = 208 if dt == Q6_K else 2  # Q4_K: dmin
@@ -355,14 +356,67 @@ def test_pairs_kernel_one_row_bitexact(gpu, oracle, dt, n, k):
     assert bits_equal(got, want), first_diff(got, want)
 
 
+@pytest.mark.parametrize("n,k", [(4096, 14336), (4099, 4096), (1, 2048), (1025, 6144), (3, 16384)])
+def test_q6k_one_row_gemv_bitexact(gpu, oracle, n, k):
+    """Q6_K at one activation row (the pair kernel on pre-quantized
+    activations): ragged last tiles of rows, odd row counts, K from 8 to 64
+    blocks; bit for bit the reference."""
+    wb = _weights(oracle, Q6_K, n, k, seed=n + 5)
+    W = gpu.Weight(wb, Q6_K, n, k)
+    x = oracle.synthetic_acts(1, k, seed=k + 5)
+    got = _dev_linear(gpu, [W], x, prequant=True)[0]
+    want = oracle.linear_a8(x, wb, Q6_K, n, k, block=256, threads=16)
+    W.release()
+    assert bits_equal(got, want), first_diff(got, want)
+
+
+def test_q6k_one_row_gemv_refusals_bias_and_group(gpu, oracle):
+    """The one-row Q6_K GEMV with a weight row whose block scale is infinite
+    (float32 path), bias, two matrices in one launch, then a refused
+    activation row (every row on the float32 path)."""
+    k = 4096
+    wbs = []
+    for n, seed in ((700, 41), (300, 42)):
+        wb = bytearray(_weights(oracle, Q6_K, n, k, seed=seed).tobytes())
+        rb = len(wb) // n
+        o = rb * 17 + 5 * 210 + 208
+        wb[o:o + 2] = b"\x00\x7c"
+        wbs.append(np.frombuffer(bytes(wb), np.uint8))
+    W = [gpu.Weight(wb, Q6_K, wb.size // (k // 256 * 210), k) for wb in wbs]
+    biases = [np.random.default_rng(i).standard_normal(w.n).astype(np.float32) for i, w in enumerate(W)]
+    x = oracle.synthetic_acts(1, k, seed=43)
+    import hiprt
+
+    for case in range(2):
+        if case == 1:
+            x[0, 2000] = np.nan
+        xd = hiprt.DeviceBuffer.from_array(x)
+        wsb = gpu.a8_workspace_bytes(1, k)
+        ws = hiprt.DeviceBuffer(wsb)
+        ys = [hiprt.DeviceBuffer(w.n * 4) for w in W]
+        bds = [hiprt.DeviceBuffer.from_array(b) for b in biases]
+        st = hiprt.Stream()
+        gpu.quantize_act_dev(xd.ptr, 1, k, 256, ws.ptr, wsb, st.handle)
+        gpu.matmul_a8_quantized_group_dev(W, xd.ptr, 1, [b.ptr for b in bds], 256, [y.ptr for y in ys], ws.ptr, wsb,
+                                          st.handle)
+        st.sync()
+        got = [y.download(np.float32).reshape(1, w.n) for y, w in zip(ys, W)]
+        for i, (w, wb) in enumerate(zip(W, wbs)):
+            want = oracle.linear_a8(x, wb, Q6_K, w.n, k, bias=biases[i], block=256)
+            assert bits_equal(got[i], want), (case, i, first_diff(got[i], want))
+    for w in W:
+        w.release()
+
+
 @pytest.mark.parametrize("dt", [Q4_K, Q6_K])
-@pytest.mark.parametrize("n,k", [(300, 14336), (4100, 4096), (7, 256), (33, 768)])
+@pytest.mark.parametrize("n,k", [(300, 14336), (4100, 4096), (8200, 2048), (7, 256), (33, 768)])
 @pytest.mark.parametrize("rows", [4, 5, 8])
 def test_mfma_gemv_bitexact(gpu, oracle, dt, n, k, rows):
     """4..8 activation rows run on the int8 matrix-core GEMV: ragged last
-    tile of 16 rows, K from one block to 56 (four waves splitting them
-    unevenly), odd block counts (Q6_K rows 2-byte aligned); the same bits
-    as the reference's per-row products."""
+    tile of 16 rows, K from one block to 56, workgroups of 4 waves (K of 1
+    and 3 blocks: idle and uneven waves), 8 waves (513 tiles) and 16 (19
+    and 257 tiles, 56 blocks split unevenly), odd block counts (Q6_K rows
+    2-byte aligned); the same bits as the reference's per-row products."""
     wb = _weights(oracle, dt, n, k, seed=n + rows)
     W = gpu.Weight(wb, dt, n, k)
     x = oracle.synthetic_acts(rows, k, seed=rows + 7)
