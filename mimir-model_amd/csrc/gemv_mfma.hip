@@ -41,10 +41,6 @@ namespace mimg {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int MF_ROWS = 16;  // weight rows per workgroup (the MFMA's A rows)
-// Blocks a wave loads ahead: Q4_K one (fewer registers, more waves;
-// measured 22.7 against 25.7 us for gate+up at 8 rows), Q6_K two.
-template <uint32_t DT>
-constexpr int mf_sets() { return DT == DT_Q4_K ? 1 : 2; }
 
 struct MfmaMat {
     const uint8_t* W;
@@ -81,15 +77,16 @@ struct MfRaw<DT_Q4_K> {
 template <>
 struct MfRaw<DT_Q6_K> {
     uint32_t ql[2][5], qh[2][5];  // per half: 16 bytes as the 5 aligned dwords holding them
-    int sc[4];                    // per 64-k step: the sub-block scale
     uint32_t dbits, shift;
-    v4i act[4];
-    float dx;
 };
 
 // A wave's staging of one block: CPR 16-byte chunks per row (Q6_K blocks
 // start 2-byte aligned: 14 chunks from the boundary below cover 210 bytes),
 // stored RST chunks apart in the wave's LDS region.
+// Q6_K also stages the block's activations: 8 rows AROW bytes apart (so
+// the 16 lanes reading 4 rows x 4 k-slices of one B operand hit distinct
+// banks), then 256 zero bytes for the lanes whose B operand is zero.
+constexpr int Q6_AROW = 320;
 template <uint32_t DT>
 struct MfWave {
     static constexpr int BYTES = DT == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES;
@@ -97,7 +94,8 @@ struct MfWave {
     static constexpr int RST = CPR | 1;
     static constexpr int CH = MF_ROWS * CPR;       // chunks per block
     static constexpr int NLD = (CH + 63) / 64;     // loads per lane and block
-    static constexpr int LBYTES = MF_ROWS * RST * 16;
+    static constexpr int WBYTES = MF_ROWS * RST * 16;
+    static constexpr int LBYTES = WBYTES + (DT == DT_Q6_K ? 8 * Q6_AROW + 256 : 0);
 };
 
 // A lane's part of every block's loads: chunk q = 64i + lane (clamped to
@@ -166,17 +164,12 @@ __device__ __forceinline__ void mf_lds_w(const uint8_t* p, int G, MfRaw<DT>& r) 
                 r.qh[h][k] = qc[k];
             }
         }
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            const int h = ks >> 1, q = 2 * (ks & 1) + (G >> 1);
-            r.sc[ks] = (int)*(const int8_t*)(p + 192 + 8 * h + (G & 1) + 2 * q);
-        }
         r.dbits = *(const uint16_t*)(p + 208);
     }
 }
 
-// The block's exact sums: lane l holds, for weight rows 4(l/16) + i (i <
-// 4) and activation row l%16, S in s[i] and (Q4_K) the mins term in mt[i].
+// Q4_K, the block's exact sums: lane l holds, for weight rows 4(l/16) + i
+// (i < 4) and activation row l%16, S in s[i] and the mins term in mt[i].
 template <uint32_t DT>
 __device__ __forceinline__ void mf_block(const MfRaw<DT>& r, int G, v4i& s, v4i& mt) {
     v4i accH = {0, 0, 0, 0}, accL = {0, 0, 0, 0}, accM = {0, 0, 0, 0};
@@ -208,38 +201,63 @@ __device__ __forceinline__ void mf_block(const MfRaw<DT>& r, int G, v4i& s, v4i&
 #pragma unroll
         for (int i = 0; i < 4; i++) s[i] = (accH[i] << 3) + accL[i];
         mt = accM;
-    } else {
-        uint32_t ql[2][4], qh[2][4];
+    }
+}
+
+// Sum over the four lanes of a quad (exact: integers).
+__device__ __forceinline__ int quad_sum(int x) {
+    x += __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, true);  // quad_perm 1,0,3,2
+    x += __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, true);  // quad_perm 2,3,0,1
+    return x;
+}
+
+// Q6_K, the block's exact sums S = sum_sub sc_sub sum_{k in sub} (q_k - 32) y_k
+// for weight rows 4G + i and activation rows 4grp + (l&15)/4. The A operand
+// is q itself (0..63: no scale, no split into int8 planes); each B operand
+// holds 4 activation rows x 4 sub-blocks of 16: lane column 4m + g carries
+// row m's 16 values of k-slice G only when G == g (zeros otherwise, from
+// bq pointing at zero bytes), so C[row][4m + g] is the sum over sub-block
+// 4ks + g alone. A second MFMA with A = -32 adds -32 sum y. Each lane then
+// multiplies by its sub-block's scale (24-bit products: |C| <= 16*32*127)
+// and a quad sum adds the four sub-blocks; s0/s1 hold groups 0/1.
+__device__ __forceinline__ void mf_block6(const MfRaw<DT_Q6_K>& r, int G, const int (&sc)[4][4],
+                                          const uint8_t* bq0, const uint8_t* bq1, int (&s0)[4], int (&s1)[4]) {
+    uint32_t ql[2][4], qh[2][4];
 #pragma unroll
-        for (int h = 0; h < 2; h++)
+    for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                ql[h][k] = __builtin_amdgcn_alignbyte(r.ql[h][k + 1], r.ql[h][k], r.shift);
-                qh[h][k] = __builtin_amdgcn_alignbyte(r.qh[h][k + 1], r.qh[h][k], r.shift);
-            }
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            // w = sc*(q - 32) in [-4096, 4064] as 128*hi + lo, lo in [0, 127]
-            const int h = ks >> 1, p = 2 * (ks & 1) + (G >> 1);
-            const s16x2 sc2 = {(short)r.sc[ks], (short)r.sc[ks]};
-            v4i aH, aL;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t q6 = (((ks & 1) ? (ql[h][k] >> 4) : ql[h][k]) & 0x0F0F0F0Fu) |
-                                    (((qh[h][k] >> (2 * p)) & 0x03030303u) << 4);
-                const s16x2 we = (as_s16x2(q6 & 0x00FF00FFu) - (s16x2){32, 32}) * sc2;
-                const s16x2 wo = (as_s16x2((q6 >> 8) & 0x00FF00FFu) - (s16x2){32, 32}) * sc2;
-                uint32_t lo, hi;
-                split4(as_u32(we), as_u32(wo), as_u32(we >> (s16x2){7, 7}), as_u32(wo >> (s16x2){7, 7}), lo, hi);
-                aL[k] = (int)lo;
-                aH[k] = (int)hi;
-            }
-            accH = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, r.act[ks], accH, 0, 0, 0);
-            accL = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, r.act[ks], accL, 0, 0, 0);
+        for (int k = 0; k < 4; k++) {
+            ql[h][k] = __builtin_amdgcn_alignbyte(r.ql[h][k + 1], r.ql[h][k], r.shift);
+            qh[h][k] = __builtin_amdgcn_alignbyte(r.qh[h][k + 1], r.qh[h][k], r.shift);
         }
+    const v4i zero = {0, 0, 0, 0}, m32 = {(int)0xE0E0E0E0, (int)0xE0E0E0E0, (int)0xE0E0E0E0, (int)0xE0E0E0E0};
 #pragma unroll
-        for (int i = 0; i < 4; i++) s[i] = (accH[i] << 7) + accL[i];
-        mt = accM;
+    for (int i = 0; i < 4; i++) s0[i] = s1[i] = 0;
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        // k = 64ks + 16G + j: ql byte 64h + 16G + j (nibble ks & 1), qh byte
+        // 32h + 16(G & 1) + j (bits 2p, 2p+1), h = ks/2, p = 2(ks & 1) + G/2
+        const int h = ks >> 1, p = 2 * (ks & 1) + (G >> 1);
+        v4i aq;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            aq[k] = (int)((((ks & 1) ? (ql[h][k] >> 4) : ql[h][k]) & 0x0F0F0F0Fu) |
+                          (((qh[h][k] >> (2 * p)) & 0x03030303u) << 4));
+        const v4i b0 = *(const v4i*)(bq0 + 64 * ks), b1 = *(const v4i*)(bq1 + 64 * ks);
+        v4i c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(aq, b0, zero, 0, 0, 0);
+        v4i c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(aq, b1, zero, 0, 0, 0);
+        c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(m32, b0, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(m32, b1, c1, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            s0[i] += __mul24(sc[i][ks], c0[i]);
+            s1[i] += __mul24(sc[i][ks], c1[i]);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        s0[i] = quad_sum(s0[i]);
+        s1[i] = quad_sum(s1[i]);
     }
 }
 
@@ -257,7 +275,7 @@ template <uint32_t DT, int NW>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K ? 5 : 1)))
 void gemv_a8k_mfma_kernel(MfmaArgs A) {
     using S = MfWave<DT>;
-    constexpr int MF_T = 64 * NW, MF_SETS = mf_sets<DT>();
+    constexpr int MF_T = 64 * NW;
     extern __shared__ __align__(16) uint8_t smem[];
     int mi = 0;
     if (A.nmat > 1 && (int)blockIdx.x >= A.mat[1].tile0) mi = 1;
@@ -290,70 +308,121 @@ void gemv_a8k_mfma_kernel(MfmaArgs A) {
     const int wr = P.wref[frow], okm = A.ok[fm];
     const float bias = P.bias ? P.bias[frow] : 0.f;
 
-    // Block b's table entries, scale bits and dx.
-    auto step = [&](const MfRaw<DT>& r, int b) {
-        v4i s, mt;
-        mf_block<DT>(r, G, s, mt);
-        if (ar < M) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                int* e = tab + (((size_t)b * MF_ROWS + 4 * G + i) * M + ar) * TW;
-                e[0] = s[i];
-                if constexpr (DT == DT_Q4_K) e[1] = mt[i];
-            }
-        }
-        if (G == 0) {
-            if constexpr (DT == DT_Q4_K) dd[b * MF_ROWS + ar] = r.hdr.x;
-            else dd[b * MF_ROWS + ar] = r.dbits;
-        }
-        if (G == 1 && ar < M) dxs[b * M + ar] = r.dx;
-    };
-    // The activation operand and scale of block b.
-    auto load_a = [&](int b, v4i* act, float& dx) {
-        const int8_t* yb = ya + (int64_t)b * 256;
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) act[ks] = *(const v4i*)(yb + 64 * ks + 16 * G);
-        dx = dxr[8 * b];
-    };
-    // Block b from load set (v, act, dx): stage it, load block
-    // b + MF_SETS*NW into the freed weight registers, read the operand
-    // back, compute, then load that block's activations. MF_SETS blocks'
-    // weights are in flight while one computes. Every load is issued unconditionally (past the last
-    // block: the last block again), so the compiler's waits before the
-    // staging count exactly the loads issued after the set's.
     const MfLanes<DT> L(P.W, A.rb, row0, N);
-    auto body = [&](int b, u32x4* v, v4i* act, float& dx) {
-        mf_stage_w<DT>(L, wl, v);
-        const int bn = min(b + MF_SETS * NW, nb - 1);
-        mf_load_w<DT>(L, bn, v);
-        if (b < nb) {
-            MfRaw<DT> r;
-            mf_lds_w<DT>(wl + ar * (S::RST * 16) + ((uint32_t)(uintptr_t)(rowp + (int64_t)b * S::BYTES) & 15), G, r);
+    if constexpr (DT == DT_Q4_K) {
+        // Block b's table entries, scale bits and dx.
+        auto step = [&](const MfRaw<DT>& r, int b) {
+            v4i s, mt;
+            mf_block<DT>(r, G, s, mt);
+            if (ar < M) {
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) r.act[ks] = act[ks];
-            r.dx = dx;
-            step(r, b);
-        }
-        load_a(bn, act, dx);
-    };
-    u32x4 v0[S::NLD], v1[S::NLD];
-    v4i a0[4], a1[4];
-    float d0, d1;
-    const int b0 = min(w, nb - 1);
-    mf_load_w<DT>(L, b0, v0);
-    load_a(b0, a0, d0);
-    __builtin_amdgcn_sched_barrier(0);  // the sets in order: the loop's waits are counted from them
-    if constexpr (MF_SETS == 2) {  // two sets in turn
-        const int b1 = min(w + NW, nb - 1);
-        mf_load_w<DT>(L, b1, v1);
-        load_a(b1, a1, d1);
-        __builtin_amdgcn_sched_barrier(0);
-        for (int b = w; b < nb; b += 2 * NW) {
-            body(b, v0, a0, d0);
-            body(b + NW, v1, a1, d1);
-        }
-    } else {
+                for (int i = 0; i < 4; i++) {
+                    int* e = tab + (((size_t)b * MF_ROWS + 4 * G + i) * M + ar) * TW;
+                    e[0] = s[i];
+                    e[1] = mt[i];
+                }
+            }
+            if (G == 0) dd[b * MF_ROWS + ar] = r.hdr.x;
+            if (G == 1 && ar < M) dxs[b * M + ar] = r.dx;
+        };
+        // The activation operand and scale of block b.
+        auto load_a = [&](int b, v4i* act, float& dx) {
+            const int8_t* yb = ya + (int64_t)b * 256;
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) act[ks] = *(const v4i*)(yb + 64 * ks + 16 * G);
+            dx = dxr[8 * b];
+        };
+        // Block b: stage it, load block b + NW into the freed weight
+        // registers, read the operand back, compute, then load that block's
+        // activations (one block's weights in flight while one computes).
+        // Every load is issued unconditionally (past the last block: the
+        // last block again), so the compiler's waits before the staging
+        // count exactly the loads issued after the set's.
+        auto body = [&](int b, u32x4* v, v4i* act, float& dx) {
+            mf_stage_w<DT>(L, wl, v);
+            const int bn = min(b + NW, nb - 1);
+            mf_load_w<DT>(L, bn, v);
+            if (b < nb) {
+                MfRaw<DT> r;
+                mf_lds_w<DT>(wl + ar * (S::RST * 16), G, r);
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++) r.act[ks] = act[ks];
+                r.dx = dx;
+                step(r, b);
+            }
+            load_a(bn, act, dx);
+        };
+        u32x4 v0[S::NLD];
+        v4i a0[4];
+        float d0;
+        mf_load_w<DT>(L, min(w, nb - 1), v0);
+        load_a(min(w, nb - 1), a0, d0);
         for (int b = w; b < nb; b += NW) body(b, v0, a0, d0);
+    } else {
+        uint8_t* wa = wl + S::WBYTES;    // activation rows [8][Q6_AROW]
+        uint8_t* wz = wa + 8 * Q6_AROW;  // 256 zero bytes
+        if (l < 16) *(u32x4*)(wz + 16 * l) = u32x4{0, 0, 0, 0};
+        // The block's activations as two coalesced chunks per lane: chunk
+        // c = 64i + l is row 4i + l/16 (clamped to M - 1), bytes 16(l % 16).
+        const int8_t* yc0 = A.q + (int64_t)min(l >> 4, M - 1) * A.K + 16 * (l & 15);
+        const int8_t* yc1 = A.q + (int64_t)min(4 + (l >> 4), M - 1) * A.K + 16 * (l & 15);
+        const uint32_t ac0 = (uint32_t)(l >> 4) * Q6_AROW + 16 * (l & 15), ac1 = ac0 + 4 * Q6_AROW;
+        // B operand sources: lane column 4m + g (m = (l&15)/4, g = l&3) reads
+        // activation row 4grp + m, k-slice G, when G == g, else zeros.
+        const int mq = (l & 15) >> 2, g = l & 3;
+        const uint8_t* bq0 = G == g ? wa + mq * Q6_AROW + 16 * G : wz;
+        const uint8_t* bq1 = G == g ? wa + (4 + mq) * Q6_AROW + 16 * G : wz;
+        // Weight rows 4G + i of the C layout: the low 4 bits of their first
+        // byte's address, for the offset of their blocks in the staging.
+        uint32_t rlo[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            rlo[i] = (uint32_t)(uintptr_t)(P.W + (int64_t)min(row0 + 4 * G + i, N - 1) * A.rb) & 15;
+        auto load6 = [&](int b, u32x4* v, v4i* ac, float& dx) {
+            mf_load_w<DT>(L, b, v);
+            ac[0] = *(const v4i*)(yc0 + (int64_t)b * 256);
+            ac[1] = *(const v4i*)(yc1 + (int64_t)b * 256);
+            dx = dxr[8 * b];
+        };
+        // Block b: stage its weights, activations and dx, load block b + NW
+        // into the freed registers (in flight while this one computes; two
+        // or three ahead measured slower: fewer waves fit), then compute
+        // from the staging.
+        auto body6 = [&](int b, u32x4* v, v4i* ac, float& dx) {
+            mf_stage_w<DT>(L, wl, v);
+            *(v4i*)(wa + ac0) = ac[0];
+            *(v4i*)(wa + ac1) = ac[1];
+            if (b < nb && G == 1 && ar < M) dxs[b * M + ar] = dx;
+            load6(min(b + NW, nb - 1), v, ac, dx);
+            if (b < nb) {
+                MfRaw<DT> r;
+                const uint32_t ob = (uint32_t)b * Q6K_BYTES;
+                mf_lds_w<DT>(wl + ar * (S::RST * 16) + (((uint32_t)(uintptr_t)rowp + ob) & 15), G, r);
+                if (G == 0) dd[b * MF_ROWS + ar] = r.dbits;
+                int sc[4][4];  // rows 4G + i, sub-blocks 4ks + g
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint8_t* sp = wl + (4 * G + i) * (S::RST * 16) + ((rlo[i] + ob) & 15) + 192 + g;
+#pragma unroll
+                    for (int ks = 0; ks < 4; ks++) sc[i][ks] = (int)*(const int8_t*)(sp + 4 * ks);
+                }
+                int s0[4], s1[4];
+                mf_block6(r, G, sc, bq0, bq1, s0, s1);
+                if (g == 0) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        int* e = tab + ((size_t)b * MF_ROWS + 4 * G + i) * M;
+                        if (mq < M) e[mq] = s0[i];
+                        if (4 + mq < M) e[4 + mq] = s1[i];
+                    }
+                }
+            }
+        };
+        u32x4 v0[S::NLD];
+        v4i c0[2];
+        float d0;
+        load6(min(w, nb - 1), v0, c0, d0);
+        for (int b = w; b < nb; b += NW) body6(b, v0, c0, d0);
     }
     const int flag = (wr != 0) | (okm == 0);
     if (t < MF_ROWS * M) refl[t] = flag;
@@ -388,13 +457,14 @@ void gemv_a8k_mfma_kernel(MfmaArgs A) {
     }
 }
 
-// Waves per workgroup: 4, or for Q6_K 8 while the grid holds fewer than
-// 4096 waves (16 per CU; down at 8 rows: 19.4 against 20.9 us). Measured at
-// the llama-8B shapes, Q4_K is fastest at 4 whatever the grid (gate+up
-// 22.5 us at 4, 28.6 at 8, 39 at 16), and Q6_K at 16 would not fit its two
-// sets in flight in the 128 registers of a 1024-thread workgroup.
+// Waves per workgroup: 4, or for Q6_K 12 while the grid holds fewer than
+// 4096 waves (16 per CU) and K has 16 blocks or more, else 8. Measured at
+// the llama-8B shapes and 8 rows: Q4_K is fastest at 4 whatever the grid
+// (gate+up 22.5 us at 4, 28.6 at 8, 39 at 16); Q6_K down 17.5 us at 12,
+// 17.9 at 8, 18.4 at 16 (which spills: 128 registers per lane).
 static int mf_waves(uint32_t dt, int64_t tiles, int nb) {
-    return dt == DT_Q6_K && tiles * 4 < 4096 && nb >= 8 ? 8 : 4;
+    if (dt == DT_Q6_K && tiles * 4 < 4096 && nb >= 8) return nb >= 16 ? 12 : 8;
+    return 4;
 }
 
 static size_t mf_lds(uint32_t dt, int nb, int M, int nw) {
@@ -411,7 +481,7 @@ bool gemv_mfma_ok(const DevWeight* const* ws, int nmat, int64_t rows) {
         tiles += (ws[i]->n + MF_ROWS - 1) / MF_ROWS;
     }
     const int nb = (int)(w.k / 256);
-    return mf_lds(w.dt, nb, (int)rows, mf_waves(w.dt, tiles, nb)) <= 96 * 1024;
+    return mf_lds(w.dt, nb, (int)rows, mf_waves(w.dt, tiles, nb)) <= 160 * 1024;  // gfx950: 160 KB of LDS per workgroup
 }
 
 hipError_t launch_gemv_a8k_mfma(const DevWeight* const* ws, int nmat, const ActPtrs& a, int64_t rows,
@@ -448,7 +518,8 @@ hipError_t launch_gemv_a8k_mfma(const DevWeight* const* ws, int nmat, const ActP
         hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q4_K, 4>), grid, block, lds, stream, A);
     } else {
         if (nw == 4) hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 4>), grid, block, lds, stream, A);
-        else hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 8>), grid, block, lds, stream, A);
+        else if (nw == 8) hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 8>), grid, block, lds, stream, A);
+        else hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 12>), grid, block, lds, stream, A);
     }
     return hipGetLastError();
 }

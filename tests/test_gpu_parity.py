@@ -262,7 +262,8 @@ def test_linear_a8k_refusals_and_bias(gpu, oracle, dt, rows, k):
     """Rows of x with NaN/Inf/huge values and rows of w with a non-finite
     block scale take the float32 path (reference interp/fast.go:323-377);
     bias is added as s + bias[j]. 6..8 rows run on the matrix-core GEMV,
-    with 4 waves per workgroup (K = 1024) and 16 (three workgroups)."""
+    with 4 waves per workgroup (K = 1024) and, for Q6_K, 12 (three
+    workgroups)."""
     n = 40
     wb = bytearray(_weights(oracle, dt, n, k, seed=8).tobytes())
     rb = len(wb) // n
@@ -413,10 +414,11 @@ def test_q6k_one_row_gemv_refusals_bias_and_group(gpu, oracle):
 @pytest.mark.parametrize("rows", [4, 5, 8])
 def test_mfma_gemv_bitexact(gpu, oracle, dt, n, k, rows):
     """4..8 activation rows run on the int8 matrix-core GEMV: ragged last
-    tile of 16 rows, K from one block to 56, workgroups of 4 waves (K of 1
-    and 3 blocks: idle and uneven waves), 8 waves (513 tiles) and 16 (19
-    and 257 tiles, 56 blocks split unevenly), odd block counts (Q6_K rows
-    2-byte aligned); the same bits as the reference's per-row products."""
+    tile of 16 rows, K from one block to 56, workgroups of 4 waves (Q4_K;
+    Q6_K with K of 1 and 3 blocks: idle and uneven waves), Q6_K 8 waves
+    (513 tiles of 8 blocks) and 12 (19 and 257 tiles: 56 and 16 blocks
+    split unevenly), odd block counts (Q6_K rows 2-byte aligned); the same
+    bits as the reference's per-row products."""
     wb = _weights(oracle, dt, n, k, seed=n + rows)
     W = gpu.Weight(wb, dt, n, k)
     x = oracle.synthetic_acts(rows, k, seed=rows + 7)
