@@ -323,15 +323,24 @@ int mimg_rope_dev(float *x, const int64_t *pos, const double *inv_freq, int64_t 
                   int interleaved, void *stream);
 
 /* The cache scatter of the graph (reference importer/llama.go:489-503): k, v
- * [T, kv_heads, d] into kcache/vcache [kv_heads, context, d] at the cache
- * indices pos[t] (slot * per-slot context + position with several slots),
- * rounded to f16 when f16 != 0 (the caches are then f16). Rows whose index
- * is outside 0..context-1 are not stored. */
+ * [T, kv_heads, d] into the caches at the cache indices pos[t] (slot *
+ * per-slot context + position with several slots), rounded to f16 when
+ * f16 != 0 (the caches are then f16). Rows whose index is outside
+ * 0..context-1 are not stored.
+ *
+ * Cache layouts (the graph's caches are [kv_heads, context, d]; these hold
+ * the same values): kcache is [kv_heads, context, d]; vcache is blocked by
+ * eight keys, [kv_heads, ceil(context/8), d, 8]: value (h, j, i) at
+ * ((h*ceil(context/8) + j/8)*d + i)*8 + j%8, so that a dim's eight
+ * consecutive keys are contiguous for the weighted sum, whose per-dim chain
+ * runs over the keys in order. vcache holds kv_heads*ceil(context/8)*8*d
+ * elements. */
 int mimg_kv_store_dev(const float *k, const float *v, const int64_t *pos, int64_t T, int kv_heads, int d,
                       int64_t context, void *kcache, void *vcache, int f16, void *stream);
 
 /* attention.v1 (f32 cache) / attention.v2 (f16 cache) with the graph's
- * mask (reference interp/fast.go:559-700, importer/llama.go:364-395):
+ * mask (reference interp/fast.go:559-700, importer/llama.go:364-395), on
+ * caches in the layouts of mimg_kv_store_dev:
  * query t of head h sees the cache entries kstart[t]..kend[t] (inclusive;
  * kstart may be NULL for 0) of kv head h / (heads / kv_heads), as the mask
  * of a cache with one or several sequences ("slots") allows; scale

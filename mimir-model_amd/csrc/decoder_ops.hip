@@ -144,8 +144,16 @@ __global__ void rope_kernel(float* __restrict__ x, const int64_t* __restrict__ p
     }
 }
 
-// k, v [T][Hkv][D] into the caches [Hkv][C][D] at the cache indices pos[t]
-// (rounded to f16 when the cache is f16).
+// The key cache is [Hkv][C][D]. The value cache is blocked by eight keys:
+// value (kv head hk, key j, dim d) at ((hk*ceil(C/8) + j/8)*D + d)*8 + j%8,
+// so that one dim's eight consecutive keys are 16 contiguous bytes (f16) for
+// the weighted sum, which runs one chain per dim in key order.
+__host__ __device__ __forceinline__ int64_t vcache_at(int hk, int64_t j, int d, int D, int64_t C) {
+    return (((int64_t)hk * ((C + 7) >> 3) + (j >> 3)) * D + d) * 8 + (j & 7);
+}
+
+// k, v [T][Hkv][D] into the caches at the cache indices pos[t] (rounded to
+// f16 when the cache is f16).
 __global__ void kv_store_kernel(const float* __restrict__ k, const float* __restrict__ v, const int64_t* __restrict__ pos,
                                 int T, int Hkv, int D, int64_t C, void* kc, void* vc, int f16) {
     const int64_t total = (int64_t)T * Hkv * D;
@@ -156,13 +164,13 @@ __global__ void kv_store_kernel(const float* __restrict__ k, const float* __rest
         const int hk = (int)(th % Hkv), t = (int)(th / Hkv);
         const int64_t p = pos[t];
         if (p < 0 || p >= C) continue;  // outside the cache: not stored
-        const int64_t at = ((int64_t)hk * C + p) * D + d;
+        const int64_t at = ((int64_t)hk * C + p) * D + d, av = vcache_at(hk, p, d, D, C);
         if (f16) {
             ((_Float16*)kc)[at] = (_Float16)k[idx];
-            ((_Float16*)vc)[at] = (_Float16)v[idx];
+            ((_Float16*)vc)[av] = (_Float16)v[idx];
         } else {
             ((float*)kc)[at] = k[idx];
-            ((float*)vc)[at] = v[idx];
+            ((float*)vc)[av] = v[idx];
         }
     }
 }
@@ -222,15 +230,17 @@ __global__ void rope_kv_kernel(float* __restrict__ q, const float* __restrict__ 
     }
     const int64_t p = cidx[t];
     if (p < 0 || p >= C) return;
-    const int hk = hh < H + Hkv ? hh - H : hh - H - Hkv;
+    const bool isk = hh < H + Hkv;
+    const int hk = isk ? hh - H : hh - H - Hkv;
     const int64_t at = ((int64_t)hk * C + p) * D;
-    void* cache = hh < H + Hkv ? kc : vc;
+    const int64_t ia = isk ? at + a : vcache_at(hk, p, a, D, C), ib = isk ? at + b : vcache_at(hk, p, b, D, C);
+    void* cache = isk ? kc : vc;
     if constexpr (F16) {
-        ((_Float16*)cache)[at + a] = (_Float16)xa;
-        ((_Float16*)cache)[at + b] = (_Float16)xb;
+        ((_Float16*)cache)[ia] = (_Float16)xa;
+        ((_Float16*)cache)[ib] = (_Float16)xb;
     } else {
-        ((float*)cache)[at + a] = xa;
-        ((float*)cache)[at + b] = xb;
+        ((float*)cache)[ia] = xa;
+        ((float*)cache)[ib] = xb;
     }
 }
 
@@ -386,8 +396,9 @@ __global__ __launch_bounds__(256) void att_scores_kernel(const float* __restrict
 //   per dim acc = fma(e_j, v_j[d], acc) in key order, then acc / sum.
 // Keys are read with one load per lane and element, two keys per group in
 // flight while the previous two are summed; the values of the workgroup's
-// dims are staged dim-major in LDS; the lane sums (wave 1) run beside the
-// chain (wave 0).
+// dims are staged dim-major in LDS from the 8-key block holding the first
+// visible key (16 bytes a dim and block); the lane sums (wave 1) run beside
+// the chain (wave 0).
 // Lane i of a row of 16 reads lane (i - n) mod 16 under row_ror:n, so
 // row_ror:12 gives lane i lane i+4 (lanes 0..3 of each group of eight read
 // lanes 4..7 of the same group).
@@ -409,6 +420,14 @@ __device__ __forceinline__ float reduce8_lane0(float l, bool four) {
     float a = l + (four ? dpp_f(l, DPP_XOR1) : dpp_f(l, DPP_ROR4));
     float b = a + (four ? dpp_f(a, DPP_XOR2) : dpp_f(a, DPP_XOR1));
     return b + (four ? dpp_f(b, DPP_ROR4) : dpp_f(b, DPP_XOR2));
+}
+
+// Elements per dim row of the staged values: maxk keys from a block start
+// (up to 7 more), rounded to blocks of 8, plus 16 bytes so that the lanes'
+// rows start in different banks.
+template <bool F16>
+__host__ __device__ constexpr int64_t att_dec_vstride(int64_t maxk) {
+    return ((maxk + 7 + 7) & ~(int64_t)7) + (F16 ? 8 : 4);
 }
 
 template <bool F16, int D, int DG>
@@ -435,9 +454,9 @@ __global__ __launch_bounds__(256) void att_decode_kernel(const float* __restrict
     }
     const int hk = h / (H / Hkv);
     const int64_t base = (int64_t)hk * C + r.k0;  // first visible cache row
-    const int64_t mk = (maxk + 3) & ~(int64_t)3, vstride = mk + VPAD;
+    const int64_t mk = (maxk + 3) & ~(int64_t)3, vstride = att_dec_vstride<F16>(maxk);
     float* sc = att_lds;            // [mk]: scores, then exponentials
-    VT* vb = (VT*)(att_lds + mk);   // [DG][vstride]: values, dim-major
+    VT* vb = (VT*)(att_lds + mk);   // [DG][vstride]: values, dim-major from key k0 & ~7
     if (tid == 0) nan_any = 0;
 
     // 1. Scores: group grp takes keys grp, grp+32, ..., two at a time, the
@@ -484,28 +503,20 @@ __global__ __launch_bounds__(256) void att_decode_kernel(const float* __restrict
         }
     }
 
-    // 2. The values of this workgroup's dims, dim-major into LDS.
-    const int64_t vbase = base * D + d0;
-    for (int64_t i = tid; i < n * PER_KEY; i += 256) {
-        const int64_t row = i / PER_KEY, piece = i % PER_KEY;
-        if constexpr (F16) {
-            const uint4 raw = *(const uint4*)((const _Float16*)vc + vbase + row * D + piece * 8);
-            const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
-            VT* dst = vb + piece * 8 * vstride + row;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                dst[(2 * e) * vstride] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
-                dst[(2 * e + 1) * vstride] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
-            }
-        } else {
-            const float4 v4 = *(const float4*)((const float*)vc + vbase + row * D + piece * 4);
-            VT* dst = vb + piece * 4 * vstride + row;
-            dst[0] = v4.x;
-            dst[vstride] = v4.y;
-            dst[2 * vstride] = v4.z;
-            dst[3 * vstride] = v4.w;
-        }
+    // 2. The values of this workgroup's dims, dim-major into LDS: the 16-byte
+    // pieces of (dim, 8-key block) from the block holding key k0, so that
+    // key k0 + j of dim d0 + l is vb[l * vstride + off + j].
+    const int64_t k0a = r.k0 & ~(int64_t)7, off = r.k0 - k0a, nblk = (off + n + 7) >> 3;
+    constexpr int PPB = F16 ? 1 : 2;  // 16-byte pieces per (dim, block)
+    const VT* vsrc = (const VT*)vc + vcache_at(hk, k0a, d0, D, C);
+    for (int64_t i = tid; i < nblk * DG * PPB; i += 256) {
+        const int64_t jb = i / (DG * PPB);
+        const int rem = (int)(i - jb * (DG * PPB)), dl = rem / PPB, pc = rem - dl * PPB;
+        const uint4 raw = *(const uint4*)(vsrc + (jb * D + dl) * 8 + pc * 4);
+        *(uint4*)(vb + dl * vstride + 8 * jb + pc * 4) = raw;
     }
+    (void)PER_KEY;
+    (void)base;
 
     // 3. Max and NaN over the scores, then the exponentials.
     mx = wave_max_f32(mx);
@@ -540,7 +551,7 @@ __global__ __launch_bounds__(256) void att_decode_kernel(const float* __restrict
         for (; j < nv; j += 8) sl = sl + sc[j];
         lane_sum[lane] = sl;
     } else if (w == 0 && lane < DG) {
-        const VT* vd = vb + lane * vstride;
+        const VT* vd = vb + lane * vstride + off;
         using VR = typename std::conditional<F16, uint2, float4>::type;
         auto fetch = [&](int64_t j, float4 (&ev)[4], VR (&vr)[4]) {
 #pragma unroll
@@ -568,7 +579,7 @@ __global__ __launch_bounds__(256) void att_decode_kernel(const float* __restrict
             }
         };
         int64_t j = 0;
-        if (n >= 16) {
+        if (n >= 16 && (off & 3) == 0) {  // (values of four keys in one aligned read)
             float4 eA[4], eB[4];
             VR vA[4], vB[4];
             fetch(0, eA, vA);
@@ -598,9 +609,57 @@ constexpr int64_t ATT_DEC_MAXK = 256;
 
 template <bool F16, int D>
 static size_t att_decode_lds(int64_t maxk) {
-    constexpr int DG = 32, VPAD = F16 ? 8 : 4, ESZ = F16 ? 2 : 4;
+    constexpr int DG = 32, ESZ = F16 ? 2 : 4;
     const int64_t mk = (maxk + 3) & ~(int64_t)3;
-    return (size_t)(mk * 4 + (int64_t)DG * (mk + VPAD) * ESZ);
+    return (size_t)(mk * 4 + (int64_t)DG * att_dec_vstride<F16>(maxk) * ESZ);
+}
+
+// Eight keys of the ordered weighted sum: acc = fma(e[k], v_k, acc) for k =
+// 0..7 in order, v_k the k-th value of the dim's 16 (f16) or 32 (f32, v0
+// then v1) bytes; att_vget reads one of them.
+template <bool F16>
+__device__ __forceinline__ void att_chain8(float& acc, const float* e, uint4 v0, uint4 v1) {
+    const float4 ea = *(const float4*)e, eb = *(const float4*)(e + 4);
+    if constexpr (F16) {
+        // (compiled to fmas with an f16 operand, v_fma_mix_f32: the
+        // conversion is exact; the chain runs at the fma's dependent-issue
+        // latency, about 10 cycles a key on MI355X, as plain f32 fmas do)
+        const uint32_t w[4] = {v0.x, v0.y, v0.z, v0.w};
+        const float ev[8] = {ea.x, ea.y, ea.z, ea.w, eb.x, eb.y, eb.z, eb.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            acc = __builtin_fmaf(ev[2 * k], (float)__builtin_bit_cast(_Float16, (uint16_t)(w[k] & 0xFFFF)), acc);
+            acc = __builtin_fmaf(ev[2 * k + 1], (float)__builtin_bit_cast(_Float16, (uint16_t)(w[k] >> 16)), acc);
+        }
+        (void)v1;
+    } else {
+        acc = __builtin_fmaf(ea.x, __uint_as_float(v0.x), acc);
+        acc = __builtin_fmaf(ea.y, __uint_as_float(v0.y), acc);
+        acc = __builtin_fmaf(ea.z, __uint_as_float(v0.z), acc);
+        acc = __builtin_fmaf(ea.w, __uint_as_float(v0.w), acc);
+        acc = __builtin_fmaf(eb.x, __uint_as_float(v1.x), acc);
+        acc = __builtin_fmaf(eb.y, __uint_as_float(v1.y), acc);
+        acc = __builtin_fmaf(eb.z, __uint_as_float(v1.z), acc);
+        acc = __builtin_fmaf(eb.w, __uint_as_float(v1.w), acc);
+    }
+}
+template <bool F16>
+__device__ __forceinline__ float att_vget(uint4 v0, uint4 v1, int k) {
+    if constexpr (F16) {
+        const uint32_t w[4] = {v0.x, v0.y, v0.z, v0.w};
+        uint32_t x = w[0];
+#pragma unroll
+        for (int i = 1; i < 4; i++)
+            if (k >> 1 == i) x = w[i];
+        return (float)__builtin_bit_cast(_Float16, (uint16_t)((k & 1) ? x >> 16 : x & 0xFFFF));
+    } else {
+        const uint32_t w[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        uint32_t x = w[0];
+#pragma unroll
+        for (int i = 1; i < 8; i++)
+            if (k == i) x = w[i];
+        return __uint_as_float(x);
+    }
 }
 
 // Many queries (prefill): a workgroup per (64 dims, head, four queries),
@@ -609,10 +668,17 @@ static size_t att_decode_lds(int64_t maxk) {
 // otherwise the chunks are staged per query. Per query the steps are those
 // of att_wsum_kernel (max, Cephes exp with eight stride-8 lane sums and the
 // f64 tail, then acc = fma(e_j, v_j[d], acc) in key order).
-// keys per staged chunk of values: 16 KB of LDS
+// keys per staged chunk of values (a multiple of 8), and elements per dim
+// row of the staged chunk: the chunk from the block holding its first key
+// (up to 7 more), plus 16 bytes so that the lanes' rows start in different
+// banks; 18 KB of LDS
 template <bool F16>
 constexpr int attq_vc() {
     return F16 ? 128 : 64;
+}
+template <bool F16>
+constexpr int attq_vs() {
+    return F16 ? attq_vc<F16>() + 8 : attq_vc<F16>() + 12;  // 68 and 76 dwords: 16 lanes' 16-byte reads hit 64 banks
 }
 
 template <bool F16>
@@ -669,258 +735,269 @@ __global__ __launch_bounds__(256) void att_wsum_q4_kernel(const void* vc, const 
     bool same = true;
 #pragma unroll
     for (int i = 0; i < 4; i++) same = same && (ns[i] == 0 || k0s[i] == k0s[first < 0 ? 0 : first]);
-    constexpr int VC = attq_vc<F16>();
+    constexpr int VC = attq_vc<F16>(), VS = attq_vs<F16>();
+    constexpr int PPB = F16 ? 1 : 2;  // 16-byte pieces per (dim, 8-key block)
     const int hk = h / (H / Hkv);
     float acc = 0.f;
-    constexpr int PER_ROW = F16 ? 8 : 16;  // 16-byte pieces per row of 64 dims
     for (int pass = 0; pass < (same ? 1 : 4); pass++) {
         const int src = same ? (first < 0 ? 0 : first) : pass;
         const int64_t pn = same ? nmax : ns[pass];
-        const int64_t vbase = ((int64_t)hk * C + k0s[src]) * D + d0;
         const bool mine = same || pass == w;
         for (int64_t c0 = 0; c0 < pn; c0 += VC) {
             const int64_t rows = pn - c0 < VC ? pn - c0 : VC;
+            // the chunk's keys k0 + c0 .. + rows - 1, dim-major from the block
+            // holding the first: key k0 + c0 + j of dim d0 + l at
+            // vb[l * VS + offc + j]
+            const int64_t ka = k0s[src] + c0, kaa = ka & ~(int64_t)7, offc = ka - kaa;
+            const int64_t nblk = (offc + rows + 7) >> 3;
+            const VT* vsrc = (const VT*)vc + vcache_at(hk, kaa, d0, D, C);
             __syncthreads();  // the previous chunk has been used
-            for (int64_t i = tid; i < rows * PER_ROW; i += 256) {
-                const int64_t row = i / PER_ROW, piece = i % PER_ROW;
-                const uint4 raw = *(const uint4*)((const VT*)vc + vbase + (c0 + row) * D + piece * (16 / sizeof(VT)));
-                *(uint4*)(vb + row * 64 + piece * (16 / sizeof(VT))) = raw;
+            for (int64_t i = tid; i < nblk * 64 * PPB; i += 256) {
+                const int64_t jb = i / (64 * PPB);
+                const int rem = (int)(i - jb * (64 * PPB)), dl = rem / PPB, pc = rem - dl * PPB;
+                *(uint4*)(vb + dl * VS + 8 * jb + pc * 4) = *(const uint4*)(vsrc + (jb * D + dl) * 8 + pc * 4);
             }
             __syncthreads();
             if (mine && !bad && c0 < n) {
                 const int64_t e1 = n - c0 < rows ? n - c0 : rows;
                 const float* e = sw + c0;
+                const VT* vd = vb + lane * VS + offc;
+                // one key at a time up to a block boundary, then eight keys
+                // per read (16-byte aligned: VS and the block starts are)
                 int64_t j = 0;
-                for (; j + 4 <= e1; j += 4) {
-                    const float4 ev = *(const float4*)(e + j);
-                    const float v0 = (float)vb[(j + 0) * 64 + lane], v1 = (float)vb[(j + 1) * 64 + lane];
-                    const float v2 = (float)vb[(j + 2) * 64 + lane], v3 = (float)vb[(j + 3) * 64 + lane];
-                    acc = __builtin_fmaf(ev.x, v0, acc);
-                    acc = __builtin_fmaf(ev.y, v1, acc);
-                    acc = __builtin_fmaf(ev.z, v2, acc);
-                    acc = __builtin_fmaf(ev.w, v3, acc);
+                for (; j < e1 && ((offc + j) & 7); j++) acc = __builtin_fmaf(e[j], (float)vd[j], acc);
+                for (; j + 8 <= e1; j += 8) {
+                    const uint4 v0 = *(const uint4*)(vd + j);
+                    uint4 v1 = v0;
+                    if constexpr (!F16) v1 = *(const uint4*)(vd + j + 4);
+                    float ev[8];
+#pragma unroll
+                    for (int k = 0; k < 8; k++) ev[k] = e[j + k];
+                    float4 ea = {ev[0], ev[1], ev[2], ev[3]}, eb = {ev[4], ev[5], ev[6], ev[7]};
+                    float et[8];
+                    *(float4*)et = ea;
+                    *(float4*)(et + 4) = eb;
+                    att_chain8<F16>(acc, et, v0, v1);
                 }
-                for (; j < e1; j++) acc = __builtin_fmaf(e[j], (float)vb[j * 64 + lane], acc);
+                for (; j < e1; j++) acc = __builtin_fmaf(e[j], (float)vd[j], acc);
             }
         }
     }
     if (t < T) out[((int64_t)t * H + h) * D + d0 + lane] = n <= 0 ? 0.f : (bad ? __builtin_nanf("") : acc / sum);
 }
 
-// LDS of att_wsum: the scores (maxk floats, padded to 4) and a chunk of
-// values in the cache's own type (f16 or f32), dim-major, within ATT_LDS
-// bytes (more only when the scores need it) so that several workgroups fit
-// on a CU; the first chunk of values is loaded into registers (at most
-// ATT_VREGS 16-byte pieces a thread) while the exponentials are computed.
-constexpr int ATT_LDS = 32 * 1024;
-constexpr int ATT_VREGS = 12;
+// The weighted sum for few queries (decode), a workgroup of four waves per
+// (64 dims d0.., head h, query t). A wave issues at most one instruction
+// every four cycles, so the wave that runs the serial chains does nothing
+// else; the others feed it:
+//   1. wave 1 (and wave 2 for an f32 cache: the second 16-byte piece) copies
+//      the dims' value blocks (8 keys x 64 dims, 1 KB in f16) into a ring of
+//      NR batches of 16 blocks in LDS with global_load_lds, NR - 1 batches
+//      ahead, starting before anything else;
+//   2. all waves: the scores of the visible keys to LDS, max, NaN check, then
+//      e = Cephes exp(s - max) for the first n&~7 keys and the f64 exp for
+//      the rest, at e[off + j] for key k0 + j (off = k0 % 8: the value
+//      blocks start at k0 - off);
+//   3. per batch, after a workgroup barrier (the copying waves wait for the
+//      batch's copies first), wave 0 lane l runs acc = fma(e_j, v_j[d0+l],
+//      acc) over the batch's keys in order (keys outside k0..k0+n-1 of the
+//      first and last block skipped, one at a time), and the copying waves
+//      start the batch NR - 1 ahead in the slot wave 0 has finished;
+//   4. wave 3's lanes 0..7 (during the first batch) sum e over the keys
+//      j < n&~7 with j = c mod 8, in order; the sum is ((s0+s4)+(s1+s5))+((s2+s6)+(s3+s7)) plus the rest
+//      in order; o[d] = acc / sum.
+// The float steps and their order are those of the reference's attendRow
+// (attn_amd64.s): the chain per dim in key order, the eight-lane exp sum.
 
-template <int DS, bool F16>
+// Global -> LDS copy of 16 bytes a lane (lane i writes at the wave's LDS
+// base + 16i), written as inline assembly so that the compiler does not
+// count it: the copying waves' waits are explicit (ATT_WAIT_VMCNT).
+__device__ __forceinline__ void att_lds_copy16(const void* g, const void* lds_wave_base) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_wave_base);
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(m0) : "memory", "m0");
+}
+// s_waitcnt with vmcnt <= n (n < 64), the other counters unconstrained.
+#define ATT_WAIT_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+
+__device__ __forceinline__ void att_barrier() {  // s_barrier without __syncthreads' vmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS reads and writes done
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+constexpr int ATT_BB = 16;  // blocks of 8 keys per batch
+template <bool F16>
+constexpr int att_nr() {  // ring batches: NR - 1 in flight, 16 copies each per copying wave (vmcnt <= 63)
+    return F16 ? 4 : 3;
+}
+template <bool F16>
+constexpr int att_batch_bytes() {
+    return ATT_BB * (F16 ? 1 : 2) * 1024;
+}
+
+template <bool F16>
 __global__ __launch_bounds__(256) void att_wsum_kernel(const void* vc, const int64_t* __restrict__ kend,
                                                        const int64_t* __restrict__ kstart, int H, int Hkv, int D,
-                                                       int64_t C, int64_t maxk, int vch,
-                                                       const float* __restrict__ ws, float* __restrict__ out) {
-    extern __shared__ float att_lds[];
+                                                       int64_t C, int64_t maxk, const float* __restrict__ ws,
+                                                       float* __restrict__ out) {
+    constexpr int PPB = F16 ? 1 : 2, NR = att_nr<F16>(), BATCH = att_batch_bytes<F16>();
+    extern __shared__ __align__(16) uint8_t att_lds8[];
+    uint8_t* ring = att_lds8;                   // [NR][ATT_BB][PPB][64 lanes][16 bytes]
+    float* e = (float*)(att_lds8 + NR * BATCH);  // e[off + j]
     __shared__ float red[4];
-    __shared__ float lane_sum[8];
+    __shared__ float lsum[8];
     __shared__ int nan_any;
-    constexpr int PER_ROW = F16 ? DS / 8 : DS / 4;  // 16-byte pieces per row of the slice
-    using VT = typename std::conditional<F16, _Float16, float>::type;
-    float* sc = att_lds;
-    VT* vb = (VT*)(att_lds + ((maxk + 3) & ~(int64_t)3));
-    const int d0 = blockIdx.x * DS, h = blockIdx.y, t = blockIdx.z, tid = threadIdx.x, w = tid >> 6;
+    const int d0 = 64 * blockIdx.x, h = blockIdx.y, t = blockIdx.z, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
     const AttRange r = att_range(kend, kstart, t, C, maxk);
     const int64_t n = r.n;
     float* orow = out + ((int64_t)t * H + h) * D + d0;
+    const int d = d0 + lane;
     if (n <= 0) {
-        if (tid < DS) orow[tid] = 0.f;
+        if (w == 0 && d < D) orow[lane] = 0.f;
         return;
     }
+    const int64_t k0a = r.k0 & ~(int64_t)7;
+    const int off = (int)(r.k0 - k0a), nb = (int)((off + n + 7) >> 3), nbat = (nb + ATT_BB - 1) / ATT_BB;
+    // 1. the copying waves start the ring (dims past D copy dim D - 1, unused)
+    const bool copier = w >= 1 && w <= PPB;
     const int hk = h / (H / Hkv);
-    const int64_t vbase = ((int64_t)hk * C + r.k0) * D + d0;
-    const int64_t rows0 = n < vch ? n : vch;
-    // the first chunk of values, into registers
-    uint4 vr[ATT_VREGS];
+    using VT = typename std::conditional<F16, _Float16, float>::type;
+    const VT* vsrc = (const VT*)vc + vcache_at(hk, k0a, d < D ? d : D - 1, D, C) + 4 * (w - 1);
+    const int64_t bstride = (int64_t)8 * D;
+    auto issue_batch = [&](int k) {  // blocks past the last: the last block again
+        uint8_t* slot = ring + (k % NR) * BATCH + (w - 1) * 1024;
 #pragma unroll
-    for (int k = 0; k < ATT_VREGS; k++) {
-        const int64_t i = tid + 256 * k;
-        const int64_t row = i / PER_ROW, piece = i % PER_ROW;
-        if (row < rows0) {
-            if constexpr (F16) vr[k] = *(const uint4*)((const _Float16*)vc + vbase + row * D + piece * 8);
-            else vr[k] = *(const uint4*)((const float*)vc + vbase + row * D + piece * 4);
+        for (int i = 0; i < ATT_BB; i++) {
+            const int b = ATT_BB * k + i < nb ? ATT_BB * k + i : nb - 1;
+            att_lds_copy16(vsrc + b * bstride, slot + i * PPB * 1024);
         }
-    }
+    };
+    if (copier)
+        for (int k = 0; k < NR - 1; k++) issue_batch(k);
+    // 2. scores, max, NaN check, exps
+    // (the copying waves load no scores: the compiler's wait for such loads
+    // would also wait for their copies issued before)
     const float* srow = ws + ((int64_t)t * H + h) * maxk;
     if (tid == 0) nan_any = 0;
     float mx = -INFINITY;
     int isnan_local = 0;
-    {
-        // the first 1024 scores in one round of loads (clamped, unstored past n)
-        float sv[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int64_t j = tid + 256 * k;
-            sv[k] = srow[j < n ? j : n - 1];
+    if (!copier) {
+        const int li = w == 0 ? lane : (w - PPB) * 64 + lane, nl = 64 * (4 - PPB);
+        for (int64_t j = li; j < n; j += nl) {
+            const float v = srow[j];
+            e[off + j] = v;
+            isnan_local |= v != v;
+            mx = fmaxf(mx, v);
         }
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int64_t j = tid + 256 * k;
-            if (j < n) {
-                sc[j] = sv[k];
-                isnan_local |= sv[k] != sv[k];
-                mx = fmaxf(mx, sv[k]);
-            }
-        }
-    }
-    for (int64_t j = tid + 1024; j < n; j += 256) {
-        const float v = srow[j];
-        sc[j] = v;
-        isnan_local |= v != v;
-        mx = fmaxf(mx, v);
     }
     mx = wave_max_f32(mx);
-    __syncthreads();  // nan_any cleared before it is set
-    if ((tid & 63) == 0) red[w] = mx;
+    att_barrier();  // nan_any cleared before it is set
+    if (lane == 0) red[w] = mx;
     if (isnan_local) nan_any = 1;
-    __syncthreads();
+    att_barrier();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    if (nan_any || __builtin_isinf(mx)) {
-        if (tid < DS) orow[tid] = __builtin_nanf("");
+    const bool bad = nan_any || __builtin_isinf(mx);
+    const int64_t nv = n >= 8 ? (n & ~(int64_t)7) : 0;
+    if (!bad)
+        for (int64_t j = tid; j < n; j += 256) {
+            const float x = e[off + j] - mx;
+            e[off + j] = j < nv ? cephes_exp(x) : (float)exp((double)x);
+        }
+    if (bad) {
+        if (w == 0 && d < D) orow[lane] = __builtin_nanf("");
+        if (copier) ATT_WAIT_VMCNT(0);  // the ring's copies land before the workgroup's LDS is released
         return;
     }
-    const int64_t nv = n >= 8 ? (n & ~(int64_t)7) : 0;
-    for (int64_t j = tid; j < n; j += 256) {
-        const float x = sc[j] - mx;
-        sc[j] = j < nv ? cephes_exp(x) : (float)exp((double)x);
-    }
-    // the first chunk of values into LDS, dim-major (vb[d][j], rows of
-    // vstride = vch + 16 bytes' worth of elements: the chain reads four keys
-    // of one dim at once, and the sixteen lanes' rows fall in distinct banks)
-    const int64_t vstride = vch + (F16 ? 8 : 4);
+    att_barrier();  // the exps are written
+    // 3. the batches
+    float acc = 0.f;
+    const int iend = off + (int)n;
+    for (int k = 0; k < nbat; k++) {
+        if (copier) ATT_WAIT_VMCNT(ATT_BB * (NR - 2));  // batch k has landed
+        att_barrier();
+        if (k == 0 && w == 3 && lane < 8) {  // 4. the lane sums, beside the first batch's chain
+            float sl = 0.f;
+            int64_t j = lane;
+            for (; j + 120 < nv; j += 128) {
+                float ev[16];
 #pragma unroll
-    for (int k = 0; k < ATT_VREGS; k++) {
-        const int64_t i = tid + 256 * k;
-        const int64_t row = i / PER_ROW, piece = i % PER_ROW;
-        if (row < rows0) {
-            if constexpr (F16) {
-                const uint32_t wv[4] = {vr[k].x, vr[k].y, vr[k].z, vr[k].w};
-                VT* dst = vb + piece * 8 * vstride + row;
+                for (int u = 0; u < 16; u++) ev[u] = e[off + j + 8 * u];
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    dst[(2 * e) * vstride] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
-                    dst[(2 * e + 1) * vstride] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
+                for (int u = 0; u < 16; u++) sl = sl + ev[u];
+            }
+            for (; j < nv; j += 8) sl = sl + e[off + j];
+            lsum[lane] = sl;
+        }
+        if (w == 0) {
+            const uint8_t* slot = ring + (k % NR) * BATCH + 16 * lane;
+            const int b0 = ATT_BB * k;
+            if (8 * b0 >= off && 8 * (b0 + ATT_BB) <= iend) {
+                // a batch of whole blocks, straight-line: every value read
+                // issued first, the exps as the chain goes (LDS latency is
+                // paid once a batch, not once a block)
+                uint4 v0[ATT_BB], v1[ATT_BB];
+#pragma unroll
+                for (int i = 0; i < ATT_BB; i++) {
+                    v0[i] = *(const uint4*)(slot + i * PPB * 1024);
+                    v1[i] = v0[i];
+                    if constexpr (!F16) v1[i] = *(const uint4*)(slot + i * PPB * 1024 + 1024);
+                }
+                const float* eb = e + 8 * b0;
+                float4 ex[2 * ATT_BB];
+#pragma unroll
+                for (int i = 0; i < 2 * ATT_BB; i++) ex[i] = *(const float4*)(eb + 4 * i);
+                __builtin_amdgcn_sched_barrier(0);  // every read issued before the chain
+#pragma unroll
+                for (int i = 0; i < ATT_BB; i++) {
+                    float ev[8];
+                    ev[0] = ex[2 * i].x, ev[1] = ex[2 * i].y, ev[2] = ex[2 * i].z, ev[3] = ex[2 * i].w;
+                    ev[4] = ex[2 * i + 1].x, ev[5] = ex[2 * i + 1].y, ev[6] = ex[2 * i + 1].z, ev[7] = ex[2 * i + 1].w;
+                    att_chain8<F16>(acc, ev, v0[i], v1[i]);
                 }
             } else {
-                const float fv[4] = {__uint_as_float(vr[k].x), __uint_as_float(vr[k].y), __uint_as_float(vr[k].z),
-                                     __uint_as_float(vr[k].w)};
-                VT* dst = vb + piece * 4 * vstride + row;
 #pragma unroll
-                for (int e = 0; e < 4; e++) dst[e * vstride] = fv[e];
-            }
-        }
-    }
-    __syncthreads();
-    // eight stride-8 lane sums in key order (wave 1, beside the chain of
-    // wave 0); HSUM and the tail at the end
-    if (tid >= 64 && tid < 72) {
-        float s = 0.f;
-        int64_t j = tid - 64;
-        for (; j + 120 < nv; j += 128) {
-            float e[16];
-#pragma unroll
-            for (int u = 0; u < 16; u++) e[u] = sc[j + 8 * u];
-#pragma unroll
-            for (int u = 0; u < 16; u++) s = s + e[u];
-        }
-        for (; j < nv; j += 8) s = s + sc[j];
-        lane_sum[tid - 64] = s;
-    }
-    float acc = 0.f;
-    for (int64_t c0 = 0; c0 < n; c0 += vch) {
-        const int64_t rows = n - c0 < vch ? n - c0 : vch;
-        if (c0 > 0) {  // later chunks (long contexts): stage, then sum
-            __syncthreads();
-            for (int64_t i = tid; i < rows * PER_ROW; i += 256) {
-                const int64_t row = i / PER_ROW, piece = i % PER_ROW;
-                if constexpr (F16) {
-                    const uint4 raw = *(const uint4*)((const _Float16*)vc + vbase + (c0 + row) * D + piece * 8);
-                    const uint32_t wv[4] = {raw.x, raw.y, raw.z, raw.w};
-                    VT* dst = vb + piece * 8 * vstride + row;
-#pragma unroll
-                    for (int e = 0; e < 4; e++) {
-                        dst[(2 * e) * vstride] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] & 0xFFFF));
-                        dst[(2 * e + 1) * vstride] = __builtin_bit_cast(_Float16, (uint16_t)(wv[e] >> 16));
-                    }
-                } else {
-                    const float4 v4 = *(const float4*)((const float*)vc + vbase + (c0 + row) * D + piece * 4);
-                    VT* dst = vb + piece * 4 * vstride + row;
-                    dst[0] = v4.x;
-                    dst[vstride] = v4.y;
-                    dst[2 * vstride] = v4.z;
-                    dst[3 * vstride] = v4.w;
+            for (int i = 0; i < ATT_BB; i++) {
+                const int b = ATT_BB * k + i;
+                if (b >= nb) break;  // uniform
+                const uint4 v0 = *(const uint4*)(slot + i * PPB * 1024);
+                uint4 v1 = v0;
+                if constexpr (!F16) v1 = *(const uint4*)(slot + i * PPB * 1024 + 1024);
+                const int i0 = 8 * b;
+                if (i0 >= off && i0 + 8 <= iend) {
+                    float ev[8];
+                    const float4 ea = *(const float4*)(e + i0), eb = *(const float4*)(e + i0 + 4);
+                    ev[0] = ea.x, ev[1] = ea.y, ev[2] = ea.z, ev[3] = ea.w;
+                    ev[4] = eb.x, ev[5] = eb.y, ev[6] = eb.z, ev[7] = eb.w;
+                    att_chain8<F16>(acc, ev, v0, v1);
+                } else {  // the first or last block, partly visible: one key at a time
+                    const int lo = i0 > off ? i0 : off, hi = i0 + 8 < iend ? i0 + 8 : iend;
+                    for (int ii = lo; ii < hi; ii++) acc = __builtin_fmaf(e[ii], att_vget<F16>(v0, v1, ii - i0), acc);
                 }
             }
-            __syncthreads();
-        }
-        if (tid < DS) {
-            // the chain in key order, 16 keys per batch of LDS reads (four
-            // keys per read of each operand); the next batch's reads are
-            // issued before this batch's multiply-adds, so the chain waits
-            // on LDS only once
-            const float* e = sc + c0;
-            const VT* vd = vb + tid * vstride;
-            using VR = typename std::conditional<F16, uint2, float4>::type;
-            auto fetch = [&](int64_t j, float4 (&ev)[4], VR (&vr)[4]) {
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    ev[u] = *(const float4*)(e + j + 4 * u);
-                    vr[u] = *(const VR*)(vd + j + 4 * u);
-                }
-            };
-            auto chain16 = [&](const float4 (&ev)[4], const VR (&vr)[4]) {
-#pragma unroll
-                for (int u = 0; u < 4; u++) {
-                    float4 vv;
-                    if constexpr (F16) {
-                        vv = make_float4((float)__builtin_bit_cast(_Float16, (uint16_t)(vr[u].x & 0xFFFF)),
-                                         (float)__builtin_bit_cast(_Float16, (uint16_t)(vr[u].x >> 16)),
-                                         (float)__builtin_bit_cast(_Float16, (uint16_t)(vr[u].y & 0xFFFF)),
-                                         (float)__builtin_bit_cast(_Float16, (uint16_t)(vr[u].y >> 16)));
-                    } else {
-                        vv = vr[u];
-                    }
-                    acc = __builtin_fmaf(ev[u].x, vv.x, acc);
-                    acc = __builtin_fmaf(ev[u].y, vv.y, acc);
-                    acc = __builtin_fmaf(ev[u].z, vv.z, acc);
-                    acc = __builtin_fmaf(ev[u].w, vv.w, acc);
-                }
-            };
-            int64_t j = 0;
-            if (rows >= 16) {
-                float4 eA[4], eB[4];
-                VR vA[4], vB[4];
-                fetch(0, eA, vA);
-                for (; j + 32 <= rows; j += 32) {
-                    fetch(j + 16, eB, vB);
-                    chain16(eA, vA);
-                    if (j + 48 <= rows) fetch(j + 32, eA, vA);
-                    chain16(eB, vB);
-                }
-                if (j + 16 <= rows) {  // the batch already in eA/vA
-                    chain16(eA, vA);
-                    j += 16;
-                }
             }
-            for (; j < rows; j++) acc = __builtin_fmaf(e[j], (float)vd[j], acc);
         }
+        if (copier) issue_batch(k + NR - 1);  // the slot of batch k - 1, which wave 0 has finished
     }
-    __syncthreads();
-    if (tid < DS) {
-        float sum = ((lane_sum[0] + lane_sum[4]) + (lane_sum[1] + lane_sum[5])) +
-                    ((lane_sum[2] + lane_sum[6]) + (lane_sum[3] + lane_sum[7]));
-        for (int64_t j = nv; j < n; j++) sum = sum + sc[j];
-        orow[tid] = acc / sum;
+    if (copier) ATT_WAIT_VMCNT(0);  // the ring's last copies (never read) land before the workgroup ends
+    att_barrier();  // the lane sums
+    if (w == 0 && d < D) {
+        float sum = ((lsum[0] + lsum[4]) + (lsum[1] + lsum[5])) + ((lsum[2] + lsum[6]) + (lsum[3] + lsum[7]));
+        for (int64_t j = nv; j < n; j++) sum = sum + e[off + j];
+        orow[lane] = acc / sum;
     }
+}
+
+static void launch_att_wsum(int T, int H, int Hkv, int D, int64_t C, int64_t maxk, int f16, const void* vc,
+                            const int64_t* kend, const int64_t* kstart, const float* ws, float* out, hipStream_t s) {
+    const size_t e_bytes = (size_t)(((maxk + 7 + 7) & ~(int64_t)7) * 4);
+    const dim3 grid((unsigned)((D + 63) / 64), (unsigned)H, (unsigned)T);
+    if (f16)
+        hipLaunchKernelGGL(att_wsum_kernel<true>, grid, dim3(256), att_nr<true>() * att_batch_bytes<true>() + e_bytes, s,
+                           vc, kend, kstart, H, Hkv, D, C, maxk, ws, out);
+    else
+        hipLaunchKernelGGL(att_wsum_kernel<false>, grid, dim3(256), att_nr<false>() * att_batch_bytes<false>() + e_bytes,
+                           s, vc, kend, kstart, H, Hkv, D, C, maxk, ws, out);
 }
 
 // swiglu.v1 (reference interp/fast.go:487-498): the reference splits the n
@@ -1080,23 +1157,6 @@ static void launch_att_scores(dim3 grid, const float* q, const void* kc, const i
                            maxk, ws);
 }
 
-template <int DS, bool F16>
-static void launch_att_wsum(int T, int H, int Hkv, int D, int64_t C, int64_t maxk, const void* vc, const int64_t* kend,
-                            const int64_t* kstart, const float* ws, float* out, hipStream_t s) {
-    constexpr int PER_ROW = F16 ? DS / 8 : DS / 4;
-    constexpr int64_t ESZ = F16 ? 2 : 4, PAD = F16 ? 8 : 4;
-    const int64_t sc_bytes = ((maxk + 3) & ~(int64_t)3) * 4;
-    // values: DS rows of vch + PAD elements (vch a multiple of 8); at least
-    // 64 keys a chunk, the rest of ATT_LDS otherwise
-    int64_t budget = ATT_LDS - 256;
-    if (budget < sc_bytes + DS * (64 + PAD) * ESZ) budget = sc_bytes + DS * (64 + PAD) * ESZ;
-    int64_t vch = (budget - sc_bytes) / (DS * ESZ) - PAD;
-    if (vch > (int64_t)ATT_VREGS * 256 / PER_ROW) vch = (int64_t)ATT_VREGS * 256 / PER_ROW;
-    vch &= ~(int64_t)7;
-    const size_t lds = (size_t)(sc_bytes + DS * (vch + PAD) * ESZ);
-    hipLaunchKernelGGL((att_wsum_kernel<DS, F16>), dim3((unsigned)(D / DS), (unsigned)H, (unsigned)T), dim3(256), lds, s,
-                       vc, kend, kstart, H, Hkv, D, C, maxk, (int)vch, ws, out);
-}
 
 hipError_t launch_attention(const float* q, const void* kc, const void* vc, const int64_t* kend, const int64_t* kstart,
                             int T, int H, int Hkv, int D, int64_t C, int64_t maxk, int f16, float* out, float* ws,
@@ -1109,7 +1169,7 @@ hipError_t launch_attention(const float* q, const void* kc, const void* vc, cons
         const dim3 grid(tiles, (unsigned)H, (unsigned)((T + 3) / 4));
         if (f16) launch_att_scores<true, 4>(grid, q, kc, kend, kstart, T, H, Hkv, D, C, maxk, ws, s);
         else launch_att_scores<false, 4>(grid, q, kc, kend, kstart, T, H, Hkv, D, C, maxk, ws, s);
-        const size_t lds = (size_t)(4 * ((maxk + 3) & ~(int64_t)3) * 4 + (f16 ? attq_vc<true>() * 64 * 2 : attq_vc<false>() * 64 * 4));
+        const size_t lds = (size_t)(4 * ((maxk + 3) & ~(int64_t)3) * 4 + (f16 ? attq_vs<true>() * 64 * 2 : attq_vs<false>() * 64 * 4));
         const dim3 g2((unsigned)(D / 64), (unsigned)H, (unsigned)((T + 3) / 4));
         if (f16)
             hipLaunchKernelGGL(att_wsum_q4_kernel<true>, g2, dim3(256), lds, s, vc, kend, kstart, T, H, Hkv, D, C, maxk,
@@ -1143,13 +1203,7 @@ hipError_t launch_attention(const float* q, const void* kc, const void* vc, cons
     const dim3 grid(tiles, (unsigned)H, (unsigned)T);
     if (f16) launch_att_scores<true, 1>(grid, q, kc, kend, kstart, T, H, Hkv, D, C, maxk, ws, s);
     else launch_att_scores<false, 1>(grid, q, kc, kend, kstart, T, H, Hkv, D, C, maxk, ws, s);
-    if (D % 16 == 0) {
-        if (f16) launch_att_wsum<16, true>(T, H, Hkv, D, C, maxk, vc, kend, kstart, ws, out, s);
-        else launch_att_wsum<16, false>(T, H, Hkv, D, C, maxk, vc, kend, kstart, ws, out, s);
-    } else {
-        if (f16) launch_att_wsum<8, true>(T, H, Hkv, D, C, maxk, vc, kend, kstart, ws, out, s);
-        else launch_att_wsum<8, false>(T, H, Hkv, D, C, maxk, vc, kend, kstart, ws, out, s);
-    }
+    launch_att_wsum(T, H, Hkv, D, C, maxk, f16, vc, kend, kstart, ws, out, s);
     return hipGetLastError();
 }
 

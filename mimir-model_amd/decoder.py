@@ -146,7 +146,8 @@ class Decoder:
         esz = 2 if self.f16 else 4
         B = hiprt.DeviceBuffer
         self.kc = [B(Hkv * self.cache_len * D * esz) for _ in range(c.layers)]
-        self.vc = [B(Hkv * self.cache_len * D * esz) for _ in range(c.layers)]
+        # the value cache is blocked by eight keys (include/mimg.h)
+        self.vc = [B(Hkv * mimg.vcache_len(self.cache_len) * D * esz) for _ in range(c.layers)]
         for buf in self.kc + self.vc:
             buf.zero()
         self.invf = B.from_array(inv_freq(c))

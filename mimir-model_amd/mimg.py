@@ -343,6 +343,28 @@ def rope_dev(x_ptr, pos_ptr, inv_freq_ptr, T, heads, d, rotary, interleaved, str
                                 _P(stream)))
 
 
+def vcache_len(context):
+    """Keys a value cache of `context` entries holds: the value cache is
+    blocked by eight keys, [kv_heads][ceil(context/8)][d][8]."""
+    return (int(context) + 7) // 8 * 8
+
+
+def pack_vcache(v):
+    """A value cache [kv_heads, context, d] (numpy) in the library's blocked
+    layout [kv_heads, ceil(context/8), d, 8] (entries past context zero)."""
+    hk, c, d = v.shape
+    cp = vcache_len(c)
+    pad = np.zeros((hk, cp, d), v.dtype)
+    pad[:, :c] = v
+    return np.ascontiguousarray(pad.reshape(hk, cp // 8, 8, d).transpose(0, 1, 3, 2))
+
+
+def unpack_vcache(b, kv_heads, context, d):
+    """The inverse of pack_vcache, from the raw blocked values."""
+    cp = vcache_len(context)
+    return np.ascontiguousarray(b.reshape(kv_heads, cp // 8, d, 8).transpose(0, 1, 3, 2).reshape(kv_heads, cp, d)[:, :context])
+
+
 def kv_store_dev(k_ptr, v_ptr, pos_ptr, T, kv_heads, d, context, kc_ptr, vc_ptr, f16, stream):
     _check(load().mimg_kv_store_dev(_P(k_ptr), _P(v_ptr), _P(pos_ptr), T, kv_heads, d, context, _P(kc_ptr),
                                     _P(vc_ptr), int(f16), _P(stream)))

@@ -120,7 +120,7 @@ def test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, slo
     k = (rng.standard_normal((T, Hkv, D)) * 2).astype(np.float32)
     v = rng.standard_normal((T, Hkv, D)).astype(np.float32)
     q = rng.standard_normal((T, H, D)).astype(np.float32)
-    kc, vc = dev(rt, base[0]), dev(rt, base[1])
+    kc, vc = dev(rt, base[0]), dev(rt, gpu.pack_vcache(base[1]))  # the value cache blocked by 8 keys
     dk, dv, dq, dc, ds = dev(rt, k), dev(rt, v), dev(rt, q), dev(rt, cidx), dev(rt, (slot * C).astype(np.int64))
     out = rt.DeviceBuffer(q.nbytes)
     wsb = gpu.attention_workspace_bytes(T, H, C)
@@ -135,7 +135,7 @@ def test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, slo
         wk[:, cidx[t]] = k[t]  # rounded to f16 (RNE) with an f16 cache
         wv[:, cidx[t]] = v[t]
     got_k = kc.download(cdt).reshape(Hkv, L, D)
-    got_v = vc.download(cdt).reshape(Hkv, L, D)
+    got_v = gpu.unpack_vcache(vc.download(cdt), Hkv, L, D)
     assert np.array_equal(got_k.view(np.uint16 if f16 else np.uint32), wk.view(np.uint16 if f16 else np.uint32))
     assert np.array_equal(got_v.view(np.uint16 if f16 else np.uint32), wv.view(np.uint16 if f16 else np.uint32))
     want = oracle.attention(q, wk, wv, cidx, slot * C if slots > 1 else None)
@@ -148,6 +148,16 @@ def test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, slo
 def test_attention_long_context_bitexact(gpu, oracle, rt, f16, C, D):
     """Long visible ranges: many score tiles and several value chunks."""
     test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, 3, 4, 2, D, 1, C=C)
+
+
+@pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
+@pytest.mark.parametrize("T,H,Hkv,D,C", [(5, 4, 1, 64, 42), (4, 8, 2, 128, 45), (5, 4, 2, 32, 42), (3, 4, 2, 128, 301)])
+def test_attention_unaligned_slots_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, C):
+    """Three slots of C entries with C not a multiple of 8: the visible ranges
+    start inside an 8-key block of the value cache (the weighted sum skips
+    the keys before them, one at a time), through the short-context kernel
+    (D = 64/128, C <= 256) and the two-kernel path (D = 32, C = 301)."""
+    test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, 3, C=C)
 
 
 @pytest.mark.parametrize("n,procs", [(3 * 8192 + 5, 16), (1792, 16), (100, 4), (100, 1), (4096, 7), (7, 16)])
@@ -663,12 +673,15 @@ def test_matmul_quantized_group_equals_single(gpu, oracle, rt):
 
 
 @pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
-@pytest.mark.parametrize("T,slots,D", [(20, 1, 64), (37, 1, 128), (24, 3, 64), (18, 2, 128)])
-def test_attention_many_queries_bitexact(gpu, oracle, rt, f16, T, slots, D):
+@pytest.mark.parametrize("T,slots,D,C", [(20, 1, 64, 64), (37, 1, 128, 64), (24, 3, 64, 64), (18, 2, 128, 64),
+                                         (24, 3, 64, 44), (18, 2, 128, 42)])
+def test_attention_many_queries_bitexact(gpu, oracle, rt, f16, T, slots, D, C):
     """Prompt-like batches (T >= 16 rows: four queries per workgroup): rows of
     one sequence at consecutive positions (the causal prefill), and rows of
-    several slots interleaved, against the C restatement bit for bit."""
-    H, Hkv, C = 4, 2, 64
+    several slots interleaved (slot starts inside an 8-key block of the value
+    cache when C is not a multiple of 8), against the C restatement bit for
+    bit."""
+    H, Hkv = 4, 2
     rng = np.random.default_rng(T + slots + D)
     L = slots * C
     cdt = np.float16 if f16 else np.float32
@@ -680,7 +693,7 @@ def test_attention_many_queries_bitexact(gpu, oracle, rt, f16, T, slots, D):
     pos = pos.astype(np.int64) + 3
     cidx = (slot * C + pos).astype(np.int64)
     kstart = (slot * C).astype(np.int64)
-    dq, dk, dv, de, ds = dev(rt, q), dev(rt, kc), dev(rt, vc), dev(rt, cidx), dev(rt, kstart)
+    dq, dk, dv, de, ds = dev(rt, q), dev(rt, kc), dev(rt, gpu.pack_vcache(vc)), dev(rt, cidx), dev(rt, kstart)
     out = rt.DeviceBuffer(q.nbytes)
     wsb = gpu.attention_workspace_bytes(T, H, C)
     ws = rt.DeviceBuffer(wsb)
