@@ -25,7 +25,22 @@ roofline: the step's longest launch, the Q4_K GEMV computing gate and up
 together, timed alone (graphs of --rotate launches over the rotation copies,
 HIP events on the launch stream), its algorithmic bytes over that time
 against 8 TB/s; traffic from the committed rocprofv3 FETCH/WRITE summary.
-The same kernel on gate alone and the Q6_K down launch are reported beside it.
+The same kernel on gate alone and the Q6_K down launch are reported beside
+it, and the read ceiling: a plain streaming read of the same gate and up
+weight bytes in one launch, timed the same way.
+
+cfg0: the single 4096 x 4096 Q4_K product of one
+activation row, quantized inside the launch, per call.
+
+prefill: the gate and down products at M = 64, 512, 2048
+activation rows on the int8 matrix-core GEMMs (Q4_K/Q6_K with activation
+blocks of 256; Q8_0 with blocks of 32) and with float32 activations on the
+fp32 matrix cores. --prefill-only times only these and prints them as one
+JSON line (with --eager, launch by launch: the form profiler runs use).
+
+cpu_baseline: the oracle's C restatement of the one-row product
+(oracle/mimref.c, AVX2, threaded over weight rows) on the host's cores, on
+a bounded sample of the cfg1 layer set.
 
 The "decode" section runs whole greedy generation on the GPU decoder
 (mimir-model_amd/decoder.py) with random Q4_K_M weights of two model shapes
@@ -35,7 +50,9 @@ with a 512-token prompt and 256 new tokens at batch 1 and at batch 8 (eight
 sequences in eight cache slots), f16 key-value cache. Reported: decode
 tokens/s (every sequence's new tokens over the device time of the decode
 steps), prompt tokens/s, and the weight bytes a decode step reads over the
-step time.
+step time. Unless --no-cpu, the CPU restatement (oracle/llama_ref.py) decodes
+the first tokens of each shape from the same weights and its ids are
+compared with the GPU's (8 tokens; the 8B shape on a 32-token prompt).
 """
 import argparse
 import json
@@ -277,9 +294,13 @@ def main():
     ap.add_argument("--rows", type=int, default=1, help="activation rows M (1 = cfg1; 8 = cfg4's batch 8)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--eager", action="store_true", help="launch without HIP graphs")
+    ap.add_argument("--eager", action="store_true", help="launch without HIP graphs (every timed section)")
     ap.add_argument("--prefill-rows", default="64,512,2048",
                     help="activation rows of the prefill GEMM measurements (comma list; empty to skip)")
+    ap.add_argument("--prefill-kinds", default="a8,q8_0,f32",
+                    help="prefill products to time: a8 (Q4_K/Q6_K x 8-bit), q8_0 (Q8_0 x 8-bit), f32")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="time only the prefill products (for profiler runs) and print them as one JSON line")
     ap.add_argument("--decode-batches", default="1,8", help="batch sizes of the llama8b decode runs")
     ap.add_argument("--decode", default="llama1b,llama8b",
                     help="whole-model decode runs (comma list of llama1b, llama8b; empty to skip)")
@@ -306,6 +327,82 @@ def main():
     ws_bytes = [mimg.a8_workspace_bytes(M, k) for k in INPUT_K]
     ws = [hiprt.DeviceBuffer(b) for b in ws_bytes]
     yd = {name: hiprt.DeviceBuffer(M * n * 4) for name, n, _, _, _, _ in CFG1}
+
+    # Prefill (BASELINE configs[2]): the gate (Q4_K) and down (Q6_K) products
+    # at M activation rows on the int8 MFMA GEMM, activations quantized
+    # beforehand; a graph of --rotate launches over the rotation copies
+    # (with --eager the same launches issued directly). Ops = 2*M*N*K; the fraction is of MI355X's dense int8 peak.
+    # With f32 (BASELINE.json north_star's f32-activation prefill,
+    # dequant_matmul.v1): the same products with float32 activations on the
+    # fp32 matrix cores (mimg_linear_f32_mfma_dev), fraction of the dense
+    # fp32 matrix peak.
+    def prefill(name, rows, f32=False, q8_layers=None):
+        _, n, k, dt, _, _ = next(c for c in CFG1 if c[0] == name)
+        block = 32 if q8_layers else 256
+        xp = hiprt.DeviceBuffer.from_array(np.random.default_rng(200 + rows).standard_normal((rows, k), dtype=np.float32))
+        wsb = mimg.a8_workspace_bytes(rows, k)
+        wsp = hiprt.DeviceBuffer(wsb)
+        yp = hiprt.DeviceBuffer(rows * n * 4)
+        mimg.quantize_act_dev(xp.ptr, rows, k, block, wsp.ptr, wsb, stream.handle)
+        src = q8_layers or layers
+
+        def launches():
+            for l in range(args.rotate):
+                if f32:
+                    mimg.linear_f32_mfma_dev(src[l][name], xp.ptr, rows, None, yp.ptr, stream.handle)
+                else:
+                    mimg.matmul_a8_quantized_dev(src[l][name], xp.ptr, rows, None, block, yp.ptr, wsp.ptr, wsb,
+                                                 stream.handle)
+
+        a, b = hiprt.Event(), hiprt.Event()
+        if args.eager:
+            launches()
+            a.record(stream)
+            launches()
+            b.record(stream)
+            b.sync()
+        else:
+            g = hiprt.Graph(stream, launches)
+            g.launch(stream)
+            a.record(stream)
+            g.launch(stream)
+            b.record(stream)
+            b.sync()
+            g.destroy()
+        us = a.elapsed_ms(b) * 1e3 / args.rotate
+        for buf in (xp, wsp, yp):
+            buf.free()
+        tops = 2.0 * rows * n * k / (us * 1e-6) / 1e12
+        if f32:
+            return {"us_per_launch": round(us, 2), "TFLOP_per_s": round(tops, 1),
+                    "frac_fp32_peak": round(tops / FP32_PEAK_TFLOPS, 4)}
+        return {"us_per_launch": round(us, 2), "TOP_per_s": round(tops, 1),
+                "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
+
+    def run_prefills():
+        prefill_res, prefill_q8, prefill_f32 = {}, {}, {}
+        prefill_rows = [int(r) for r in args.prefill_rows.split(",") if r]
+        q8_layers = make_q8_0_weights(stream, args.rotate, log) if prefill_rows and "q8_0" in kinds else None
+        for rows in prefill_rows:
+            for name in ("gate", "down"):
+                if "a8" in kinds:
+                    prefill_res[f"{name}_M{rows}"] = prefill(name, rows)
+                    log(f"  prefill {name} M={rows}: {prefill_res[f'{name}_M{rows}']}")
+                if q8_layers:
+                    prefill_q8[f"{name}_M{rows}"] = prefill(name, rows, q8_layers=q8_layers)
+                    log(f"  prefill Q8_0 {name} M={rows}: {prefill_q8[f'{name}_M{rows}']}")
+                if "f32" in kinds:
+                    prefill_f32[f"{name}_M{rows}"] = prefill(name, rows, f32=True)
+                    log(f"  prefill f32 {name} M={rows}: {prefill_f32[f'{name}_M{rows}']}")
+        if q8_layers:
+            q8_layers.clear()
+        return prefill_res, prefill_q8, prefill_f32
+
+    kinds = args.prefill_kinds.split(",")
+    if args.prefill_only:
+        pr, pq, pf = run_prefills()
+        print(json.dumps({"prefill": pr, "prefill_q8_0": pq, "prefill_f32": pf, "graphs": not args.eager}), flush=True)
+        return
 
     # A decoder layer's calls: q, k and v share the attention input and gate
     # and up the FFN input, so each pair/triple is one grouped call
@@ -451,63 +548,7 @@ def main():
         f"gate alone: {g_us:.2f} us, {g_gbs:.0f} GB/s; down GEMV (Q6_K 4096x14336): {d_us:.2f} us/launch, "
         f"{d_gbs:.0f} GB/s")
 
-    # Prefill (BASELINE configs[2]): the gate (Q4_K) and down (Q6_K) products
-    # at M activation rows on the int8 MFMA GEMM, activations quantized
-    # beforehand; a graph of --rotate launches over the rotation copies.
-    # Ops = 2*M*N*K; the fraction is of MI355X's dense int8 peak.
-    # With f32 (BASELINE.json north_star's f32-activation prefill,
-    # dequant_matmul.v1): the same products with float32 activations on the
-    # fp32 matrix cores (mimg_linear_f32_mfma_dev), fraction of the dense
-    # fp32 matrix peak.
-    def prefill(name, rows, f32=False, q8_layers=None):
-        _, n, k, dt, _, _ = next(c for c in CFG1 if c[0] == name)
-        block = 32 if q8_layers else 256
-        xp = hiprt.DeviceBuffer.from_array(np.random.default_rng(200 + rows).standard_normal((rows, k), dtype=np.float32))
-        wsb = mimg.a8_workspace_bytes(rows, k)
-        wsp = hiprt.DeviceBuffer(wsb)
-        yp = hiprt.DeviceBuffer(rows * n * 4)
-        mimg.quantize_act_dev(xp.ptr, rows, k, block, wsp.ptr, wsb, stream.handle)
-        src = q8_layers or layers
-
-        def launches():
-            for l in range(args.rotate):
-                if f32:
-                    mimg.linear_f32_mfma_dev(src[l][name], xp.ptr, rows, None, yp.ptr, stream.handle)
-                else:
-                    mimg.matmul_a8_quantized_dev(src[l][name], xp.ptr, rows, None, block, yp.ptr, wsp.ptr, wsb,
-                                                 stream.handle)
-
-        g = hiprt.Graph(stream, launches)
-        g.launch(stream)
-        a, b = hiprt.Event(), hiprt.Event()
-        a.record(stream)
-        g.launch(stream)
-        b.record(stream)
-        b.sync()
-        g.destroy()
-        us = a.elapsed_ms(b) * 1e3 / args.rotate
-        for buf in (xp, wsp, yp):
-            buf.free()
-        tops = 2.0 * rows * n * k / (us * 1e-6) / 1e12
-        if f32:
-            return {"us_per_launch": round(us, 2), "TFLOP_per_s": round(tops, 1),
-                    "frac_fp32_peak": round(tops / FP32_PEAK_TFLOPS, 4)}
-        return {"us_per_launch": round(us, 2), "TOP_per_s": round(tops, 1),
-                "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4)}
-
-    prefill_res, prefill_f32, prefill_q8 = {}, {}, {}
-    prefill_rows = [int(r) for r in args.prefill_rows.split(",") if r]
-    q8_layers = make_q8_0_weights(stream, args.rotate, log) if prefill_rows else None
-    for rows in prefill_rows:
-        for name in ("gate", "down"):
-            prefill_res[f"{name}_M{rows}"] = prefill(name, rows)
-            log(f"  prefill {name} M={rows}: {prefill_res[f'{name}_M{rows}']}")
-            prefill_q8[f"{name}_M{rows}"] = prefill(name, rows, q8_layers=q8_layers)
-            log(f"  prefill Q8_0 {name} M={rows}: {prefill_q8[f'{name}_M{rows}']}")
-            prefill_f32[f"{name}_M{rows}"] = prefill(name, rows, f32=True)
-            log(f"  prefill f32 {name} M={rows}: {prefill_f32[f'{name}_M{rows}']}")
-    if q8_layers:
-        q8_layers.clear()
+    prefill_res, prefill_q8, prefill_f32 = run_prefills()
 
     # The host-memory entry point a cgo caller uses (x copied in, y copied
     # back, the call returns when y is in host memory): PCIe- and

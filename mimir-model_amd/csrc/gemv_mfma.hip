@@ -12,22 +12,30 @@
 // tot = fma(f32(S_b), d_b*dx_b, tot) (and off for Q4_K's mins) in block
 // order: bit for bit the one-row kernel.
 //
-// Work split: a 256-thread workgroup owns 16 weight rows of one matrix; its
-// four waves take blocks w, w+4, w+8, ... A wave's MFMA operand is 16 rows
+// Work split: a workgroup owns 16 weight rows of one matrix; its NW waves
+// (4; for Q6_K on small grids 8 or 12) take blocks w, w+NW, w+2NW, ...
+// A wave's MFMA operand is 16 rows
 // x 16 bytes per lane, and loads in that layout touch 16 rows 2-3 KB apart
 // in every instruction (measured on MI355X: 31 us for the 66 MB of gate+up
 // at 8 rows, against 17-18 us for the same bytes loaded 64 consecutive
 // chunks per instruction, whether the runs are 144 bytes or whole rows).
 // So a wave loads its block's 16 x 144 (Q4_K) or 16 x 224 (Q6_K, from the
 // 16-byte boundary below each row's block) bytes as consecutive 16-byte
-// chunks, two blocks ahead, writes them to its own LDS region (rows an odd
+// chunks, one block ahead, writes them to its own LDS region (rows an odd
 // number of chunks apart, so the 16 rows start in different banks) and
 // reads its operand back in MFMA layout: no barrier, the wave's LDS
 // accesses run in order. (A workgroup-wide staging of four blocks with a
 // barrier per stage measured slower: 32 us without any arithmetic.) The
 // activations (lane l: activation row l%16, rows past M clamped, their
-// columns never read) come straight from global memory (L2-resident).
-// Per block a wave runs 12 (Q4_K) or 8 (Q6_K) MFMAs and writes the block's
+// columns never read) come from global memory (L2-resident): straight into
+// the B operand for Q4_K, through the wave's LDS region for Q6_K.
+// Q4_K: per block 12 MFMAs on the GEMM's planes (sh*q, sl*q, and m_s for
+// the mins). Q6_K: the raw 6-bit values q (0..63) are the A operand, and
+// the B operand puts each lane group's activation slice into its own four
+// result columns, so one MFMA gives the per-16 sums of q*y for four
+// sub-blocks apart; the sub-block scales are applied to those int32 sums
+// (exact) and the -32 offset is one more MFMA with every A byte -32.
+// A wave writes the block's
 // exact (S, M) per (row, activation row) to an LDS table; then one lane per
 // (row, activation row) runs the float chain over the table in block order.
 // Rows of x the quantizer refused and weight rows with a non-finite block
