@@ -211,6 +211,24 @@ int mimg_rms_norm_linear_a8_group_dev(const uint64_t *w, int count, const float 
                                       const float *scale, float eps, float *x_out, const float *const *bias,
                                       float *const *y, void *stream);
 
+/* mimg_rms_norm_linear_a8_group_dev on w = {q, k, v} at one activation
+ * row followed by mimg_rope_kv_dev (T = 1) on its outputs, in one launch:
+ * rope.v1 (reference interp/fast.go:507-557) rotates q (written to q,
+ * [heads, d]) and k, and the cache scatter of importer/llama.go:489-503
+ * stores the rotated k and v into kcache/vcache at cache_index[0] (not
+ * stored outside 0..context-1). Bit for bit the two calls; the k and v
+ * outputs are not written anywhere else. q must not overlap x, resid, scale
+ * or x_out (MIMG_ERR_ARG). Returns MIMG_NOT_HANDLED (nothing launched)
+ * where the fused norm GEMV does not take the shape, where q, k, v are not
+ * [heads*d], [kv_heads*d], [kv_heads*d] rows, or where a workgroup's rows
+ * would not be whole rotation pairs of one head: the caller then makes the
+ * two calls. No reference counterpart beyond the ops it equals. */
+int mimg_rms_norm_qkv_rope_kv_dev(const uint64_t *w, const float *x, const float *resid, const float *scale,
+                                  float eps, float *x_out, const float *const *bias, float *q, const int64_t *pos,
+                                  const int64_t *cache_index, const double *inv_freq, int heads, int kv_heads, int d,
+                                  int rotary, int interleaved, int64_t context, void *kcache, void *vcache, int f16,
+                                  void *stream);
+
 /* The product alone, for activations already quantized into ws by
  * mimg_quantize_act_dev with the same rows, K and block. */
 int mimg_matmul_a8_quantized_dev(uint64_t w, const float *x, int64_t rows, const float *bias, int block,

@@ -8,6 +8,14 @@
 
 namespace mimg {
 
+// The key cache is [Hkv][C][D]. The value cache is blocked by eight keys:
+// value (kv head hk, key j, dim d) at ((hk*ceil(C/8) + j/8)*D + d)*8 + j%8,
+// so that one dim's eight consecutive keys are 16 contiguous bytes (f16) for
+// the weighted sum, which runs one chain per dim in key order.
+__host__ __device__ __forceinline__ int64_t vcache_at(int hk, int64_t j, int d, int D, int64_t C) {
+    return (((int64_t)hk * ((C + 7) >> 3) + (j >> 3)) * D + d) * 8 + (j & 7);
+}
+
 __device__ __forceinline__ double wave_sum_f64(double v) {
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
     return v;

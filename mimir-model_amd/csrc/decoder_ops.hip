@@ -144,13 +144,6 @@ __global__ void rope_kernel(float* __restrict__ x, const int64_t* __restrict__ p
     }
 }
 
-// The key cache is [Hkv][C][D]. The value cache is blocked by eight keys:
-// value (kv head hk, key j, dim d) at ((hk*ceil(C/8) + j/8)*D + d)*8 + j%8,
-// so that one dim's eight consecutive keys are 16 contiguous bytes (f16) for
-// the weighted sum, which runs one chain per dim in key order.
-__host__ __device__ __forceinline__ int64_t vcache_at(int hk, int64_t j, int d, int D, int64_t C) {
-    return (((int64_t)hk * ((C + 7) >> 3) + (j >> 3)) * D + d) * 8 + (j & 7);
-}
 
 // k, v [T][Hkv][D] into the caches at the cache indices pos[t] (rounded to
 // f16 when the cache is f16).

@@ -113,7 +113,44 @@ struct FusedArgs {
     const float* scale;
     float eps;
     float* x_out;
+    // rope.v1 and the cache scatter in the epilogue (matrices q, k, v of a
+    // decoder layer at one row; rope_kv_kernel's pairs and steps): rows of q
+    // and k are dealt to workgroups in rotation pairs, so that a workgroup
+    // holds both rows of each pair it rotates
+    int rope;
+    const int64_t* pos;   // [1]
+    const int64_t* cidx;  // [1]
+    const double* inv_freq;
+    int D, rotary, interleaved, f16;
+    int64_t C;
+    void* kc;
+    void* vc;
 };
+
+// Row of local row r of tile `tile` of matrix mi: with rope (RD = the head
+// dim, 64 or 128; 0 without), q (mi 0) and k (mi 1) rows come in pairs:
+// local rows 2j, 2j+1 are rope_kv_kernel's dims (a, b) of pair
+// P = tile*R/2 + j (head P / (RD/2), pair P % (RD/2)); v and every matrix
+// without rope keep their rows in order.
+template <int RD>
+__device__ __forceinline__ int fused_row(const FusedArgs& A, int mi, int tile, int R, int r) {
+    if (RD == 0 || mi == 2) return tile * R + r;
+    constexpr int half = RD / 2;
+    const int h2 = A.rotary / 2;
+    const int P = tile * (R / 2) + (r >> 1), hh = P / half, i = P - hh * half;
+    int a, b;
+    if (A.interleaved) {
+        a = 2 * i;
+        b = a + 1;
+    } else if (i < h2) {
+        a = i;
+        b = i + h2;
+    } else {
+        a = A.rotary + 2 * (i - h2);
+        b = a + 1;
+    }
+    return hh * RD + ((r & 1) ? b : a);
+}
 
 // rms_norm.v1 of the row (rms_norm_kernel's order: thread t sums the float4s
 // t + 256k of x + resid, then the wave and workgroup sums), and the
@@ -268,9 +305,10 @@ __device__ __forceinline__ ActLane act_lane_lds(const QuantLds& Q, int b, int l)
 // are U rows of one block, whose activation is read from LDS once. Weights
 // are addressed as 32-bit offsets from the tile's base; the row flags and
 // bias are loaded first and looked at last.
-template <uint32_t DT, int U, bool SHARED, bool NORM>
-__device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F, int tile, uint8_t* smem,
+template <uint32_t DT, int U, bool SHARED, bool NORM, int RD>
+__device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F, int mi, int tile, uint8_t* smem,
                                            double* npart) {
+    constexpr bool ROPE = RD != 0;
     constexpr int BYTES = DT == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     const int nb = A.nb, R = F.R, np = R * nb;
     const int64_t K = A.K;
@@ -284,10 +322,13 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     i32x4* part = (i32x4*)(smem + ((K + nb * 4 + (K / 32) * 2 + (K / 16) * 2 + 15) & ~(int64_t)15));
     int* refl = (int*)(part + (size_t)R * nb);  // [R]: the row's weight is refused
     float* yl = (float*)(smem + (((size_t)((uint8_t*)(refl + R) - smem) + 15) & ~(size_t)15));  // NORM: [K] y
-    const int64_t tbyte = (int64_t)row0 * F.rb;
+    // rows as 32-bit offsets from the tile's first row (its lowest)
+    const int rbase = fused_row<RD>(A, mi, tile, R, 0);
+    const int64_t tbyte = (int64_t)rbase * F.rb;
     const uint8_t* Wt = F.W + (tbyte & ~(int64_t)3);
     const uint32_t tadj = (uint32_t)(tbyte & 3), rb32 = (uint32_t)F.rb;
     const int rlast = min(R, F.N - row0) - 1;
+    float* yr = (float*)(smem + (((size_t)((uint8_t*)(refl + R) - smem) + 15) & ~(size_t)15) + (NORM ? (size_t)K * 4 : 0));  // rope: [R]
 
     // 1. x (the first 16 blocks), the row flags and bias, then the first U
     // pairs' weights, all in flight; the load counter retires in order, so
@@ -297,7 +338,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     NormRegs N;
     if constexpr (NORM) norm_load(A, N);
     else load_x16(A.x, min(bq, nb - 1), j, xv);
-    const int frow = min(row0 + min(t, R - 1), F.N - 1);
+    const int frow = min(fused_row<RD>(A, mi, tile, R, min(t, R - 1)), F.N - 1);
     const int wr = F.wref[frow];
     const float bias = F.bias ? F.bias[frow] : 0.f;
     __builtin_amdgcn_sched_barrier(0);
@@ -315,7 +356,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
                 b = p / R;
                 r = min(p - b * R, rlast);
             }
-            const uint32_t off = tadj + (uint32_t)r * rb32 + (uint32_t)b * BYTES;
+            const uint32_t off = tadj + (uint32_t)(fused_row<RD>(A, mi, tile, R, r) - rbase) * rb32 + (uint32_t)b * BYTES;
             if constexpr (DT == DT_Q4_K) {
                 raw[u].hdr = *(const u32x4*)(Wt + off);
                 raw[u].qv = *(const u32x4*)(Wt + (off + 16 * l + 16));
@@ -340,6 +381,18 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
         }
     }
     const bool row_refused = __syncthreads_or(bad ? 1 : 0) != 0;
+
+    // (rope: the rotation of this thread's pair, while the weights arrive)
+    float rc = 1.f, rs = 0.f;
+    if (ROPE && mi != 2 && t < R / 2) {
+        constexpr int half = RD / 2;
+        const int P = tile * (R / 2) + t, i = P - (P / half) * half;
+        if (i < A.rotary / 2) {
+            const double ang = (double)A.pos[0] * A.inv_freq[i];
+            rc = (float)cos(ang);
+            rs = (float)sin(ang);
+        }
+    }
 
     // 3. Exact block sums of this workgroup's pairs.
     for (int p0 = 0; p0 < np; p0 += 32 * U) {
@@ -370,8 +423,8 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
 
     // 4. The serial float chain of each row, in block order.
     if (t < R) {
-        const int row = row0 + t;
-        if (row < F.N && wr == 0 && !row_refused) {
+        const int row = fused_row<RD>(A, mi, tile, R, t);
+        if (row0 + t < F.N && wr == 0 && !row_refused) {
             float tot = 0.f, off = 0.f;
             for (int b = 0; b < nb; b++) {
                 const i32x4 v = part[t * nb + b];
@@ -380,21 +433,65 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
             }
             float res = DT == DT_Q4_K ? tot - off : tot;
             if (F.bias) res += bias;
-            F.y[row] = res;
+            if (ROPE) yr[t] = res;
+            else F.y[row] = res;
         }
     }
     // 5. The float32 path for refused rows (fused order: one activation row).
     for (int r = g; r < R; r += 32) {
-        const int row = row0 + r;
-        if (row < F.N && (refl[r] != 0 || row_refused)) {
+        const int row = fused_row<RD>(A, mi, tile, R, r);
+        if (row0 + r < F.N && (refl[r] != 0 || row_refused)) {
             float res = f32dot_g8<DT>(F.W + (int64_t)row * F.rb, NORM ? (const float*)yl : A.x, K, true);
             if (F.bias) res += F.bias[row];
-            if (l == 0) F.y[row] = res;
+            if (l == 0) {
+                if (ROPE) yr[r] = res;
+                else F.y[row] = res;
+            }
+        }
+    }
+    if constexpr (!ROPE) return;
+    // 6. rope.v1 and the cache scatter (rope_kv_kernel's steps, T = 1): q
+    // rotated to y, k rotated and v to the caches at cidx[0].
+    __syncthreads();
+    const int64_t p = A.cidx[0];
+    if (mi == 2) {
+        const int row = row0 + t;
+        if (t < R && row < F.N && p >= 0 && p < A.C) {
+            const int hk = row / RD, dd = row - hk * RD;
+            const int64_t at = vcache_at(hk, p, dd, RD, A.C);
+            if (A.f16) ((_Float16*)A.vc)[at] = (_Float16)yr[t];
+            else ((float*)A.vc)[at] = yr[t];
+        }
+        return;
+    }
+    if (t < R / 2) {
+        constexpr int half = RD / 2;
+        const int P = tile * (R / 2) + t, hh = P / half, i = P - hh * half;
+        const int ra = fused_row<RD>(A, mi, tile, R, 2 * t), rbb = fused_row<RD>(A, mi, tile, R, 2 * t + 1);
+        float xa = yr[2 * t], xb = yr[2 * t + 1];
+        if (i < A.rotary / 2) {
+            const float x1 = xa, x2 = xb;
+            xa = x1 * rc - x2 * rs;
+            xb = x2 * rc + x1 * rs;
+        }
+        if (mi == 0) {
+            F.y[ra] = xa;
+            F.y[rbb] = xb;
+        } else if (p >= 0 && p < A.C) {
+            const int64_t at = ((int64_t)hh * A.C + p) * RD;
+            const int da = ra - hh * RD, db = rbb - hh * RD;
+            if (A.f16) {
+                ((_Float16*)A.kc)[at + da] = (_Float16)xa;
+                ((_Float16*)A.kc)[at + db] = (_Float16)xb;
+            } else {
+                ((float*)A.kc)[at + da] = xa;
+                ((float*)A.kc)[at + db] = xb;
+            }
         }
     }
 }
 
-template <int U, bool SHARED, bool NORM>
+template <int U, bool SHARED, bool NORM, int RD = 0>
 __global__ __launch_bounds__(256) void gemv_a8k_fused_kernel(FusedArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double npart[4];
@@ -403,14 +500,15 @@ __global__ __launch_bounds__(256) void gemv_a8k_fused_kernel(FusedArgs A) {
     if (A.nmat > 2 && (int)blockIdx.x >= A.mat[2].tile0) mi = 2;
     const FusedMat F = mi == 0 ? A.mat[0] : mi == 1 ? A.mat[1] : A.mat[2];
     const int tile = (int)blockIdx.x - F.tile0;
-    if (F.dt == DT_Q4_K) fused_body<DT_Q4_K, U, SHARED, NORM>(A, F, tile, smem, npart);
-    else fused_body<DT_Q6_K, U, SHARED, NORM>(A, F, tile, smem, npart);
+    if (F.dt == DT_Q4_K) fused_body<DT_Q4_K, U, SHARED, NORM, RD>(A, F, mi, tile, smem, npart);
+    else fused_body<DT_Q6_K, U, SHARED, NORM, RD>(A, F, mi, tile, smem, npart);
 }
 
 static size_t fused_lds_bytes(int64_t K, int nb, int maxR, bool norm = false) {
     size_t q = ((size_t)K + nb * 4 + (K / 32) * 2 + (K / 16) * 2 + 15) & ~(size_t)15;
     const size_t base = q + (size_t)maxR * nb * 16 + (size_t)maxR * 4;
-    return norm ? ((base + 15) & ~(size_t)15) + (size_t)K * 4 : base;
+    // (+ the rope epilogue's row values, [maxR] floats)
+    return ((base + 15) & ~(size_t)15) + (norm ? (size_t)K * 4 : 0) + (size_t)maxR * 4;
 }
 
 // Rows per workgroup for a matrix: pairs per workgroup at most 32*U*2 (two
@@ -433,7 +531,7 @@ bool fused_gemv_ok(const DevWeight* const* ws, int nmat) {
 
 static hipError_t launch_fused(const DevWeight* const* ws, int nmat, const float* x, const float* resid,
                                const float* scale, float eps, float* x_out, bool norm, const float* const* bias,
-                               float* const* y, hipStream_t stream) {
+                               float* const* y, hipStream_t stream, const FusedRope* rope = nullptr) {
     if (!fused_gemv_ok(ws, nmat)) return hipErrorInvalidValue;
     FusedArgs A;
     A.nmat = nmat;
@@ -442,6 +540,25 @@ static hipError_t launch_fused(const DevWeight* const* ws, int nmat, const float
     A.scale = scale;
     A.eps = eps;
     A.x_out = x_out;
+    A.rope = 0;
+    A.pos = A.cidx = nullptr;
+    A.inv_freq = nullptr;
+    A.D = A.rotary = A.interleaved = A.f16 = 0;
+    A.C = 0;
+    A.kc = A.vc = nullptr;
+    if (rope) {
+        A.rope = 1;
+        A.pos = rope->pos;
+        A.cidx = rope->cidx;
+        A.inv_freq = rope->inv_freq;
+        A.D = rope->d;
+        A.rotary = rope->rotary;
+        A.interleaved = rope->interleaved;
+        A.f16 = rope->f16;
+        A.C = rope->context;
+        A.kc = rope->kcache;
+        A.vc = rope->vcache;
+    }
     A.K = ws[0]->k;
     A.nb = (int)(A.K / 256);
     int tiles = 0, maxR = 1;
@@ -465,6 +582,14 @@ static hipError_t launch_fused(const DevWeight* const* ws, int nmat, const float
     const size_t lds = fused_lds_bytes(A.K, A.nb, maxR, norm);
     // every matrix has the same R (it depends on K only)
     const bool shared = A.mat[0].R % 4 == 0;
+    if (rope) {
+        if (!norm || !shared || (rope->d != 64 && rope->d != 128)) return hipErrorInvalidValue;
+        if (rope->d == 64)
+            hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, true, true, 64>), dim3(tiles), dim3(256), lds, stream, A);
+        else
+            hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, true, true, 128>), dim3(tiles), dim3(256), lds, stream, A);
+        return hipGetLastError();
+    }
     if (norm && shared)
         hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, true, true>), dim3(tiles), dim3(256), lds, stream, A);
     else if (norm)
@@ -492,6 +617,24 @@ hipError_t launch_gemv_a8k_fused_norm(const DevWeight* const* ws, int nmat, cons
                                       float* const* y, hipStream_t stream) {
     if (!fused_norm_ok(ws, nmat) || !x_out) return hipErrorInvalidValue;
     return launch_fused(ws, nmat, x, resid, scale, eps, x_out, true, bias, y, stream);
+}
+
+// q, k, v with rope and the cache scatter in the epilogue: each workgroup's
+// rows must be whole rotation pairs of one head.
+bool fused_norm_rope_ok(const DevWeight* const* ws, int heads, int kv_heads, int d, int rotary) {
+    if (!fused_norm_ok(ws, 3) || (d != 64 && d != 128) || rotary <= 0 || rotary % 2 || rotary > d) return false;
+    const int64_t K = ws[0]->k;
+    const int R = fused_rows((int)(K / 256), K);
+    if (R % 4 || (d / 2) % (R / 2)) return false;
+    return ws[0]->n == (int64_t)heads * d && ws[1]->n == (int64_t)kv_heads * d && ws[2]->n == (int64_t)kv_heads * d;
+}
+
+hipError_t launch_gemv_a8k_fused_norm_rope(const DevWeight* const* ws, const float* x, const float* resid,
+                                           const float* scale, float eps, float* x_out, const float* const* bias,
+                                           float* q, const FusedRope& rope, hipStream_t stream) {
+    if (!fused_norm_rope_ok(ws, rope.heads, rope.kv_heads, rope.d, rope.rotary) || !x_out) return hipErrorInvalidValue;
+    float* y[3] = {q, nullptr, nullptr};
+    return launch_fused(ws, 3, x, resid, scale, eps, x_out, true, bias, y, stream, &rope);
 }
 
 }  // namespace mimg

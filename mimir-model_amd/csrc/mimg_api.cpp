@@ -953,6 +953,62 @@ int mimg_rms_norm_linear_a8_group_dev(const uint64_t* whs, int count, const floa
     return MIMG_OK;
 }
 
+int mimg_rms_norm_qkv_rope_kv_dev(const uint64_t* whs, const float* x, const float* resid, const float* scale,
+                                  float eps, float* x_out, const float* const* bias, float* q, const int64_t* pos,
+                                  const int64_t* cache_index, const double* inv_freq, int heads, int kv_heads, int d,
+                                  int rotary, int interleaved, int64_t context, void* kcache, void* vcache, int f16,
+                                  void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!whs || !x || !x_out || !q || !pos || !cache_index || !inv_freq || !kcache || !vcache)
+        return fail(MIMG_ERR_ARG, "null pointer");
+    if (!aligned(x, 16) || !aligned(x_out, 16) || (resid && !aligned(resid, 16)) || (scale && !aligned(scale, 16)))
+        return fail(MIMG_ERR_ARG, "x, x_out, resid and scale must be 16-byte aligned");
+    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads || d <= 0 || d % 2 || d > 1024 || rotary <= 0 || rotary % 2 ||
+        rotary > d || context <= 0)
+        return fail(MIMG_ERR_ARG, "rope: heads %d, kv heads %d, D %d, rotary %d, context %lld", heads, kv_heads, d,
+                    rotary, (long long)context);
+    Held held[3];
+    const DevWeight* dw[3];
+    for (int i = 0; i < 3; i++) {
+        if ((rc = held[i].acquire(whs[i]))) return rc;
+        Weight* w = held[i].get();
+        if (w->dw.k != held[0].get()->dw.k) return fail(MIMG_ERR_ARG, "q, k and v must share K");
+        bool use_f32;
+        if ((rc = a8_checks(w, 1, 256, &use_f32))) return rc;
+        if (use_f32) return fail(MIMG_NOT_HANDLED, "%s has no 8-bit kernel for blocks of 256", dt_name(w->dw.dt));
+        dw[i] = &w->dw;
+    }
+    const int64_t K = dw[0]->k;
+    const uint64_t xb = (uint64_t)K * 4, qb = (uint64_t)dw[0]->n * 4;
+    auto overlap = [](const void* a, uint64_t la, const void* b, uint64_t lb) {
+        return a && b && (uintptr_t)a < (uintptr_t)b + lb && (uintptr_t)b < (uintptr_t)a + la;
+    };
+    if (overlap(x_out, xb, x, xb) || overlap(x_out, xb, resid, xb) || overlap(x_out, xb, scale, xb))
+        return fail(MIMG_ERR_ARG, "x_out must not overlap x, resid or scale (every workgroup reads them)");
+    if (overlap(q, qb, x, xb) || overlap(q, qb, resid, xb) || overlap(q, qb, scale, xb) || overlap(q, qb, x_out, xb))
+        return fail(MIMG_ERR_ARG, "q overlaps x, resid, scale or x_out");
+    if ((int64_t)heads * d + 2 * (int64_t)kv_heads * d > fused_max_n() ||
+        !fused_norm_rope_ok(dw, heads, kv_heads, d, rotary))
+        return fail(MIMG_NOT_HANDLED, "no fused norm + q/k/v + rope launch for K %lld, D %d", (long long)K, d);
+    const float* bs[3] = {bias ? bias[0] : nullptr, bias ? bias[1] : nullptr, bias ? bias[2] : nullptr};
+    FusedRope r;
+    r.pos = pos;
+    r.cidx = cache_index;
+    r.inv_freq = inv_freq;
+    r.heads = heads;
+    r.kv_heads = kv_heads;
+    r.d = d;
+    r.rotary = rotary;
+    r.interleaved = interleaved;
+    r.f16 = f16;
+    r.context = context;
+    r.kcache = kcache;
+    r.vcache = vcache;
+    HIP_TRY(launch_gemv_a8k_fused_norm_rope(dw, x, resid, scale, eps, x_out, bs, q, r, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
 int mimg_dequantize_dev(uint32_t dtype, const void* src, uint64_t len, float* dst, int64_t n, void* stream) {
     int rc = ensure_device();
     if (rc) return rc;

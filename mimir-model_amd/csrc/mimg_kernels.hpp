@@ -101,6 +101,20 @@ bool fused_norm_ok(const DevWeight* const* ws, int nmat);
 hipError_t launch_gemv_a8k_fused_norm(const DevWeight* const* ws, int nmat, const float* x, const float* resid,
                                       const float* scale, float eps, float* x_out, const float* const* bias,
                                       float* const* y, hipStream_t stream);
+// The rope.v1 + cache scatter epilogue of the fused q/k/v GEMV at one row.
+struct FusedRope {
+    const int64_t* pos;
+    const int64_t* cidx;
+    const double* inv_freq;
+    int heads, kv_heads, d, rotary, interleaved, f16;
+    int64_t context;
+    void* kcache;
+    void* vcache;
+};
+bool fused_norm_rope_ok(const DevWeight* const* ws, int heads, int kv_heads, int d, int rotary);
+hipError_t launch_gemv_a8k_fused_norm_rope(const DevWeight* const* ws, const float* x, const float* resid,
+                                           const float* scale, float eps, float* x_out, const float* const* bias,
+                                           float* q, const FusedRope& rope, hipStream_t stream);
 
 // Many activation rows (quantized in blocks of 32) against one Q8_0 matrix
 // with K a multiple of 256, on the int8 matrix cores (gemm_q8_0.hip): exact

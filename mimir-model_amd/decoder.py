@@ -113,7 +113,7 @@ class Decoder:
     """
 
     def __init__(self, config, tensors, a8=True, cache_f16=False, max_rows=64, slots=1, procs=16, kquant_block=256,
-                 f32_tile_rows=0):
+                 f32_tile_rows=0, fuse_rope=True):
         c = self.c = config if isinstance(config, Config) else Config(**config)
         self.a8, self.f16, self.slots = bool(a8), bool(cache_f16), int(slots)
         # activation blocks for Q4_K/Q6_K weights: 256 is dequant_matmul_a8.v2
@@ -156,6 +156,9 @@ class Decoder:
         self.x_pair = (self.x, B(E * 4))
         self.x_alt = self.x_pair[1]
         self.norm_fused = {}  # names -> whether the fused norm GEMV takes them
+        # one row: norm, q/k/v, rope and the cache scatter in one launch
+        # (until the library answers NotHandled for the shape)
+        self.rope_fused = bool(fuse_rope)
         self.q, self.o = B(R * H * D * 4), B(R * H * D * 4)
         self.k, self.v = B(R * Hkv * D * 4), B(R * Hkv * D * 4)
         self.g, self.u, self.sw = B(R * F * 4), B(R * F * 4), B(R * F * 4)
@@ -207,7 +210,7 @@ class Decoder:
         ws = [self.w[n] for n in names]
         blocks = {self._block(w) for w in ws}
         key = tuple(names)
-        if self.a8 and single_fused and T == 1 and self.norm_fused.get(key, True):
+        if self.a8 and single_fused and T == 1 and blocks == {256} and self.norm_fused.get(key, True):
             # one launch: x + resid into the other x buffer, the norm and the
             # q/k/v products (NotHandled: launched nothing, shape not taken)
             bs = [None if b is None or b not in self.vec else self.vec[b].ptr for b in (biases or [None] * len(names))]
@@ -230,6 +233,28 @@ class Decoder:
         mimg.rms_norm_dev(self.x.ptr, resid, self.vec[norm].ptr, c.norm_eps, T, E, self.h.ptr, s)
         self._linears(names, self.h.ptr, T, ys, biases)
 
+    def _norm_qkv_rope(self, l, resid, qkv, qkv_b, pos, cidx):
+        """At one row with 8-bit activations: the attention norm, the q/k/v
+        products, rope and the cache scatter in one launch (x + resid lands in
+        the other x buffer). False where that launch does not take the shape
+        (nothing launched): the caller makes the separate calls."""
+        if not self.a8 or not self.rope_fused or any(self._block(self.w[n]) != 256 for n in qkv):
+            return False
+        c, s = self.c, self.stream.handle
+        p = f"blk.{l}."
+        bs = [None if b is None or b not in self.vec else self.vec[b].ptr for b in qkv_b]
+        try:
+            mimg.rms_norm_qkv_rope_kv_dev([self.w[n] for n in qkv], self.x.ptr, resid,
+                                          self.vec[p + "attn_norm.weight"].ptr, c.norm_eps, self.x_alt.ptr,
+                                          bs if any(bs) else None, self.q.ptr, pos, cidx, self.invf.ptr, c.heads,
+                                          c.kv_heads, c.head_dim, c.rope_dims, c.interleaved, self.cache_len,
+                                          self.kc[l].ptr, self.vc[l].ptr, self.f16, s)
+        except mimg.NotHandled:
+            self.rope_fused = False
+            return False
+        self.x, self.x_alt = self.x_alt, self.x
+        return True
+
     def _forward(self, T, ids=None, pos=None, cidx=None, kstart=None, head_rows=None):
         """Enqueues the forward pass of T rows (device arrays of token ids,
         positions, cache indices and slot starts; by default the decoder's
@@ -249,10 +274,12 @@ class Decoder:
             p = f"blk.{l}."
             qkv = [p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"]
             qkv_b = [p + "attn_q.bias", p + "attn_k.bias", p + "attn_v.bias"]
-            self._norm_linears(resid, p + "attn_norm.weight", T, qkv, [self.q.ptr, self.k.ptr, self.v.ptr], qkv_b,
-                               single_fused=True)
-            mimg.rope_kv_dev(self.q.ptr, self.k.ptr, self.v.ptr, pos, cidx, self.invf.ptr, T, H, Hkv, D, c.rope_dims,
-                             c.interleaved, self.cache_len, self.kc[l].ptr, self.vc[l].ptr, self.f16, s)
+            if not (T == 1 and self._norm_qkv_rope(l, resid, qkv, qkv_b, pos, cidx)):
+                self._norm_linears(resid, p + "attn_norm.weight", T, qkv, [self.q.ptr, self.k.ptr, self.v.ptr], qkv_b,
+                                   single_fused=True)
+                mimg.rope_kv_dev(self.q.ptr, self.k.ptr, self.v.ptr, pos, cidx, self.invf.ptr, T, H, Hkv, D,
+                                 c.rope_dims, c.interleaved, self.cache_len, self.kc[l].ptr, self.vc[l].ptr, self.f16,
+                                 s)
             mimg.attention_dev(self.q.ptr, self.kc[l].ptr, self.vc[l].ptr, cidx, kstart, T, H, Hkv, D,
                                self.cache_len, c.context, self.f16, self.o.ptr, self.att_ws.ptr, self.att_ws_bytes, s)
             self._linears([p + "attn_output.weight"], self.o.ptr, T, [self.ao.ptr])

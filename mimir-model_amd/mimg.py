@@ -47,6 +47,8 @@ SIGNATURES = {
                                       ctypes.POINTER(_P), _P, _U64, _P]),
     "mimg_rms_norm_linear_a8_group_dev": (_I, [ctypes.POINTER(_U64), _I, _P, _P, _P, ctypes.c_float, _P,
                                                ctypes.POINTER(_P), ctypes.POINTER(_P), _P]),
+    "mimg_rms_norm_qkv_rope_kv_dev": (_I, [ctypes.POINTER(_U64), _P, _P, _P, ctypes.c_float, _P, ctypes.POINTER(_P),
+                                           _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _P, _P, _I, _P]),
     "mimg_matmul_a8_quantized_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P, _U64, _P]),
     "mimg_linear_f32_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
     "mimg_linear_f32_mfma_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
@@ -263,6 +265,20 @@ def rms_norm_linear_a8_group_dev(weights, x_ptr, resid_ptr, scale_ptr, eps, x_ou
     bs = None if bias_ptrs is None else (_P * n)(*[_P(p) if p else None for p in bias_ptrs])
     _check(load().mimg_rms_norm_linear_a8_group_dev(hs, n, _P(x_ptr), _o(resid_ptr), _o(scale_ptr), eps,
                                                     _P(x_out_ptr), bs, ys, _P(stream)))
+
+
+def rms_norm_qkv_rope_kv_dev(weights, x_ptr, resid_ptr, scale_ptr, eps, x_out_ptr, bias_ptrs, q_ptr, pos_ptr,
+                             cidx_ptr, inv_freq_ptr, heads, kv_heads, d, rotary, interleaved, context, kc_ptr, vc_ptr,
+                             f16, stream):
+    """One row: rms_norm_linear_a8_group_dev on (q, k, v) then rope_kv_dev,
+    in one launch (k and v go to the caches only); raises NotHandled where
+    the fused launch does not apply (then make the two calls)."""
+    hs = (_U64 * 3)(*[w.handle for w in weights])
+    bs = None if bias_ptrs is None else (_P * 3)(*[_P(p) if p else None for p in bias_ptrs])
+    _check(load().mimg_rms_norm_qkv_rope_kv_dev(hs, _P(x_ptr), _o(resid_ptr), _o(scale_ptr), eps, _P(x_out_ptr), bs,
+                                                _P(q_ptr), _P(pos_ptr), _P(cidx_ptr), _P(inv_freq_ptr), heads,
+                                                kv_heads, d, rotary, int(interleaved), context, _P(kc_ptr),
+                                                _P(vc_ptr), int(f16), _P(stream)))
 
 
 def matmul_a8_quantized_dev(w, x_ptr, rows, bias_ptr, block, y_ptr, ws_ptr, ws_bytes, stream):

@@ -529,6 +529,98 @@ def test_rms_norm_linear_group_equals_two_calls(gpu, oracle, rt, name):
         w.release()
 
 
+_ROPE_QKV = {
+    # K, heads, kv heads, D, rotary, interleaved, f16 cache, context, cache index, case
+    "llama8b": (4096, 32, 8, 128, 128, True, True, 40, 37, None),
+    "llama1b_f32": (2048, 32, 8, 64, 64, True, False, 24, 5, None),
+    "qwen2_halves_bias": (1024, 8, 2, 128, 128, False, True, 16, 15, "bias"),
+    "partial_rotary": (1024, 16, 4, 64, 32, False, False, 16, 0, None),
+    "refused_row": (1024, 8, 8, 128, 128, True, True, 16, 9, "huge"),
+    "outside_cache": (1024, 16, 4, 64, 64, True, True, 16, 16, "outside_cache"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(_ROPE_QKV))
+def test_rms_norm_qkv_rope_kv_equals_separate_calls(gpu, oracle, rt, name):
+    """The attention norm, q/k/v products, rope and the cache scatter in one
+    launch at one row: q, both caches (every entry) and x_out bit for bit
+    rms_norm_linear_a8_group_dev then rope_kv_dev, for llama (adjacent
+    pairs) and qwen2 (halves) rotation, a partial rotary span, biases, f16
+    and f32 caches, a refused activation row (float32 path) and a cache
+    index outside the cache (nothing stored)."""
+    K, H, Hkv, D, rot, inter, f16, C, p, case = _ROPE_QKV[name]
+    rng = np.random.default_rng(K + H + D)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    r = rng.standard_normal((1, K)).astype(np.float32)
+    sc = rng.standard_normal(K).astype(np.float32)
+    if case == "huge":
+        sc[101] = np.float32(1e30)
+    specs = [(Q4_K, H * D), (Q4_K, Hkv * D), (Q6_K, Hkv * D)]
+    W = [gpu.Weight(oracle.synthetic_weight(dt, n, K, seed=60 + i), dt, n, K) for i, (dt, n) in enumerate(specs)]
+    bias = [rng.standard_normal(n).astype(np.float32) if case == "bias" else None for _, n in specs]
+    dbs = [dev(rt, b) if b is not None else None for b in bias]
+    bptrs = [b.ptr if b else 0 for b in dbs]
+    inv = (1.0 / (10000.0 ** (np.arange(0, rot, 2, dtype=np.float64) / rot))).astype(np.float64)
+    dinv = dev(rt, inv)
+    dpos, dcidx = dev(rt, np.array([p + 3], np.int64)), dev(rt, np.array([p], np.int64))
+    esz = 2 if f16 else 4
+    kbytes, vbytes = Hkv * C * D * esz, Hkv * gpu.vcache_len(C) * D * esz
+    init_k = rng.integers(0, 255, kbytes, dtype=np.uint8)
+    init_v = rng.integers(0, 255, vbytes, dtype=np.uint8)
+    s = rt.Stream()
+    dsc, dr = dev(rt, sc), dev(rt, r)
+
+    # fused
+    dx, xo, dq = dev(rt, x), rt.DeviceBuffer(K * 4), rt.DeviceBuffer(H * D * 4)
+    kc, vc = dev(rt, init_k), dev(rt, init_v)
+    gpu.rms_norm_qkv_rope_kv_dev(W, dx.ptr, dr.ptr, dsc.ptr, 1e-5, xo.ptr, bptrs if case == "bias" else None, dq.ptr,
+                                 dpos.ptr, dcidx.ptr, dinv.ptr, H, Hkv, D, rot, inter, C, kc.ptr, vc.ptr, f16,
+                                 s.handle)
+    s.sync()
+    got = (xo.download(np.float32), dq.download(np.float32), kc.download(np.uint8), vc.download(np.uint8))
+
+    # the two calls
+    dx2, xo2 = dev(rt, x), rt.DeviceBuffer(K * 4)
+    ys = [rt.DeviceBuffer(n * 4) for _, n in specs]
+    kc2, vc2 = dev(rt, init_k), dev(rt, init_v)
+    gpu.rms_norm_linear_a8_group_dev(W, dx2.ptr, dr.ptr, dsc.ptr, 1e-5, xo2.ptr, bptrs if case == "bias" else None,
+                                     [y.ptr for y in ys], s.handle)
+    gpu.rope_kv_dev(ys[0].ptr, ys[1].ptr, ys[2].ptr, dpos.ptr, dcidx.ptr, dinv.ptr, 1, H, Hkv, D, rot, inter, C,
+                    kc2.ptr, vc2.ptr, f16, s.handle)
+    s.sync()
+    want = (xo2.download(np.float32), ys[0].download(np.float32), kc2.download(np.uint8), vc2.download(np.uint8))
+    assert np.array_equal(got[0].view(np.uint32), want[0].view(np.uint32))
+    assert np.array_equal(got[1].view(np.uint32), want[1].view(np.uint32)), np.flatnonzero(got[1] != want[1])[:8]
+    assert np.array_equal(got[2], want[2])
+    assert np.array_equal(got[3], want[3])
+    if case == "outside_cache":
+        assert np.array_equal(got[2], init_k) and np.array_equal(got[3], init_v)
+    else:
+        assert not np.array_equal(got[2], init_k) and not np.array_equal(got[3], init_v)
+    for w in W:
+        w.release()
+
+
+def test_rms_norm_qkv_rope_kv_not_handled(gpu, oracle, rt):
+    """Shapes the fused rope launch does not take are refused before any
+    launch: q/k/v rows that are not heads*d, kv_heads*d, kv_heads*d, and a
+    head whose rotation pairs would split unevenly over workgroups."""
+    s = rt.Stream()
+    K = 1024
+    W = [gpu.Weight(oracle.synthetic_weight(Q4_K, n, K, seed=7), Q4_K, n, K) for n in (512, 128, 128)]
+    dx, xo, dq = rt.DeviceBuffer(K * 4), rt.DeviceBuffer(K * 4), rt.DeviceBuffer(512 * 4)
+    p = dev(rt, np.zeros(1, np.int64))
+    inv = dev(rt, np.ones(32, np.float64))
+    kc, vc = rt.DeviceBuffer(1 << 16), rt.DeviceBuffer(1 << 16)
+    # (K = 1024: 32 rows, 16 rotation pairs, per workgroup)
+    for H, Hkv, D in ((8, 2, 32), (32, 8, 16)):
+        with pytest.raises(gpu.NotHandled):
+            gpu.rms_norm_qkv_rope_kv_dev(W, dx.ptr, None, None, 1e-5, xo.ptr, None, dq.ptr, p.ptr, p.ptr, inv.ptr, H,
+                                         Hkv, D, D, True, 8, kc.ptr, vc.ptr, True, s.handle)
+    for w in W:
+        w.release()
+
+
 def test_rms_norm_linear_group_not_handled(gpu, oracle, rt):
     """Shapes the fused norm GEMV does not take are refused before any launch
     (NotHandled: the caller makes the two calls), and an x_out that overlaps
@@ -813,6 +905,8 @@ def test_block32_a8_graph_matches_the_restatement(gpu, name):
         ids_r.append(llama_ref.argmax(lg_r))
         lg_g = dec.forward([ids_g[-1]], [P + i])[0]
         lg_r = ref.forward([ids_r[-1]], [P + i])[0]
+        # one-row steps too take blocks of 32 (no block-256 one-row launch)
+        assert np.max(np.abs(lg_g - lg_r)) <= 1e-5 * np.max(np.abs(lg_r))
     assert ids_g == ids_r
     del dec
     _release(g, sec, tensors, gpu)
