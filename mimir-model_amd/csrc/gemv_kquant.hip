@@ -32,6 +32,7 @@
 // Rows of x the quantizer refused and rows of w with a non-finite block scale
 // take the float32 path (reference linearA8, interp/fast.go:323-377), in the
 // reference's AVX2 order (f32path.hpp).
+#include "decoder_math.hpp"
 #include "f32path.hpp"
 #include "kquant_lane.hpp"
 #include "mimg_device.hpp"
@@ -67,6 +68,10 @@ struct GemvArgs {
     int fused;            // float32 fallback order: total rows <= 8
     PairMat mat[3];
     int nmat;
+    // swiglu in the epilogue (one row; mat[0] gate, mat[1] up): out[n] =
+    // swiglu.v1 of (gate row n, up row n) with the reference's pieces
+    float* sw;
+    int64_t sw_total, sw_chunk;
 };
 
 template <uint32_t DT>
@@ -108,16 +113,21 @@ __device__ __forceinline__ void quad_of(int pb, int nb, int& b, int& r0) {
 // weights: the load counter being in order, anything issued after the
 // weights would wait for all of them. Every load is unconditional (clamped
 // in bounds) in straight-line code, and every loaded pair is consumed.
-template <uint32_t DT, int M, int R>
+// SW (swiglu epilogue, M = 1, R = 2U): local rows 0..U-1 are gate rows
+// tile*U.., rows U..2U-1 the same rows of up; a quad of U rows is one
+// matrix's, so each quad loads from its matrix's tile base. The rows'
+// results meet in LDS and out[n] = swiglu(gate[n], up[n]) is written.
+template <uint32_t DT, int M, int R, bool SW = false>
 __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
     constexpr int U = MIMG_PAIRS_U;
     constexpr bool SHARED = R % U == 0;  // a group's U pairs share one block
     constexpr bool PRE = M == 1;         // activation loaded before the weights
+    static_assert(!SW || (M == 1 && R == 2 * U && SHARED), "swiglu epilogue: one row, a gate and an up quad");
     // This workgroup's matrix of the launch.
     int mi = 0;
-    if (A.nmat > 1 && (int)blockIdx.x >= A.mat[1].tile0) mi = 1;
-    if (A.nmat > 2 && (int)blockIdx.x >= A.mat[2].tile0) mi = 2;
+    if (!SW && A.nmat > 1 && (int)blockIdx.x >= A.mat[1].tile0) mi = 1;
+    if (!SW && A.nmat > 2 && (int)blockIdx.x >= A.mat[2].tile0) mi = 2;
     const PairMat P = mi == 0 ? A.mat[0] : mi == 1 ? A.mat[1] : A.mat[2];
     A.W = P.W;
     A.wref = P.wref;
@@ -126,13 +136,14 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
     A.N = P.N;
     A.y_stride = P.N;
     const int g = threadIdx.x >> 3, l = threadIdx.x & 7, t = threadIdx.x;
-    const int nb = A.nb, row0 = ((int)blockIdx.x - P.tile0) * R, npairs = R * nb;
+    const int nb = A.nb, row0 = ((int)blockIdx.x - P.tile0) * (SW ? U : R), npairs = R * nb;
     // The tile's R rows: a 4-byte-aligned base (Q6_K rows are 2-byte
-    // aligned) and 32-bit offsets from it.
+    // aligned) and 32-bit offsets from it (SW: the U rows of each matrix).
     const int64_t tbyte = (int64_t)row0 * A.rb;
     const uint8_t* Wt = A.W + (tbyte & ~(int64_t)3);
     const uint32_t tadj = (uint32_t)(tbyte & 3), rb32 = (uint32_t)A.rb;
-    const int rlast = min(R, A.N - row0) - 1;        // last row of the tile in the matrix
+    const uint8_t* Wt1 = SW ? A.mat[1].W + (tbyte & ~(int64_t)3) : Wt;
+    const int rlast = SW ? R - 1 : min(R, A.N - row0) - 1;  // last row of the tile in the matrix
     i32x4* part = (i32x4*)smem;                                 // [R][nb][M]: S, M term, bits(d*dx), bits(dmin*dx)
     int* refused = (int*)(smem + (size_t)R * nb * M * 16);      // [R*M]: the pair takes the float32 path
 
@@ -142,9 +153,12 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
     // wait for them before the weights are requested).
     int fm = min(t, R * M - 1) % M;
     asm volatile("v_mov_b32 %0, %1" : "=v"(fm) : "v"(fm));  // a vector index: ok[] through the vector cache
-    const int frow = min(row0 + min(t, R * M - 1) / M, A.N - 1);
-    const int wr = A.wref[frow], okm = A.ok[fm];
-    const float bias = A.bias ? A.bias[frow] : 0.f;
+    const int fr = min(t, R * M - 1) / M;
+    const PairMat& FM = SW && fr >= U ? A.mat[1] : A.mat[0];
+    const int frow = SW ? row0 + (fr & (U - 1)) : min(row0 + fr, A.N - 1);
+    const int wr = SW ? FM.wref[frow] : A.wref[frow], okm = A.ok[fm];
+    const float* fbias = SW ? FM.bias : A.bias;
+    const float bias = fbias ? fbias[frow] : 0.f;
     __builtin_amdgcn_sched_barrier(0);
 
     for (int p0 = 0; p0 < npairs; p0 += 32 * U) {
@@ -178,12 +192,13 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
                 b = p / R;
                 r = min(p - b * R, rlast);
             }
-            const uint32_t off = tadj + (uint32_t)r * rb32 + (uint32_t)b * KQ<DT>::BYTES;
+            const uint8_t* Wb = SW && r >= U ? Wt1 : Wt;
+            const uint32_t off = tadj + (uint32_t)(SW ? (r & (U - 1)) : r) * rb32 + (uint32_t)b * KQ<DT>::BYTES;
             if constexpr (DT == DT_Q4_K) {
-                hdr[u] = *(const u32x4*)(Wt + off);
-                qv[u] = *(const u32x4*)(Wt + (off + 16 * l + 16));
+                hdr[u] = *(const u32x4*)(Wb + off);
+                qv[u] = *(const u32x4*)(Wb + (off + 16 * l + 16));
             } else {
-                raw[u] = q6k_load_at(Wt, off, l);
+                raw[u] = q6k_load_at(Wb, off, l);
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -238,8 +253,9 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
     __syncthreads();
 
     // The serial float chain, one lane per (weight row, activation row).
+    float* yr = (float*)(refused + R * M);  // SW: [R] the rows' results
     if (t < R * M) {
-        const int r = t / M, m = t - r * M, row = row0 + r;
+        const int r = t / M, m = t - r * M, row = SW ? row0 + (r & (U - 1)) : row0 + r;
         if (row < A.N && !flag) {
             float tot = 0.f, off = 0.f;
             for (int b = 0; b < nb; b++) {
@@ -248,19 +264,42 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
                 if (DT == DT_Q4_K) off = __builtin_fmaf((float)v.y, __int_as_float(v.w), off);
             }
             float res = DT == DT_Q4_K ? tot - off : tot;
-            if (A.bias) res += bias;
-            A.y[(int64_t)m * A.y_stride + row] = res;
+            if (fbias) res += bias;
+            if (SW) yr[r] = res;
+            else A.y[(int64_t)m * A.y_stride + row] = res;
         }
     }
     // The float32 path for refused pairs, one group of eight lanes per pair.
     for (int qq = g; qq < R * M; qq += 32) {
-        const int r = qq / M, m = qq - r * M, row = row0 + r;
+        const int r = qq / M, m = qq - r * M, row = SW ? row0 + (r & (U - 1)) : row0 + r;
         if (row < A.N && refused[qq]) {
-            float res = f32dot_g8<DT>(A.W + (int64_t)row * A.rb, A.x + (int64_t)m * A.K, A.K, A.fused != 0);
-            if (A.bias) res += A.bias[row];
-            if (l == 0) A.y[(int64_t)m * A.y_stride + row] = res;
+            const PairMat& RM = SW && r >= U ? A.mat[1] : A.mat[0];
+            const uint8_t* Wr = SW ? RM.W : A.W;
+            const float* br = SW ? RM.bias : A.bias;
+            float res = f32dot_g8<DT>(Wr + (int64_t)row * A.rb, A.x + (int64_t)m * A.K, A.K, A.fused != 0);
+            if (br) res += br[row];
+            if (l == 0) {
+                if (SW) yr[r] = res;
+                else A.y[(int64_t)m * A.y_stride + row] = res;
+            }
         }
     }
+    if constexpr (SW) {
+        // swiglu.v1 of (gate, up) row n: the reference's SiluMulF32 on its pieces
+        __syncthreads();
+        const int n = row0 + t;
+        if (t < U && n < A.N) A.sw[n] = swiglu_at(yr[t], yr[t + U], n, A.sw_total, A.sw_chunk);
+    }
+}
+
+// gate and up at one row with swiglu in the epilogue (Q4_K, N % U == 0).
+static hipError_t launch_pairs_swiglu(GemvArgs A, hipStream_t stream) {
+    constexpr int U = MIMG_PAIRS_U, R = 2 * U;
+    A.mat[0].tile0 = A.mat[1].tile0 = 0;
+    const int tiles = A.N / U;
+    const size_t lds = (size_t)R * A.nb * 16 + (size_t)R * 4 + (size_t)R * 4;
+    hipLaunchKernelGGL((gemv_a8k_pairs_kernel<DT_Q4_K, 1, R, true>), dim3((unsigned)tiles), dim3(256), lds, stream, A);
+    return hipGetLastError();
 }
 
 template <uint32_t DT, int M, int R>
@@ -313,6 +352,48 @@ static hipError_t launch_dt(GemvArgs A, int rows, hipStream_t stream) {
     return hipErrorInvalidValue;
 }
 
+bool gemv_swiglu_ok(const DevWeight& gate, const DevWeight& up) {
+    return gate.dt == DT_Q4_K && up.dt == DT_Q4_K && gate.n == up.n && gate.k == up.k && gate.k % 256 == 0 &&
+           gate.n % MIMG_PAIRS_U == 0 && gate.k <= 16384 && gate.n <= (1 << 30);
+}
+
+hipError_t launch_gemv_a8k_swiglu(const DevWeight& gate, const DevWeight& up, const ActPtrs& a, const float* x,
+                                  const float* const* bias, float* out, int64_t total, int64_t chunk,
+                                  hipStream_t stream) {
+    if (!gemv_swiglu_ok(gate, up)) return hipErrorInvalidValue;
+    GemvArgs A;
+    A.W = gate.data;
+    A.rb = gate.row_bytes;
+    A.N = (int)gate.n;
+    A.nb = (int)(gate.k / 256);
+    A.K = gate.k;
+    A.q = a.q;
+    A.d32 = a.d32;
+    A.s16 = a.xs;
+    A.ok = a.ok;
+    A.wref = gate.wref;
+    A.x = x;
+    A.bias = bias ? bias[0] : nullptr;
+    A.y = nullptr;
+    A.y_stride = gate.n;
+    A.fused = 1;
+    A.nmat = 2;
+    const DevWeight* w2[2] = {&gate, &up};
+    for (int i = 0; i < 3; i++) {
+        const DevWeight& wi = *w2[i < 2 ? i : 0];
+        A.mat[i].W = wi.data;
+        A.mat[i].wref = wi.wref;
+        A.mat[i].bias = i < 2 && bias ? bias[i] : nullptr;
+        A.mat[i].y = nullptr;
+        A.mat[i].N = (int)wi.n;
+        A.mat[i].tile0 = 0;
+    }
+    A.sw = out;
+    A.sw_total = total;
+    A.sw_chunk = chunk;
+    return launch_pairs_swiglu(A, stream);
+}
+
 hipError_t launch_gemv_a8k(const DevWeight* const* ws, int nmat, const ActPtrs& a, int64_t rows,
                            int64_t total_rows, const float* x, const float* const* bias, float* const* y,
                            hipStream_t stream) {
@@ -338,6 +419,8 @@ hipError_t launch_gemv_a8k(const DevWeight* const* ws, int nmat, const ActPtrs& 
     A.y_stride = w.n;
     A.fused = total_rows <= 8;
     A.nmat = nmat;
+    A.sw = nullptr;
+    A.sw_total = A.sw_chunk = 0;
     for (int i = 0; i < 3; i++) {
         const DevWeight& wi = *ws[i < nmat ? i : 0];
         A.mat[i].W = wi.data;

@@ -953,6 +953,46 @@ int mimg_rms_norm_linear_a8_group_dev(const uint64_t* whs, int count, const floa
     return MIMG_OK;
 }
 
+int mimg_matmul_a8_quantized_swiglu_dev(const uint64_t* whs, const float* x, int64_t rows, const float* const* bias,
+                                        int block, float* out, int procs, const void* ws, uint64_t ws_bytes,
+                                        void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!whs || !out) return fail(MIMG_ERR_ARG, "null pointer");
+    Held held[2];
+    const Weight* w[2];
+    for (int i = 0; i < 2; i++) {
+        if ((rc = held[i].acquire(whs[i]))) return rc;
+        Weight* wi = held[i].get();
+        bool use_f32;
+        if ((rc = a8_checks(wi, rows, block, &use_f32))) return rc;
+        if (use_f32) return fail(MIMG_ERR_ARG, "%s has no 8-bit kernel for blocks of %d", dt_name(wi->dw.dt), block);
+        w[i] = wi;
+    }
+    if (rows == 0) return MIMG_OK;
+    if (rows != 1 || block != 256 || !gemv_swiglu_ok(w[0]->dw, w[1]->dw))
+        return fail(MIMG_NOT_HANDLED, "no swiglu epilogue for %lld rows, block %d, %s/%s", (long long)rows, block,
+                    dt_name(w[0]->dw.dt), dt_name(w[1]->dw.dt));
+    if (!x || !ws || !aligned(ws, 256)) return fail(MIMG_ERR_ARG, "null or misaligned pointer");
+    const int64_t K = w[0]->dw.k, N = w[0]->dw.n;
+    ActLayout l = act_layout(rows, K);
+    if (ws_bytes < l.total)
+        return fail(MIMG_ERR_WORKSPACE, "workspace %llu < %llu bytes", (unsigned long long)ws_bytes, (unsigned long long)l.total);
+    int64_t ns[1] = {N};
+    float* ys[1] = {out};
+    if ((rc = check_outputs(x, rows, K, ns, ys, 1))) return rc;
+    if ((uintptr_t)out < (uintptr_t)ws + ws_bytes && (uintptr_t)ws < (uintptr_t)out + (uint64_t)N * 4)
+        return fail(MIMG_ERR_ARG, "out overlaps the workspace");
+    // swiglu.v1's pieces (the reference's parallel(): GOMAXPROCS procs)
+    const int64_t total = N, wk = procs < total ? procs : total;
+    int64_t chunk = total;
+    if (wk > 1) chunk = total / (wk * 8) > 1 ? total / (wk * 8) : 1;
+    const float* bs[2] = {bias ? bias[0] : nullptr, bias ? bias[1] : nullptr};
+    HIP_TRY(launch_gemv_a8k_swiglu(w[0]->dw, w[1]->dw, act_ptrs((void*)ws, l), x, bs, out, total, chunk,
+                                   (hipStream_t)stream));
+    return MIMG_OK;
+}
+
 int mimg_rms_norm_qkv_rope_kv_dev(const uint64_t* whs, const float* x, const float* resid, const float* scale,
                                   float eps, float* x_out, const float* const* bias, float* q, const int64_t* pos,
                                   const int64_t* cache_index, const double* inv_freq, int heads, int kv_heads, int d,

@@ -67,6 +67,13 @@ bool gemv_mfma_ok(const DevWeight* const* ws, int nmat, int64_t rows);
 hipError_t launch_gemv_a8k_mfma(const DevWeight* const* ws, int nmat, const ActPtrs& a, int64_t rows,
                                 int64_t total_rows, const float* x, const float* const* bias, float* const* y,
                                 hipStream_t stream);
+// gate and up (Q4_K, same shape) at one pre-quantized row with swiglu.v1
+// in the epilogue: out[n] = swiglu(gate[n], up[n]) with the reference's
+// pieces of `chunk` elements of `total` (gemv_kquant.hip).
+bool gemv_swiglu_ok(const DevWeight& gate, const DevWeight& up);
+hipError_t launch_gemv_a8k_swiglu(const DevWeight& gate, const DevWeight& up, const ActPtrs& a, const float* x,
+                                  const float* const* bias, float* out, int64_t total, int64_t chunk,
+                                  hipStream_t stream);
 hipError_t launch_gemv_a8k(const DevWeight* const* ws, int nmat, const ActPtrs& a, int64_t rows,
                            int64_t total_rows, const float* x, const float* const* bias, float* const* y,
                            hipStream_t stream);

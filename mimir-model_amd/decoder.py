@@ -113,7 +113,7 @@ class Decoder:
     """
 
     def __init__(self, config, tensors, a8=True, cache_f16=False, max_rows=64, slots=1, procs=16, kquant_block=256,
-                 f32_tile_rows=0, fuse_rope=True):
+                 f32_tile_rows=0, fuse_rope=True, fuse_swiglu=True):
         c = self.c = config if isinstance(config, Config) else Config(**config)
         self.a8, self.f16, self.slots = bool(a8), bool(cache_f16), int(slots)
         # activation blocks for Q4_K/Q6_K weights: 256 is dequant_matmul_a8.v2
@@ -159,6 +159,8 @@ class Decoder:
         # one row: norm, q/k/v, rope and the cache scatter in one launch
         # (until the library answers NotHandled for the shape)
         self.rope_fused = bool(fuse_rope)
+        # one row: gate/up products with swiglu in their epilogue
+        self.swiglu_fused = bool(fuse_swiglu)
         self.q, self.o = B(R * H * D * 4), B(R * H * D * 4)
         self.k, self.v = B(R * Hkv * D * 4), B(R * Hkv * D * 4)
         self.g, self.u, self.sw = B(R * F * 4), B(R * F * 4), B(R * F * 4)
@@ -233,6 +235,36 @@ class Decoder:
         mimg.rms_norm_dev(self.x.ptr, resid, self.vec[norm].ptr, c.norm_eps, T, E, self.h.ptr, s)
         self._linears(names, self.h.ptr, T, ys, biases)
 
+    def _ffn_one_row(self, l):
+        """The FFN at one row with 8-bit activations of blocks of 256: x +=
+        the attention output; h = rms_norm(x) * scale quantized (one launch);
+        gate and up products with swiglu in their epilogue (one launch); the
+        quantizer on the swiglu output; down. False (nothing launched) where
+        the swiglu epilogue does not take the shape."""
+        c, s = self.c, self.stream.handle
+        p = f"blk.{l}."
+        gate, up, down = (self.w[p + n] for n in ("ffn_gate.weight", "ffn_up.weight", "ffn_down.weight"))
+        F, E = c.ffn, c.embed
+        if not (self.a8 and self.swiglu_fused and gate.dt == mimg.Q4_K and up.dt == mimg.Q4_K and
+                self._block(gate) == 256 and self._block(down) in (32, 256) and gate.n == up.n == F and F % 4 == 0
+                and E % 256 == 0 and E <= 16384 and F <= 32768 and p + "ffn_gate.bias" not in self.vec
+                and p + "ffn_up.bias" not in self.vec):
+            return False
+        mimg.rms_norm_quant_dev(self.x.ptr, self.ao.ptr, self.vec[p + "ffn_norm.weight"].ptr, c.norm_eps, 1, E,
+                                self.h.ptr, 256, self.ws.ptr, self.ws_bytes, s)
+        try:
+            mimg.matmul_a8_quantized_swiglu_dev([gate, up], self.h.ptr, 1, None, 256, self.sw.ptr, self.procs,
+                                                self.ws.ptr, self.ws_bytes, s)
+        except mimg.NotHandled:  # (the norm is done: the products and swiglu separately)
+            self.swiglu_fused = False
+            mimg.matmul_a8_quantized_group_dev([gate, up], self.h.ptr, 1, None, 256, [self.g.ptr, self.u.ptr],
+                                               self.ws.ptr, self.ws_bytes, s)
+            mimg.swiglu_dev(self.g.ptr, self.u.ptr, self.sw.ptr, F, self.procs, s)
+        mimg.quantize_act_dev(self.sw.ptr, 1, F, self._block(down), self.ws.ptr, self.ws_bytes, s)
+        mimg.matmul_a8_quantized_group_dev([down], self.sw.ptr, 1, None, self._block(down), [self.ao.ptr],
+                                           self.ws.ptr, self.ws_bytes, s)
+        return True
+
     def _norm_qkv_rope(self, l, resid, qkv, qkv_b, pos, cidx):
         """At one row with 8-bit activations: the attention norm, the q/k/v
         products, rope and the cache scatter in one launch (x + resid lands in
@@ -283,16 +315,20 @@ class Decoder:
             mimg.attention_dev(self.q.ptr, self.kc[l].ptr, self.vc[l].ptr, cidx, kstart, T, H, Hkv, D,
                                self.cache_len, c.context, self.f16, self.o.ptr, self.att_ws.ptr, self.att_ws_bytes, s)
             self._linears([p + "attn_output.weight"], self.o.ptr, T, [self.ao.ptr])
-            self._norm_linears(self.ao.ptr, p + "ffn_norm.weight", T, [p + "ffn_gate.weight", p + "ffn_up.weight"],
-                               [self.g.ptr, self.u.ptr])
             down = self.w[p + "ffn_down.weight"]
-            if self.a8 and self._block(down) in (32, 256) and F <= 32768:
+            if T == 1 and self._ffn_one_row(l):
+                pass
+            elif self.a8 and self._block(down) in (32, 256) and F <= 32768:
+                self._norm_linears(self.ao.ptr, p + "ffn_norm.weight", T, [p + "ffn_gate.weight", p + "ffn_up.weight"],
+                                   [self.g.ptr, self.u.ptr])
                 # (out a buffer of its own: the refusal screen reads g and u)
                 mimg.swiglu_quant_dev(self.g.ptr, self.u.ptr, self.sw.ptr, T, F, self.procs, self._block(down),
                                       self.ws.ptr, self.ws_bytes, s)
                 mimg.matmul_a8_quantized_group_dev([down], self.sw.ptr, T, None, self._block(down), [self.ao.ptr],
                                                    self.ws.ptr, self.ws_bytes, s)
             else:
+                self._norm_linears(self.ao.ptr, p + "ffn_norm.weight", T, [p + "ffn_gate.weight", p + "ffn_up.weight"],
+                                   [self.g.ptr, self.u.ptr])
                 mimg.swiglu_dev(self.g.ptr, self.u.ptr, self.g.ptr, T * F, self.procs, s)
                 self._linears([p + "ffn_down.weight"], self.g.ptr, T, [self.ao.ptr])
             resid = self.ao.ptr

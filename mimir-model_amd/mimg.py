@@ -47,6 +47,8 @@ SIGNATURES = {
                                       ctypes.POINTER(_P), _P, _U64, _P]),
     "mimg_rms_norm_linear_a8_group_dev": (_I, [ctypes.POINTER(_U64), _I, _P, _P, _P, ctypes.c_float, _P,
                                                ctypes.POINTER(_P), ctypes.POINTER(_P), _P]),
+    "mimg_matmul_a8_quantized_swiglu_dev": (_I, [ctypes.POINTER(_U64), _P, _I64, ctypes.POINTER(_P), _I, _P, _I, _P,
+                                                 _U64, _P]),
     "mimg_rms_norm_qkv_rope_kv_dev": (_I, [ctypes.POINTER(_U64), _P, _P, _P, ctypes.c_float, _P, ctypes.POINTER(_P),
                                            _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _P, _P, _I, _P]),
     "mimg_matmul_a8_quantized_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P, _U64, _P]),
@@ -265,6 +267,16 @@ def rms_norm_linear_a8_group_dev(weights, x_ptr, resid_ptr, scale_ptr, eps, x_ou
     bs = None if bias_ptrs is None else (_P * n)(*[_P(p) if p else None for p in bias_ptrs])
     _check(load().mimg_rms_norm_linear_a8_group_dev(hs, n, _P(x_ptr), _o(resid_ptr), _o(scale_ptr), eps,
                                                     _P(x_out_ptr), bs, ys, _P(stream)))
+
+
+def matmul_a8_quantized_swiglu_dev(weights, x_ptr, rows, bias_ptrs, block, out_ptr, procs, ws_ptr, ws_bytes, stream):
+    """gate/up products of activations already quantized into ws, and
+    swiglu of the two into out, in one launch; raises NotHandled where the
+    fused launch does not apply (then make the group and swiglu calls)."""
+    hs = (_U64 * 2)(*[w.handle for w in weights])
+    bs = None if bias_ptrs is None else (_P * 2)(*[_P(p) if p else None for p in bias_ptrs])
+    _check(load().mimg_matmul_a8_quantized_swiglu_dev(hs, _P(x_ptr), rows, bs, block, _P(out_ptr), procs, _P(ws_ptr),
+                                                      ws_bytes, _P(stream)))
 
 
 def rms_norm_qkv_rope_kv_dev(weights, x_ptr, resid_ptr, scale_ptr, eps, x_out_ptr, bias_ptrs, q_ptr, pos_ptr,

@@ -601,6 +601,81 @@ def test_rms_norm_qkv_rope_kv_equals_separate_calls(gpu, oracle, rt, name):
         w.release()
 
 
+_SWIGLU_FUSED = {
+    # K, N, procs, case
+    "llama8b_ffn": (4096, 14336, 16, None),
+    "procs3_tails": (1024, 1000, 3, None),  # pieces of 41 elements: f64 tails in every piece
+    "procs1": (2048, 512, 1, "bias"),
+    "refused_row": (1024, 256, 16, "huge"),
+    "refused_weight": (1024, 512, 7, "inf_scale"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(_SWIGLU_FUSED))
+def test_matmul_swiglu_equals_group_then_swiglu(gpu, oracle, rt, name):
+    """gate/up products with swiglu in the epilogue: out bit for bit
+    matmul_a8_quantized_group_dev then swiglu_dev (the reference's pieces for
+    several GOMAXPROCS, f64 tails included), with biases, a refused
+    activation row and a weight row with a non-finite block scale (both on
+    the float32 path)."""
+    K, N, procs, case = _SWIGLU_FUSED[name]
+    rng = np.random.default_rng(K + N + procs)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    if case == "huge":
+        x[0, 5] = np.float32(3e18)  # above 2^60: the row is refused
+    wbs = []
+    for i in range(2):
+        wb = oracle.synthetic_weight(Q4_K, N, K, seed=80 + i)
+        if case == "inf_scale" and i == 1:
+            wb = bytearray(wb.tobytes())
+            o = len(wb) // N * 9 + 2 * 144
+            wb[o:o + 2] = b"\x00\x7c"  # up row 9, block 2: d = +inf
+            wb = np.frombuffer(bytes(wb), np.uint8)
+        wbs.append(wb)
+    W = [gpu.Weight(wb, Q4_K, N, K) for wb in wbs]
+    bias = [rng.standard_normal(N).astype(np.float32) for _ in range(2)] if case == "bias" else None
+    dbs = [dev(rt, b) for b in bias] if bias else None
+    s = rt.Stream()
+    dx = dev(rt, x)
+    wsb = gpu.a8_workspace_bytes(1, K)
+    ws = rt.DeviceBuffer(wsb)
+    gpu.quantize_act_dev(dx.ptr, 1, K, 256, ws.ptr, wsb, s.handle)
+    out = rt.DeviceBuffer(N * 4)
+    gpu.matmul_a8_quantized_swiglu_dev(W, dx.ptr, 1, [b.ptr for b in dbs] if dbs else None, 256, out.ptr, procs,
+                                       ws.ptr, wsb, s.handle)
+    g, u, want = rt.DeviceBuffer(N * 4), rt.DeviceBuffer(N * 4), rt.DeviceBuffer(N * 4)
+    gpu.matmul_a8_quantized_group_dev(W, dx.ptr, 1, [b.ptr for b in dbs] if dbs else None, 256, [g.ptr, u.ptr],
+                                      ws.ptr, wsb, s.handle)
+    gpu.swiglu_dev(g.ptr, u.ptr, want.ptr, N, procs, s.handle)
+    s.sync()
+    a, b = out.download(np.float32), want.download(np.float32)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), np.flatnonzero(a.view(np.uint32) != b.view(np.uint32))[:8]
+    if case == "inf_scale":
+        assert W[1].info()[1] == 1
+    for w in W:
+        w.release()
+
+
+def test_matmul_swiglu_not_handled(gpu, oracle, rt):
+    """Shapes without the swiglu epilogue are refused before any launch:
+    two rows, blocks of 32, a Q6_K weight, mismatched shapes."""
+    s = rt.Stream()
+    K = 512
+    q4 = [gpu.Weight(oracle.synthetic_weight(Q4_K, 64, K, seed=9 + i), Q4_K, 64, K) for i in range(2)]
+    q6 = gpu.Weight(oracle.synthetic_weight(Q6_K, 64, K, seed=11), Q6_K, 64, K)
+    q4b = gpu.Weight(oracle.synthetic_weight(Q4_K, 32, K, seed=12), Q4_K, 32, K)
+    x = rt.DeviceBuffer(2 * K * 4)
+    wsb = gpu.a8_workspace_bytes(2, K)
+    ws, out = rt.DeviceBuffer(wsb), rt.DeviceBuffer(64 * 4 * 2)
+    for ws_pair, rows, block in (((q4[0], q4[1]), 2, 256), ((q4[0], q4[1]), 1, 32), ((q4[0], q6), 1, 256),
+                                 ((q4[0], q4b), 1, 256)):
+        with pytest.raises(gpu.NotHandled):
+            gpu.matmul_a8_quantized_swiglu_dev(list(ws_pair), x.ptr, rows, None, block, out.ptr, 16, ws.ptr, wsb,
+                                               s.handle)
+    for w in q4 + [q6, q4b]:
+        w.release()
+
+
 def test_rms_norm_qkv_rope_kv_not_handled(gpu, oracle, rt):
     """Shapes the fused rope launch does not take are refused before any
     launch: q/k/v rows that are not heads*d, kv_heads*d, kv_heads*d, and a
