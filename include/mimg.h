@@ -224,6 +224,23 @@ int mimg_matmul_a8_quantized_swiglu_dev(const uint64_t *w, const float *x, int64
                                         int block, float *out, int procs, const void *ws, uint64_t ws_bytes,
                                         void *stream);
 
+/* The q, k, v products (w = {q, k, v}) of 4 to 8 activation rows already
+ * quantized into ws (blocks of 256), then rope.v1 on q and k and the cache
+ * scatter of k and v at cache_index[t] of each row t (reference
+ * interp/fast.go:507-557, importer/llama.go:489-503), in two launches (q
+ * with k, then v) instead of four: bit for bit
+ * mimg_matmul_a8_quantized_group_dev then mimg_rope_kv_dev, with q written
+ * to q [rows, heads, d] and k and v to the caches only. Returns
+ * MIMG_NOT_HANDLED (nothing launched) outside 4..8 rows, block 256, d 64 or
+ * 128, q and k of one dtype and q, k, v of heads*d, kv_heads*d, kv_heads*d
+ * rows. No reference counterpart beyond the ops it equals. */
+int mimg_matmul_a8_quantized_qkv_rope_kv_dev(const uint64_t *w, const float *x, int64_t rows,
+                                             const float *const *bias, int block, float *q, const int64_t *pos,
+                                             const int64_t *cache_index, const double *inv_freq, int heads,
+                                             int kv_heads, int d, int rotary, int interleaved, int64_t context,
+                                             void *kcache, void *vcache, int f16, const void *ws, uint64_t ws_bytes,
+                                             void *stream);
+
 /* mimg_rms_norm_linear_a8_group_dev on w = {q, k, v} at one activation
  * row followed by mimg_rope_kv_dev (T = 1) on its outputs, in one launch:
  * rope.v1 (reference interp/fast.go:507-557) rotates q (written to q,

@@ -341,6 +341,16 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     const int frow = min(fused_row<RD>(A, mi, tile, R, min(t, R - 1)), F.N - 1);
     const int wr = F.wref[frow];
     const float bias = F.bias ? F.bias[frow] : 0.f;
+    const int64_t pidx = ROPE ? A.cidx[0] : 0;  // (the rope epilogue's cache index)
+    // (rope: the position and this thread's pair frequency, before the weights)
+    int rot_i = 0;
+    if (ROPE) {
+        const int P = tile * (R / 2) + min(t, R / 2 - 1);
+        rot_i = P - (P / (RD / 2 > 0 ? RD / 2 : 1)) * (RD / 2 > 0 ? RD / 2 : 1);
+    }
+    const bool rot_on = ROPE && mi != 2 && t < R / 2 && rot_i < A.rotary / 2;
+    const int64_t rot_pos = rot_on ? A.pos[0] : 0;
+    const double rot_f = rot_on ? A.inv_freq[rot_i] : 0.0;
     __builtin_amdgcn_sched_barrier(0);
     FusedRaw<DT> raw[U];
     auto load = [&](int p0) {
@@ -384,14 +394,10 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
 
     // (rope: the rotation of this thread's pair, while the weights arrive)
     float rc = 1.f, rs = 0.f;
-    if (ROPE && mi != 2 && t < R / 2) {
-        constexpr int half = RD / 2;
-        const int P = tile * (R / 2) + t, i = P - (P / half) * half;
-        if (i < A.rotary / 2) {
-            const double ang = (double)A.pos[0] * A.inv_freq[i];
-            rc = (float)cos(ang);
-            rs = (float)sin(ang);
-        }
+    if (rot_on) {
+        const double ang = (double)rot_pos * rot_f;
+        rc = (float)cos(ang);
+        rs = (float)sin(ang);
     }
 
     // 3. Exact block sums of this workgroup's pairs.
@@ -453,7 +459,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     // 6. rope.v1 and the cache scatter (rope_kv_kernel's steps, T = 1): q
     // rotated to y, k rotated and v to the caches at cidx[0].
     __syncthreads();
-    const int64_t p = A.cidx[0];
+    const int64_t p = pidx;
     if (mi == 2) {
         const int row = row0 + t;
         if (t < R && row < F.N && p >= 0 && p < A.C) {

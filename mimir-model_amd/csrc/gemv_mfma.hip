@@ -40,6 +40,7 @@
 // (row, activation row) runs the float chain over the table in block order.
 // Rows of x the quantizer refused and weight rows with a non-finite block
 // scale take the float32 path (reference interp/fast.go:323-377).
+#include "decoder_math.hpp"
 #include "f32path.hpp"
 #include "mimg_device.hpp"
 #include "mimg_kernels.hpp"
@@ -57,7 +58,15 @@ struct MfmaMat {
     float* y;             // [M][N]
     int N;
     int tile0;            // first workgroup of this matrix
+    int kind;             // MF_PLAIN, or the decoder epilogues below
 };
+
+// Epilogues of the attention input's products (rope.v1 and the cache
+// scatter of rope_kv_kernel, with the head dim RD a template constant):
+// q rotated to y, k rotated into the key cache, v into the value cache at
+// the cache index of each activation row. The rows of q and k are dealt to
+// workgroups in rotation pairs.
+enum { MF_PLAIN = 0, MF_ROPE_Q = 1, MF_ROPE_K = 2, MF_STORE_V = 3 };
 
 struct MfmaArgs {
     MfmaMat mat[3];
@@ -70,7 +79,38 @@ struct MfmaArgs {
     const int32_t* ok;   // [M]
     const float* x;      // [M][K] f32 (float32 path)
     int fused;           // float32 path order: total rows <= 8
+    // rope and cache scatter (matrices of another kind than MF_PLAIN)
+    const int64_t* pos;   // [M]
+    const int64_t* cidx;  // [M]
+    const double* inv_freq;
+    int rotary, interleaved, f16;
+    int64_t C;
+    void* kc;
+    void* vc;
 };
+
+// Row of local row r of tile `tile`: q and k rows in rotation pairs (local
+// rows 2j, 2j+1 are dims (a, b) of pair P = 8 tile + j: head P / (RD/2),
+// pair P % (RD/2), as rope_kv_kernel numbers them), other rows in order.
+template <int RD>
+__device__ __forceinline__ int mf_row(const MfmaArgs& A, const MfmaMat& P, int tile, int r) {
+    if (RD == 0 || (P.kind != MF_ROPE_Q && P.kind != MF_ROPE_K)) return tile * 16 + r;
+    constexpr int half = RD / 2;
+    const int h2 = A.rotary / 2;
+    const int Q = tile * 8 + (r >> 1), hh = Q / half, i = Q - hh * half;
+    int a, b;
+    if (A.interleaved) {
+        a = 2 * i;
+        b = a + 1;
+    } else if (i < h2) {
+        a = i;
+        b = i + h2;
+    } else {
+        a = A.rotary + 2 * (i - h2);
+        b = a + 1;
+    }
+    return hh * RD + ((r & 1) ? b : a);
+}
 
 // One lane's loads for one block (all unconditional, in bounds).
 template <uint32_t DT>
@@ -114,14 +154,15 @@ struct MfLanes {
     const uint8_t* row[MfWave<DT>::NLD];  // the row's first byte (+16j for Q4_K)
     uint32_t j16[MfWave<DT>::NLD];        // 16j (Q6_K)
     uint32_t lds[MfWave<DT>::NLD];
-    __device__ MfLanes(const uint8_t* W, int64_t rb, int row0, int N) {
+    template <class RowOf>
+    __device__ MfLanes(const uint8_t* W, int64_t rb, RowOf rowof) {
         using S = MfWave<DT>;
         const int l = threadIdx.x & 63;
 #pragma unroll
         for (int i = 0; i < S::NLD; i++) {
             const int q = min(64 * i + l, S::CH - 1);
             const int r = q / S::CPR, j = q - S::CPR * r;
-            row[i] = W + (int64_t)min(row0 + r, N - 1) * rb + (DT == DT_Q4_K ? 16 * j : 0);
+            row[i] = W + (int64_t)rowof(r) * rb + (DT == DT_Q4_K ? 16 * j : 0);
             j16[i] = 16 * j;
             lds[i] = 16 * (S::RST * r + j);
         }
@@ -275,11 +316,23 @@ __device__ __forceinline__ void mf_block6(const MfRaw<DT_Q6_K>& r, int G, const 
 template <uint32_t DT>
 __host__ __device__ constexpr size_t mf_lds_bytes(int nb, int M, int nw) {
     return nw * (size_t)MfWave<DT>::LBYTES + (size_t)nb * MF_ROWS * M * (DT == DT_Q4_K ? 8 : 4) + (size_t)nb * MF_ROWS * 4 + (size_t)nb * M * 4 +
-           (size_t)MF_ROWS * M * 4;
+           (size_t)MF_ROWS * M * 4 * 2;  // (+ the results [16][M] for the decoder epilogues)
+}
+
+// v row `row` (kv head row / RD, dim row % RD) of activation row m into the
+// value cache at the row's cache index (not stored outside the cache).
+template <int RD>
+__device__ __forceinline__ void mf_store_v(const MfmaArgs& A, int row, int64_t p, float v) {
+    if constexpr (RD != 0) {
+        if (p < 0 || p >= A.C) return;
+        const int64_t at = vcache_at(row / RD, p, row % RD, RD, A.C);
+        if (A.f16) ((_Float16*)A.vc)[at] = (_Float16)v;
+        else ((float*)A.vc)[at] = v;
+    }
 }
 
 // Q4_K fits 5 waves per SIMD (at most 102 registers) with one block ahead.
-template <uint32_t DT, int NW>
+template <uint32_t DT, int NW, int RD = 0>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K ? 5 : 1)))
 void gemv_a8k_mfma_kernel(MfmaArgs A) {
     using S = MfWave<DT>;
@@ -292,17 +345,20 @@ void gemv_a8k_mfma_kernel(MfmaArgs A) {
     const int t = threadIdx.x, l = t & 63, ar = l & 15, G = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: the block loop is scalar
     const int nb = A.nb, M = A.M, N = P.N;
-    const int row0 = ((int)blockIdx.x - P.tile0) * MF_ROWS;
+    const int tile = (int)blockIdx.x - P.tile0, row0 = tile * MF_ROWS;
+    const bool epi = RD != 0 && P.kind != MF_PLAIN;  // a decoder epilogue (uniform)
+    auto rowof = [&](int r) { return min(mf_row<RD>(A, P, tile, r), N - 1); };
     constexpr int TW = DT == DT_Q4_K ? 2 : 1;  // table words per entry
     uint8_t* wl = smem + w * S::LBYTES;                               // this wave's staging
     int* tab = (int*)(smem + NW * S::LBYTES);                         // [nb][16][M][TW]
     uint32_t* dd = (uint32_t*)(tab + (size_t)nb * MF_ROWS * M * TW);  // [nb][16]
     float* dxs = (float*)(dd + (size_t)nb * MF_ROWS);                 // [nb][M]
     int* refl = (int*)(dxs + (size_t)nb * M);                         // [16][M]
+    float* yres = (float*)(refl + (size_t)MF_ROWS * M);                // [16][M]: results (epilogues)
 
     // This lane's weight row (A operand; rows past N read the last row) and
     // activation row (B operand).
-    const uint8_t* rowp = P.W + (int64_t)min(row0 + ar, N - 1) * A.rb;
+    const uint8_t* rowp = P.W + (int64_t)rowof(ar) * A.rb;
     const int am = min(ar, M - 1);
     const int8_t* ya = A.q + (int64_t)am * A.K;
     const float* dxr = A.d32 + (int64_t)am * (A.K / 32);
@@ -312,11 +368,32 @@ void gemv_a8k_mfma_kernel(MfmaArgs A) {
     const int ft = min(t, MF_ROWS * M - 1), fr = ft / M;
     int fm = ft - fr * M;
     asm volatile("v_mov_b32 %0, %1" : "=v"(fm) : "v"(fm));  // a vector index: ok[] through the vector cache
-    const int frow = min(row0 + fr, N - 1);
+    const int frow = rowof(fr);
     const int wr = P.wref[frow], okm = A.ok[fm];
     const float bias = P.bias ? P.bias[frow] : 0.f;
+    const int64_t pidx = RD != 0 && P.kind != MF_PLAIN ? A.cidx[fm] : 0;  // (epilogues: cache index of row fm)
+    // (rope: this lane's position and frequency, loaded before the weights)
+    const bool rot_lane = RD != 0 && (P.kind == MF_ROPE_Q || P.kind == MF_ROPE_K) && t < MF_ROWS * M;
+    int rot_i = 0;
+    if (RD != 0) {
+        const int Q = tile * 8 + (fr >> 1);
+        rot_i = Q - (Q / (RD > 0 ? RD / 2 : 1)) * (RD > 0 ? RD / 2 : 1);
+    }
+    const bool rot_on = rot_lane && rot_i < A.rotary / 2;
+    const int64_t rot_pos = rot_on ? A.pos[fm] : 0;
+    const double rot_f = rot_on ? A.inv_freq[rot_i] : 0.0;
 
-    const MfLanes<DT> L(P.W, A.rb, row0, N);
+    const MfLanes<DT> L(P.W, A.rb, rowof);
+    // rope: the rotation of chain lane t's (row t/M, activation row t%M),
+    // computed once the first weights are requested
+    float rc = 1.f, rs = 0.f;
+    auto rotation = [&]() {
+        if (rot_on) {
+            const double ang = (double)rot_pos * rot_f;
+            rc = (float)cos(ang);
+            rs = (float)sin(ang);
+        }
+    };
     if constexpr (DT == DT_Q4_K) {
         // Block b's table entries, scale bits and dx.
         auto step = [&](const MfRaw<DT>& r, int b) {
@@ -365,6 +442,7 @@ void gemv_a8k_mfma_kernel(MfmaArgs A) {
         float d0;
         mf_load_w<DT>(L, min(w, nb - 1), v0);
         load_a(min(w, nb - 1), a0, d0);
+        rotation();
         for (int b = w; b < nb; b += NW) body(b, v0, a0, d0);
     } else {
         uint8_t* wa = wl + S::WBYTES;    // activation rows [8][Q6_AROW]
@@ -385,7 +463,7 @@ void gemv_a8k_mfma_kernel(MfmaArgs A) {
         uint32_t rlo[4];
 #pragma unroll
         for (int i = 0; i < 4; i++)
-            rlo[i] = (uint32_t)(uintptr_t)(P.W + (int64_t)min(row0 + 4 * G + i, N - 1) * A.rb) & 15;
+            rlo[i] = (uint32_t)(uintptr_t)(P.W + (int64_t)rowof(4 * G + i) * A.rb) & 15;
         auto load6 = [&](int b, u32x4* v, v4i* ac, float& dx) {
             mf_load_w<DT>(L, b, v);
             ac[0] = *(const v4i*)(yc0 + (int64_t)b * 256);
@@ -430,6 +508,7 @@ void gemv_a8k_mfma_kernel(MfmaArgs A) {
         v4i c0[2];
         float d0;
         load6(min(w, nb - 1), v0, c0, d0);
+        rotation();
         for (int b = w; b < nb; b += NW) body6(b, v0, c0, d0);
     }
     const int flag = (wr != 0) | (okm == 0);
@@ -438,8 +517,8 @@ void gemv_a8k_mfma_kernel(MfmaArgs A) {
 
     // The serial float chain, one lane per (weight row, activation row).
     if (t < MF_ROWS * M) {
-        const int r = t / M, m = t - r * M, row = row0 + r;
-        if (row < N && !flag) {
+        const int r = t / M, m = t - r * M, row = rowof(r);
+        if (row0 + r < N && !flag) {
             float tot = 0.f, off = 0.f;
             for (int b = 0; b < nb; b++) {
                 const int* e = tab + (((size_t)b * MF_ROWS + r) * M + m) * TW;
@@ -450,17 +529,50 @@ void gemv_a8k_mfma_kernel(MfmaArgs A) {
             }
             float res = DT == DT_Q4_K ? tot - off : tot;
             if (P.bias) res += bias;
-            P.y[(int64_t)m * N + row] = res;
+            if (epi && P.kind == MF_STORE_V) mf_store_v<RD>(A, row, pidx, res);
+            else if (epi) yres[r * M + m] = res;
+            else P.y[(int64_t)m * N + row] = res;
         }
     }
     // The float32 path for refused pairs, one group of eight lanes per pair.
     const int g = t >> 3;
     for (int qq = g; qq < MF_ROWS * M; qq += MF_T / 8) {
-        const int r = qq / M, m = qq - r * M, row = row0 + r;
-        if (row < N && refl[qq]) {
+        const int r = qq / M, m = qq - r * M, row = rowof(r);
+        if (row0 + r < N && refl[qq]) {
             float res = f32dot_g8<DT>(P.W + (int64_t)row * A.rb, A.x + (int64_t)m * A.K, A.K, A.fused != 0);
             if (P.bias) res += P.bias[row];
-            if ((t & 7) == 0) P.y[(int64_t)m * N + row] = res;
+            if ((t & 7) == 0) {
+                if (epi && P.kind == MF_STORE_V) mf_store_v<RD>(A, row, A.cidx[m], res);
+                else if (epi) yres[qq] = res;
+                else P.y[(int64_t)m * N + row] = res;
+            }
+        }
+    }
+    if constexpr (RD != 0) {
+        if (!epi || P.kind == MF_STORE_V) return;
+        // every (row, activation row) result of q or k is in yres: one lane each
+        __syncthreads();
+        if (t < MF_ROWS * M) {
+            const int r = t / M, m = t - r * M, row = rowof(r);
+            const int64_t p = pidx;  // (t < 16 M: the cache index of row m)
+            float own = yres[t];
+            {
+                // rope_kv_kernel's steps on (dim a, dim b) = rows (2j, 2j+1)
+                const float other = yres[(r ^ 1) * M + m];
+                const int Q = tile * 8 + (r >> 1), hh = Q / (RD / 2), i = Q - hh * (RD / 2);
+                float o = own;
+                if (i < A.rotary / 2) {
+                    const float x1 = (r & 1) ? other : own, x2 = (r & 1) ? own : other;
+                    o = (r & 1) ? x2 * rc + x1 * rs : x1 * rc - x2 * rs;
+                }
+                if (P.kind == MF_ROPE_Q) {
+                    P.y[(int64_t)m * N + row] = o;
+                } else if (p >= 0 && p < A.C) {
+                    const int64_t at = ((int64_t)hh * A.C + p) * RD + (row - hh * RD);
+                    if (A.f16) ((_Float16*)A.kc)[at] = (_Float16)o;
+                    else ((float*)A.kc)[at] = o;
+                }
+            }
         }
     }
 }
@@ -517,8 +629,14 @@ hipError_t launch_gemv_a8k_mfma(const DevWeight* const* ws, int nmat, const ActP
         A.mat[i].y = i < nmat ? y[i] : nullptr;
         A.mat[i].N = (int)wi.n;
         A.mat[i].tile0 = tiles;
+        A.mat[i].kind = MF_PLAIN;
         if (i < nmat) tiles += (int)((wi.n + MF_ROWS - 1) / MF_ROWS);
     }
+    A.pos = A.cidx = nullptr;
+    A.inv_freq = nullptr;
+    A.rotary = A.interleaved = A.f16 = 0;
+    A.C = 0;
+    A.kc = A.vc = nullptr;
     const int nw = mf_waves(w.dt, tiles, A.nb);
     const size_t lds = mf_lds(w.dt, A.nb, A.M, nw);
     const dim3 grid((unsigned)tiles), block((unsigned)(64 * nw));
@@ -530,6 +648,80 @@ hipError_t launch_gemv_a8k_mfma(const DevWeight* const* ws, int nmat, const ActP
         else hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 12>), grid, block, lds, stream, A);
     }
     return hipGetLastError();
+}
+
+// q, k (rope) and v (cache scatter) at 2..8 activation rows: two launches,
+// q and k together, then v.
+bool gemv_mfma_qkv_ok(const DevWeight* const* ws, int64_t rows, int heads, int kv_heads, int d, int rotary) {
+    if ((d != 64 && d != 128) || rotary <= 0 || rotary % 2 || rotary > d) return false;
+    if (ws[0]->n != (int64_t)heads * d || ws[1]->n != (int64_t)kv_heads * d || ws[2]->n != (int64_t)kv_heads * d)
+        return false;
+    return gemv_mfma_ok(ws, 2, rows) && gemv_mfma_ok(ws + 2, 1, rows);
+}
+
+template <int RD>
+static hipError_t launch_mfma_epi(MfmaArgs A, uint32_t dt, hipStream_t stream) {
+    int tiles = 0;
+    for (int i = 0; i < A.nmat; i++) {
+        A.mat[i].tile0 = tiles;
+        tiles += (A.mat[i].N + MF_ROWS - 1) / MF_ROWS;
+    }
+    const int nw = mf_waves(dt, tiles, A.nb);
+    const size_t lds = mf_lds(dt, A.nb, A.M, nw);
+    const dim3 grid((unsigned)tiles), block((unsigned)(64 * nw));
+    if (dt == DT_Q4_K) {
+        hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q4_K, 4, RD>), grid, block, lds, stream, A);
+    } else {
+        if (nw == 4) hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 4, RD>), grid, block, lds, stream, A);
+        else if (nw == 8) hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 8, RD>), grid, block, lds, stream, A);
+        else hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 12, RD>), grid, block, lds, stream, A);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_a8k_mfma_qkv(const DevWeight* const* ws, const ActPtrs& a, int64_t rows, const float* x,
+                                    const float* const* bias, float* q, const int64_t* pos, const int64_t* cidx,
+                                    const double* inv_freq, int heads, int kv_heads, int d, int rotary,
+                                    int interleaved, int64_t context, void* kc, void* vc, int f16,
+                                    hipStream_t stream) {
+    if (!gemv_mfma_qkv_ok(ws, rows, heads, kv_heads, d, rotary)) return hipErrorInvalidValue;
+    for (int part = 0; part < 2; part++) {
+        const int nmat = part == 0 ? 2 : 1;
+        const DevWeight* const* wp = ws + (part == 0 ? 0 : 2);
+        MfmaArgs A;
+        A.nmat = nmat;
+        A.rb = wp[0]->row_bytes;
+        A.nb = (int)(wp[0]->k / 256);
+        A.M = (int)rows;
+        A.K = wp[0]->k;
+        A.q = a.q;
+        A.d32 = a.d32;
+        A.ok = a.ok;
+        A.x = x;
+        A.fused = rows <= 8;
+        for (int i = 0; i < 3; i++) {
+            const DevWeight& wi = *wp[i < nmat ? i : 0];
+            A.mat[i].W = wi.data;
+            A.mat[i].wref = wi.wref;
+            A.mat[i].bias = i < nmat && bias ? bias[(part == 0 ? 0 : 2) + i] : nullptr;
+            A.mat[i].y = part == 0 && i == 0 ? q : nullptr;
+            A.mat[i].N = (int)wi.n;
+            A.mat[i].tile0 = 0;
+            A.mat[i].kind = part == 1 ? MF_STORE_V : i == 0 ? MF_ROPE_Q : MF_ROPE_K;
+        }
+        A.pos = pos;
+        A.cidx = cidx;
+        A.inv_freq = inv_freq;
+        A.rotary = rotary;
+        A.interleaved = interleaved;
+        A.f16 = f16;
+        A.C = context;
+        A.kc = kc;
+        A.vc = vc;
+        const hipError_t e = d == 64 ? launch_mfma_epi<64>(A, wp[0]->dt, stream) : launch_mfma_epi<128>(A, wp[0]->dt, stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace mimg

@@ -993,6 +993,49 @@ int mimg_matmul_a8_quantized_swiglu_dev(const uint64_t* whs, const float* x, int
     return MIMG_OK;
 }
 
+int mimg_matmul_a8_quantized_qkv_rope_kv_dev(const uint64_t* whs, const float* x, int64_t rows,
+                                             const float* const* bias, int block, float* q, const int64_t* pos,
+                                             const int64_t* cache_index, const double* inv_freq, int heads,
+                                             int kv_heads, int d, int rotary, int interleaved, int64_t context,
+                                             void* kcache, void* vcache, int f16, const void* ws, uint64_t ws_bytes,
+                                             void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!whs || !q || !pos || !cache_index || !inv_freq || !kcache || !vcache) return fail(MIMG_ERR_ARG, "null pointer");
+    if (heads <= 0 || kv_heads <= 0 || heads % kv_heads || d <= 0 || d % 2 || d > 1024 || rotary <= 0 || rotary % 2 ||
+        rotary > d || context <= 0)
+        return fail(MIMG_ERR_ARG, "rope: heads %d, kv heads %d, D %d, rotary %d, context %lld", heads, kv_heads, d,
+                    rotary, (long long)context);
+    Held held[3];
+    const DevWeight* dw[3];
+    for (int i = 0; i < 3; i++) {
+        if ((rc = held[i].acquire(whs[i]))) return rc;
+        Weight* w = held[i].get();
+        if (w->dw.k != held[0].get()->dw.k) return fail(MIMG_ERR_ARG, "q, k and v must share K");
+        bool use_f32;
+        if ((rc = a8_checks(w, rows, block, &use_f32))) return rc;
+        if (use_f32) return fail(MIMG_NOT_HANDLED, "%s has no 8-bit kernel for blocks of %d", dt_name(w->dw.dt), block);
+        dw[i] = &w->dw;
+    }
+    if (rows == 0) return MIMG_OK;
+    if (block != 256 || rows < mfma_min_rows() || rows > 8 || dw[0]->dt != dw[1]->dt ||
+        !gemv_mfma_qkv_ok(dw, rows, heads, kv_heads, d, rotary))
+        return fail(MIMG_NOT_HANDLED, "no q/k/v + rope launch for %lld rows, block %d, D %d", (long long)rows, block, d);
+    if (!x || !ws || !aligned(ws, 256)) return fail(MIMG_ERR_ARG, "null or misaligned pointer");
+    const int64_t K = dw[0]->k;
+    ActLayout l = act_layout(rows, K);
+    if (ws_bytes < l.total)
+        return fail(MIMG_ERR_WORKSPACE, "workspace %llu < %llu bytes", (unsigned long long)ws_bytes, (unsigned long long)l.total);
+    int64_t ns[1] = {dw[0]->n};
+    float* ys[1] = {q};
+    if ((rc = check_outputs(x, rows, K, ns, ys, 1))) return rc;
+    const float* bs[3] = {bias ? bias[0] : nullptr, bias ? bias[1] : nullptr, bias ? bias[2] : nullptr};
+    HIP_TRY(launch_gemv_a8k_mfma_qkv(dw, act_ptrs((void*)ws, l), rows, x, bs, q, pos, cache_index, inv_freq, heads,
+                                     kv_heads, d, rotary, interleaved, context, kcache, vcache, f16,
+                                     (hipStream_t)stream));
+    return MIMG_OK;
+}
+
 int mimg_rms_norm_qkv_rope_kv_dev(const uint64_t* whs, const float* x, const float* resid, const float* scale,
                                   float eps, float* x_out, const float* const* bias, float* q, const int64_t* pos,
                                   const int64_t* cache_index, const double* inv_freq, int heads, int kv_heads, int d,

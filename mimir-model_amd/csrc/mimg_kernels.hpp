@@ -108,6 +108,14 @@ bool fused_norm_ok(const DevWeight* const* ws, int nmat);
 hipError_t launch_gemv_a8k_fused_norm(const DevWeight* const* ws, int nmat, const float* x, const float* resid,
                                       const float* scale, float eps, float* x_out, const float* const* bias,
                                       float* const* y, hipStream_t stream);
+// q and k (rope) and v (cache scatter) at 2..8 activation rows on the
+// matrix cores (gemv_mfma.hip), as the separate products and rope_kv.
+bool gemv_mfma_qkv_ok(const DevWeight* const* ws, int64_t rows, int heads, int kv_heads, int d, int rotary);
+hipError_t launch_gemv_a8k_mfma_qkv(const DevWeight* const* ws, const ActPtrs& a, int64_t rows, const float* x,
+                                    const float* const* bias, float* q, const int64_t* pos, const int64_t* cidx,
+                                    const double* inv_freq, int heads, int kv_heads, int d, int rotary,
+                                    int interleaved, int64_t context, void* kc, void* vc, int f16,
+                                    hipStream_t stream);
 // The rope.v1 + cache scatter epilogue of the fused q/k/v GEMV at one row.
 struct FusedRope {
     const int64_t* pos;

@@ -161,6 +161,8 @@ class Decoder:
         self.rope_fused = bool(fuse_rope)
         # one row: gate/up products with swiglu in their epilogue
         self.swiglu_fused = bool(fuse_swiglu)
+        # 4..8 rows: q/k/v products with rope and the cache scatter
+        self.qkv_rows_fused = bool(fuse_rope)
         self.q, self.o = B(R * H * D * 4), B(R * H * D * 4)
         self.k, self.v = B(R * Hkv * D * 4), B(R * Hkv * D * 4)
         self.g, self.u, self.sw = B(R * F * 4), B(R * F * 4), B(R * F * 4)
@@ -235,6 +237,34 @@ class Decoder:
         mimg.rms_norm_dev(self.x.ptr, resid, self.vec[norm].ptr, c.norm_eps, T, E, self.h.ptr, s)
         self._linears(names, self.h.ptr, T, ys, biases)
 
+    def _qkv_rope_rows(self, l, resid, qkv, qkv_b, T, pos, cidx):
+        """4..8 rows with 8-bit activations of blocks of 256: x += resid and
+        the quantized rms_norm (one launch), then the q, k, v products with
+        rope and the cache scatter in their epilogues (two launches). False
+        (nothing launched) where the library has no such launch."""
+        c, s = self.c, self.stream.handle
+        p = f"blk.{l}."
+        ws = [self.w[n] for n in qkv]
+        if not (self.a8 and self.qkv_rows_fused and all(self._block(w) == 256 for w in ws) and c.embed <= 32768
+                and c.head_dim in (64, 128) and ws[0].dt == ws[1].dt):
+            return False
+        bs = [None if b is None or b not in self.vec else self.vec[b].ptr for b in qkv_b]
+        mimg.rms_norm_quant_dev(self.x.ptr, resid, self.vec[p + "attn_norm.weight"].ptr, c.norm_eps, T, c.embed,
+                                self.h.ptr, 256, self.ws.ptr, self.ws_bytes, s)
+        try:
+            mimg.matmul_a8_quantized_qkv_rope_kv_dev(ws, self.h.ptr, T, bs if any(bs) else None, 256, self.q.ptr, pos,
+                                                     cidx, self.invf.ptr, c.heads, c.kv_heads, c.head_dim,
+                                                     c.rope_dims, c.interleaved, self.cache_len, self.kc[l].ptr,
+                                                     self.vc[l].ptr, self.f16, self.ws.ptr, self.ws_bytes, s)
+        except mimg.NotHandled:  # (the norm is done: the products and rope separately)
+            self.qkv_rows_fused = False
+            mimg.matmul_a8_quantized_group_dev(ws, self.h.ptr, T, bs if any(bs) else None, 256,
+                                               [self.q.ptr, self.k.ptr, self.v.ptr], self.ws.ptr, self.ws_bytes, s)
+            mimg.rope_kv_dev(self.q.ptr, self.k.ptr, self.v.ptr, pos, cidx, self.invf.ptr, T, c.heads, c.kv_heads,
+                             c.head_dim, c.rope_dims, c.interleaved, self.cache_len, self.kc[l].ptr, self.vc[l].ptr,
+                             self.f16, s)
+        return True
+
     def _ffn_one_row(self, l):
         """The FFN at one row with 8-bit activations of blocks of 256: x +=
         the attention output; h = rms_norm(x) * scale quantized (one launch);
@@ -306,7 +336,8 @@ class Decoder:
             p = f"blk.{l}."
             qkv = [p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"]
             qkv_b = [p + "attn_q.bias", p + "attn_k.bias", p + "attn_v.bias"]
-            if not (T == 1 and self._norm_qkv_rope(l, resid, qkv, qkv_b, pos, cidx)):
+            if not (T == 1 and self._norm_qkv_rope(l, resid, qkv, qkv_b, pos, cidx)) and \
+                    not (4 <= T <= 8 and self._qkv_rope_rows(l, resid, qkv, qkv_b, T, pos, cidx)):
                 self._norm_linears(resid, p + "attn_norm.weight", T, qkv, [self.q.ptr, self.k.ptr, self.v.ptr], qkv_b,
                                    single_fused=True)
                 mimg.rope_kv_dev(self.q.ptr, self.k.ptr, self.v.ptr, pos, cidx, self.invf.ptr, T, H, Hkv, D,

@@ -90,7 +90,11 @@ class DeviceBuffer:
         return out
 
     def zero(self):
+        """Zero-fills the buffer and waits for it: hipMemset runs on the null
+        stream, which the library's non-blocking streams do not wait for, so
+        a kernel enqueued right after could otherwise race with the fill."""
         check(rt().hipMemset(ctypes.c_void_p(self.ptr), 0, self.nbytes), "hipMemset")
+        check(rt().hipDeviceSynchronize(), "hipDeviceSynchronize")
 
     def free(self):
         if self.ptr:

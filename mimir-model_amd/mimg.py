@@ -49,6 +49,8 @@ SIGNATURES = {
                                                ctypes.POINTER(_P), ctypes.POINTER(_P), _P]),
     "mimg_matmul_a8_quantized_swiglu_dev": (_I, [ctypes.POINTER(_U64), _P, _I64, ctypes.POINTER(_P), _I, _P, _I, _P,
                                                  _U64, _P]),
+    "mimg_matmul_a8_quantized_qkv_rope_kv_dev": (_I, [ctypes.POINTER(_U64), _P, _I64, ctypes.POINTER(_P), _I, _P, _P,
+                                                      _P, _P, _I, _I, _I, _I, _I, _I64, _P, _P, _I, _P, _U64, _P]),
     "mimg_rms_norm_qkv_rope_kv_dev": (_I, [ctypes.POINTER(_U64), _P, _P, _P, ctypes.c_float, _P, ctypes.POINTER(_P),
                                            _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _P, _P, _I, _P]),
     "mimg_matmul_a8_quantized_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P, _U64, _P]),
@@ -277,6 +279,20 @@ def matmul_a8_quantized_swiglu_dev(weights, x_ptr, rows, bias_ptrs, block, out_p
     bs = None if bias_ptrs is None else (_P * 2)(*[_P(p) if p else None for p in bias_ptrs])
     _check(load().mimg_matmul_a8_quantized_swiglu_dev(hs, _P(x_ptr), rows, bs, block, _P(out_ptr), procs, _P(ws_ptr),
                                                       ws_bytes, _P(stream)))
+
+
+def matmul_a8_quantized_qkv_rope_kv_dev(weights, x_ptr, rows, bias_ptrs, block, q_ptr, pos_ptr, cidx_ptr,
+                                        inv_freq_ptr, heads, kv_heads, d, rotary, interleaved, context, kc_ptr,
+                                        vc_ptr, f16, ws_ptr, ws_bytes, stream):
+    """q, k, v products of activations already quantized into ws, rope and
+    the cache scatter (4..8 rows); raises NotHandled where it does not apply
+    (then make the group call and rope_kv_dev)."""
+    hs = (_U64 * 3)(*[w.handle for w in weights])
+    bs = None if bias_ptrs is None else (_P * 3)(*[_P(p) if p else None for p in bias_ptrs])
+    _check(load().mimg_matmul_a8_quantized_qkv_rope_kv_dev(hs, _P(x_ptr), rows, bs, block, _P(q_ptr), _P(pos_ptr),
+                                                           _P(cidx_ptr), _P(inv_freq_ptr), heads, kv_heads, d, rotary,
+                                                           int(interleaved), context, _P(kc_ptr), _P(vc_ptr), int(f16),
+                                                           _P(ws_ptr), ws_bytes, _P(stream)))
 
 
 def rms_norm_qkv_rope_kv_dev(weights, x_ptr, resid_ptr, scale_ptr, eps, x_out_ptr, bias_ptrs, q_ptr, pos_ptr,

@@ -676,6 +676,69 @@ def test_matmul_swiglu_not_handled(gpu, oracle, rt):
         w.release()
 
 
+_ROPE_QKV_ROWS = {
+    # rows, K, heads, kv heads, D, rotary, interleaved, f16 cache, context, case
+    "llama8b_b8": (8, 4096, 32, 8, 128, 128, True, True, 40, None),
+    "llama1b_b5_f32": (5, 2048, 32, 8, 64, 64, True, False, 24, None),
+    "qwen2_b4_bias": (4, 1024, 8, 2, 128, 128, False, True, 16, "bias"),
+    "partial_b6": (6, 1024, 16, 4, 64, 32, False, False, 16, None),
+    "refused_b8": (8, 1024, 8, 8, 128, 128, True, True, 16, "huge"),
+    "q6k_qk_b7": (7, 1024, 8, 2, 64, 64, True, True, 16, "q6k"),
+}
+
+
+@pytest.mark.parametrize("name", sorted(_ROPE_QKV_ROWS))
+def test_qkv_rope_kv_rows_equal_separate_calls(gpu, oracle, rt, name):
+    """4..8 rows: q, k, v products of quantized activations with rope and
+    the cache scatter in their epilogues: q and both caches (every entry)
+    bit for bit matmul_a8_quantized_group_dev then rope_kv_dev, rows in
+    different slots (one cache index past the cache), adjacent-pair and
+    half rotation, a partial rotary span, biases, f16/f32 caches, a refused
+    activation row and Q6_K q/k."""
+    T, K, H, Hkv, D, rot, inter, f16, C, case = _ROPE_QKV_ROWS[name]
+    rng = np.random.default_rng(T * K + H + D)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    if case == "huge":
+        x[3, 17] = np.float32(5e18)
+    qk_dt = Q6_K if case == "q6k" else Q4_K
+    specs = [(qk_dt, H * D), (qk_dt, Hkv * D), (Q6_K, Hkv * D)]
+    W = [gpu.Weight(oracle.synthetic_weight(dt, n, K, seed=70 + i), dt, n, K) for i, (dt, n) in enumerate(specs)]
+    bias = [rng.standard_normal(n).astype(np.float32) if case == "bias" else None for _, n in specs]
+    dbs = [dev(rt, b) if b is not None else None for b in bias]
+    bptrs = [b.ptr if b else 0 for b in dbs] if case == "bias" else None
+    inv = (1.0 / (500000.0 ** (np.arange(0, rot, 2, dtype=np.float64) / rot))).astype(np.float64)
+    dinv = dev(rt, inv)
+    cidx = np.array([(t * 5 + 3) % (C + 1) for t in range(T)], np.int64)  # one index may equal C: not stored
+    cidx[-1] = C
+    pos = (cidx + 11).astype(np.int64)
+    dpos, dcidx = dev(rt, pos), dev(rt, cidx)
+    esz = 2 if f16 else 4
+    kbytes, vbytes = Hkv * C * D * esz, Hkv * gpu.vcache_len(C) * D * esz
+    init_k = rng.integers(0, 255, kbytes, dtype=np.uint8)
+    init_v = rng.integers(0, 255, vbytes, dtype=np.uint8)
+    s = rt.Stream()
+    dx = dev(rt, x)
+    wsb = gpu.a8_workspace_bytes(T, K)
+    ws = rt.DeviceBuffer(wsb)
+    gpu.quantize_act_dev(dx.ptr, T, K, 256, ws.ptr, wsb, s.handle)
+    dq, kc, vc = rt.DeviceBuffer(T * H * D * 4), dev(rt, init_k), dev(rt, init_v)
+    gpu.matmul_a8_quantized_qkv_rope_kv_dev(W, dx.ptr, T, bptrs, 256, dq.ptr, dpos.ptr, dcidx.ptr, dinv.ptr, H, Hkv,
+                                            D, rot, inter, C, kc.ptr, vc.ptr, f16, ws.ptr, wsb, s.handle)
+    ys = [rt.DeviceBuffer(T * n * 4) for _, n in specs]
+    kc2, vc2 = dev(rt, init_k), dev(rt, init_v)
+    gpu.matmul_a8_quantized_group_dev(W, dx.ptr, T, bptrs, 256, [y.ptr for y in ys], ws.ptr, wsb, s.handle)
+    gpu.rope_kv_dev(ys[0].ptr, ys[1].ptr, ys[2].ptr, dpos.ptr, dcidx.ptr, dinv.ptr, T, H, Hkv, D, rot, inter, C,
+                    kc2.ptr, vc2.ptr, f16, s.handle)
+    s.sync()
+    a, b = dq.download(np.float32), ys[0].download(np.float32)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), np.flatnonzero(a.view(np.uint32) != b.view(np.uint32))[:8]
+    assert np.array_equal(kc.download(np.uint8), kc2.download(np.uint8))
+    assert np.array_equal(vc.download(np.uint8), vc2.download(np.uint8))
+    assert not np.array_equal(kc.download(np.uint8), init_k)
+    for w in W:
+        w.release()
+
+
 def test_rms_norm_qkv_rope_kv_not_handled(gpu, oracle, rt):
     """Shapes the fused rope launch does not take are refused before any
     launch: q/k/v rows that are not heads*d, kv_heads*d, kv_heads*d, and a
