@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 LDS_BYTES = 160 * 1024
-ATT_DEC_MAXK, ATT_BB = 256, 16
+ATT_DEC_MAXK = 256
 
 
 def att_range(kend, kstart, t, C, maxk):
@@ -100,22 +100,25 @@ def check_decode(b, ranges):
 
 def check_wsum(b, ranges):
     D, C = b.D, b.C
-    PPB, NR = (1, 4) if b.f16 else (2, 3)
-    batch = ATT_BB * PPB * 1024
+    PPB, BB, NR = (1, 16, 4) if b.f16 else (2, 16, 3)
+    CPB = BB // 2 if b.f16 else BB  # copies a batch a copying wave (waves 1 and 2)
+    batch = BB * PPB * 1024
     e_len = (b.maxk + 14) & ~7
     assert NR * batch + e_len * 4 + 64 <= LDS_BYTES
+    assert 16 * 63 + 16 + ((BB - 1) * PPB + PPB - 1) * 1024 <= batch  # a lane's slot reads and copies
     for t, (k0, n) in enumerate(ranges):
         if n <= 0:
             continue
         k0a, off = k0 & ~7, k0 - (k0 & ~7)
         nb = (off + n + 7) >> 3
-        nbat = (nb + ATT_BB - 1) // ATT_BB
-        assert off + n - 1 < e_len  # e[off + j]
-        assert 8 * nb <= e_len or off + n <= e_len
-        for bt in range(nbat):  # whole-batch chain reads e[8*b0 .. 8*(b0+BB)) only when 8*(b0+BB) <= off+n
-            b0 = ATT_BB * bt
-            if 8 * b0 >= off and 8 * (b0 + ATT_BB) <= off + n:
-                assert 8 * (b0 + ATT_BB) <= e_len
+        nv = n & ~7 if n >= 8 else 0
+        assert off + n - 1 < e_len  # e[off + j]; the exps' clamped reads e[off + min(j, nv - 1)], e[off + nv + tid]
+        for bt in range((nb + BB - 1) // BB):  # a whole batch's chain reads e[8*b0 .. 8*(b0+BB)) only when inside
+            b0 = BB * bt
+            if 8 * b0 >= off and 8 * (b0 + BB) <= off + n:
+                assert 8 * (b0 + BB) <= e_len
+        # copies: NR - 1 batches ahead of batch 0 and one a batch after, blocks past nb: the last again
+        assert (NR - 1) * CPB <= 63  # copies in flight a copying wave (vmcnt)
         for h in range(b.H):
             hk = h // (b.H // b.Hkv)
             for d0 in range(0, D, 64):
@@ -125,6 +128,7 @@ def check_wsum(b, ranges):
                         src = b.vcache_at(hk, k0a, d) + 4 * w1
                         last = src + (nb - 1) * 8 * D + 16 // b.esz - 1  # blocks past nb: the last again
                         b.check(src, last, b.vc_len, "wsum: value element")
+                # scores: loads of j and, past the end, the last key (j clamped to n - 1)
                 b.check((t * b.H + h) * b.maxk, (t * b.H + h) * b.maxk + n - 1, b.ws_len, "wsum: scores")
 
 
@@ -172,6 +176,9 @@ def run_launch(T, H, Hkv, D, C, maxk, f16, kend, kstart):
     if D in (64, 128) and maxk <= ATT_DEC_MAXK:
         check_decode(b, ranges)
         return "decode"
+    # (att_scores_gqa_kernel, taken for D 64/128 and 2/4/8 query heads per
+    # kv head, reads the same key rows per tile and writes the same score
+    # rows as the per-head kernel checked here)
     check_scores(b, ranges, 1)
     check_wsum(b, ranges)
     return "two"
@@ -210,3 +217,5 @@ def test_attention_addresses_in_bounds(D, f16):
         seen.add(run_launch(T, H, Hkv, D, C, maxk, f16, kend, kstart if slots > 1 or T > 5 else None))
     if D in (64, 128):
         assert seen == {"many", "decode", "two"}
+    elif D % 64 == 0:
+        assert seen == {"many", "two"}

@@ -151,6 +151,18 @@ def test_attention_long_context_bitexact(gpu, oracle, rt, f16, C, D):
 
 
 @pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
+@pytest.mark.parametrize("T,H,Hkv,D,slots,C", [(2, 32, 8, 128, 2, 1100), (3, 16, 2, 64, 1, 3000), (8, 32, 8, 128, 8, 300),
+                                               (4, 8, 4, 64, 2, 1100), (1, 32, 8, 128, 1, 2100),
+                                               (2, 32, 8, 128, 2, 400)])
+def test_attention_grouped_heads_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, slots, C):
+    """Past 256 keys at few queries, when tiles x kv heads x queries reaches
+    256 workgroups, the scores of the query heads that share a kv head come
+    from one workgroup (groups of 2, 4 and 8 heads, slots; the last case stays
+    per head): bit for bit the restatement."""
+    test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, slots, C=C)
+
+
+@pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
 @pytest.mark.parametrize("T,H,Hkv,D,C", [(5, 4, 1, 64, 42), (4, 8, 2, 128, 45), (5, 4, 2, 32, 42), (3, 4, 2, 128, 301)])
 def test_attention_unaligned_slots_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, C):
     """Three slots of C entries with C not a multiple of 8: the visible ranges
