@@ -41,11 +41,11 @@ MIMG_HD inline int quant_rne(float x, float amax, float inv) {
     }
     const double h = n + (dd > 0.0 ? 0.5 : -0.5);
     const double e = __builtin_fma(h, (double)amax, -t);
-    const double lo = h - 0.5;
+    const double lo = h - 0.5;  // an integer in [-128, 128]
     double q;
     if (e > 0.0) q = lo;
     else if (e < 0.0) q = lo + 1.0;
-    else q = (__builtin_fmod(lo, 2.0) == 0.0) ? lo : lo + 1.0;
+    else q = ((int)lo & 1) == 0 ? lo : lo + 1.0;  // (even lo; f64 fmod is a slow software loop on the GPU)
     return (int)q;
 }
 
