@@ -9,7 +9,12 @@
 // workgroup quantizes the same row the same way, so no second launch and no
 // global workspace), then forms the exact int32 block sums of its pairs (as
 // gemv_kquant.hip, block-major pairs) and runs the serial float chain of
-// each row in block order.
+// each row in block order. Where the tiles fill every CU two or three times
+// over, a workgroup holds two or three such 256-thread teams, each with its
+// own tile, and only the first quantizes x into the LDS row they share: the
+// row's re-reads per CU drop by that factor (measured on MI355X: the cfg1
+// layer set 52.7 -> 50.6 us per step, q/k/v 768 tiles as 256 workgroups of
+// three teams, o 512 tiles as 256 of two).
 //
 // Quantization (reference Q8.QuantizeBlocks, internal/kernels/q8.go:50-97):
 // per block of 256, amax = max|x| (the row is refused if any |x| is NaN or
@@ -125,6 +130,9 @@ struct FusedArgs {
     int64_t C;
     void* kc;
     void* vc;
+    // LDS: the quantized row (and the normed row) shared by the workgroup's
+    // teams, then one region per team (pair table, flags, rope values)
+    int lds_row, lds_team;
 };
 
 // Row of local row r of tile `tile` of matrix mi: with rope (RD = the head
@@ -305,39 +313,46 @@ __device__ __forceinline__ ActLane act_lane_lds(const QuantLds& Q, int b, int l)
 // are U rows of one block, whose activation is read from LDS once. Weights
 // are addressed as 32-bit offsets from the tile's base; the row flags and
 // bias are loaded first and looked at last.
+//
+// A workgroup of several teams (256 threads each, one tile each) quantizes
+// the row once: the lead team (threads 0..255) loads x and fills the shared
+// LDS row while every team's weights are in flight; the other teams meet it
+// at the same barriers. `smem` is the shared row, `tmem` the team's region.
 template <uint32_t DT, int U, bool SHARED, bool NORM, int RD>
 __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F, int mi, int tile, uint8_t* smem,
-                                           double* npart) {
+                                           uint8_t* tmem, double* npart, bool lead) {
     constexpr bool ROPE = RD != 0;
     constexpr int BYTES = DT == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     const int nb = A.nb, R = F.R, np = R * nb;
     const int64_t K = A.K;
-    const int g = threadIdx.x >> 3, l = threadIdx.x & 7, t = threadIdx.x;
+    const int t = threadIdx.x & 255, g = t >> 3, l = t & 7;
     const int row0 = tile * R;
     QuantLds Q;
     Q.q = (int8_t*)smem;
     Q.dx = (float*)(smem + K);
     Q.xs = (int16_t*)(Q.dx + nb);
     Q.ys16 = (int16_t*)(Q.xs + K / 32);
-    i32x4* part = (i32x4*)(smem + ((K + nb * 4 + (K / 32) * 2 + (K / 16) * 2 + 15) & ~(int64_t)15));
+    float* yl = (float*)(smem + ((K + nb * 4 + (K / 32) * 2 + (K / 16) * 2 + 15) & ~(int64_t)15));  // NORM: [K] y
+    i32x4* part = (i32x4*)tmem;
     int* refl = (int*)(part + (size_t)R * nb);  // [R]: the row's weight is refused
-    float* yl = (float*)(smem + (((size_t)((uint8_t*)(refl + R) - smem) + 15) & ~(size_t)15));  // NORM: [K] y
+    float* yr = (float*)(tmem + (((size_t)((uint8_t*)(refl + R) - tmem) + 15) & ~(size_t)15));  // rope: [R]
     // rows as 32-bit offsets from the tile's first row (its lowest)
     const int rbase = fused_row<RD>(A, mi, tile, R, 0);
     const int64_t tbyte = (int64_t)rbase * F.rb;
     const uint8_t* Wt = F.W + (tbyte & ~(int64_t)3);
     const uint32_t tadj = (uint32_t)(tbyte & 3), rb32 = (uint32_t)F.rb;
     const int rlast = min(R, F.N - row0) - 1;
-    float* yr = (float*)(smem + (((size_t)((uint8_t*)(refl + R) - smem) + 15) & ~(size_t)15) + (NORM ? (size_t)K * 4 : 0));  // rope: [R]
 
-    // 1. x (the first 16 blocks), the row flags and bias, then the first U
-    // pairs' weights, all in flight; the load counter retires in order, so
-    // the quantizer waits for x alone.
+    // 1. x (the first 16 blocks; lead team), the row flags and bias, then
+    // the first U pairs' weights, all in flight; the load counter retires in
+    // order, so the quantizer waits for x alone.
     const int j = t & 15, bq = t >> 4;
     float4 xv[4];
     NormRegs N;
-    if constexpr (NORM) norm_load(A, N);
-    else load_x16(A.x, min(bq, nb - 1), j, xv);
+    if (lead) {
+        if constexpr (NORM) norm_load(A, N);
+        else load_x16(A.x, min(bq, nb - 1), j, xv);
+    }
     const int frow = min(fused_row<RD>(A, mi, tile, R, min(t, R - 1)), F.N - 1);
     const int wr = F.wref[frow];
     const float bias = F.bias ? F.bias[frow] : 0.f;
@@ -379,11 +394,12 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     __builtin_amdgcn_sched_barrier(0);
 
     // 2. Quantize x (NORM: rms_norm(x + resid) * scale) into LDS while the
-    // weights arrive.
-    bool bad;
+    // weights arrive (lead team; the others wait at its barrier).
+    bool bad = false;
     if constexpr (NORM) {
-        bad = norm_quantize_lds(A, N, blockIdx.x == 0, yl, npart, Q);
-    } else {
+        if (lead) bad = norm_quantize_lds(A, N, blockIdx.x == 0, yl, npart, Q);
+        else lds_barrier();
+    } else if (lead) {
         bad = bq < nb ? quantize_block_lds(xv, bq, j, Q) : false;
         for (int b = bq + 16; b < nb; b += 16) {  // rows longer than 4096
             load_x16(A.x, b, j, xv);
@@ -497,24 +513,52 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     }
 }
 
-template <int U, bool SHARED, bool NORM, int RD = 0>
-__global__ __launch_bounds__(256) void gemv_a8k_fused_kernel(FusedArgs A) {
+// TEAMS tiles per workgroup (the launch gives every workgroup TEAMS whole
+// tiles): team k of workgroup w runs tile TEAMS*w + k.
+template <int U, bool SHARED, bool NORM, int RD = 0, int TEAMS = 1>
+__global__ __launch_bounds__(256 * TEAMS) void gemv_a8k_fused_kernel(FusedArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double npart[4];
+    // (a scalar: the lead team's branches around its barrier are uniform
+    // jumps, so each wave runs exactly one side and one s_barrier)
+    const int team = TEAMS == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8));
+    const int gt = (int)blockIdx.x * TEAMS + team;
     int mi = 0;
-    if (A.nmat > 1 && (int)blockIdx.x >= A.mat[1].tile0) mi = 1;
-    if (A.nmat > 2 && (int)blockIdx.x >= A.mat[2].tile0) mi = 2;
+    if (A.nmat > 1 && gt >= A.mat[1].tile0) mi = 1;
+    if (A.nmat > 2 && gt >= A.mat[2].tile0) mi = 2;
     const FusedMat F = mi == 0 ? A.mat[0] : mi == 1 ? A.mat[1] : A.mat[2];
-    const int tile = (int)blockIdx.x - F.tile0;
-    if (F.dt == DT_Q4_K) fused_body<DT_Q4_K, U, SHARED, NORM, RD>(A, F, mi, tile, smem, npart);
-    else fused_body<DT_Q6_K, U, SHARED, NORM, RD>(A, F, mi, tile, smem, npart);
+    const int tile = gt - F.tile0;
+    uint8_t* tmem = smem + A.lds_row + (size_t)team * A.lds_team;
+    if (F.dt == DT_Q4_K) fused_body<DT_Q4_K, U, SHARED, NORM, RD>(A, F, mi, tile, smem, tmem, npart, team == 0);
+    else fused_body<DT_Q6_K, U, SHARED, NORM, RD>(A, F, mi, tile, smem, tmem, npart, team == 0);
 }
 
-static size_t fused_lds_bytes(int64_t K, int nb, int maxR, bool norm = false) {
-    size_t q = ((size_t)K + nb * 4 + (K / 32) * 2 + (K / 16) * 2 + 15) & ~(size_t)15;
-    const size_t base = q + (size_t)maxR * nb * 16 + (size_t)maxR * 4;
-    // (+ the rope epilogue's row values, [maxR] floats)
-    return ((base + 15) & ~(size_t)15) + (norm ? (size_t)K * 4 : 0) + (size_t)maxR * 4;
+// LDS of the shared row: q, dx, xs, ys16 (and the normed row, K floats).
+static size_t fused_lds_row(int64_t K, int nb, bool norm) {
+    const size_t q = ((size_t)K + nb * 4 + (K / 32) * 2 + (K / 16) * 2 + 15) & ~(size_t)15;
+    return q + (norm ? (size_t)K * 4 : 0);
+}
+// LDS of one team: the pair table, the row flags, the rope epilogue's row values.
+static size_t fused_lds_team(int nb, int maxR) {
+    const size_t base = (size_t)maxR * nb * 16 + (size_t)maxR * 4;
+    return (((base + 15) & ~(size_t)15) + (size_t)maxR * 4 + 15) & ~(size_t)15;
+}
+static size_t fused_lds_bytes(int64_t K, int nb, int maxR, bool norm = false, int teams = 1) {
+    return fused_lds_row(K, nb, norm) + (size_t)teams * fused_lds_team(nb, maxR);
+}
+
+// Tiles per workgroup: teams share one quantization of the row, so a
+// workgroup of three (or two) teams re-reads x (and resid, scale) once for
+// three tiles. Taken only where the workgroups still cover every CU.
+static int fused_teams(int tiles) {
+    static const int force = [] {
+        const char* e = getenv("MIMG_FUSED_TEAMS");
+        return e ? atoi(e) : 0;
+    }();
+    if (force >= 1 && force <= 3) return tiles % force == 0 ? force : 1;
+    if (tiles >= 3 * 256 && tiles % 3 == 0) return 3;
+    if (tiles >= 2 * 256 && tiles % 2 == 0) return 2;
+    return 1;
 }
 
 // Rows per workgroup for a matrix: pairs per workgroup at most 32*U*2 (two
@@ -585,25 +629,29 @@ static hipError_t launch_fused(const DevWeight* const* ws, int nmat, const float
             maxR = max(maxR, F.R);
         }
     }
-    const size_t lds = fused_lds_bytes(A.K, A.nb, maxR, norm);
+    const int teams = fused_teams(tiles);
+    A.lds_row = (int)fused_lds_row(A.K, A.nb, norm);
+    A.lds_team = (int)fused_lds_team(A.nb, maxR);
+    const size_t lds = fused_lds_bytes(A.K, A.nb, maxR, norm, teams);
+    const dim3 grid(tiles / teams), block(256 * teams);
     // every matrix has the same R (it depends on K only)
     const bool shared = A.mat[0].R % 4 == 0;
+#define MIMG_FUSED_LAUNCH(SH, NO, RD_)                                                                              \
+    do {                                                                                                           \
+        if (teams == 3) hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, SH, NO, RD_, 3>), grid, block, lds, stream, A); \
+        else if (teams == 2)                                                                                       \
+            hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, SH, NO, RD_, 2>), grid, block, lds, stream, A);           \
+        else hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, SH, NO, RD_, 1>), grid, block, lds, stream, A);          \
+    } while (0)
     if (rope) {
         if (!norm || !shared || (rope->d != 64 && rope->d != 128)) return hipErrorInvalidValue;
-        if (rope->d == 64)
-            hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, true, true, 64>), dim3(tiles), dim3(256), lds, stream, A);
-        else
-            hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, true, true, 128>), dim3(tiles), dim3(256), lds, stream, A);
-        return hipGetLastError();
-    }
-    if (norm && shared)
-        hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, true, true>), dim3(tiles), dim3(256), lds, stream, A);
-    else if (norm)
-        hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, false, true>), dim3(tiles), dim3(256), lds, stream, A);
-    else if (shared)
-        hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, true, false>), dim3(tiles), dim3(256), lds, stream, A);
-    else
-        hipLaunchKernelGGL((gemv_a8k_fused_kernel<4, false, false>), dim3(tiles), dim3(256), lds, stream, A);
+        if (rope->d == 64) MIMG_FUSED_LAUNCH(true, true, 64);
+        else MIMG_FUSED_LAUNCH(true, true, 128);
+    } else if (norm && shared) MIMG_FUSED_LAUNCH(true, true, 0);
+    else if (norm) MIMG_FUSED_LAUNCH(false, true, 0);
+    else if (shared) MIMG_FUSED_LAUNCH(true, false, 0);
+    else MIMG_FUSED_LAUNCH(false, false, 0);
+#undef MIMG_FUSED_LAUNCH
     return hipGetLastError();
 }
 

@@ -477,6 +477,10 @@ _NORM_GROUPS = {
     "llama1b_qkv": (2048, [(Q4_K, 2048), (Q4_K, 512), (Q6_K, 512)], False, None),
     "refused_row": (1024, [(Q6_K, 300)], True, "huge"),
     "refused_weight": (3072, [(Q4_K, 96), (Q6_K, 64)], True, "inf_scale"),
+    # 768 and 512 tiles of 8 rows: three and two tiles a workgroup, one norm
+    "llama8b_full_qkv": (4096, [(Q4_K, 4096), (Q4_K, 1024), (Q6_K, 1024)], True, None),
+    "teams_refused_row": (4096, [(Q4_K, 4096), (Q4_K, 1024), (Q6_K, 1024)], True, "huge"),
+    "teams_refused_weight": (4096, [(Q4_K, 4096)], True, "inf_scale"),
 }
 
 
@@ -499,13 +503,14 @@ def test_rms_norm_linear_group_equals_two_calls(gpu, oracle, rt, name):
         wb = oracle.synthetic_weight(dt, n, K, seed=40 + i)
         if case == "inf_scale" and i == 0:
             wb = bytearray(wb.tobytes())
-            o = len(wb) // n * 17 + 144
-            wb[o:o + 2] = b"\x00\x7c"  # row 17, block 1: d = +inf
+            for row in (9, 17):  # tiles 1 and 2 of 8 rows: another team's, the next workgroup's
+                o = len(wb) // n * row + 144
+                wb[o:o + 2] = b"\x00\x7c"  # block 1: d = +inf
             wb = np.frombuffer(bytes(wb), np.uint8)
         wbs.append(wb)
     W = [gpu.Weight(wb, dt, n, K) for wb, (dt, n) in zip(wbs, specs)]
     if case == "inf_scale":
-        assert W[0].info()[1] == 1
+        assert W[0].info()[1] == 2
     bias = [rng.standard_normal(n).astype(np.float32) if i != 1 else None for i, (_, n) in enumerate(specs)]
     s = rt.Stream()
     dx, dsc = dev(rt, x), dev(rt, sc)

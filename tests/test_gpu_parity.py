@@ -326,12 +326,15 @@ def _dev_linear(gpu, weights, x, biases=None, group=True, prequant=False):
     return [y.download(np.float32).reshape(rows, w.n) for y, w in zip(ys, weights)]
 
 
+@pytest.mark.parametrize("shape", ["small", "llama8b"])
 @pytest.mark.parametrize("rows", [1, 3, 8])
-def test_group_qkv_bitexact(gpu, oracle, rows):
+def test_group_qkv_bitexact(gpu, oracle, rows, shape):
     """q, k (Q4_K) and v (Q6_K) sharing one input in one grouped call (a single
-    fused launch at one row) equal the separate reference products."""
+    fused launch at one row; at the Llama-3-8B shape its 768 tiles run three
+    to a workgroup) equal the separate reference products."""
     k = 4096
-    specs = [(Q4_K, 512, 21), (Q4_K, 128, 22), (Q6_K, 128, 23)]
+    nq, nkv = (512, 128) if shape == "small" else (4096, 1024)
+    specs = [(Q4_K, nq, 21), (Q4_K, nkv, 22), (Q6_K, nkv, 23)]
     wbs = [_weights(oracle, dt, n, k, seed) for dt, n, seed in specs]
     W = [gpu.Weight(wb, dt, n, k) for wb, (dt, n, _) in zip(wbs, specs)]
     x = oracle.synthetic_acts(rows, k, seed=24)
@@ -486,6 +489,33 @@ def test_fused_refusals_large_k(gpu, oracle, dt):
     want = oracle.linear_a8(x, wb, dt, n, k, bias=bias, block=256)
     W.release()
     assert bits_equal(got, want), first_diff(got, want)
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K])
+def test_fused_teams_refusals(gpu, oracle, dt):
+    """The one-row fused launch with two tiles of 8 rows per workgroup (a
+    4096 x 4096 matrix: 512 tiles, the second team's rows 8..15 in the
+    first workgroup) with a refused weight row in that team's tile, then a
+    refused activation row (every product on the float32 path)."""
+    n, k = 4096, 4096
+    bb = 210 if dt == Q6_K else 144
+    wb = bytearray(_weights(oracle, dt, n, k, seed=37).tobytes())
+    rb = len(wb) // n
+    for row in (9, 4000):
+        o = rb * row + 2 * bb + (208 if dt == Q6_K else 0)
+        wb[o:o + 2] = b"\x00\x7c"  # +inf block scale
+    wb = np.frombuffer(bytes(wb), np.uint8)
+    W = gpu.Weight(wb, dt, n, k)
+    assert W.info()[1] == 2
+    bias = np.random.default_rng(6).standard_normal(n).astype(np.float32)
+    x = oracle.synthetic_acts(1, k, seed=38)
+    for case in range(2):
+        if case == 1:
+            x[0, 3333] = np.nan  # the row is refused
+        got = _dev_linear(gpu, [W], x, biases=[bias], group=False)[0]
+        want = oracle.linear_a8(x, wb, dt, n, k, bias=bias, block=256)
+        assert bits_equal(got, want), (case, first_diff(got, want))
+    W.release()
 
 
 def test_fused_quantizer_ties(gpu, oracle):
