@@ -138,6 +138,27 @@ __device__ __forceinline__ void split4(uint32_t pe, uint32_t po, uint32_t he, ui
 __device__ __forceinline__ uint32_t as_u32(s16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ s16x2 as_s16x2(uint32_t v) { return __builtin_bit_cast(s16x2, v); }
 
+// A barrier for LDS only: it waits for this wave's LDS operations, not for
+// its outstanding global loads and stores.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Whether p holds on any thread of the workgroup's nw waves: one LDS flag
+// per wave (slot[nw], written once per launch) and one LDS-only barrier.
+// (HIP's __syncthreads_or takes three barriers and first waits for every
+// load and store the wave has in flight.)
+__device__ __forceinline__ bool wg_any(bool p, int* slot, int nw) {
+    const bool any = __any(p);
+    if ((threadIdx.x & 63) == 0) slot[threadIdx.x >> 6] = any ? 1 : 0;
+    lds_barrier();
+    int r = 0;
+    for (int i = 0; i < nw; i++) r |= slot[i];
+    return r != 0;
+}
+
 }  // namespace mimg
 
 #include "quant_rne.hpp"

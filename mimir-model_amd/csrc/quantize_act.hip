@@ -178,7 +178,8 @@ __global__ __launch_bounds__(1024) void quantize_act_kernel(const float* __restr
         bad |= qa_chunk<BLOCK>(vv[i], row, c * 256 + 4 * lane, K, a, lane);
     }
     }
-    int any_bad = __syncthreads_or(bad ? 1 : 0);
+    __shared__ int wflag[16];
+    const bool any_bad = wg_any(bad, wflag, (int)(blockDim.x >> 6));
     if (threadIdx.x == 0) a.ok[row] = any_bad ? 0 : 1;
 }
 
