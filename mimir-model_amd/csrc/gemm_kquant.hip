@@ -17,8 +17,12 @@
 // value (-128..127) and hi in [-16, 16], S = 256*sum(hi*y) + sum(lo*y):
 // with u = w + 128 in a 16-bit lane, hi is u's high byte and lo its low
 // byte with the top bit flipped. Each MFMA sum is exact in int32 (|sum| <
-// 2^31 for 256-element blocks). Q4_K's M term is a third MFMA plane whose
-// operand is m_s for the 32 k of sub-block s.
+// 2^31 for 256-element blocks). Q4_K's M term = sum_s m_s xs_s comes from
+// the activation's per-32 sums xs: one v_mfma_f32_32x32x16_f16 a row tile
+// and block, with xs split as 64 hi + lo so that every operand is an exact
+// f16 and every partial sum an integer below 2^24 (measured on MI355X
+// against a third int8 plane with operand m_s over the 256 k: gate
+// M = 2048 525 -> 460 us, M = 512 122 -> 114 us).
 //
 // Operands: the activation rows are the MFMA's row operand and the weight
 // rows its column operand, so a lane of the 32 x 32 result holds one weight
@@ -46,6 +50,9 @@ namespace mimg {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 // Workgroup shape: NW waves along the weight rows (32 each), WM along the
 // activation rows (64 each: two MFMA row tiles).
@@ -66,9 +73,13 @@ struct GemmLayout {
     static constexpr int WBYTES = WDMA * T * 16;         // incl. slack for unconditional copies
     static constexpr int ADMA = BM * 16 / T;
     static constexpr int ABYTES = BM * 256;
-    static constexpr int BUF = WBYTES + ABYTES;
+    // Q4_K: the block's per-32 activation sums xs (eight int16, 16 bytes) of
+    // the BM rows, one copy per thread of a group of 256 (slots past BM:
+    // the last row again)
+    static constexpr int XBYTES = DT == DT_Q4_K ? 256 * 16 : 0;
+    static constexpr int BUF = WBYTES + ABYTES + XBYTES;
     static constexpr int DXBYTES = T * 4;                // one dword copy per thread (BM used)
-    static_assert(ADMA * T == BM * 16 && T >= BM && WM == 2, "GEMM tile shape");
+    static_assert(ADMA * T == BM * 16 && T >= BM && BM <= 256 && WM == 2, "GEMM tile shape");
 };
 
 struct GemmArgs {
@@ -81,6 +92,7 @@ struct GemmArgs {
     int64_t K;
     const int8_t* q;       // [M][K]
     const float* d32;      // [M][K/32]
+    const int16_t* xs;     // [M][K/32]
     const int32_t* ok;     // [M]
     const float* x;        // [M][K] f32 (fallback)
     int fused;             // float32 fallback order (rows of the whole call <= 8)
@@ -154,6 +166,12 @@ __device__ __forceinline__ void gemm_issue_block(const GemmArgs& A, int n0, int 
         const int m = min(m0 + min(t, L::BM - 1), A.M - 1);
         lds_copy4(A.d32 + (int64_t)m * (A.K / 32) + 8 * b, dl + 4 * (64 * wave));  // slots t >= BM are slack
     }
+    if constexpr (DT == DT_Q4_K) {
+        if (wave < 4) {
+            const int m = min(m0 + min(t, L::BM - 1), A.M - 1);
+            lds_copy16(A.xs + (int64_t)m * (A.K / 32) + 8 * b, al + L::ABYTES + 16 * (64 * wave));
+        }
+    }
 }
 
 // The same copies issued by the four trailing waves only (rank tr of 256),
@@ -188,6 +206,10 @@ __device__ __forceinline__ void gemm_issue_block_tr(const GemmArgs& A, int n0, i
     {
         const int m = min(m0 + min(tr, L::BM - 1), A.M - 1);
         lds_copy4(A.d32 + (int64_t)m * (A.K / 32) + 8 * b, dl + 4 * (64 * wt));
+    }
+    if constexpr (DT == DT_Q4_K) {
+        const int m = min(m0 + min(tr, L::BM - 1), A.M - 1);
+        lds_copy16(A.xs + (int64_t)m * (A.K / 32) + 8 * b, al + L::ABYTES + 16 * (64 * wt));
     }
 }
 
@@ -243,7 +265,8 @@ __global__ __launch_bounds__(64 * NW * WM) void gemm_a8k_kernel(GemmArgs A) {
     float tot[2][16], off[2][16];
 #pragma unroll
     for (int i = 0; i < 16; i++) tot[0][i] = tot[1][i] = off[0][i] = off[1][i] = 0.f;
-    v16i accH[2], accL[2], accM[2];
+    v16i accH[2], accL[2];
+    v16f accM[2];  // Q4_K: the mins term, exact integers in f32
     float dN = 0.f, dminN = 0.f;
 
     // Block b's integer sums (the MFMAs) from LDS buffer b & 1.
@@ -269,7 +292,7 @@ __global__ __launch_bounds__(64 * NW * WM) void gemm_a8k_kernel(GemmArgs A) {
 #pragma unroll
             for (int ks = 0; ks < 8; ks++) {
                 const v4i a0 = arow(ks, 0), a1 = arow(ks, 1);
-                const uint32_t sc = byte_of(s.sc, ks), mm = byte_of(s.m, ks);
+                const uint32_t sc = byte_of(s.sc, ks);
                 // sc = 8*sh + sl with sh, sl <= 7: sh*q and sl*q (q <= 15) are at
                 // most 105, so each plane is the packed nibbles times a small
                 // constant (16-bit lanes, no carry between the bytes).
@@ -277,21 +300,60 @@ __global__ __launch_bounds__(64 * NW * WM) void gemm_a8k_kernel(GemmArgs A) {
                 const s16x2 shp = {sh, sh}, slp = {sl, sl};
                 const int shift = 4 * (ks & 1);  // sub-block 2c: low nibbles, 2c+1: high
                 const u32x4 qd = qv[ks >> 1];
-                v4i bH, bL, bM;
+                v4i bH, bL;
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const s16x2 nib = as_s16x2((qd[k] >> shift) & 0x0F0F0F0Fu);
                     bH[k] = (int)as_u32(nib * shp);
                     bL[k] = (int)as_u32(nib * slp);
-                    bM[k] = (int)__builtin_amdgcn_perm(0u, mm, 0x00000000u);
                 }
                 const v16i z = {};
                 accH[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bH, ks ? accH[0] : z, 0, 0, 0);
                 accH[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bH, ks ? accH[1] : z, 0, 0, 0);
                 accL[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bL, ks ? accL[0] : z, 0, 0, 0);
                 accL[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bL, ks ? accL[1] : z, 0, 0, 0);
-                accM[0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bM, ks ? accM[0] : z, 0, 0, 0);
-                accM[1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bM, ks ? accM[1] : z, 0, 0, 0);
+            }
+            // The mins term M = sum_s m_s xs_s of every (weight row,
+            // activation row) on one f16 MFMA a row tile (k = 16: the eight
+            // sub-blocks twice). xs = 64 hi + lo with hi in [-64, 63] and lo
+            // in [0, 63]: the row operand holds hi_s at k = s (lanes g = 0)
+            // and lo_s at k = 8 + s (g = 1), the weight operand 64 m_s and
+            // m_s. Every product and partial sum is an integer below 2^24,
+            // so the f32 result is M exactly. The f16 values are built as
+            // f16(1024 + v) from the bits 0x6400 + v, minus 1024.
+            {
+                const uint32_t mw[2] = {(uint32_t)s.m, (uint32_t)(s.m >> 32)};
+                const h2 mul = g ? h2{(_Float16)1.0f, (_Float16)1.0f} : h2{(_Float16)64.0f, (_Float16)64.0f};
+                const h2 c1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+                v8h bm;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t u = __builtin_amdgcn_perm(0u, mw[j >> 1], (j & 1) ? 0x0C030C02u : 0x0C010C00u);
+                    const h2 f = (__builtin_bit_cast(h2, u | 0x64006400u) - c1024) * mul;
+                    bm[2 * j] = f.x;
+                    bm[2 * j + 1] = f.y;
+                }
+                const uint8_t* xl = al + L::ABYTES;
+                const short sh = g ? 0 : 6;
+                const s16x2 sh2 = {sh, sh};
+                const uint32_t msk = g ? 0x003F003Fu : 0xFFFFFFFFu;
+                const h2 cf = g ? c1024 : h2{(_Float16)1088.0f, (_Float16)1088.0f};
+                const s16x2 cadd = g ? s16x2{0x6400, 0x6400} : s16x2{0x6440, 0x6440};
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++) {
+                    const u32x4 xw = *(const u32x4*)(xl + 16 * (64 * wm + 32 * tt + a));
+                    const uint32_t xd[4] = {xw.x, xw.y, xw.z, xw.w};
+                    v8h av;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const uint32_t v = as_u32(as_s16x2(xd[j]) >> sh2) & msk;
+                        const h2 f = __builtin_bit_cast(h2, as_u32(as_s16x2(v) + cadd)) - cf;
+                        av[2 * j] = f.x;
+                        av[2 * j + 1] = f.y;
+                    }
+                    const v16f zf = {};
+                    accM[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bm, zf, 0, 0, 0);
+                }
             }
         } else {
             const uint8_t* wr = wl + (32 * wn + a) * L::WSLOT + q6k_slot_off(A, nrow, b);
@@ -352,8 +414,7 @@ __global__ __launch_bounds__(64 * NW * WM) void gemm_a8k_kernel(GemmArgs A) {
                     const int i = 4 * j + r;
                     const int S = (accH[tt][i] << (DT == DT_Q4_K ? 3 : 8)) + accL[tt][i];
                     tot[tt][i] = __builtin_fmaf((float)S, dN * dxr[r], tot[tt][i]);
-                    if constexpr (DT == DT_Q4_K)
-                        off[tt][i] = __builtin_fmaf((float)accM[tt][i], dminN * dxr[r], off[tt][i]);
+                    if constexpr (DT == DT_Q4_K) off[tt][i] = __builtin_fmaf(accM[tt][i], dminN * dxr[r], off[tt][i]);
                 }
             }
         }
@@ -441,6 +502,7 @@ hipError_t launch_gemm_a8k(const DevWeight& w, const ActPtrs& a, int64_t rows, i
     A.K = w.k;
     A.q = a.q;
     A.d32 = a.d32;
+    A.xs = a.xs;
     A.ok = a.ok;
     A.x = x;
     A.fused = total_rows <= 8;
