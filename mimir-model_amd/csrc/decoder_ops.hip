@@ -283,11 +283,32 @@ __device__ __forceinline__ float kv_load(const void* c, int64_t i) {
 // holds l_c): ((l0+l1)+(l2+l3))+((l4+l5)+(l6+l7)) for keys in the groups of
 // four, ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7)) for the last n%4; lane 0 of the
 // group returns it.
+// The partner values move by DPP within each group of eight lanes: lane
+// c ^ 1 and c ^ 2 by quad permutes, c ^ 4 by row shifts of four into the
+// upper and the lower half-group (bank masks). Float addition commutes, so
+// every lane of the group ends with the same sum.
+__device__ __forceinline__ float xchg1(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), DPP_QUAD_1032, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float xchg2(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), DPP_QUAD_2301, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float xchg4(float v) {
+    constexpr int ROW_SHL4 = 0x104, ROW_SHR4 = 0x114;
+    const int x = __float_as_int(v);
+    int t = __builtin_amdgcn_update_dpp(x, x, ROW_SHR4, 0xF, 0xA, false);  // lanes 4-7, 12-15 of a row: lane - 4
+    t = __builtin_amdgcn_update_dpp(t, x, ROW_SHL4, 0xF, 0x5, false);      // lanes 0-3, 8-11: lane + 4
+    return __int_as_float(t);
+}
 __device__ __forceinline__ float att_reduce8(float l, bool four, int gbase, int c) {
-    const int x1 = four ? 1 : 4, x2 = four ? 2 : 1, x3 = four ? 4 : 2;
-    float p = l + __shfl(l, gbase + (c ^ x1));
-    p = p + __shfl(p, gbase + (c ^ x2));
-    return p + __shfl(p, gbase + (c ^ x3));
+    (void)gbase;
+    (void)c;
+    const float a = l + xchg1(l), b = a + xchg2(a);
+    const float pf = b + xchg4(b);  // ((l0+l1)+(l2+l3))+((l4+l5)+(l6+l7))
+    if (__all(four)) return pf;
+    const float e = l + xchg4(l), f = e + xchg1(e);
+    const float pn = f + xchg2(f);  // ((l0+l4)+(l1+l5))+((l2+l6)+(l3+l7))
+    return four ? pf : pn;
 }
 
 // DM = D/8 for D = 64 or 128 (unrolled; every load of a lane in flight at
