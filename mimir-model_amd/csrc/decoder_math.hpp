@@ -16,16 +16,60 @@ __host__ __device__ __forceinline__ int64_t vcache_at(int hk, int64_t j, int d, 
     return (((int64_t)hk * ((C + 7) >> 3) + (j >> 3)) * D + d) * 8 + (j & 7);
 }
 
+// The value of lane i ^ M (M a power of two below 64): DPP within a row of
+// 16 lanes for M <= 8 (quad permutes for 1 and 2; row shifts of four into
+// each half-row, by bank mask, for 4; a rotation by eight for 8), a
+// swizzle within 32 lanes for 16, a permute for 32. The wave reductions
+// below add (or take the max of) the same partners in the same order as a
+// loop of __shfl_xor(v, M) for M = 32, 16, ..., 1, so their results are
+// the same bits.
+template <int M>
+__device__ __forceinline__ int lane_xor(int x) {
+    if constexpr (M == 1) return __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    else if constexpr (M == 2) return __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    else if constexpr (M == 4) {
+        const int t = __builtin_amdgcn_update_dpp(x, x, 0x114, 0xF, 0xA, false);  // row_shr:4 into lanes 4-7, 12-15
+        return __builtin_amdgcn_update_dpp(t, x, 0x104, 0xF, 0x5, false);         // row_shl:4 into lanes 0-3, 8-11
+    } else if constexpr (M == 8) return __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);  // row_ror:8
+    else if constexpr (M == 16) return __builtin_amdgcn_ds_swizzle(x, 0x401F);  // bit-mask mode: lane ^ 16
+    else return __shfl_xor(x, 32);
+}
+template <int M>
+__device__ __forceinline__ float lane_xor_f32(float v) {
+    return __int_as_float(lane_xor<M>(__float_as_int(v)));
+}
+template <int M>
+__device__ __forceinline__ double lane_xor_f64(double v) {
+    const long long b = __double_as_longlong(v);
+    const int lo = lane_xor<M>((int)(b & 0xFFFFFFFFll)), hi = lane_xor<M>((int)(b >> 32));
+    return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
+}
+
 __device__ __forceinline__ double wave_sum_f64(double v) {
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    v += lane_xor_f64<32>(v);
+    v += lane_xor_f64<16>(v);
+    v += lane_xor_f64<8>(v);
+    v += lane_xor_f64<4>(v);
+    v += lane_xor_f64<2>(v);
+    v += lane_xor_f64<1>(v);
     return v;
 }
 __device__ __forceinline__ float wave_sum_f32(float v) {
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    v += lane_xor_f32<32>(v);
+    v += lane_xor_f32<16>(v);
+    v += lane_xor_f32<8>(v);
+    v += lane_xor_f32<4>(v);
+    v += lane_xor_f32<2>(v);
+    v += lane_xor_f32<1>(v);
     return v;
 }
 __device__ __forceinline__ float wave_max_f32(float v) {
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+    v = fmaxf(v, lane_xor_f32<32>(v));
+    v = fmaxf(v, lane_xor_f32<16>(v));
+    v = fmaxf(v, lane_xor_f32<8>(v));
+    v = fmaxf(v, lane_xor_f32<4>(v));
+    v = fmaxf(v, lane_xor_f32<2>(v));
+    v = fmaxf(v, lane_xor_f32<1>(v));
     return v;
 }
 

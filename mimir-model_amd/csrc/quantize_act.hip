@@ -62,8 +62,8 @@ __device__ __forceinline__ bool qa_chunk(const float4 v, int64_t row, int64_t e0
         m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_QUAD_2301, 0xF, 0xF, false)));
         m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_HALF_MIRROR, 0xF, 0xF, false)));
         m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_ROW_MIRROR, 0xF, 0xF, false)));
-        m = fmaxf(m, __shfl_xor(m, 16));
-        m = fmaxf(m, __shfl_xor(m, 32));
+        m = fmaxf(m, lane_xor_f32<16>(m));
+        m = fmaxf(m, lane_xor_f32<32>(m));
         amax = m;
         bbad = __any(lbad);
     } else {
