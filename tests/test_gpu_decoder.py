@@ -214,6 +214,28 @@ def test_argmax_first_index(gpu, rt):
     s.sync()
     want0 = int(np.nanargmax(y[0]))
     assert dz.download(np.int32).tolist() == [want0, 0, 0]
+    # aligned rows (whole float4s): NaNs inside the float4 of the maximum, a
+    # tie inside one float4, all -inf, +inf twice, a NaN first value
+    z = rng.standard_normal((6, n)).astype(np.float32)
+    z[0, 4000:4004] = [np.nan, 3.0, 70.0, np.nan]
+    z[1, 808:812] = [1.0, 80.0, 2.0, 80.0]
+    z[2, :] = -np.inf
+    z[3, 99] = z[3, 60001] = np.inf
+    z[4, 0] = np.nan
+    z[4, 5000] = 90.0
+    z[5, 1::2] = np.nan
+    z[5, 20002] = 75.0
+
+    def ref(row):  # the reference's loop: best = 0, then x[i] > x[best]
+        if np.isnan(row[0]):
+            return 0
+        return int(np.flatnonzero(row == np.nanmax(row))[0])
+
+    dzz, dzo = dev(rt, z), rt.DeviceBuffer(6 * 4)
+    gpu.argmax_dev(dzz.ptr, 6, n, dzo.ptr, s.handle)
+    s.sync()
+    got = dzo.download(np.int32).tolist()
+    assert got == [ref(r) for r in z] == [4002, 809, 0, 99, 0, 20002]
 
 
 def test_greedy_advance(gpu, rt):
