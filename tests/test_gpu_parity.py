@@ -95,11 +95,15 @@ def test_encoder_gpu_equals_oracle(gpu, oracle, dt):
 
 # ---------------------------------------------------- activation quantizer
 
+@pytest.mark.parametrize("k", [2048, 4096, 4352, 14336])
 @pytest.mark.parametrize("block", [256, 32])
-def test_quantize_act_bitexact(gpu, oracle, block):
+def test_quantize_act_bitexact(gpu, oracle, block, k):
+    """Rows of up to 16 chunks of 256 run in one workgroup, longer rows in
+    several plus a scanning one: both, with refusals in the first and the
+    last chunks."""
     import hiprt
 
-    rows, k = 10, 2048
+    rows = 10
     rng = np.random.default_rng(block)
     x = rng.standard_normal((rows, k)).astype(np.float32)
     x[1] *= np.float32(1e-30)
@@ -108,9 +112,9 @@ def test_quantize_act_bitexact(gpu, oracle, block):
     x[4, 100] = np.nan
     x[5, 1000] = np.float32(2.0 ** 61)
     # refusals in the row's last chunks (another workgroup than the first)
-    x[7, 2000] = np.nan
-    x[8, 1500] = -np.inf
-    x[9, 2047] = np.float32(2.0 ** 60)  # at the limit: not refused
+    x[7, k - 48] = np.nan
+    x[8, k - 548] = -np.inf
+    x[9, k - 1] = np.float32(2.0 ** 60)  # at the limit: not refused
     amax = np.abs(x[6, :block]).max()
     x[6, 1:5] = np.float32([0.5, 1.5, 2.5, -3.5]) * amax / np.float32(127)
     ws_bytes = gpu.a8_workspace_bytes(rows, k)
