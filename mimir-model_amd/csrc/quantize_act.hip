@@ -257,16 +257,20 @@ static hipError_t launch_qa(const float* x, int64_t rows, int64_t K, int block, 
                             hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
     const int64_t chunks = (K + 255) / 256;
-    // Rows of at most 16 chunks (K <= 4096) take one workgroup of a wave per
-    // chunk: no scanning workgroup reads the row a second time, and the
-    // refusal flag is one LDS vote (measured on MI355X: the cfg1 step
-    // 51.2 -> 50.8 us, 8B decode batch 8 +0.9 %). MIMG_QA_ONEWG_CHUNKS
-    // moves the limit, for measurement.
+    // Rows of at most 16 chunks (K <= 4096), and any row of a call with 64
+    // rows or more, take one workgroup of up to 16 waves: no scanning
+    // workgroup reads the row a second time, and the refusal flag is one LDS
+    // vote (measured on MI355X: the cfg1 step 51.2 -> 50.8 us, 8B decode
+    // batch 8 +0.9 %; the 8B prompt of 512 rows +3 % with swiglu + quantize
+    // at K = 14336 so). Few long rows keep many workgroups a row (one
+    // workgroup a row at K = 14336 made the 8B decode step 2.7 % slower).
+    // MIMG_QA_ONEWG_CHUNKS moves the chunk limit, for measurement.
     static const int64_t one_wg = [] {
         const char* e = getenv("MIMG_QA_ONEWG_CHUNKS");
         return e ? (int64_t)atoll(e) : (int64_t)16;
     }();
-    if (MODE != QA_NORM && rows <= 65535 && chunks > one_wg) {
+    const bool fits_one = MODE == QA_PLAIN || chunks <= 16 * 8;  // swiglu: one round of loads
+    if (MODE != QA_NORM && rows <= 65535 && chunks > one_wg && (rows < 64 || !fits_one)) {
         dim3 grid((unsigned)(1 + (chunks + QA_MW_WAVES - 1) / QA_MW_WAVES), (unsigned)rows), blk(64 * QA_MW_WAVES);
         if (block == 256)
             hipLaunchKernelGGL((quantize_act_mw_kernel<256, MODE == QA_NORM ? QA_PLAIN : MODE>), grid, blk, 0, stream,

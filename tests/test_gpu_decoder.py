@@ -831,7 +831,8 @@ def test_swiglu_quant_out_must_be_its_own_buffer(gpu, rt):
         assert not isinstance(e.value, gpu.NotHandled)
 
 
-@pytest.mark.parametrize("rows,n,block,procs", [(1, 14336, 256, 16), (4, 8192, 256, 7), (3, 1792, 32, 16)])
+@pytest.mark.parametrize("rows,n,block,procs", [(1, 14336, 256, 16), (4, 8192, 256, 7), (3, 1792, 32, 16),
+                                                (64, 14336, 256, 16)])
 def test_swiglu_quant_equals_two_launches(gpu, rt, rows, n, block, procs):
     rng = np.random.default_rng(rows + n)
     g = (rng.standard_normal((rows, n)) * 3).astype(np.float32)

@@ -144,6 +144,42 @@ def test_quantize_act_bitexact(gpu, oracle, block, k):
         assert np.array_equal(ys[i], a.q.astype(np.int32).reshape(-1, 16).sum(1)), i
 
 
+@pytest.mark.parametrize("block", [256, 32])
+def test_quantize_act_many_long_rows(gpu, oracle, block):
+    """64 rows of K = 14336 (one workgroup a row from 64 rows): every row
+    bit for bit the restatement, refusals anywhere in the row."""
+    import hiprt
+
+    rows, k = 64, 14336
+    rng = np.random.default_rng(64 + block)
+    x = rng.standard_normal((rows, k)).astype(np.float32)
+    x[3, 14000] = np.nan
+    x[17, 9000] = np.float32(2.0 ** 61)
+    x[40, 255] = -np.inf
+    x[63, 14335] = np.float32(2.0 ** 60)  # at the limit: not refused
+    ws_bytes = gpu.a8_workspace_bytes(rows, k)
+    off = gpu.a8_workspace_offsets(rows, k)
+    ws = hiprt.DeviceBuffer(ws_bytes)
+    ws.zero()
+    xd = hiprt.DeviceBuffer.from_array(x)
+    s = hiprt.Stream()
+    gpu.quantize_act_dev(xd.ptr, rows, k, block, ws.ptr, ws_bytes, s.handle)
+    s.sync()
+    h = ws.download(np.uint8)
+    q = h[off[0]:off[0] + rows * k].view(np.int8).reshape(rows, k)
+    d = h[off[1]:off[1] + rows * k // 32 * 4].view(np.float32).reshape(rows, -1)
+    xs = h[off[2]:off[2] + rows * k // 32 * 2].view(np.int16).reshape(rows, -1)
+    ok = h[off[5]:off[5] + rows * 4].view(np.int32)
+    for i in range(rows):
+        a = oracle.Act(x[i], block)
+        assert bool(ok[i]) == a.ok, i
+        if not a.ok:
+            continue
+        assert np.array_equal(q[i], a.q), i
+        assert bits_equal(d[i], a.d), i
+        assert np.array_equal(xs[i], a.xs), i
+
+
 # ------------------------------------------- block-256 8-bit products (GEMV)
 
 def _weights(oracle, dt, n, k, seed):
