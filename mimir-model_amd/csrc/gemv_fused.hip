@@ -167,12 +167,21 @@ __device__ __forceinline__ int fused_row(const FusedArgs& A, int mi, int tile, i
 // layout). y also goes to LDS (yl) for the float32 path of refused rows.
 // Returns this thread's refusal flag. K % 1024 == 0, K <= 4096.
 constexpr int NORM_R = 4;  // float4s per thread of the normed row, K <= 4096
+// Rounds of the normed row's quantization the lead team runs (the rest go
+// to the other teams, NORM_PER each).
+template <int TEAMS>
+constexpr int NORM_KL = TEAMS == 1 ? NORM_R : 2;
+template <int TEAMS>
+constexpr int NORM_PER = TEAMS == 1 ? 0 : (NORM_R - 2) / (TEAMS - 1);
 
 // The row's loads, issued before the weights (the load counter retires in
 // order): x, resid, scale as float4s t + 256k (clamped; used where inside).
 struct NormRegs {
     float4 x[NORM_R], r[NORM_R], s[NORM_R];
 };
+// (The lead team loads x and resid of every round and the scale of the
+// rounds it quantizes itself, KL; a helper team the scale of its rounds.)
+template <int KL>
 __device__ __forceinline__ void norm_load(const FusedArgs& A, NormRegs& N) {
     const int n4 = (int)(A.K / 4);
 #pragma unroll
@@ -180,10 +189,81 @@ __device__ __forceinline__ void norm_load(const FusedArgs& A, NormRegs& N) {
         const int i = min((int)threadIdx.x + 256 * k, n4 - 1);
         N.x[k] = ((const float4*)A.x)[i];
         if (A.resid) N.r[k] = ((const float4*)A.resid)[i];
-        if (A.scale) N.s[k] = ((const float4*)A.scale)[i];
+        if (k < KL && A.scale) N.s[k] = ((const float4*)A.scale)[i];
+    }
+}
+template <int PER>
+__device__ __forceinline__ void norm_load_helper(const FusedArgs& A, NormRegs& N, int k0) {
+    const int n4 = (int)(A.K / 4), t = threadIdx.x & 255;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int i = min(t + 256 * (k0 + j), n4 - 1);
+        if (A.scale) N.s[j] = ((const float4*)A.scale)[i];
     }
 }
 
+// One round k of the normed row (float4 t + 256k of it, t the thread of its
+// team): y = (v*inv)*scale to yl, quantized into Q as block (t + 256k)/64.
+// Returns the lane's refusal flag.
+__device__ __forceinline__ bool norm_round(const FusedArgs& A, int t, int k, float4 v, float4 s4, float inv, float* yl,
+                                           const QuantLds& Q) {
+    const int lane = t & 63, i = t + 256 * k;
+    float4 o = {v.x * inv, v.y * inv, v.z * inv, v.w * inv};
+    if (A.scale) {
+        o.x = o.x * s4.x;
+        o.y = o.y * s4.y;
+        o.z = o.z * s4.z;
+        o.w = o.w * s4.w;
+    }
+    ((float4*)yl)[i] = o;
+    // block b = i / 64 of 256: this wave's, lane's four at 4*lane
+    const int b = i >> 6;
+    const float xv[4] = {o.x, o.y, o.z, o.w};
+    float av[4] = {fabsf(o.x), fabsf(o.y), fabsf(o.z), fabsf(o.w)};
+    bool lbad = false;
+    float m = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        lbad |= !(av[e] <= 0x1p60f);
+        m = fmaxf(m, av[e]);
+    }
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_QUAD_1032, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_QUAD_2301, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_HALF_MIRROR, 0xF, 0xF, false)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_ROW_MIRROR, 0xF, 0xF, false)));
+    m = fmaxf(m, lane_xor_f32<16>(m));
+    m = fmaxf(m, lane_xor_f32<32>(m));
+    const float amax = m;
+    const bool bbad = __any(lbad);
+    const bool quant = !bbad && amax > 0.f;
+    const float qinv = quant ? 1.0f / amax : 0.f;
+    int qv[4];
+    bool fast[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) fast[e] = quant_rne_fast(xv[e], amax, qinv, qv[e]);
+#pragma unroll
+    for (int e = 0; e < 4; e++) qv[e] = !quant ? 0 : fast[e] ? qv[e] : quant_rne(xv[e], amax, qinv);
+    *(uint32_t*)(Q.q + 4 * i) = (uint32_t)(qv[0] & 0xFF) | ((uint32_t)(qv[1] & 0xFF) << 8) |
+                                ((uint32_t)(qv[2] & 0xFF) << 16) | ((uint32_t)(qv[3] & 0xFF) << 24);
+    const int s4i = qv[0] + qv[1] + qv[2] + qv[3];
+    int s16 = s4i + __builtin_amdgcn_mov_dpp(s4i, DPP_QUAD_1032, 0xF, 0xF, false);
+    s16 += __builtin_amdgcn_mov_dpp(s16, DPP_QUAD_2301, 0xF, 0xF, false);
+    const int s32 = s16 + __builtin_amdgcn_mov_dpp(s16, DPP_HALF_MIRROR, 0xF, 0xF, false);
+    if ((lane & 3) == 0) Q.ys16[i >> 2] = (int16_t)s16;
+    if ((lane & 7) == 0) Q.xs[i >> 3] = (int16_t)s32;
+    if (lane == 0) Q.dx[b] = amax / 127.0f;
+    return lbad;
+}
+
+__device__ __forceinline__ float norm_inv(const FusedArgs& A, const double* part) {
+    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
+    return (float)(1.0 / sqrt((double)(float)(tot / (double)A.K) + (double)A.eps));
+}
+
+// The lead team: x + resid of every round, the sum of squares, then the
+// rounds k < KL; rounds from KL on go to the helper teams, which read
+// x + resid from yl (written here before the barrier) and overwrite it with y.
+template <int KL>
 __device__ __forceinline__ bool norm_quantize_lds(const FusedArgs& A, const NormRegs& N, bool write_x, float* yl,
                                                   double* part, const QuantLds& Q) {
     constexpr int NR = NORM_R;
@@ -203,6 +283,7 @@ __device__ __forceinline__ bool norm_quantize_lds(const FusedArgs& A, const Norm
                 v[k].w = v[k].w + N.r[k].w;
             }
             if (write_x) ((float4*)A.x_out)[i] = v[k];
+            if (k >= KL) ((float4*)yl)[i] = v[k];
             ss += (double)v[k].x * (double)v[k].x + (double)v[k].y * (double)v[k].y +
                   (double)v[k].z * (double)v[k].z + (double)v[k].w * (double)v[k].w;
         }
@@ -210,59 +291,29 @@ __device__ __forceinline__ bool norm_quantize_lds(const FusedArgs& A, const Norm
     ss = wave_sum_f64(ss);
     if (lane == 0) part[w] = ss;
     lds_barrier();
-    const double tot = (part[0] + part[1]) + (part[2] + part[3]);
-    const float inv = (float)(1.0 / sqrt((double)(float)(tot / (double)A.K) + (double)A.eps));
+    const float inv = norm_inv(A, part);
     bool bad = false;
 #pragma unroll
-    for (int k = 0; k < NR; k++) {
-        const int i = t + 256 * k;
-        if (i >= n4) continue;  // uniform within the wave (K % 1024 == 0)
-        float4 o = {v[k].x * inv, v[k].y * inv, v[k].z * inv, v[k].w * inv};
-        if (A.scale) {
-            const float4 s4 = N.s[k];
-            o.x = o.x * s4.x;
-            o.y = o.y * s4.y;
-            o.z = o.z * s4.z;
-            o.w = o.w * s4.w;
-        }
-        ((float4*)yl)[i] = o;
-        // block b = i / 64 of 256: this wave's, lane's four at 4*lane
-        const int b = i >> 6;
-        const float xv[4] = {o.x, o.y, o.z, o.w};
-        float av[4] = {fabsf(o.x), fabsf(o.y), fabsf(o.z), fabsf(o.w)};
-        bool lbad = false;
-        float m = 0.f;
+    for (int k = 0; k < KL; k++) {
+        if (t + 256 * k >= n4) continue;  // uniform within the wave (K % 1024 == 0)
+        bad |= norm_round(A, t, k, v[k], N.s[k], inv, yl, Q);
+    }
+    return bad;
+}
+
+// A helper team's rounds k0 .. k0 + PER - 1, after the lead's barrier.
+template <int PER>
+__device__ __forceinline__ bool norm_quantize_helper(const FusedArgs& A, const NormRegs& N, int k0, float* yl,
+                                                     double* part, const QuantLds& Q) {
+    const int t = threadIdx.x & 255, n4 = (int)(A.K / 4);
+    lds_barrier();
+    const float inv = norm_inv(A, part);
+    bool bad = false;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-            lbad |= !(av[e] <= 0x1p60f);
-            m = fmaxf(m, av[e]);
-        }
-        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_QUAD_1032, 0xF, 0xF, false)));
-        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_QUAD_2301, 0xF, 0xF, false)));
-        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_HALF_MIRROR, 0xF, 0xF, false)));
-        m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), DPP_ROW_MIRROR, 0xF, 0xF, false)));
-        m = fmaxf(m, lane_xor_f32<16>(m));
-        m = fmaxf(m, lane_xor_f32<32>(m));
-        const float amax = m;
-        const bool bbad = __any(lbad);
-        bad |= lbad;
-        const bool quant = !bbad && amax > 0.f;
-        const float qinv = quant ? 1.0f / amax : 0.f;
-        int qv[4];
-        bool fast[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) fast[e] = quant_rne_fast(xv[e], amax, qinv, qv[e]);
-#pragma unroll
-        for (int e = 0; e < 4; e++) qv[e] = !quant ? 0 : fast[e] ? qv[e] : quant_rne(xv[e], amax, qinv);
-        *(uint32_t*)(Q.q + 4 * i) = (uint32_t)(qv[0] & 0xFF) | ((uint32_t)(qv[1] & 0xFF) << 8) |
-                                    ((uint32_t)(qv[2] & 0xFF) << 16) | ((uint32_t)(qv[3] & 0xFF) << 24);
-        const int s4 = qv[0] + qv[1] + qv[2] + qv[3];
-        int s16 = s4 + __builtin_amdgcn_mov_dpp(s4, DPP_QUAD_1032, 0xF, 0xF, false);
-        s16 += __builtin_amdgcn_mov_dpp(s16, DPP_QUAD_2301, 0xF, 0xF, false);
-        const int s32 = s16 + __builtin_amdgcn_mov_dpp(s16, DPP_HALF_MIRROR, 0xF, 0xF, false);
-        if ((lane & 3) == 0) Q.ys16[i >> 2] = (int16_t)s16;
-        if ((lane & 7) == 0) Q.xs[i >> 3] = (int16_t)s32;
-        if (lane == 0) Q.dx[b] = amax / 127.0f;
+    for (int j = 0; j < PER; j++) {
+        const int k = k0 + j;
+        if (t + 256 * k >= n4) continue;  // uniform
+        bad |= norm_round(A, t, k, ((const float4*)yl)[t + 256 * k], N.s[j], inv, yl, Q);
     }
     return bad;
 }
@@ -310,9 +361,11 @@ __device__ __forceinline__ ActLane act_lane_lds(const QuantLds& Q, int b, int l)
 // the row once: the lead team (threads 0..255) loads x and fills the shared
 // LDS row while every team's weights are in flight; the other teams meet it
 // at the same barriers. `smem` is the shared row, `tmem` the team's region.
-template <uint32_t DT, int U, bool SHARED, bool NORM, int RD>
+template <uint32_t DT, int U, bool SHARED, bool NORM, int RD, int TEAMS>
 __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F, int mi, int tile, uint8_t* smem,
-                                           uint8_t* tmem, double* npart, int* wflag, int nwaves, bool lead) {
+                                           uint8_t* tmem, double* npart, int* wflag, int team) {
+    const bool lead = team == 0;
+    constexpr int nwaves = 4 * TEAMS;
     constexpr bool ROPE = RD != 0;
     constexpr int BYTES = DT == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     const int nb = A.nb, R = F.R, np = R * nb;
@@ -342,8 +395,10 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     float4 xv[4];
     NormRegs N;
     if (lead) {
-        if constexpr (NORM) norm_load(A, N);
+        if constexpr (NORM) norm_load<NORM_KL<TEAMS>>(A, N);
         else load_x16(A.x, min(bq, nb - 1), j, xv);
+    } else if constexpr (NORM && TEAMS > 1) {
+        norm_load_helper<NORM_PER<TEAMS>>(A, N, NORM_KL<TEAMS> + (team - 1) * NORM_PER<TEAMS>);
     }
     const int frow = min(fused_row<RD>(A, mi, tile, R, min(t, R - 1)), F.N - 1);
     const int wr = F.wref[frow];
@@ -389,8 +444,8 @@ __device__ __forceinline__ void fused_body(const FusedArgs& A, const FusedMat& F
     // weights arrive (lead team; the others wait at its barrier).
     bool bad = false;
     if constexpr (NORM) {
-        if (lead) bad = norm_quantize_lds(A, N, blockIdx.x == 0, yl, npart, Q);
-        else lds_barrier();
+        if (lead) bad = norm_quantize_lds<NORM_KL<TEAMS>>(A, N, blockIdx.x == 0, yl, npart, Q);
+        else bad = norm_quantize_helper<NORM_PER<TEAMS>>(A, N, NORM_KL<TEAMS> + (team - 1) * NORM_PER<TEAMS>, yl, npart, Q);
     } else if (lead) {
         bad = bq < nb ? quantize_block_lds(xv, bq, j, Q) : false;
         for (int b = bq + 16; b < nb; b += 16) {  // rows longer than 4096
@@ -526,8 +581,8 @@ __global__ __launch_bounds__(256 * TEAMS) void gemv_a8k_fused_kernel(FusedArgs A
     const int tile = gt - F.tile0;
     uint8_t* tmem = smem + A.lds_row + (size_t)team * A.lds_team;
     if (F.dt == DT_Q4_K)
-        fused_body<DT_Q4_K, U, SHARED, NORM, RD>(A, F, mi, tile, smem, tmem, npart, wflag, 4 * TEAMS, team == 0);
-    else fused_body<DT_Q6_K, U, SHARED, NORM, RD>(A, F, mi, tile, smem, tmem, npart, wflag, 4 * TEAMS, team == 0);
+        fused_body<DT_Q4_K, U, SHARED, NORM, RD, TEAMS>(A, F, mi, tile, smem, tmem, npart, wflag, team);
+    else fused_body<DT_Q6_K, U, SHARED, NORM, RD, TEAMS>(A, F, mi, tile, smem, tmem, npart, wflag, team);
 }
 
 // LDS of the shared row: q, dx, xs, ys16 (and the normed row, K floats).
