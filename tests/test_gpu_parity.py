@@ -558,10 +558,12 @@ def test_fused_teams_refusals(gpu, oracle, dt):
     W.release()
 
 
-def test_fused_quantizer_ties(gpu, oracle):
+@pytest.mark.parametrize("k,n", [(1024, 64), (4096, 4096)])
+def test_fused_quantizer_ties(gpu, oracle, k, n):
     """Activations on exact half-integer steps (127 x / amax = n + 1/2) and
-    next to them: the in-kernel quantizer must round exactly as the reference."""
-    k, n = 1024, 64
+    next to them: the in-kernel quantizer must round exactly as the reference
+    (one team a workgroup, 16 threads a block; 4096 x 4096: two teams, 32
+    threads a block)."""
     wb = _weights(oracle, Q4_K, n, k, seed=35)
     W = gpu.Weight(wb, Q4_K, n, k)
     rng = np.random.default_rng(36)
