@@ -503,6 +503,10 @@ _NORM_GROUPS = {
     "llama8b_full_qkv": (4096, [(Q4_K, 4096), (Q4_K, 1024), (Q6_K, 1024)], True, None),
     "teams_refused_row": (4096, [(Q4_K, 4096), (Q4_K, 1024), (Q6_K, 1024)], True, "huge"),
     "teams_refused_weight": (4096, [(Q4_K, 4096)], True, "inf_scale"),
+    # rows of two and three rounds of 1024: the helper teams' rounds past the
+    # row are skipped (512 tiles of 16 rows, two teams; 768 of 10, three)
+    "teams_k2048": (2048, [(Q4_K, 4096), (Q4_K, 2048), (Q6_K, 2048)], True, None),
+    "teams_k3072": (3072, [(Q4_K, 5120), (Q4_K, 1280), (Q6_K, 1280)], True, "inf_scale"),
 }
 
 
