@@ -304,6 +304,9 @@ def main():
     ap.add_argument("--decode-batches", default="1,8", help="batch sizes of the llama8b decode runs")
     ap.add_argument("--decode", default="llama1b,llama8b",
                     help="whole-model decode runs (comma list of llama1b, llama8b; empty to skip)")
+    ap.add_argument("--step", default="group", choices=["chain", "group"],
+                    help="group: one launch per grouped call (default); chain: the four grouped products as one chain "
+                         "launch (mimg_linear_a8_chain_dev, one row only)")
     ap.add_argument("--roofline-replays", type=int, default=8,
                     help="replays of the graph of --rotate single-kernel launches timed for the roofline")
     args = ap.parse_args()
@@ -410,7 +413,20 @@ def main():
     # their own.
     groups = [[c for c in CFG1 if c[5] == i] for i in range(len(INPUT_K))]
 
+    use_chain = args.step == "chain"
+    if use_chain and M != 1:
+        raise SystemExit("--step chain runs one activation row (--rows 1)")
+    sync_bytes = mimg.chain_sync_bytes()
+    sync = hiprt.DeviceBuffer(sync_bytes)
+    mimg.chain_sync_init(sync.ptr, sync_bytes, stream.handle)
+
     def enqueue_step(l):
+        if use_chain:
+            # the layer set as one launch: four phases, each phase's weights
+            # streamed without a break after the one before
+            mimg.linear_a8_chain_dev([([layers[l][c[0]] for c in grp], xd[i].ptr, None, [yd[c[0]].ptr for c in grp])
+                                      for i, grp in enumerate(groups)], sync.ptr, sync_bytes, stream.handle)
+            return
         for i, grp in enumerate(groups):
             mimg.linear_a8_group_dev([layers[l][c[0]] for c in grp], xd[i].ptr, M, None, 256,
                                      [yd[c[0]].ptr for c in grp], ws[i].ptr, ws_bytes[i], stream.handle)
@@ -442,7 +458,12 @@ def main():
     ms_gpu = e0.elapsed_ms(e1)
     ms_per_step = ms_gpu / args.steps
     value = step_bytes(M) / (ms_per_step * 1e-3) / 1e9
-    log(f"  timed: {args.steps} steps, {ms_per_step * 1e3:.2f} us/step (events), wall {wall * 1e6 / args.steps:.2f} us/step, {value:.1f} GB/s")
+    log(f"  timed ({'chain' if use_chain else 'group calls'}): {args.steps} steps, {ms_per_step * 1e3:.2f} us/step "
+        f"(events), wall {wall * 1e6 / args.steps:.2f} us/step, {value:.1f} GB/s")
+    if use_chain:
+        st = mimg.chain_status(sync.ptr)
+        if st:
+            raise SystemExit(f"chain status {st}: a device barrier wait timed out")
 
     # Roofline of the dominant kernel of the step: the Q4_K GEMV launch that
     # computes gate and up together (2 x 14336 x 4096, 66 MB; the step's

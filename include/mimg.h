@@ -180,6 +180,45 @@ int mimg_linear_a8_group_dev(const uint64_t *w, int count, const float *x, int64
                              const float *const *bias, int block, float *const *y, void *ws,
                              uint64_t ws_bytes, void *stream);
 
+/* One phase of mimg_linear_a8_chain_dev: the grouped product of `count`
+ * (1..3) weights sharing K on the input row x, as mimg_linear_a8_group_dev
+ * with one activation row and blocks of 256. */
+typedef struct {
+    const float *x;       /* [K], 16-byte aligned */
+    int count;
+    uint64_t w[3];
+    const float *bias[3]; /* each [N_i] or NULL */
+    float *y[3];          /* each [N_i] */
+} mimg_chain_phase;
+
+/* A chain of 1..8 such phases in one launch, bit for bit the calls
+ * mimg_linear_a8_group_dev(phase 0), then phase 1, ... in order: a
+ * phase's x may be an output of an earlier phase of the chain (the
+ * q/k/v -> o -> gate/up -> down sequence of calls importer/llama.go:423-534
+ * writes for one decoder layer, each a dequant_matmul_a8.v2 at
+ * interp/fast.go:246-379). The weights of every phase stream from HBM
+ * without a break between the phases; a phase waits for the one before it
+ * on a device-wide barrier whose counters live in `sync` (at least
+ * mimg_chain_sync_bytes(), 256-byte aligned, zeroed once before its first
+ * use, e.g. by mimg_chain_sync_init; its counters only grow, so a captured
+ * graph of the call can be replayed). Calls that share a sync buffer must
+ * not overlap in time. y of a phase must not overlap that phase's x, nor
+ * another y of the same phase (MIMG_ERR_ARG). Returns MIMG_NOT_HANDLED
+ * (nothing launched) unless every weight is Q4_K or Q6_K with K a multiple
+ * of 256 up to 16384, its rows a multiple of 16 bytes (Q6_K: K a multiple
+ * of 2048) and at most 16 KB: the caller then makes the group calls.
+ * A phase whose barrier wait exceeds its bound (only if the GPU cannot hold
+ * every workgroup of the launch at once) finishes without valid outputs and
+ * sets the status word that mimg_chain_status reports. */
+int mimg_linear_a8_chain_dev(const mimg_chain_phase *phases, int nphase, void *sync, uint64_t sync_bytes,
+                             void *stream);
+uint64_t mimg_chain_sync_bytes(void);
+/* Zeroes a sync buffer on `stream` (a fill kernel, safe under capture). */
+int mimg_chain_sync_init(void *sync, uint64_t sync_bytes, void *stream);
+/* Reads the status word of a sync buffer into *status (0: every barrier
+ * wait completed) and clears it; synchronises with the device. */
+int mimg_chain_status(void *sync, uint32_t *status);
+
 /* mimg_linear_a8_dev without a workspace argument, for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc): the quantized activations go to a scratch array

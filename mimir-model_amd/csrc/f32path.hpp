@@ -82,7 +82,15 @@ __device__ __forceinline__ float hsum_group8(float y0, float y1, float y2, float
 // refused rows only, so it is written for few live registers (loops kept
 // rolled, each chunk's scales decoded once) rather than speed: it is inlined
 // into the 8-bit kernels and must not raise their register count.
-template <uint32_t DT>
+// A read of x: plain, or (COH) an agent-scope load that sees stores made
+// by other workgroups of the same launch (a row produced inside a kernel).
+template <bool COH>
+__device__ __forceinline__ float ldx(const float* p) {
+    if constexpr (COH) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return *p;
+}
+
+template <uint32_t DT, bool COH = false>
 __device__ float f32dot_g8(const uint8_t* row, const float* x, int64_t K, bool fused) {
     const int l = threadIdx.x & 7;
     float Y[4] = {0.f, 0.f, 0.f, 0.f};
@@ -92,7 +100,7 @@ __device__ float f32dot_g8(const uint8_t* row, const float* x, int64_t K, bool f
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 int64_t e = 32 * s + 8 * r + l;
-                Y[r] = __builtin_fmaf(x[e], decode_weight<DT>(row, e), Y[r]);
+                Y[r] = __builtin_fmaf(ldx<COH>(x + e), decode_weight<DT>(row, e), Y[r]);
             }
     } else if (DT == DT_Q4_K) {
 #pragma unroll 1
@@ -122,8 +130,8 @@ __device__ float f32dot_g8(const uint8_t* row, const float* x, int64_t K, bool f
                     const uint32_t byte = q[i];
                     const float wl = s0 * (float)(byte & 0xF) - o0;
                     const float wh = s1 * (float)(byte >> 4) - o1;
-                    Y[ra] = __builtin_fmaf(wl, xc[i], Y[ra]);
-                    Y[ra + 1] = __builtin_fmaf(wh, xc[32 + i], Y[ra + 1]);
+                    Y[ra] = __builtin_fmaf(wl, ldx<COH>(xc + i), Y[ra]);
+                    Y[ra + 1] = __builtin_fmaf(wh, ldx<COH>(xc + 32 + i), Y[ra + 1]);
                 }
             }
         }
@@ -138,7 +146,7 @@ __device__ float f32dot_g8(const uint8_t* row, const float* x, int64_t K, bool f
                     for (int p = 0; p < 4; p++) {
                         int e = 128 * h + 32 * p + 8 * st + l;
                         float w = q6k_weight(row + b * Q6K_BYTES, e);
-                        Y[p] = __builtin_fmaf(w, x[256 * b + e], Y[p]);
+                        Y[p] = __builtin_fmaf(w, ldx<COH>(x + 256 * b + e), Y[p]);
                     }
     } else {
 #pragma unroll 1
@@ -147,7 +155,7 @@ __device__ float f32dot_g8(const uint8_t* row, const float* x, int64_t K, bool f
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const float w = d * (float)(int8_t)row[b * Q80_BYTES + 2 + 8 * r + l];
-                Y[r] = __builtin_fmaf(w, x[32 * b + 8 * r + l], Y[r]);
+                Y[r] = __builtin_fmaf(w, ldx<COH>(x + 32 * b + 8 * r + l), Y[r]);
             }
         }
     }

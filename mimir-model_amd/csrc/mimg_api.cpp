@@ -65,6 +65,9 @@ std::map<uintptr_t, Upload> g_uploads;
 
 std::mutex g_mu;
 int g_device = -1;
+// Workgroups of a chain launch: one per CU when the chain kernel fits a CU
+// (set by mimg_init), else 0.
+int g_chain_wgs = 0;
 
 // Scratch of mimg_linear_a8_noalloc_dev: the quantized activations
 // (act_layout) in a file-scope device array, so that the call allocates
@@ -474,6 +477,11 @@ int mimg_init(int device) {
             return fail(MIMG_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
         g_scratch[device] = p;
     }
+    if (chain_occupancy() >= 1) {
+        int cus = 0;
+        HIP_TRY(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+        g_chain_wgs = cus;
+    }
     g_device = device;
     return MIMG_OK;
 }
@@ -874,6 +882,126 @@ int mimg_linear_a8_dev(uint64_t wh, const float* x, int64_t rows, const float* b
     const float* bs[1] = {bias};
     float* ys[1] = {y};
     return mimg_linear_a8_group_dev(&wh, 1, x, rows, bs, block, ys, ws, ws_bytes, stream);
+}
+
+// The most rows any of G workgroups gets of a chain phase: the kernel's
+// byte-balanced split (workgroup g takes the rows starting in bytes
+// [floor(g*B/G), floor((g+1)*B/G)) of the phase's B weight bytes).
+static int64_t chain_max_wg_rows(const ChainPhase& P, int G) {
+    auto row_at = [&](int64_t b) {
+        int64_t start = 0, base = 0;
+        for (int i = 0; i < P.nmat; i++) {
+            const int64_t rb = P.m[i].rb, end = start + (int64_t)P.m[i].N * rb;
+            if (b <= end || i == P.nmat - 1) {
+                const int64_t num = b > start ? b - start : 0;
+                int64_t q = (num + rb - 1) / rb;
+                if (q > P.m[i].N) q = P.m[i].N;
+                return base + q;
+            }
+            start = end;
+            base += P.m[i].N;
+        }
+        return base;
+    };
+    int64_t most = 0, prev = row_at(0);
+    for (int g = 0; g < G; g++) {
+        const int64_t next = row_at(P.bytes * (g + 1) / G);
+        if (next - prev > most) most = next - prev;
+        prev = next;
+    }
+    return most;
+}
+
+uint64_t mimg_chain_sync_bytes(void) { return CHAIN_SYNC_BYTES; }
+
+int mimg_chain_sync_init(void* sync, uint64_t sync_bytes, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!sync || !aligned(sync, 256) || sync_bytes < CHAIN_SYNC_BYTES)
+        return fail(MIMG_ERR_ARG, "sync must be 256-byte aligned and hold mimg_chain_sync_bytes() = %llu bytes",
+                    (unsigned long long)CHAIN_SYNC_BYTES);
+    HIP_TRY(launch_chain_zero(sync, CHAIN_SYNC_BYTES, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
+int mimg_chain_status(void* sync, uint32_t* status) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!sync || !status) return fail(MIMG_ERR_ARG, "sync and status must not be null");
+    HIP_TRY(hipDeviceSynchronize());
+    HIP_TRY(hipMemcpy(status, sync, 4, hipMemcpyDeviceToHost));
+    const uint32_t zero = 0;
+    HIP_TRY(hipMemcpy(sync, &zero, 4, hipMemcpyHostToDevice));
+    return MIMG_OK;
+}
+
+int mimg_linear_a8_chain_dev(const mimg_chain_phase* phases, int nphase, void* sync, uint64_t sync_bytes,
+                             void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!phases || nphase < 1 || nphase > CHAIN_MAXP)
+        return fail(MIMG_ERR_ARG, "a chain holds 1 to %d phases, got %d", CHAIN_MAXP, nphase);
+    if (!sync || !aligned(sync, 256) || sync_bytes < CHAIN_SYNC_BYTES)
+        return fail(MIMG_ERR_ARG, "sync must be 256-byte aligned and hold mimg_chain_sync_bytes() = %llu bytes",
+                    (unsigned long long)CHAIN_SYNC_BYTES);
+    const int cus = g_chain_wgs;
+    if (cus <= 0) return fail(MIMG_NOT_HANDLED, "the chain kernel cannot be resident on this device");
+    Held held[CHAIN_MAXP * 3];
+    ChainArgs A;
+    memset(&A, 0, sizeof A);
+    for (int p = 0; p < nphase; p++) {
+        const mimg_chain_phase& ph = phases[p];
+        if (ph.count < 1 || ph.count > 3) return fail(MIMG_ERR_ARG, "phase %d: a group holds 1 to 3 weights, got %d", p, ph.count);
+        if (!ph.x || !aligned(ph.x, 16)) return fail(MIMG_ERR_ARG, "phase %d: x must be 16-byte aligned", p);
+        ChainPhase& P = A.ph[p];
+        P.x = ph.x;
+        P.nmat = ph.count;
+        int64_t ns[3];
+        for (int i = 0; i < ph.count; i++) {
+            Held& h = held[3 * p + i];
+            if ((rc = h.acquire(ph.w[i]))) return rc;
+            const DevWeight& dw = h->dw;
+            if (i > 0 && dw.k != P.K) return fail(MIMG_ERR_ARG, "phase %d: the weights of a group must share K", p);
+            if (!ph.y[i]) return fail(MIMG_ERR_ARG, "phase %d: output %d is null", p, i);
+            if (dw.dt != DT_Q4_K && dw.dt != DT_Q6_K)
+                return fail(MIMG_NOT_HANDLED, "phase %d: %s has no chain kernel", p, dt_name(dw.dt));
+            if (dw.k % 256 || dw.k > CHAIN_MAXK || dw.row_bytes % 16 || dw.row_bytes > CHAIN_STAGE_BYTES ||
+                dw.n > (1 << 30))
+                return fail(MIMG_NOT_HANDLED, "phase %d: %s [%lld, %lld] does not fit the chain's stages", p,
+                            dt_name(dw.dt), (long long)dw.n, (long long)dw.k);
+            P.K = (int32_t)dw.k;
+            P.nb = (int32_t)(dw.k / 256);
+            ChainMat& M = P.m[i];
+            M.W = dw.data;
+            M.wref = dw.wref;
+            M.bias = ph.bias[i];
+            M.y = ph.y[i];
+            M.N = (int32_t)dw.n;
+            M.dt = (int32_t)dw.dt;
+            M.rb = (int32_t)dw.row_bytes;
+            M.nref = dw.n_refused > 0 ? 1 : 0;
+            const int64_t by_bytes = CHAIN_STAGE_BYTES / dw.row_bytes, by_pairs = CHAIN_MAX_PAIRS / P.nb;
+            M.rps = (int32_t)(by_bytes < by_pairs ? by_bytes : by_pairs);
+            P.bytes += dw.n * dw.row_bytes;
+            ns[i] = dw.n;
+        }
+        if ((rc = check_outputs(ph.x, 1, P.K, ns, ph.y, ph.count))) return rc;
+        if (chain_max_wg_rows(P, cus) * P.nb > CHAIN_TABLE_ENTRIES)
+            return fail(MIMG_NOT_HANDLED, "phase %d: more than %d (row, block) pairs for a workgroup", p,
+                        CHAIN_TABLE_ENTRIES);
+        for (int i = 0; i < ph.count; i++)
+            for (int j = i + 1; j < ph.count; j++) {
+                const uintptr_t a0 = (uintptr_t)ph.y[i], a1 = a0 + (uint64_t)ns[i] * 4;
+                const uintptr_t b0 = (uintptr_t)ph.y[j], b1 = b0 + (uint64_t)ns[j] * 4;
+                if (a0 < b1 && b0 < a1) return fail(MIMG_ERR_ARG, "phase %d: outputs %d and %d overlap", p, i, j);
+            }
+    }
+    A.nphase = nphase;
+    A.G = cus;
+    A.lines = cus < CHAIN_LINES ? cus : CHAIN_LINES;
+    A.sync = (uint64_t*)sync;
+    HIP_TRY(launch_chain(A, (hipStream_t)stream));
+    return MIMG_OK;
 }
 
 int mimg_linear_a8_noalloc_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, int block, float* y,

@@ -189,4 +189,38 @@ struct ReadRanges {
 hipError_t launch_stream_read(const ReadRanges& r, int per, uint32_t* sink, hipStream_t s);
 hipError_t launch_normal_fill(uint64_t seed, float stdv, float* dst, int64_t n, hipStream_t stream);
 
+// A chain of dependent one-row products in one launch (chain.hip): phase p
+// is the grouped 8-bit product (blocks of 256) of up to three Q4_K / Q6_K
+// matrices with its input row x; a phase may read rows earlier phases
+// wrote. One workgroup per CU, all resident at once (G = the CU count).
+constexpr int CHAIN_MAXP = 8;            // phases per launch
+constexpr int CHAIN_MAXK = 16384;        // input row length
+constexpr int CHAIN_STAGE_BYTES = 16384; // a stage: whole rows, at most this many bytes
+constexpr int CHAIN_MAX_PAIRS = 128;     // (row, block) pairs per stage
+constexpr int CHAIN_LINES = 16;          // line counters of a device barrier
+constexpr int CHAIN_TABLE_ENTRIES = 2560;  // (row, block) pairs of one phase per workgroup
+struct ChainMat {
+    const uint8_t* W;     // rows of rb bytes (rb a multiple of 16)
+    const uint8_t* wref;  // [N] weight-row refusal flags
+    const float* bias;    // [N] or null
+    float* y;             // [N]
+    int32_t N, dt, rb, rps;  // rps: rows per stage
+    int32_t nref, pad;    // rows with a refused block scale (0: wref is not read)
+};
+struct ChainPhase {
+    const float* x;       // [K], 16-byte aligned
+    int64_t bytes;        // weight bytes of the phase's matrices
+    int32_t K, nb, nmat, pad;
+    ChainMat m[3];
+};
+struct ChainArgs {
+    ChainPhase ph[CHAIN_MAXP];
+    uint64_t* sync;       // status word, then (nphase-1) x (1 + CHAIN_LINES) counters 128 bytes apart
+    int32_t nphase, G, lines, pad;
+};
+constexpr uint64_t CHAIN_SYNC_BYTES = 128ull * (1 + (CHAIN_MAXP - 1) * (1 + CHAIN_LINES));
+int chain_occupancy();  // resident chain workgroups per CU
+hipError_t launch_chain(const ChainArgs& A, hipStream_t stream);
+hipError_t launch_chain_zero(void* p, uint64_t bytes, hipStream_t stream);  // bytes: a multiple of 8
+
 }  // namespace mimg

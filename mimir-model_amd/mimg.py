@@ -45,6 +45,10 @@ SIGNATURES = {
     "mimg_linear_a8_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P, _U64, _P]),
     "mimg_linear_a8_group_dev": (_I, [ctypes.POINTER(_U64), _I, _P, _I64, ctypes.POINTER(_P), _I,
                                       ctypes.POINTER(_P), _P, _U64, _P]),
+    "mimg_linear_a8_chain_dev": (_I, [_P, _I, _P, _U64, _P]),
+    "mimg_chain_sync_bytes": (_U64, []),
+    "mimg_chain_sync_init": (_I, [_P, _U64, _P]),
+    "mimg_chain_status": (_I, [_P, ctypes.POINTER(_U32)]),
     "mimg_rms_norm_linear_a8_group_dev": (_I, [ctypes.POINTER(_U64), _I, _P, _P, _P, ctypes.c_float, _P,
                                                ctypes.POINTER(_P), ctypes.POINTER(_P), _P]),
     "mimg_matmul_a8_quantized_swiglu_dev": (_I, [ctypes.POINTER(_U64), _P, _I64, ctypes.POINTER(_P), _I, _P, _I, _P,
@@ -257,6 +261,43 @@ def linear_a8_group_dev(weights, x_ptr, rows, bias_ptrs, block, y_ptrs, ws_ptr, 
     bs = None if bias_ptrs is None else (_P * n)(*[_P(p) if p else None for p in bias_ptrs])
     _check(load().mimg_linear_a8_group_dev(hs, n, _P(x_ptr), rows, bs, block, ys,
                                            _P(ws_ptr) if ws_ptr else None, ws_bytes, _P(stream)))
+
+
+class _ChainPhase(ctypes.Structure):
+    """mimg_chain_phase (include/mimg.h)."""
+    _fields_ = [("x", _P), ("count", _I), ("w", _U64 * 3), ("bias", _P * 3), ("y", _P * 3)]
+
+
+def chain_sync_bytes():
+    return int(load().mimg_chain_sync_bytes())
+
+
+def chain_sync_init(sync_ptr, sync_bytes, stream):
+    _check(load().mimg_chain_sync_init(_P(sync_ptr), sync_bytes, _P(stream)))
+
+
+def chain_status(sync_ptr):
+    """The sync buffer's status word (0: every barrier wait completed), cleared."""
+    v = _U32(0)
+    _check(load().mimg_chain_status(_P(sync_ptr), ctypes.byref(v)))
+    return int(v.value)
+
+
+def linear_a8_chain_dev(phases, sync_ptr, sync_bytes, stream):
+    """One launch for a chain of one-row grouped products, bit for bit the
+    linear_a8_group_dev calls in order (rows 1, block 256). phases: a list of
+    (weights, x_ptr, bias_ptrs or None, y_ptrs); raises NotHandled where the
+    chain kernel does not apply."""
+    arr = (_ChainPhase * len(phases))()
+    for i, (weights, x_ptr, bias_ptrs, y_ptrs) in enumerate(phases):
+        ph = arr[i]
+        ph.x = x_ptr
+        ph.count = len(weights)
+        for j, w in enumerate(weights):
+            ph.w[j] = w.handle
+            ph.y[j] = y_ptrs[j]
+            ph.bias[j] = bias_ptrs[j] if bias_ptrs and bias_ptrs[j] else None
+    _check(load().mimg_linear_a8_chain_dev(ctypes.cast(arr, _P), len(phases), _P(sync_ptr), sync_bytes, _P(stream)))
 
 
 def rms_norm_linear_a8_group_dev(weights, x_ptr, resid_ptr, scale_ptr, eps, x_out_ptr, bias_ptrs, y_ptrs, stream):
