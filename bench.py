@@ -353,6 +353,9 @@ def main():
             for l in range(args.rotate):
                 if f32:
                     mimg.linear_f32_mfma_dev(src[l][name], xp.ptr, rows, None, yp.ptr, stream.handle)
+                elif q8_layers:
+                    mimg.matmul_a8_quantized_q8_0_tiled_dev(src[l][name], xp.ptr, rows, None, yp.ptr, wsp.ptr, wsb,
+                                                            stream.handle)
                 else:
                     mimg.matmul_a8_quantized_dev(src[l][name], xp.ptr, rows, None, block, yp.ptr, wsp.ptr, wsb,
                                                  stream.handle)
@@ -650,8 +653,9 @@ def main():
         },
         "prefill_q8_0": {
             "workload": "cfg2's Q8_0 variant: gate 14336x4096 and down 4096x14336 Q8_0 (62 MB each), "
-                        "dequant_matmul_a8.v1 (activation blocks of 32) on the int8 MFMA GEMM, one float chain of "
-                        "exact block sums (within the spec's a8 tolerance), activations quantized beforehand",
+                        "dequant_matmul_a8.v1 (activation blocks of 32) on the int8 MFMA GEMM "
+                        "(mimg_matmul_a8_quantized_q8_0_tiled_dev, opt-in: one float chain of exact block sums, "
+                        "within the spec's a8 tolerance), activations quantized beforehand",
             "results": prefill_q8,
         },
         "prefill_f32": {

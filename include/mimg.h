@@ -61,8 +61,12 @@ int mimg_init(int device);
 /* Waits for the device, frees every registered weight (a view's bytes with
  * its section), every uploaded weights section and the calling thread's
  * stream and buffers (other threads' go when those threads exit), and
- * forgets the device, so mimg_init may be called again. No call may be in
- * flight on another thread. */
+ * forgets the device, so mimg_init may be called again. A weight that a
+ * call on another thread still holds is unlinked instead and freed after
+ * that call returns (with its section, for a view), at the next release,
+ * registration or shutdown; such a call must not start new work after the
+ * shutdown. Synchronises the device and frees memory: not during a graph
+ * capture. */
 void mimg_shutdown(void);
 
 /* Text of the last error of the calling thread ("" if none). */
@@ -111,7 +115,11 @@ int mimg_register_weight_view(const void *dev, uint64_t len, uint32_t dtype, int
  * release keeps the weight alive until it returns, so sessions on several
  * threads may share weights (reference interp/pool.go:30-40,
  * interp/interp.go:409-523 run sessions concurrently); the handle itself
- * is unknown to calls that start after the last release. */
+ * is unknown to calls that start after the last release; such a call hands
+ * the weight over when it returns, and it is freed at the next release,
+ * registration or shutdown (a call may be enqueuing under graph capture,
+ * where nothing may be freed). Releases and registrations may synchronise
+ * the device and free memory: not during a graph capture. */
 int mimg_release_weight(uint64_t handle);
 
 /* Device address of a weight's bytes and the number of its rows that the
@@ -131,9 +139,10 @@ int mimg_weight_info(uint64_t handle, const void **dev_ptr, int64_t *n_refused);
  * MIMG_ERR_ARG for block not in {32, 256} (the reference's error).
  * Order: blocks of 256 are bit for bit the reference (dotQ8KRef); blocks of
  * 32 follow the AVX2 lane order of dotQ8_0Q8AVX2 / dotQ4KQ8AVX2 /
- * dotQ6KQ8AVX2 up to 15 rows, and from 16 rows Q8_0 (K a multiple of 256)
- * runs on the matrix cores with exact block sums and one float chain,
- * within the spec's tolerance (spec/stdlib.md:260-275). */
+ * dotQ6KQ8AVX2 at every row count, so a row's result never depends on the
+ * other rows of the call (mimg_matmul_a8_quantized_q8_0_tiled_dev is the
+ * matrix-core form of the Q8_0 product, a tolerance claim a caller opts
+ * into). */
 int mimg_dequant_matmul_a8(uint64_t w, const float *x, int64_t rows, const float *bias, int block,
                            float *y);
 
@@ -303,6 +312,23 @@ int mimg_rms_norm_qkv_rope_kv_dev(const uint64_t *w, const float *x, const float
 int mimg_matmul_a8_quantized_dev(uint64_t w, const float *x, int64_t rows, const float *bias, int block,
                                  float *y, const void *ws, uint64_t ws_bytes, void *stream);
 
+/* Q8_0 weights times activations quantized in blocks of 32 (ws from
+ * mimg_quantize_act_dev with block 32), on the int8 matrix cores: each
+ * output is one float chain over its blocks, tot = fma(f32(S_b),
+ * d_b*dx_b, tot) with S_b the exact int32 block sum, then the bias. This is
+ * NOT the reference's order (dotQ8_0Q8AVX2, internal/kernels/
+ * kernels_amd64.s:1007-1043, keeps eight lane chains), so the results are a
+ * tolerance claim: within the spec's dequant_matmul_a8 bound
+ * (spec/stdlib.md:260-275) of the exact product. Each row's result depends
+ * on that row alone. mimg_linear_a8_dev and the other entry points keep the
+ * reference's lane order at every row count; a caller opts into this one.
+ * Refused rows (NaN or |x| > 2^60, non-finite weight scales) take the
+ * reference-order float32 path. Returns MIMG_NOT_HANDLED for shapes it
+ * does not tile. No reference counterpart: a faster form of the products
+ * interp/fast.go:282-379 makes, for callers that accept the tolerance. */
+int mimg_matmul_a8_quantized_q8_0_tiled_dev(uint64_t w, const float *x, int64_t rows, const float *bias, float *y,
+                                            const void *ws, uint64_t ws_bytes, void *stream);
+
 /* mimg_matmul_a8_quantized_dev for a group of 1 to 3 weights sharing K and
  * the quantized activations (e.g. q, k and v after
  * mimg_rms_norm_quant_dev); bias may be NULL or hold NULLs. No reference
@@ -421,9 +447,16 @@ int mimg_rope_dev(float *x, const int64_t *pos, const double *inv_freq, int64_t 
  * ((h*ceil(context/8) + j/8)*d + i)*8 + j%8, so that a dim's eight
  * consecutive keys are contiguous for the weighted sum, whose per-dim chain
  * runs over the keys in order. vcache holds kv_heads*ceil(context/8)*8*d
- * elements. */
+ * elements (mimg_vcache_elems), more than kv_heads*context*d when context
+ * is not a multiple of 8: a buffer sized for the graph's layout is too
+ * small. */
 int mimg_kv_store_dev(const float *k, const float *v, const int64_t *pos, int64_t T, int kv_heads, int d,
                       int64_t context, void *kcache, void *vcache, int f16, void *stream);
+
+/* Elements (f16 or f32, as the cache) of a value cache in the blocked layout
+ * above: kv_heads * ceil(context/8) * 8 * d; 0 for a non-positive argument.
+ * Every entry point that takes a vcache reads or writes up to this many. */
+uint64_t mimg_vcache_elems(int64_t kv_heads, int64_t context, int64_t d);
 
 /* attention.v1 (f32 cache) / attention.v2 (f16 cache) with the graph's
  * mask (reference interp/fast.go:559-700, importer/llama.go:364-395), on

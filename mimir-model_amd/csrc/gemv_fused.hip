@@ -603,11 +603,6 @@ static size_t fused_lds_bytes(int64_t K, int nb, int maxR, bool norm = false, in
 // workgroup of three (or two) teams re-reads x (and resid, scale) once for
 // three tiles. Taken only where the workgroups still cover every CU.
 static int fused_teams(int tiles) {
-    static const int force = [] {
-        const char* e = getenv("MIMG_FUSED_TEAMS");
-        return e ? atoi(e) : 0;
-    }();
-    if (force >= 1 && force <= 3) return tiles % force == 0 ? force : 1;
     if (tiles >= 3 * 256 && tiles % 3 == 0) return 3;
     if (tiles >= 2 * 256 && tiles % 2 == 0) return 2;
     return 1;

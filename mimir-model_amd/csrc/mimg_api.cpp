@@ -60,6 +60,7 @@ struct Weight {
 struct Upload {
     uint64_t len;
     int64_t views;
+    bool orphan = false;  // mimg_shutdown left it for views still held by calls: the last view frees it
 };
 std::map<uintptr_t, Upload> g_uploads;
 
@@ -89,11 +90,23 @@ struct ThreadCtx {
     hipStream_t stream = nullptr;
     void* buf[4] = {nullptr, nullptr, nullptr, nullptr};
     size_t cap[4] = {0, 0, 0, 0};
-    ~ThreadCtx() {
-        for (int i = 0; i < 4; i++)
+    void* pin[3] = {nullptr, nullptr, nullptr};  // pinned host staging: x, bias, y
+    size_t pcap[3] = {0, 0, 0};
+    void release() {
+        for (int i = 0; i < 4; i++) {
             if (buf[i]) (void)hipFree(buf[i]);
+            buf[i] = nullptr;
+            cap[i] = 0;
+        }
+        for (int i = 0; i < 3; i++) {
+            if (pin[i]) (void)hipHostFree(pin[i]);
+            pin[i] = nullptr;
+            pcap[i] = 0;
+        }
         if (stream) (void)hipStreamDestroy(stream);
+        stream = nullptr;
     }
+    ~ThreadCtx() { release(); }
 };
 thread_local ThreadCtx t_ctx;
 
@@ -148,18 +161,45 @@ int thread_buf(int i, size_t bytes, void** out) {
     return MIMG_OK;
 }
 
+// Pinned host staging buffer i of the calling thread, grown as needed.
+int thread_pin(int i, size_t bytes, void** out) {
+    if (bytes == 0) bytes = 256;
+    if (t_ctx.pcap[i] < bytes) {
+        if (t_ctx.pin[i]) HIP_TRY(hipHostFree(t_ctx.pin[i]));
+        t_ctx.pin[i] = nullptr;
+        t_ctx.pcap[i] = 0;
+        HIP_TRY(hipHostMalloc(&t_ctx.pin[i], bytes, hipHostMallocDefault));
+        t_ctx.pcap[i] = bytes;
+    }
+    *out = t_ctx.pin[i];
+    return MIMG_OK;
+}
+
 // Frees a weight that is out of the maps and used by no call (g_mu held).
 // Kernels enqueued on it by earlier calls may still run: wait for them.
 void destroy_locked(Weight* w) {
     (void)hipDeviceSynchronize();
     if (w->view_of) {
         auto it = g_uploads.find((uintptr_t)w->view_of);
-        if (it != g_uploads.end()) it->second.views--;
+        if (it != g_uploads.end() && --it->second.views == 0 && it->second.orphan) {
+            (void)hipFree((void*)it->first);
+            g_uploads.erase(it);
+        }
     } else {
         (void)hipFree(w->data);
     }
     (void)hipFree(w->wref);
     delete w;
+}
+
+// Weights released while a call held them: the last holder hands them here
+// instead of freeing them itself (a holder may be enqueuing onto a stream
+// under graph capture, where synchronising and freeing are not allowed).
+// mimg_release_weight, the registrations and mimg_shutdown free them.
+std::vector<Weight*> g_grave;
+void drain_grave_locked() {
+    for (Weight* w : g_grave) destroy_locked(w);
+    g_grave.clear();
 }
 
 // A weight held by one call from its lookup to its return. While any call
@@ -184,7 +224,7 @@ class Held {
     void reset() {
         if (!w_) return;
         std::lock_guard<std::mutex> lk(g_mu);
-        if (--w_->inflight == 0 && w_->dead) destroy_locked(w_);
+        if (--w_->inflight == 0 && w_->dead) g_grave.push_back(w_);
         w_ = nullptr;
     }
     Weight* get() const { return w_; }
@@ -238,6 +278,10 @@ int register_impl(const void* src, uint64_t len, uint32_t dtype, int64_t n, int6
     int rc = check_shape(dtype, len, n, k);
     if (rc) return rc;
     if ((rc = ensure_device())) return rc;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        drain_grave_locked();
+    }
     auto key = std::make_tuple((uintptr_t)src, len, dtype, n, k);
     const uint64_t fp = from_host ? fingerprint((const uint8_t*)src, len) : 0;
     if (from_host) {
@@ -314,29 +358,9 @@ bool fused_q8_blocks(uint32_t dt, int block) {
     return false;
 }
 
-// Everything after quantization: the product of the quantized rows.
-// The products of up to three weights (same K, each with an 8-bit kernel for
-// `block`) with activations already quantized into `a`: block-256 weights of
-// one dtype share a launch per chunk of 8 rows.
-static int64_t env_or(const char* name, int64_t dflt) {
-    const char* e = getenv(name);
-    return e ? (int64_t)atoll(e) : dflt;
-}
-
-// Workgroups per CU of the tile-looping one-row GEMV (0: one workgroup per
-// tile instead). MIMG_TILES_WPC overrides, for tuning.
-static int64_t tiles_wpc() {
-    static const int64_t v = env_or("MIMG_TILES_WPC", 0);
-    return v;
-}
-
 // Activation rows from which the blocks-of-256 products use the MFMA GEMM
-// instead of the GEMV in chunks of eight rows. MIMG_GEMM_MIN_ROWS
-// overrides, for tuning.
-static int64_t gemm_min_rows() {
-    static const int64_t v = env_or("MIMG_GEMM_MIN_ROWS", 16);
-    return v;
-}
+// (bit-identical to the GEMV) instead of the GEMV in chunks of eight rows.
+constexpr int64_t GEMM_MIN_ROWS = 16;
 
 // Every workgroup of a product reads all of x (the float32 path of refused
 // rows included) while others write y: y[i] must not overlap x.
@@ -351,36 +375,26 @@ static int check_outputs(const float* x, int64_t rows, int64_t K, const int64_t*
 
 // Activation rows (of a chunk of at most eight) from which the GEMV runs
 // on the matrix cores (measured, cfg1 layer set: 100 against 105 us per
-// step at 4 rows, 99 against 95 at 3). MIMG_MFMA_MIN_ROWS overrides, for
-// tuning (9: never).
-static int64_t mfma_min_rows() {
-    static const int64_t v = env_or("MIMG_MFMA_MIN_ROWS", 4);
-    return v;
-}
+// step at 4 rows, 99 against 95 at 3).
+constexpr int64_t MFMA_MIN_ROWS = 4;
 
+// Everything after quantization: the products of up to three weights (same
+// K, each with an 8-bit kernel for `block`) with activations already
+// quantized into `a`; block-256 weights of one dtype share a launch per
+// chunk of 8 rows. Every path keeps each row's result independent of the
+// other rows of the call: block 256 from GEMM_MIN_ROWS on the MFMA GEMM
+// (bit-identical to the GEMV), blocks of 32 always the GEMV in the
+// reference's lane order.
 int matmul_quantized(const Weight* const* w, int count, const float* x, int64_t rows, const float* const* bias,
                      int block, float* const* y, const ActPtrs& a, hipStream_t s) {
     const int64_t K = w[0]->dw.k, R32 = K / 32, R16 = K / 16;
-    if (block == 256 && rows >= gemm_min_rows()) {
+    if (block == 256 && rows >= GEMM_MIN_ROWS) {
         bool all = true;
         for (int i = 0; i < count; i++) all = all && gemm_a8k_ok(w[i]->dw);
         if (all) {
             for (int i = 0; i < count; i++) {
                 hipError_t e = launch_gemm_a8k(w[i]->dw, a, rows, rows, x, bias ? bias[i] : nullptr, y[i], s);
                 if (e != hipSuccess) return fail(MIMG_ERR_HIP, "GEMM launch: %s", hipGetErrorString(e));
-            }
-            return MIMG_OK;
-        }
-    }
-    if (block == 32 && rows >= gemm_min_rows()) {
-        // Q8_0 with blocks of 32 on the int8 MFMA GEMM (one chain of exact
-        // block sums, within the spec's tolerance; see gemm_q8_0.hip)
-        bool all = true;
-        for (int i = 0; i < count; i++) all = all && gemm_q8_0_ok(w[i]->dw);
-        if (all) {
-            for (int i = 0; i < count; i++) {
-                hipError_t e = launch_gemm_q8_0(w[i]->dw, a, rows, rows, x, bias ? bias[i] : nullptr, y[i], s);
-                if (e != hipSuccess) return fail(MIMG_ERR_HIP, "Q8_0 GEMM launch: %s", hipGetErrorString(e));
             }
             return MIMG_OK;
         }
@@ -411,9 +425,7 @@ int matmul_quantized(const Weight* const* w, int count, const float* x, int64_t 
                     done[j] = true;
                     n++;
                 }
-                if (mr == 1 && tiles_wpc() > 0 && gemv_tiles_ok(*dws[0], 1))
-                    e = launch_gemv_a8k_tiles(dws, n, c, rows, x + r0 * K, bs, ys, (int)tiles_wpc(), s);
-                else if (mr >= mfma_min_rows() && gemv_mfma_ok(dws, n, mr))
+                if (mr >= MFMA_MIN_ROWS && gemv_mfma_ok(dws, n, mr))
                     e = launch_gemv_a8k_mfma(dws, n, c, mr, rows, x + r0 * K, bs, ys, s);
                 else
                     e = launch_gemv_a8k(dws, n, c, mr, rows, x + r0 * K, bs, ys, s);
@@ -491,24 +503,35 @@ void mimg_shutdown(void) {
     if (g_device < 0) return;
     (void)hipSetDevice(g_device);
     (void)hipDeviceSynchronize();
+    drain_grave_locked();
     for (auto& kv : g_weights) {
         Weight* w = kv.second;
-        if (!w->view_of) (void)hipFree(w->data);  // a view's bytes belong to its section
+        if (w->inflight > 0) {
+            w->dead = true;  // a call on another thread still holds it: that call hands it to the grave
+            continue;
+        }
+        if (w->view_of) {
+            auto it = g_uploads.find((uintptr_t)w->view_of);
+            if (it != g_uploads.end()) it->second.views--;
+        } else {
+            (void)hipFree(w->data);  // a view's bytes belong to its section
+        }
         (void)hipFree(w->wref);
         delete w;
     }
     g_weights.clear();
     g_keys.clear();
-    for (auto& kv : g_uploads) (void)hipFree((void*)kv.first);
-    g_uploads.clear();
-    // the calling thread's stream and buffers; other threads' go at their exit
-    for (int i = 0; i < 4; i++) {
-        if (t_ctx.buf[i]) (void)hipFree(t_ctx.buf[i]);
-        t_ctx.buf[i] = nullptr;
-        t_ctx.cap[i] = 0;
+    for (auto it = g_uploads.begin(); it != g_uploads.end();) {
+        if (it->second.views > 0) {  // views still held by calls in flight free it last
+            it->second.orphan = true;
+            ++it;
+        } else {
+            (void)hipFree((void*)it->first);
+            it = g_uploads.erase(it);
+        }
     }
-    if (t_ctx.stream) (void)hipStreamDestroy(t_ctx.stream);
-    t_ctx.stream = nullptr;
+    // the calling thread's stream and buffers; other threads' go at their exit
+    t_ctx.release();
     g_device = -1;
 }
 
@@ -528,10 +551,11 @@ int mimg_release_weight(uint64_t handle) {
     auto it = g_weights.find(handle);
     if (it == g_weights.end()) return fail(MIMG_ERR_HANDLE, "unknown weight handle %llu", (unsigned long long)handle);
     Weight* w = it->second;
+    drain_grave_locked();
     if (--w->refs > 0) return MIMG_OK;
     if (w->has_key) g_keys.erase(w->key);
     g_weights.erase(it);
-    if (w->inflight > 0) w->dead = true;  // the last call holding it frees it
+    if (w->inflight > 0) w->dead = true;  // the last call holding it hands it to the grave
     else destroy_locked(w);
     return MIMG_OK;
 }
@@ -576,6 +600,7 @@ int mimg_register_weight_view(const void* dev, uint64_t len, uint32_t dtype, int
     uint8_t* base = nullptr;
     {
         std::lock_guard<std::mutex> lk(g_mu);
+        drain_grave_locked();
         auto it = g_uploads.upper_bound((uintptr_t)dev);
         if (it != g_uploads.begin()) {
             --it;
@@ -801,19 +826,29 @@ int mimg_matmul_a8_quantized_dev(uint64_t wh, const float* x, int64_t rows, cons
     return matmul_quantized(ws1, 1, x, rows, bs1, block, ys1, act_ptrs((void*)ws, l), (hipStream_t)stream);
 }
 
+int mimg_matmul_a8_quantized_q8_0_tiled_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, float* y,
+                                            const void* ws, uint64_t ws_bytes, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    Held w;
+    if ((rc = w.acquire(wh))) return rc;
+    if (w->dw.dt != DT_Q8_0) return fail(MIMG_ERR_ARG, "%s: the tiled product is for Q8_0 weights", dt_name(w->dw.dt));
+    if (rows < 0) return fail(MIMG_ERR_ARG, "rows = %lld", (long long)rows);
+    if (rows == 0) return MIMG_OK;
+    if (!x || !y || !ws || !aligned(ws, 256)) return fail(MIMG_ERR_ARG, "null or misaligned pointer");
+    ActLayout l = act_layout(rows, w->dw.k);
+    if (ws_bytes < l.total) return fail(MIMG_ERR_WORKSPACE, "workspace %llu < %llu bytes", (unsigned long long)ws_bytes, (unsigned long long)l.total);
+    if ((rc = check_outputs(x, rows, w->dw.k, &w->dw.n, &y, 1))) return rc;
+    if (!gemm_q8_0_ok(w->dw)) return fail(MIMG_NOT_HANDLED, "no tiled Q8_0 product for this shape");
+    HIP_TRY(launch_gemm_q8_0(w->dw, act_ptrs((void*)ws, l), rows, rows, x, bias, y, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
 // When a single activation row is quantized inside the GEMV kernel: every
 // workgroup then quantizes the whole row, which pays while the group is
 // small (q/k/v, o); for long rows or many weight rows a separate quantize
-// launch costs less (measured on MI355X). MIMG_FUSED_MAXK / MIMG_FUSED_MAXN
-// override the limits, for tuning.
-static int64_t fused_max_k() {
-    static const int64_t v = env_or("MIMG_FUSED_MAXK", 4096);
-    return v;
-}
-static int64_t fused_max_n() {
-    static const int64_t v = env_or("MIMG_FUSED_MAXN", 8192);
-    return v;
-}
+// launch costs less (measured on MI355X).
+constexpr int64_t FUSED_MAX_K = 4096, FUSED_MAX_N = 8192;
 
 int mimg_linear_a8_group_dev(const uint64_t* whs, int count, const float* x, int64_t rows, const float* const* bias,
                              int block, float* const* y, void* ws, uint64_t ws_bytes, void* stream) {
@@ -840,7 +875,7 @@ int mimg_linear_a8_group_dev(const uint64_t* whs, int count, const float* x, int
     int64_t total_n = 0, ns[3];
     for (int i = 0; i < count; i++) total_n += (ns[i] = w[i]->dw.n);
     if ((rc = check_outputs(x, rows, w[0]->dw.k, ns, y, count))) return rc;
-    if (!any_f32 && rows == 1 && block == 256 && w[0]->dw.k <= fused_max_k() && total_n <= fused_max_n() &&
+    if (!any_f32 && rows == 1 && block == 256 && w[0]->dw.k <= FUSED_MAX_K && total_n <= FUSED_MAX_N &&
         fused_gemv_ok(dw, count)) {
         float* ys[3];
         const float* bs[3];
@@ -913,6 +948,11 @@ static int64_t chain_max_wg_rows(const ChainPhase& P, int G) {
 }
 
 uint64_t mimg_chain_sync_bytes(void) { return CHAIN_SYNC_BYTES; }
+
+uint64_t mimg_vcache_elems(int64_t kv_heads, int64_t context, int64_t d) {
+    if (kv_heads <= 0 || context <= 0 || d <= 0) return 0;
+    return (uint64_t)kv_heads * (uint64_t)((context + 7) / 8 * 8) * (uint64_t)d;
+}
 
 int mimg_chain_sync_init(void* sync, uint64_t sync_bytes, void* stream) {
     int rc = ensure_device();
@@ -1017,7 +1057,9 @@ int mimg_linear_a8_noalloc_dev(uint64_t wh, const float* x, int64_t rows, const 
         K = w->dw.k;
     }
     if (rows < 0) return fail(MIMG_ERR_ARG, "rows = %lld", (long long)rows);
-    const uint64_t need = act_layout(rows, K).total;
+    // (rows past SCRATCH_BYTES / K cannot fit; checked before the size
+    // arithmetic, which a huge rows value would overflow)
+    const uint64_t need = (uint64_t)rows > SCRATCH_BYTES / (uint64_t)K ? SCRATCH_BYTES + 1 : act_layout(rows, K).total;
     if (need > SCRATCH_BYTES)
         return fail(MIMG_ERR_WORKSPACE,
                     "%lld rows x K = %lld need %llu bytes of scratch; the library's static scratch holds %llu "
@@ -1069,7 +1111,7 @@ int mimg_rms_norm_linear_a8_group_dev(const uint64_t* whs, int count, const floa
         if (hits(x) || hits(resid) || hits(scale) || hits(x_out))
             return fail(MIMG_ERR_ARG, "output %d overlaps x, resid, scale or x_out", i);
     }
-    if (total_n > fused_max_n() || !fused_norm_ok(dw, count))
+    if (total_n > FUSED_MAX_N || !fused_norm_ok(dw, count))
         return fail(MIMG_NOT_HANDLED, "no fused norm GEMV for K %lld, %lld rows", (long long)K, (long long)total_n);
     float* ys[3];
     const float* bs[3];
@@ -1146,7 +1188,7 @@ int mimg_matmul_a8_quantized_qkv_rope_kv_dev(const uint64_t* whs, const float* x
         dw[i] = &w->dw;
     }
     if (rows == 0) return MIMG_OK;
-    if (block != 256 || rows < mfma_min_rows() || rows > 8 || dw[0]->dt != dw[1]->dt ||
+    if (block != 256 || rows < MFMA_MIN_ROWS || rows > 8 || dw[0]->dt != dw[1]->dt ||
         !gemv_mfma_qkv_ok(dw, rows, heads, kv_heads, d, rotary))
         return fail(MIMG_NOT_HANDLED, "no q/k/v + rope launch for %lld rows, block %d, D %d", (long long)rows, block, d);
     if (!x || !ws || !aligned(ws, 256)) return fail(MIMG_ERR_ARG, "null or misaligned pointer");
@@ -1199,7 +1241,7 @@ int mimg_rms_norm_qkv_rope_kv_dev(const uint64_t* whs, const float* x, const flo
         return fail(MIMG_ERR_ARG, "x_out must not overlap x, resid or scale (every workgroup reads them)");
     if (overlap(q, qb, x, xb) || overlap(q, qb, resid, xb) || overlap(q, qb, scale, xb) || overlap(q, qb, x_out, xb))
         return fail(MIMG_ERR_ARG, "q overlaps x, resid, scale or x_out");
-    if ((int64_t)heads * d + 2 * (int64_t)kv_heads * d > fused_max_n() ||
+    if ((int64_t)heads * d + 2 * (int64_t)kv_heads * d > FUSED_MAX_N ||
         !fused_norm_rope_ok(dw, heads, kv_heads, d, rotary))
         return fail(MIMG_NOT_HANDLED, "no fused norm + q/k/v + rope launch for K %lld, D %d", (long long)K, d);
     const float* bs[3] = {bias ? bias[0] : nullptr, bias ? bias[1] : nullptr, bias ? bias[2] : nullptr};
@@ -1419,22 +1461,32 @@ static int host_call(uint64_t wh, const float* x, int64_t rows, const float* bia
     if (!x || !y) return fail(MIMG_ERR_ARG, "null pointer");
     if ((rc = ensure_thread_stream())) return rc;
     const int64_t K = w->dw.k, N = w->dw.n;
-    void *x_d, *y_d, *b_d = nullptr, *ws = nullptr;
-    if ((rc = thread_buf(0, (size_t)(rows * K * 4), &x_d))) return rc;
-    if ((rc = thread_buf(1, (size_t)(rows * N * 4), &y_d))) return rc;
-    if (bias && (rc = thread_buf(2, (size_t)N * 4, &b_d))) return rc;
+    const size_t xb = (size_t)(rows * K * 4), yb = (size_t)(rows * N * 4), bb = (size_t)N * 4;
+    void *x_d, *y_d, *b_d = nullptr, *ws = nullptr, *x_p, *y_p, *b_p = nullptr;
+    if ((rc = thread_buf(0, xb, &x_d))) return rc;
+    if ((rc = thread_buf(1, yb, &y_d))) return rc;
+    if (bias && (rc = thread_buf(2, bb, &b_d))) return rc;
     uint64_t wsb = act_layout(rows, K).total;
     if (!use_f32 && (rc = thread_buf(3, wsb, &ws))) return rc;
+    // The caller's x, bias and y are pageable (a Go slice): they pass through
+    // the thread's pinned buffers, so each direction is one DMA transfer and
+    // the call synchronises once.
+    if ((rc = thread_pin(0, xb, &x_p))) return rc;
+    if ((rc = thread_pin(2, yb, &y_p))) return rc;
+    if (bias && (rc = thread_pin(1, bb, &b_p))) return rc;
+    memcpy(x_p, x, xb);
+    if (bias) memcpy(b_p, bias, bb);
     hipStream_t s = t_ctx.stream;
-    HIP_TRY(hipMemcpyAsync(x_d, x, (size_t)(rows * K * 4), hipMemcpyHostToDevice, s));
-    if (bias) HIP_TRY(hipMemcpyAsync(b_d, bias, (size_t)N * 4, hipMemcpyHostToDevice, s));
+    HIP_TRY(hipMemcpyAsync(x_d, x_p, xb, hipMemcpyHostToDevice, s));
+    if (bias) HIP_TRY(hipMemcpyAsync(b_d, b_p, bb, hipMemcpyHostToDevice, s));
     if (use_f32)
         rc = mimg_linear_f32_dev(wh, (const float*)x_d, rows, (const float*)b_d, (float*)y_d, s);
     else
         rc = mimg_linear_a8_dev(wh, (const float*)x_d, rows, (const float*)b_d, block, (float*)y_d, ws, wsb, s);
     if (rc) return rc;
-    HIP_TRY(hipMemcpyAsync(y, y_d, (size_t)(rows * N * 4), hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipMemcpyAsync(y_p, y_d, yb, hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
+    memcpy(y, y_p, yb);
     return MIMG_OK;
 }
 

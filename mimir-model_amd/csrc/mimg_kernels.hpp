@@ -78,14 +78,6 @@ hipError_t launch_gemv_a8k(const DevWeight* const* ws, int nmat, const ActPtrs& 
                            int64_t total_rows, const float* x, const float* const* bias, float* const* y,
                            hipStream_t stream);
 
-// One activation row (already quantized) against up to three Q4_K/Q6_K
-// matrices of one dtype and K <= 16384, tile-looping kernel with
-// `wgs_per_cu` workgroups per CU (gemv_tiles.hip).
-bool gemv_tiles_ok(const DevWeight& w, int64_t rows);
-hipError_t launch_gemv_a8k_tiles(const DevWeight* const* ws, int nmat, const ActPtrs& a, int64_t total_rows,
-                                 const float* x, const float* const* bias, float* const* y, int wgs_per_cu,
-                                 hipStream_t stream);
-
 // Many activation rows (already quantized) against one Q4_K/Q6_K matrix,
 // on the int8 matrix cores (gemm_kquant.hip); bit-identical to the GEMV.
 bool gemm_a8k_ok(const DevWeight& w);

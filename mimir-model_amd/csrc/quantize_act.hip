@@ -203,11 +203,7 @@ static hipError_t launch_qa(const float* x, int64_t rows, int64_t K, int block, 
     // batch 8 +0.9 %; the 8B prompt of 512 rows +3 % with swiglu + quantize
     // at K = 14336 so). Few long rows keep many workgroups a row (one
     // workgroup a row at K = 14336 made the 8B decode step 2.7 % slower).
-    // MIMG_QA_ONEWG_CHUNKS moves the chunk limit, for measurement.
-    static const int64_t one_wg = [] {
-        const char* e = getenv("MIMG_QA_ONEWG_CHUNKS");
-        return e ? (int64_t)atoll(e) : (int64_t)16;
-    }();
+    constexpr int64_t one_wg = 16;
     const bool fits_one = MODE == QA_PLAIN || chunks <= 16 * 8;  // swiglu: one round of loads
     if (MODE != QA_NORM && rows <= 65535 && chunks > one_wg && (rows < 64 || !fits_one)) {
         dim3 grid((unsigned)(1 + (chunks + QA_MW_WAVES - 1) / QA_MW_WAVES), (unsigned)rows), blk(64 * QA_MW_WAVES);

@@ -47,6 +47,7 @@ SIGNATURES = {
                                       ctypes.POINTER(_P), _P, _U64, _P]),
     "mimg_linear_a8_chain_dev": (_I, [_P, _I, _P, _U64, _P]),
     "mimg_chain_sync_bytes": (_U64, []),
+    "mimg_vcache_elems": (_U64, [_I64, _I64, _I64]),
     "mimg_chain_sync_init": (_I, [_P, _U64, _P]),
     "mimg_chain_status": (_I, [_P, ctypes.POINTER(_U32)]),
     "mimg_rms_norm_linear_a8_group_dev": (_I, [ctypes.POINTER(_U64), _I, _P, _P, _P, ctypes.c_float, _P,
@@ -58,6 +59,7 @@ SIGNATURES = {
     "mimg_rms_norm_qkv_rope_kv_dev": (_I, [ctypes.POINTER(_U64), _P, _P, _P, ctypes.c_float, _P, ctypes.POINTER(_P),
                                            _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _P, _P, _I, _P]),
     "mimg_matmul_a8_quantized_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P, _U64, _P]),
+    "mimg_matmul_a8_quantized_q8_0_tiled_dev": (_I, [_U64, _P, _I64, _P, _P, _P, _U64, _P]),
     "mimg_linear_f32_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
     "mimg_linear_f32_mfma_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
     "mimg_dequantize_dev": (_I, [_U32, _P, _U64, _P, _I64, _P]),
@@ -355,6 +357,15 @@ def matmul_a8_quantized_dev(w, x_ptr, rows, bias_ptr, block, y_ptr, ws_ptr, ws_b
                                                block, _P(y_ptr), _P(ws_ptr), ws_bytes, _P(stream)))
 
 
+def matmul_a8_quantized_q8_0_tiled_dev(w, x_ptr, rows, bias_ptr, y_ptr, ws_ptr, ws_bytes, stream):
+    """Q8_0 x activations quantized in blocks of 32 on the int8 matrix cores:
+    one float chain of exact block sums per output, a tolerance claim (not
+    the reference's lane order; the default entry points keep that)."""
+    _check(load().mimg_matmul_a8_quantized_q8_0_tiled_dev(w.handle, _P(x_ptr), rows,
+                                                          _P(bias_ptr) if bias_ptr else None, _P(y_ptr),
+                                                          _P(ws_ptr), ws_bytes, _P(stream)))
+
+
 def matmul_a8_quantized_group_dev(weights, x_ptr, rows, bias_ptrs, block, y_ptrs, ws_ptr, ws_bytes, stream):
     n = len(weights)
     hs = (_U64 * n)(*[w.handle for w in weights])
@@ -432,6 +443,11 @@ def vcache_len(context):
     """Keys a value cache of `context` entries holds: the value cache is
     blocked by eight keys, [kv_heads][ceil(context/8)][d][8]."""
     return (int(context) + 7) // 8 * 8
+
+
+def vcache_elems(kv_heads, context, d):
+    """Elements of a blocked value cache (mimg_vcache_elems)."""
+    return int(load().mimg_vcache_elems(kv_heads, context, d))
 
 
 def pack_vcache(v):

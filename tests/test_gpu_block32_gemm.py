@@ -1,8 +1,14 @@
-"""dequant_matmul_a8 with activation blocks of 32 and Q8_0 weights from 16
-activation rows: the int8 MFMA GEMM (gemm_q8_0.hip). Its float order, one
-chain of exact block sums, is not the eight-lane order of the reference's
-dotQ8_0Q8AVX2 (kernels_amd64.s:1007-1043), so the claim is the spec's
-tolerance for dequant_matmul_a8 (reference spec/stdlib.md:260-275):
+"""Q8_0 weights with activation blocks of 32 from 16 rows.
+
+The default entry points (dequant_matmul_a8 with block 32) keep the
+reference's eight-lane order of dotQ8_0Q8AVX2 (kernels_amd64.s:1007-1043)
+at every row count, so they equal the oracle bit for bit and a row's bits
+do not depend on the rows beside it.
+
+mimg_matmul_a8_quantized_q8_0_tiled_dev is the opt-in matrix-core form (the
+int8 MFMA GEMM, gemm_q8_0.hip): one chain of exact block sums, not the
+reference's lane order, so its claim is the spec's tolerance for
+dequant_matmul_a8 (reference spec/stdlib.md:260-275):
     |y - exact| <= (K+2) u (sum_k (|x_k| + s_k) B_k + |bias|) + sum_k s_k |wd_k|
 with wd the reference decode of the weights (the oracle's mim.Dequantize,
 bit for bit), B_k = |wd_k| for Q8_0, s_k the largest |x| of k's block of 32
@@ -19,6 +25,27 @@ pytestmark = pytest.mark.gpu
 
 Q8_0 = 64
 U = 2.0 ** -24
+
+
+def tiled(gpu, W, x, bias=None):
+    """The opt-in matrix-core Q8_0 product of x (quantized in blocks of 32)."""
+    import hiprt
+
+    rows, k = x.shape
+    xd = hiprt.DeviceBuffer.from_array(np.ascontiguousarray(x, np.float32))
+    wsb = gpu.a8_workspace_bytes(rows, k)
+    ws = hiprt.DeviceBuffer(wsb)
+    yd = hiprt.DeviceBuffer(rows * W.n * 4)
+    bd = hiprt.DeviceBuffer.from_array(bias) if bias is not None else None
+    s = hiprt.Stream()
+    gpu.quantize_act_dev(xd.ptr, rows, k, 32, ws.ptr, wsb, s.handle)
+    gpu.matmul_a8_quantized_q8_0_tiled_dev(W, xd.ptr, rows, bd.ptr if bd else None, yd.ptr, ws.ptr, wsb, s.handle)
+    s.sync()
+    y = yd.download(np.float32).reshape(rows, W.n)
+    for b in (xd, ws, yd, bd):
+        if b is not None:
+            b.free()
+    return y
 
 
 def _bound_check(oracle, wb, x, n, k, got, bias=None):
@@ -45,7 +72,7 @@ def test_q8_0_gemm_within_a8_bound(gpu, oracle, rows, n, k, with_bias):
     x = oracle.synthetic_acts(rows, k, seed=k + 3)
     bias = np.random.default_rng(4).standard_normal(n).astype(np.float32) if with_bias else None
     W = gpu.Weight(wb, Q8_0, n, k)
-    got = gpu.dequant_matmul_a8(W, x, bias=bias, block=32)
+    got = tiled(gpu, W, x, bias)
     W.release()
     _bound_check(oracle, wb, x, n, k, got, bias)
 
@@ -57,8 +84,8 @@ def test_q8_0_gemm_rows_are_independent(gpu, oracle):
     wb = oracle.synthetic_weight(Q8_0, n, k, seed=5)
     x = oracle.synthetic_acts(1100, k, seed=6)
     W = gpu.Weight(wb, Q8_0, n, k)
-    many = gpu.dequant_matmul_a8(W, x, block=32)
-    few = gpu.dequant_matmul_a8(W, x[:40], block=32)
+    many = tiled(gpu, W, x)
+    few = tiled(gpu, W, x[:40])
     W.release()
     assert bits_equal(many[:40], few), first_diff(many[:40], few)
 
@@ -79,7 +106,7 @@ def test_q8_0_gemm_refusals_match_the_reference_path(gpu, oracle):
     bias = np.random.default_rng(9).standard_normal(n).astype(np.float32)
     W = gpu.Weight(wb, Q8_0, n, k)
     assert W.info()[1] == 2
-    got = gpu.dequant_matmul_a8(W, x, bias=bias, block=32)
+    got = tiled(gpu, W, x, bias)
     W.release()
     want = oracle.linear_a8(x, wb, Q8_0, n, k, bias=bias, block=32, threads=16)
     refused_rows, refused_cols = [3, 50], [11, 200]
@@ -107,7 +134,24 @@ def test_cfg2_q8_0_variant_within_a8_bound(gpu, oracle, name, n, k, seed, rows):
     x = oracle.synthetic_acts(rows, k, seed=300 + rows)
     print(f"cfg2 Q8_0 {name} rows {rows}", flush=True)
     W = gpu.Weight(wb, Q8_0, n, k)
-    got = gpu.dequant_matmul_a8(W, x, block=32)
+    got = tiled(gpu, W, x)
     W.release()
-    pick = np.unique(np.linspace(0, rows - 1, 64).astype(int))
+    pick = np.arange(rows) if rows <= 512 else np.unique(np.linspace(0, rows - 1, 256).astype(int))
     _bound_check(oracle, wb, x[pick], n, k, got[pick])
+
+
+@pytest.mark.parametrize("rows,n,k", [(16, 64, 256), (40, 300, 1024), (130, 77, 2048)])
+def test_q8_0_block32_default_path_is_the_lane_order(gpu, oracle, rows, n, k):
+    """From 16 rows the default entry point keeps the reference's lane order:
+    bit for bit the oracle, and each row alone gives the same bits as inside
+    the call (what the matrix-core form above does not promise)."""
+    wb = oracle.synthetic_weight(Q8_0, n, k, seed=rows + k)
+    x = oracle.synthetic_acts(rows, k, seed=rows)
+    bias = np.random.default_rng(rows).standard_normal(n).astype(np.float32)
+    W = gpu.Weight(wb, Q8_0, n, k)
+    got = gpu.dequant_matmul_a8(W, x, bias=bias, block=32)
+    alone = np.concatenate([gpu.dequant_matmul_a8(W, x[i:i + 1], bias=bias, block=32) for i in (0, rows // 2, rows - 1)])
+    W.release()
+    want = oracle.linear_a8(x, wb, Q8_0, n, k, bias=bias, block=32, threads=8)
+    assert bits_equal(got, want), first_diff(got, want)
+    assert bits_equal(alone, got[[0, rows // 2, rows - 1]]), first_diff(alone, got[[0, rows // 2, rows - 1]])

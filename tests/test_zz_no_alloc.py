@@ -67,4 +67,10 @@ def test_no_alloc_refuses_what_the_scratch_cannot_hold(gpu, oracle):
     with pytest.raises(gpu.MimgError) as e:
         gpu.linear_a8_noalloc_dev(W, x.ptr, rows, None, 256, y.ptr, s.handle)
     assert e.value.code == -6 and "scratch" in str(e.value)
+    # row counts whose workspace size would overflow 64 bits are refused the
+    # same way (the check comes before the size arithmetic; nothing is read)
+    for huge in (1 << 62, (1 << 63) - 1, (1 << 64) // k + 1):
+        with pytest.raises(gpu.MimgError) as e:
+            gpu.linear_a8_noalloc_dev(W, x.ptr, huge, None, 256, y.ptr, s.handle)
+        assert e.value.code == -6, huge
     W.release()
