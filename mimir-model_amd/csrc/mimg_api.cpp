@@ -168,7 +168,8 @@ int thread_pin(int i, size_t bytes, void** out) {
         if (t_ctx.pin[i]) HIP_TRY(hipHostFree(t_ctx.pin[i]));
         t_ctx.pin[i] = nullptr;
         t_ctx.pcap[i] = 0;
-        HIP_TRY(hipHostMalloc(&t_ctx.pin[i], bytes, hipHostMallocDefault));
+        // mapped and coherent: kernels may read and write it in place
+        HIP_TRY(hipHostMalloc(&t_ctx.pin[i], bytes, hipHostMallocMapped | hipHostMallocCoherent));
         t_ctx.pcap[i] = bytes;
     }
     *out = t_ctx.pin[i];
@@ -1449,6 +1450,10 @@ int mimg_dequantize(uint32_t dtype, const void* src, uint64_t len, float* dst, i
     return MIMG_OK;
 }
 
+// Host calls whose x and y together take at most this many bytes run on
+// the pinned buffers in place.
+constexpr size_t HOST_DIRECT_BYTES = 1 << 20;
+
 static int host_call(uint64_t wh, const float* x, int64_t rows, const float* bias, int block, float* y, bool a8) {
     int rc = ensure_device();
     if (rc) return rc;
@@ -1463,20 +1468,39 @@ static int host_call(uint64_t wh, const float* x, int64_t rows, const float* bia
     const int64_t K = w->dw.k, N = w->dw.n;
     const size_t xb = (size_t)(rows * K * 4), yb = (size_t)(rows * N * 4), bb = (size_t)N * 4;
     void *x_d, *y_d, *b_d = nullptr, *ws = nullptr, *x_p, *y_p, *b_p = nullptr;
-    if ((rc = thread_buf(0, xb, &x_d))) return rc;
-    if ((rc = thread_buf(1, yb, &y_d))) return rc;
-    if (bias && (rc = thread_buf(2, bb, &b_d))) return rc;
     uint64_t wsb = act_layout(rows, K).total;
     if (!use_f32 && (rc = thread_buf(3, wsb, &ws))) return rc;
     // The caller's x, bias and y are pageable (a Go slice): they pass through
-    // the thread's pinned buffers, so each direction is one DMA transfer and
-    // the call synchronises once.
+    // the thread's pinned buffers, and the call synchronises once.
     if ((rc = thread_pin(0, xb, &x_p))) return rc;
     if ((rc = thread_pin(2, yb, &y_p))) return rc;
     if (bias && (rc = thread_pin(1, bb, &b_p))) return rc;
     memcpy(x_p, x, xb);
     if (bias) memcpy(b_p, bias, bb);
     hipStream_t s = t_ctx.stream;
+    if (!use_f32 && xb + yb <= HOST_DIRECT_BYTES) {
+        // Small 8-bit calls (decode rows): the quantizer reads x once and
+        // the products write y in the pinned buffers themselves, so the call
+        // is two kernels and one synchronisation, with no copy commands.
+        // (Only rows taking the float32 path read x again. The fused
+        // producers and the float32 kernels read x in every workgroup: they
+        // take copies.)
+        void *xm, *ym, *bm = nullptr;
+        HIP_TRY(hipHostGetDevicePointer(&xm, x_p, 0));
+        HIP_TRY(hipHostGetDevicePointer(&ym, y_p, 0));
+        if (bias) HIP_TRY(hipHostGetDevicePointer(&bm, b_p, 0));
+        const float* bs[1] = {(const float*)bm};
+        float* ys[1] = {(float*)ym};
+        if ((rc = mimg_quantize_act_dev((const float*)xm, rows, K, block, ws, wsb, s))) return rc;
+        if ((rc = mimg_matmul_a8_quantized_group_dev(&wh, 1, (const float*)xm, rows, bs, block, ys, ws, wsb, s)))
+            return rc;
+        HIP_TRY(hipStreamSynchronize(s));
+        memcpy(y, y_p, yb);
+        return MIMG_OK;
+    }
+    if ((rc = thread_buf(0, xb, &x_d))) return rc;
+    if ((rc = thread_buf(1, yb, &y_d))) return rc;
+    if (bias && (rc = thread_buf(2, bb, &b_d))) return rc;
     HIP_TRY(hipMemcpyAsync(x_d, x_p, xb, hipMemcpyHostToDevice, s));
     if (bias) HIP_TRY(hipMemcpyAsync(b_d, b_p, bb, hipMemcpyHostToDevice, s));
     if (use_f32)
