@@ -55,6 +55,7 @@ the first tokens of each shape from the same weights and its ids are
 compared with the GPU's (8 tokens; the 8B shape on a 32-token prompt).
 """
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -227,6 +228,26 @@ def decode_cpu_check(cfg, tensors, prompt, gpu_ids, n, log):
             "prompt_tok_per_s": round(P / t_prompt, 2), "cores": threads, "kind": "port"}
 
 
+def cfg4_oracle_check(tensors, prompt, gpu_ids, log):
+    """The batch-1 8B run against tests/golden/cfg4_ids.json: the CPU
+    restatement's first 32 greedy ids for the same weights (checked by their
+    digests) and the same 512-token prompt."""
+    sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+    import make_cfg4_ids as mk
+    import synthetic
+
+    with open(mk.FIXTURE) as f:
+        fx = json.load(f)
+    same_weights = mk.digests(synthetic.host_bytes({n: tensors[n] for n in mk.DIGESTED})) == fx["weights_sha256"]
+    same_prompt = np.array_equal(prompt, mk.prompts(synthetic.LLAMA_8B["vocab"])[0])
+    n = len(fx["ids"])
+    equal = same_weights and same_prompt and [int(v) for v in gpu_ids[:n]] == fx["ids"]
+    log(f"  llama8b 512-token prompt: first {n} GPU ids {'==' if equal else '!='} the CPU restatement's "
+        f"(fixture; weights {'match' if same_weights else 'differ'})")
+    return {"ids_equal_cpu_restatement": bool(equal), "tokens_checked": n, "weights_match_fixture": bool(same_weights),
+            "fixture": "tests/golden/cfg4_ids.json"}
+
+
 def decode_bench(name, log, graph=True, cpu=False, batches=(1, 8)):
     """Greedy generation on the GPU decoder with a random model of the
     named shape (module docstring); batches selects the 8B runs."""
@@ -237,7 +258,9 @@ def decode_bench(name, log, graph=True, cpu=False, batches=(1, 8)):
     runs = [(32, 128, 1)] if name == "llama1b" else [(512, 256, b) for b in batches]
     cfg["context"] = max(p + n for p, n, _ in runs)
     t0 = time.time()
-    tensors = synthetic.build(cfg, seed=1, log=log)
+    # the 8B weights are the GPU tests' (seed 3), whose 512-token prompt ids
+    # the CPU restatement wrote into tests/golden/cfg4_ids.json
+    tensors = synthetic.build(cfg, seed=1 if name == "llama1b" else 3, log=log)
     slots = max(b for _, _, b in runs)
     rows = max(min(p * b, 512) for p, _, b in runs)
     dec = decoder.Decoder(cfg, tensors, a8=True, cache_f16=True, max_rows=rows, slots=slots)
@@ -267,6 +290,8 @@ def decode_bench(name, log, graph=True, cpu=False, batches=(1, 8)):
             out[key]["cpu_restatement"] = decode_cpu_check(cfg, tensors, prompts[0], ids[0], 8, log)
         if batch == 1:
             b1_ids = ids[0]
+            if name == "llama8b" and P == 512:
+                out[key]["oracle_ids"] = cfg4_oracle_check(tensors, prompts[0], ids[0], log)
         elif P == runs[0][0] and runs[0][2] == 1:
             # slot 0 holds the batch-1 run's prompt: the same ids
             out[key]["slot0_ids_equal_batch1"] = bool(np.array_equal(ids[0], b1_ids))
@@ -543,6 +568,42 @@ def main():
     log(f"  read ceiling (gate+up weight bytes, one launch): {c_us:.2f} us, {c_gbs:.0f} GB/s "
         f"({', '.join(f'{p}x16B: {u:.2f} us' for p, u in ceil.items())})")
 
+    # An HBM ceiling independent of this library's read kernel, in the same
+    # run: a 1 GiB device-to-device hipMemcpyAsync (the runtime's own copy;
+    # it reads and writes 1 GiB), beside the read kernel over the same 1 GiB
+    # (one launch, so its ramp and drain weigh less than at 66 MB).
+    big = 1 << 30
+    src_big, dst_big = hiprt.DeviceBuffer(big), hiprt.DeviceBuffer(big)
+    hiprt.check(hiprt.rt().hipMemsetAsync(ctypes.c_void_p(src_big.ptr), 1, big, ctypes.c_void_p(stream.handle)), "memset")
+
+    def timed_us(fn, reps=5):
+        fn()
+        a, b = hiprt.Event(), hiprt.Event()
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        b.sync()
+        return a.elapsed_ms(b) * 1e3 / reps
+
+    copy_us = timed_us(lambda: hiprt.check(hiprt.rt().hipMemcpyAsync(
+        ctypes.c_void_p(dst_big.ptr), ctypes.c_void_p(src_big.ptr), big, hiprt.D2D, ctypes.c_void_p(stream.handle)),
+        "hipMemcpyAsync"))
+    read_big_us = {per: timed_us(lambda: mimg.stream_read_dev([(src_big.ptr, big)], per, sink.ptr, stream.handle))
+                   for per in (4, 8, 16)}
+    rb_per = min(read_big_us, key=read_big_us.get)
+    src_big.free()
+    dst_big.free()
+    hbm_ceiling = {
+        "d2d_copy_1GiB": {"us": round(copy_us, 2), "GB_per_s": round(2 * big / (copy_us * 1e-6) / 1e9, 1),
+                          "bytes_moved": 2 * big, "note": "hipMemcpyAsync device to device: reads and writes 1 GiB"},
+        "read_kernel_1GiB": {"us": round(read_big_us[rb_per], 2), "loads_per_thread": rb_per,
+                             "GB_per_s": round(big / (read_big_us[rb_per] * 1e-6) / 1e9, 1)},
+    }
+    log(f"  HBM ceiling: 1 GiB d2d copy {copy_us:.1f} us ({hbm_ceiling['d2d_copy_1GiB']['GB_per_s']:.0f} GB/s "
+        f"read+write); read kernel over 1 GiB {read_big_us[rb_per]:.1f} us "
+        f"({hbm_ceiling['read_kernel_1GiB']['GB_per_s']:.0f} GB/s)")
+
     # the single 4096 x 4096 Q4_K product (the q matrix,
     # weight seed 0) of one activation row (seed 1), as the reference calls
     # it: dequant_matmul_a8.v2, x quantized inside the one-row launch; a
@@ -637,6 +698,7 @@ def main():
                              "bytes": gu_weight_bytes, "avg_launch_us": round(c_us, 3), "achieved": round(c_gbs, 1),
                              "frac": round(c_gbs / HBM_PEAK_GBS, 4), "loads_per_thread": c_per,
                              "kernel_over_ceiling": round(r_gbs / c_gbs, 4)},
+            "hbm_ceiling": hbm_ceiling,
         },
         "cfg0": {
             "workload": "cfg0: one 4096x4096 Q4_K product (weight seed 0) of one activation row (seed 1), "

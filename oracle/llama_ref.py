@@ -122,8 +122,11 @@ class Decoder:
         rb = len(w) // V
         return np.stack([mimref.dequantize(dt, w[rb * t: rb * (t + 1)], E) for t in tokens]).astype(np.float32)
 
-    def forward(self, tokens, positions):
-        """Logits [T, vocab] for tokens at positions (the cache is updated)."""
+    def forward(self, tokens, positions, last_only=False):
+        """Logits [T, vocab] for tokens at positions (the cache is updated);
+        last_only: the last row's logits only, [1, vocab] (each row of the
+        head's product is computed alone, so it is that row of the full
+        result)."""
         m, c = self.m, self.m.c
         T, H, Hkv, D = len(tokens), c["heads"], c["kv_heads"], c["head_dim"]
         positions = np.asarray(positions, np.int64)
@@ -147,6 +150,8 @@ class Decoder:
             h = rms_norm(x, m.t[p + "ffn_norm.weight"][2], c["norm_eps"])
             a = swiglu(self.linear(h, p + "ffn_gate.weight"), self.linear(h, p + "ffn_up.weight"), self.procs)
             x = (x + self.linear(a, p + "ffn_down.weight")).astype(np.float32)
+        if last_only:
+            x = x[-1:]
         x = rms_norm(x, m.t["output_norm.weight"][2], c["norm_eps"])
         head = "output.weight" if "output.weight" in m.t else "token_embd.weight"
         return self.linear(x, head)

@@ -10,6 +10,10 @@ the reference's own (cmd/mim-run/main_test.go:178-257): 2e-5 of the largest
 logit and the same greedy ids without 8-bit activations, llama.cpp's
 deviation from the float64 oracle (x1.1 with the cache in f16) with them;
 and the same greedy ids as the CPU restatement with them."""
+import json
+import os
+import sys
+
 import numpy as np
 import pytest
 
@@ -454,6 +458,92 @@ def test_llama8b_shape_eight_slots_match_single_sequences(gpu, llama8b):
         single.reset()
         want = single.generate(prompts[i:i + 1], n_new)[0].tolist()
         assert got[i].tolist() == want, f"slot {i}"
+
+
+def _cfg4_fixture():
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    import make_cfg4_ids
+
+    with open(make_cfg4_ids.FIXTURE) as f:
+        return make_cfg4_ids, json.load(f)
+
+
+def test_llama8b_512_prompt_greedy_matches_oracle_ids(gpu, llama8b):
+    """Config 4 at its stated size, batch 1: a 512-token prompt (uniform ids,
+    seed 7) in one batch of 512 prompt rows, then 32 greedy tokens, f16
+    cache; the GPU decoder picks the CPU restatement's ids
+    (tests/golden/cfg4_ids.json, written by make_cfg4_ids.py from the same
+    device-built weights, whose bytes the digests pin)."""
+    import decoder
+    import synthetic
+
+    mk, fx = _cfg4_fixture()
+    cfg, tensors = llama8b
+    host = synthetic.host_bytes({name: tensors[name] for name in mk.DIGESTED})
+    assert mk.digests(host) == fx["weights_sha256"], "the device no longer builds the fixture's weights"
+    prompt = mk.prompts(cfg["vocab"])[0]
+    dec = decoder.Decoder(dict(cfg, context=mk.PROMPT_LEN + mk.N_NEW), tensors, a8=True, cache_f16=True,
+                          max_rows=mk.PROMPT_LEN)
+    got = dec.generate([prompt], mk.N_NEW)[0].tolist()
+    del dec
+    print("llama8b 512-token prompt, GPU ids", got, flush=True)
+    assert got == fx["ids"], next(i for i, (a, b) in enumerate(zip(got, fx["ids"])) if a != b)
+
+
+def test_llama8b_eight_512_prompts_match_single_sequences(gpu, llama8b):
+    """Config 4's batch of 8 at its stated size: eight distinct 512-token
+    prompts in eight slots (the reference's slots, importer/llama.go:378-395),
+    their 4096 prompt rows in batches of 384 (so batches straddle slots),
+    then 32 greedy steps as one batch of eight rows; each slot's ids equal
+    its prompt's single-sequence run (slot 0's prompt is the batch-1 test's,
+    whose ids equal the CPU restatement's)."""
+    import decoder
+
+    mk, fx = _cfg4_fixture()
+    cfg, tensors = llama8b
+    prompts = mk.prompts(cfg["vocab"])
+    c = dict(cfg, context=mk.PROMPT_LEN + mk.N_NEW)
+    batch = decoder.Decoder(c, tensors, a8=True, cache_f16=True, max_rows=384, slots=mk.SLOTS)
+    got = batch.generate(prompts, mk.N_NEW)
+    del batch
+    assert got[0].tolist() == fx["ids"]
+    single = decoder.Decoder(c, tensors, a8=True, cache_f16=True, max_rows=mk.PROMPT_LEN, slots=1)
+    for i in range(1, mk.SLOTS):
+        single.reset()
+        want = single.generate(prompts[i:i + 1], mk.N_NEW)[0].tolist()
+        assert got[i].tolist() == want, f"slot {i}"
+
+
+@pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
+@pytest.mark.parametrize("slots", [1, 8])
+def test_attention_prompt_512_rows_bitexact(gpu, oracle, rt, f16, slots):
+    """Config 4's prompt rows through attention: 512 query rows with the 8B
+    heads (32 query heads, 8 kv heads, head dim 128) in a cache of 544
+    entries a slot; one sequence at positions 0..511 (the causal prefill),
+    or eight slots of 64 rows each; bit for bit the C restatement."""
+    H, Hkv, D, T, C = 32, 8, 128, 512, 544
+    rng = np.random.default_rng(512 + slots)
+    L = slots * C
+    cdt = np.float16 if f16 else np.float32
+    kc = (rng.standard_normal((Hkv, L, D)) * 2).astype(cdt)
+    vc = rng.standard_normal((Hkv, L, D)).astype(cdt)
+    q = rng.standard_normal((T, H, D)).astype(np.float32)
+    per = T // slots
+    slot = np.arange(T) // per
+    pos = (np.arange(T) % per).astype(np.int64)
+    cidx = (slot * C + pos).astype(np.int64)
+    kstart = (slot * C).astype(np.int64)
+    dq, dk, dv, de, ds = dev(rt, q), dev(rt, kc), dev(rt, gpu.pack_vcache(vc)), dev(rt, cidx), dev(rt, kstart)
+    out = rt.DeviceBuffer(q.nbytes)
+    wsb = gpu.attention_workspace_bytes(T, H, C)
+    ws = rt.DeviceBuffer(wsb)
+    s = rt.Stream()
+    gpu.attention_dev(dq.ptr, dk.ptr, dv.ptr, de.ptr, ds.ptr if slots > 1 else None, T, H, Hkv, D, L, C, f16, out.ptr,
+                      ws.ptr, wsb, s.handle)
+    s.sync()
+    want = oracle.attention(q, kc, vc, cidx, kstart if slots > 1 else None)
+    got = out.download(np.float32).reshape(T, H, D)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), float(np.max(np.abs(got - want)))
 
 
 # ------------------------------------------------------ fused launches
