@@ -15,13 +15,15 @@
 // sh*q and sl*q (each <= 105), S = 8*H + L; Q6_K w = 128*hi + lo, lo in
 // [0,127], hi in [-32,31]; Q4_K's M term is a third plane with A = m_s.
 //
-// Tiling: wave w takes weight rows 16w..16w+15 (A operand: lane l holds row
-// l%16 and the 16 k of group l/16) against activation tiles of 16 (B, same k
-// mapping); C lane l holds rows 4(l/16)+r, column l%16. Per block of 256 the
-// raw weight blocks, the int8 activation rows and their scales are copied
-// into LDS with global_load_lds, double-buffered. Activation rows sit in LDS
-// with their 16-byte chunks XOR-swizzled by row (chunk c of row m at
-// c ^ (m & 15)). Refused rows take the float32 path at the end.
+// Tiling (a shape C: T threads, NW waves along the weight rows, BM
+// activation rows, NS stages): wave w takes weight rows 16(w % NW).. (A
+// operand: lane l holds row l%16 and the 16 k of group l/16) against
+// activation tiles of 16 (B, same k mapping); C lane l holds rows 4(l/16)+r,
+// column l%16. Per block of 256 the raw weight blocks, the int8 activation
+// rows and their scales are copied into LDS with global_load_lds, NS blocks
+// in flight (a ring of NS stages). Activation rows sit in LDS with their
+// 16-byte chunks XOR-swizzled by row (chunk c of row m at c ^ (m & 15)).
+// Refused rows take the float32 path at the end.
 #include "f32path.hpp"
 #include "mimg_device.hpp"
 #include "mimg_kernels.hpp"
@@ -31,38 +33,43 @@ namespace g16 {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-#ifndef MIMG_GEMM_BM
-#define MIMG_GEMM_BM 128
-#endif
-#ifndef MIMG_GEMM_THREADS
-#define MIMG_GEMM_THREADS 512
-#endif
-#ifndef MIMG_GEMM_NW
-#define MIMG_GEMM_NW 4
-#endif
-constexpr int GM_T = MIMG_GEMM_THREADS;   // threads per workgroup (256: one wave per SIMD, 512: two)
-constexpr int GM_NW = MIMG_GEMM_NW;       // waves along the weight rows (16 rows each)
-constexpr int GM_BN = 16 * GM_NW;         // weight rows per workgroup
-constexpr int GM_BM = MIMG_GEMM_BM;       // activation rows per workgroup
-constexpr int GM_WM = GM_T / 64 / GM_NW;  // waves along the activation rows
-constexpr int GM_TM = GM_BM / 16 / GM_WM; // activation tiles of 16 per wave
-static_assert(GM_WM * GM_NW * 64 == GM_T && GM_TM * GM_WM * 16 == GM_BM && GM_T >= GM_BN && GM_T >= GM_BM,
-              "GEMM tile shape");
-constexpr int GM_ACH = GM_BM * 16 / GM_T; // activation copy instructions per thread per block
+// A workgroup shape: T threads, NW waves along the weight rows (16 rows
+// each), BM activation rows, NS stages in the copy ring.
+template <int T_, int NW_, int BM_, int NS_>
+struct GCfg {
+    static constexpr int T = T_;          // threads per workgroup
+    static constexpr int NW = NW_;        // waves along the weight rows
+    static constexpr int BN = 16 * NW;    // weight rows per workgroup
+    static constexpr int BM = BM_;        // activation rows per workgroup
+    static constexpr int NS = NS_;        // blocks in flight
+    static constexpr int WM = T / 64 / NW;    // waves along the activation rows
+    static constexpr int TM = BM / 16 / WM;   // activation tiles of 16 per wave
+    static constexpr int ACH = BM * 16 / T;   // activation copy instructions per thread per block
+    static_assert(WM * NW * 64 == T && TM * WM * 16 == BM && T >= BN && T >= BM && ACH * T == BM * 16,
+                  "GEMM tile shape");
+};
+// 64 weight rows x 128 activation rows, eight waves (large grids), and the
+// shapes of few activation rows (up to 64): 32 or 16 weight rows, so that
+// the grid holds as many workgroups as the GPU has CUs.
+using CfgWide = GCfg<512, 4, 128, 2>;
+using CfgM64N32 = GCfg<256, 2, 64, 3>;
+using CfgM64N16 = GCfg<256, 1, 64, 3>;
 
-template <uint32_t DT>
+template <uint32_t DT, class C>
 struct GemmLayout {
     // LDS bytes per weight row slot: Q4_K blocks are 16-byte aligned and
     // copied as 9 chunks; Q6_K blocks (2-byte aligned) are copied as the 54
     // aligned dwords that cover them.
     static constexpr int WSLOT = DT == DT_Q4_K ? 144 : 216;
-    static constexpr int WDMA = DT == DT_Q4_K ? (GM_BN * 9 + GM_T - 1) / GM_T   // copy instructions per
-                                             : (GM_BN * 54 + GM_T - 1) / GM_T;  // thread per block
-    static constexpr int WBYTES = WDMA * GM_T * (DT == DT_Q4_K ? 16 : 4);  // incl. slack for unconditional copies
-    static constexpr int ABYTES = GM_BM * 256;
-    static constexpr int DXBYTES = GM_T * 4;
+    static constexpr int WDMA = DT == DT_Q4_K ? (C::BN * 9 + C::T - 1) / C::T   // copy instructions per
+                                             : (C::BN * 54 + C::T - 1) / C::T;  // thread per block
+    static constexpr int WBYTES = WDMA * C::T * (DT == DT_Q4_K ? 16 : 4);  // incl. slack for unconditional copies
+    static constexpr int ABYTES = C::BM * 256;
+    static constexpr int DXBYTES = C::T * 4;
     static constexpr int BUF = WBYTES + ABYTES + DXBYTES;
-    static constexpr int NDMA = WDMA + GM_ACH + 1;
+    static constexpr int NDMA = WDMA + C::ACH + 1;
+    static_assert(C::NS * BUF <= 160 * 1024, "GEMM stages exceed LDS");
+    static_assert((C::NS - 1) * NDMA < 64, "the ring's copies in flight exceed the wait counter");
 };
 
 struct GemmArgs {
@@ -115,49 +122,50 @@ __device__ __forceinline__ void gm_barrier() {
 
 // Issues the copies of block b into LDS buffer `buf` (every thread issues
 // exactly NDMA instructions, so the wait counts are the same in each wave).
-template <uint32_t DT>
+template <uint32_t DT, class C>
 __device__ __forceinline__ void gemm_issue_block(const GemmArgs& A, int n0, int m0, int b, uint8_t* buf) {
-    using L = GemmLayout<DT>;
-    const int t = threadIdx.x, wave = t >> 6;  // wave of the workgroup (0 .. GM_T/64-1)
+    using L = GemmLayout<DT, C>;
+    const int t = threadIdx.x, wave = t >> 6;  // wave of the workgroup (0 .. T/64-1)
     uint8_t* wl = buf;
     uint8_t* al = buf + L::WBYTES;
     uint8_t* dl = al + L::ABYTES;
     if constexpr (DT == DT_Q4_K) {
 #pragma unroll
         for (int i = 0; i < L::WDMA; i++) {
-            const int c = min(GM_T * i + t, GM_BN * 9 - 1);  // chunk of 16 bytes
+            const int c = min(C::T * i + t, C::BN * 9 - 1);  // chunk of 16 bytes
             const int r = c / 9, j = c - 9 * r;
             const int n = min(n0 + r, A.N - 1);
-            lds_copy16(A.W + (int64_t)n * A.rb + (int64_t)b * Q4K_BYTES + 16 * j, wl + 16 * (GM_T * i + 64 * wave));
+            lds_copy16(A.W + (int64_t)n * A.rb + (int64_t)b * Q4K_BYTES + 16 * j, wl + 16 * (C::T * i + 64 * wave));
         }
     } else {
 #pragma unroll
         for (int i = 0; i < L::WDMA; i++) {
-            const int c = min(GM_T * i + t, GM_BN * 54 - 1);  // dword
+            const int c = min(C::T * i + t, C::BN * 54 - 1);  // dword
             const int r = c / 54, j = c - 54 * r;
             const int n = min(n0 + r, A.N - 1);
             const uint8_t* blk = A.W + (int64_t)n * A.rb + (int64_t)b * Q6K_BYTES;
             const uint8_t* base = (const uint8_t*)__builtin_align_down(blk, 4);
-            lds_copy4(base + 4 * j, wl + 4 * (GM_T * i + 64 * wave));
+            lds_copy4(base + 4 * j, wl + 4 * (C::T * i + 64 * wave));
         }
     }
 #pragma unroll
-    for (int i = 0; i < GM_ACH; i++) {
-        const int c = GM_T * i + t;              // LDS chunk: row c/16, slot c%16
+    for (int i = 0; i < C::ACH; i++) {
+        const int c = C::T * i + t;              // LDS chunk: row c/16, slot c%16
         const int r = c >> 4, s = c & 15;
         const int m = min(m0 + r, A.M - 1);
-        lds_copy16(A.q + (int64_t)m * A.K + 256 * b + 16 * (s ^ (r & 15)), al + 16 * (GM_T * i + 64 * wave));
+        lds_copy16(A.q + (int64_t)m * A.K + 256 * b + 16 * (s ^ (r & 15)), al + 16 * (C::T * i + 64 * wave));
     }
     {
-        const int m = min(m0 + min(t, GM_BM - 1), A.M - 1);
-        lds_copy4(A.d32 + (int64_t)m * (A.K / 32) + 8 * b, dl + 4 * (64 * wave));  // slots t >= GM_BM are slack
+        const int m = min(m0 + min(t, C::BM - 1), A.M - 1);
+        lds_copy4(A.d32 + (int64_t)m * (A.K / 32) + 8 * b, dl + 4 * (64 * wave));  // slots t >= BM are slack
     }
 }
 
-template <uint32_t DT>
-__global__ __launch_bounds__(GM_T) void gemm_a8k_kernel(GemmArgs A) {
-    using L = GemmLayout<DT>;
-    __shared__ __align__(16) uint8_t smem[2 * L::BUF];
+template <uint32_t DT, class C>
+__global__ __launch_bounds__(C::T) void gemm_a8k_kernel(GemmArgs A) {
+    using L = GemmLayout<DT, C>;
+    constexpr int GM_NW = C::NW, GM_BN = C::BN, GM_BM = C::BM, GM_TM = C::TM, GM_T = C::T, NS = C::NS;
+    __shared__ __align__(16) uint8_t smem[NS * L::BUF];
     __shared__ int flags[2];
     const int t = threadIdx.x, l = t & 63;
     const int wn = (t >> 6) % GM_NW, wm = (t >> 6) / GM_NW;  // this wave's weight rows 16wn.., activation tiles wm*GM_TM..
@@ -187,15 +195,17 @@ __global__ __launch_bounds__(GM_T) void gemm_a8k_kernel(GemmArgs A) {
         for (int r = 0; r < 4; r++) tot[mt][r] = off[mt][r] = 0.f;
     }
 
-    gemm_issue_block<DT>(A, n0, m0, 0, smem);
+    // The ring: blocks 0 .. NS-2 first; at block b, block b + NS - 1 goes
+    // into the stage block b - 1 used (every wave is past it: the barrier
+    // that ends block b - 1). Past the last block the last one is copied
+    // again into the free stage, so every thread always has the same
+    // number of copies in flight and one wait count serves every block.
+#pragma unroll
+    for (int i = 0; i < NS - 1; i++) gemm_issue_block<DT, C>(A, n0, m0, min(i, nb - 1), smem + i * L::BUF);
     for (int b = 0; b < nb; b++) {
-        uint8_t* buf = smem + (b & 1) * L::BUF;
-        if (b + 1 < nb) {
-            gemm_issue_block<DT>(A, n0, m0, b + 1, smem + ((b + 1) & 1) * L::BUF);
-            GM_WAIT_VMCNT(L::NDMA);  // block b's copies (issued earlier) have landed
-        } else {
-            GM_WAIT_VMCNT(0);
-        }
+        uint8_t* buf = smem + (b % NS) * L::BUF;
+        gemm_issue_block<DT, C>(A, n0, m0, min(b + NS - 1, nb - 1), smem + ((b + NS - 1) % NS) * L::BUF);
+        GM_WAIT_VMCNT((NS - 1) * L::NDMA);  // block b's copies (issued NS - 1 blocks earlier) have landed
         gm_barrier();
         const uint8_t* wl = buf;
         const uint8_t* al = buf + L::WBYTES;
@@ -321,8 +331,9 @@ __global__ __launch_bounds__(GM_T) void gemm_a8k_kernel(GemmArgs A) {
             accM[mt] = v4i{0, 0, 0, 0};
         }
         GM_WAIT_LGKM0();
-        gm_barrier();  // buffer b&1 is reloaded in the next iteration
+        gm_barrier();  // stage b % NS is reloaded in the next iteration
     }
+    GM_WAIT_VMCNT(0);  // the ring's extra copies have landed before the workgroup's LDS is given back
 
     // Outputs: lane holds rows n = n0 + 16*wave + 4G + r of column m.
     const int nbase = n0 + 16 * wn + 4 * G;
@@ -358,7 +369,20 @@ __global__ __launch_bounds__(GM_T) void gemm_a8k_kernel(GemmArgs A) {
 
 }  // namespace g16
 
+template <class C>
+static hipError_t launch_g16(const g16::GemmArgs& A, uint32_t dt, int64_t n, int64_t rows, hipStream_t stream) {
+    using namespace g16;
+    const dim3 grid((unsigned)((n + C::BN - 1) / C::BN), (unsigned)((rows + C::BM - 1) / C::BM));
+    if (dt == DT_Q4_K)
+        hipLaunchKernelGGL((gemm_a8k_kernel<DT_Q4_K, C>), grid, dim3(C::T), 0, stream, A);
+    else
+        hipLaunchKernelGGL((gemm_a8k_kernel<DT_Q6_K, C>), grid, dim3(C::T), 0, stream, A);
+    return hipGetLastError();
+}
+
 // The 16 x 16 x 64 form of the prefill GEMM (see the top of this file).
+// Up to 64 activation rows: 64-row tiles, 32 weight rows a workgroup where
+// that gives at least 256 workgroups, else 16; more rows: 64 x 128 tiles.
 hipError_t launch_gemm_a8k_16(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows, const float* x,
                            const float* bias, float* y, hipStream_t stream) {
     using namespace g16;
@@ -378,12 +402,11 @@ hipError_t launch_gemm_a8k_16(const DevWeight& w, const ActPtrs& a, int64_t rows
     A.ok = a.ok;
     A.x = x;
     A.fused = total_rows <= 8;
-    dim3 grid((unsigned)((w.n + GM_BN - 1) / GM_BN), (unsigned)((rows + GM_BM - 1) / GM_BM));
-    if (w.dt == DT_Q4_K)
-        hipLaunchKernelGGL(gemm_a8k_kernel<DT_Q4_K>, grid, dim3(GM_T), 0, stream, A);
-    else
-        hipLaunchKernelGGL(gemm_a8k_kernel<DT_Q6_K>, grid, dim3(GM_T), 0, stream, A);
-    return hipGetLastError();
+    if (rows <= 64) {
+        if ((w.n + 31) / 32 >= 256) return launch_g16<CfgM64N32>(A, w.dt, w.n, rows, stream);
+        return launch_g16<CfgM64N16>(A, w.dt, w.n, rows, stream);
+    }
+    return launch_g16<CfgWide>(A, w.dt, w.n, rows, stream);
 }
 
 }  // namespace mimg
