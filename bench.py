@@ -240,15 +240,15 @@ def cfg4_oracle_check(tensors, prompt, gpu_ids, log):
         fx = json.load(f)
     same_weights = mk.digests(synthetic.host_bytes({n: tensors[n] for n in mk.DIGESTED})) == fx["weights_sha256"]
     same_prompt = np.array_equal(prompt, mk.prompts(synthetic.LLAMA_8B["vocab"])[0])
-    n = len(fx["ids"])
-    equal = same_weights and same_prompt and [int(v) for v in gpu_ids[:n]] == fx["ids"]
+    n = min(len(fx["ids"]), len(gpu_ids))
+    equal = same_weights and same_prompt and [int(v) for v in gpu_ids[:n]] == fx["ids"][:n]
     log(f"  llama8b 512-token prompt: first {n} GPU ids {'==' if equal else '!='} the CPU restatement's "
         f"(fixture; weights {'match' if same_weights else 'differ'})")
     return {"ids_equal_cpu_restatement": bool(equal), "tokens_checked": n, "weights_match_fixture": bool(same_weights),
             "fixture": "tests/golden/cfg4_ids.json"}
 
 
-def decode_bench(name, log, graph=True, cpu=False, batches=(1, 8)):
+def decode_bench(name, log, graph=True, cpu=False, batches=(1, 8), new_tokens=None):
     """Greedy generation on the GPU decoder with a random model of the
     named shape (module docstring); batches selects the 8B runs."""
     import decoder
@@ -256,6 +256,8 @@ def decode_bench(name, log, graph=True, cpu=False, batches=(1, 8)):
 
     cfg = dict(synthetic.LLAMA_1B if name == "llama1b" else synthetic.LLAMA_8B)
     runs = [(32, 128, 1)] if name == "llama1b" else [(512, 256, b) for b in batches]
+    if new_tokens:  # profiler runs: fewer decode steps
+        runs = [(p, new_tokens, b) for p, _, b in runs]
     cfg["context"] = max(p + n for p, n, _ in runs)
     t0 = time.time()
     # the 8B weights are the GPU tests' (seed 3), whose 512-token prompt ids
@@ -322,11 +324,14 @@ def main():
     ap.add_argument("--eager", action="store_true", help="launch without HIP graphs (every timed section)")
     ap.add_argument("--prefill-rows", default="64,512,2048",
                     help="activation rows of the prefill GEMM measurements (comma list; empty to skip)")
-    ap.add_argument("--prefill-kinds", default="a8,q8_0,f32",
-                    help="prefill products to time: a8 (Q4_K/Q6_K x 8-bit), q8_0 (Q8_0 x 8-bit), f32")
+    ap.add_argument("--prefill-kinds", default="a8,q8_0,b32,f32",
+                    help="prefill products to time: a8 (Q4_K/Q6_K x 8-bit blocks of 256), q8_0 (Q8_0 x 8-bit), "
+                         "b32 (Q4_K/Q6_K x 8-bit blocks of 32, the tiled opt-in), f32")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time only the prefill products (for profiler runs) and print them as one JSON line")
     ap.add_argument("--decode-batches", default="1,8", help="batch sizes of the llama8b decode runs")
+    ap.add_argument("--decode-tokens", type=int, default=0,
+                    help="new tokens per decode run (default: the configs' 128 and 256; fewer for profiler runs)")
     ap.add_argument("--decode", default="llama1b,llama8b",
                     help="whole-model decode runs (comma list of llama1b, llama8b; empty to skip)")
     ap.add_argument("--step", default="group", choices=["chain", "group"],
@@ -364,9 +369,9 @@ def main():
     # dequant_matmul.v1): the same products with float32 activations on the
     # fp32 matrix cores (mimg_linear_f32_mfma_dev), fraction of the dense
     # fp32 matrix peak.
-    def prefill(name, rows, f32=False, q8_layers=None):
+    def prefill(name, rows, f32=False, q8_layers=None, b32=False):
         _, n, k, dt, _, _ = next(c for c in CFG1 if c[0] == name)
-        block = 32 if q8_layers else 256
+        block = 32 if (q8_layers or b32) else 256
         xp = hiprt.DeviceBuffer.from_array(np.random.default_rng(200 + rows).standard_normal((rows, k), dtype=np.float32))
         wsb = mimg.a8_workspace_bytes(rows, k)
         wsp = hiprt.DeviceBuffer(wsb)
@@ -381,6 +386,9 @@ def main():
                 elif q8_layers:
                     mimg.matmul_a8_quantized_q8_0_tiled_dev(src[l][name], xp.ptr, rows, None, yp.ptr, wsp.ptr, wsb,
                                                             stream.handle)
+                elif b32:
+                    mimg.matmul_a8_quantized_b32_tiled_dev(src[l][name], xp.ptr, rows, None, yp.ptr, wsp.ptr, wsb,
+                                                           stream.handle)
                 else:
                     mimg.matmul_a8_quantized_dev(src[l][name], xp.ptr, rows, None, block, yp.ptr, wsp.ptr, wsb,
                                                  stream.handle)
@@ -412,6 +420,7 @@ def main():
 
     def run_prefills():
         prefill_res, prefill_q8, prefill_f32 = {}, {}, {}
+        prefill_b32.clear()
         prefill_rows = [int(r) for r in args.prefill_rows.split(",") if r]
         q8_layers = make_q8_0_weights(stream, args.rotate, log) if prefill_rows and "q8_0" in kinds else None
         for rows in prefill_rows:
@@ -422,6 +431,9 @@ def main():
                 if q8_layers:
                     prefill_q8[f"{name}_M{rows}"] = prefill(name, rows, q8_layers=q8_layers)
                     log(f"  prefill Q8_0 {name} M={rows}: {prefill_q8[f'{name}_M{rows}']}")
+                if "b32" in kinds:
+                    prefill_b32[f"{name}_M{rows}"] = prefill(name, rows, b32=True)
+                    log(f"  prefill {name} blocks of 32 M={rows}: {prefill_b32[f'{name}_M{rows}']}")
                 if "f32" in kinds:
                     prefill_f32[f"{name}_M{rows}"] = prefill(name, rows, f32=True)
                     log(f"  prefill f32 {name} M={rows}: {prefill_f32[f'{name}_M{rows}']}")
@@ -430,9 +442,11 @@ def main():
         return prefill_res, prefill_q8, prefill_f32
 
     kinds = args.prefill_kinds.split(",")
+    prefill_b32 = {}
     if args.prefill_only:
         pr, pq, pf = run_prefills()
-        print(json.dumps({"prefill": pr, "prefill_q8_0": pq, "prefill_f32": pf, "graphs": not args.eager}), flush=True)
+        print(json.dumps({"prefill": pr, "prefill_q8_0": pq, "prefill_kquant_b32": prefill_b32, "prefill_f32": pf,
+                          "graphs": not args.eager}), flush=True)
         return
 
     # A decoder layer's calls: q, k and v share the attention input and gate
@@ -720,6 +734,13 @@ def main():
                         "within the spec's a8 tolerance), activations quantized beforehand",
             "results": prefill_q8,
         },
+        "prefill_kquant_b32": {
+            "workload": "cfg2's gate (Q4_K) and down (Q6_K) with activation blocks of 32 (a dequant_matmul_a8.v1 "
+                        "graph) on the int8 MFMA GEMM (mimg_matmul_a8_quantized_b32_tiled_dev, opt-in: the "
+                        "reference's per-block form with one float chain, within the spec's a8 tolerance), "
+                        "activations quantized beforehand",
+            "results": prefill_b32,
+        },
         "prefill_f32": {
             "workload": "the same gate/down products with float32 activations (dequant_matmul.v1) on the fp32 "
                         "matrix cores, within the spec bound (K+1)u sum|xw|",
@@ -736,7 +757,8 @@ def main():
     decode_res = {}
     for name in [d for d in args.decode.split(",") if d]:
         decode_res.update(decode_bench(name, log, graph=not args.eager, cpu=not args.no_cpu,
-                                       batches=[int(b) for b in args.decode_batches.split(",") if b]))
+                                       batches=[int(b) for b in args.decode_batches.split(",") if b],
+                                       new_tokens=args.decode_tokens))
     if decode_res:
         result["decode"] = decode_res
     if not args.no_cpu:

@@ -329,6 +329,27 @@ int mimg_matmul_a8_quantized_dev(uint64_t w, const float *x, int64_t rows, const
 int mimg_matmul_a8_quantized_q8_0_tiled_dev(uint64_t w, const float *x, int64_t rows, const float *bias, float *y,
                                             const void *ws, uint64_t ws_bytes, void *stream);
 
+/* The matrix-core products with activation blocks of 32 for Q8_0, Q4_K and
+ * Q6_K weights (ws from mimg_quantize_act_dev with block 32): Q8_0 as
+ * mimg_matmul_a8_quantized_q8_0_tiled_dev; Q4_K and Q6_K in the reference's
+ * per-block form of dotQ4KQ8AVX2 / dotQ6KQ8AVX2 (internal/kernels/
+ * kernels_amd64.s:428-597, 760-882) with one float chain where those keep
+ * eight lanes: per weight block, over its activation blocks j in order,
+ * t = fma(f32(S_j), dx_j, t) with S_j the exact int32 sum of sc * q * y over
+ * block j (Q6_K: both sub-blocks of 16 with their scales), tot = fma(d, t,
+ * tot); Q4_K also off = fma(dmin * f32(m_j), dbs_j, off); result tot - off
+ * (Q4_K) or tot, plus the bias. Each weight byte is read once per tile of
+ * activation rows (the lane-order GEMV of the other entry points reads it
+ * once per eight rows). A tolerance claim as the Q8_0 form: within the
+ * spec's dequant_matmul_a8 bound (spec/stdlib.md:260-275); each row's result
+ * depends on that row alone; refused rows take the reference-order float32
+ * path. Returns MIMG_NOT_HANDLED for shapes or weight alignments it does
+ * not tile (Q4_K blocks must start 16-byte aligned, Q6_K 2-byte). No
+ * reference counterpart: a faster form of the products interp/fast.go:282-379
+ * makes, for callers that accept the tolerance. */
+int mimg_matmul_a8_quantized_b32_tiled_dev(uint64_t w, const float *x, int64_t rows, const float *bias, float *y,
+                                           const void *ws, uint64_t ws_bytes, void *stream);
+
 /* mimg_matmul_a8_quantized_dev for a group of 1 to 3 weights sharing K and
  * the quantized activations (e.g. q, k and v after
  * mimg_rms_norm_quant_dev); bias may be NULL or hold NULLs. No reference

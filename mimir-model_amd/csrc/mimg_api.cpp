@@ -845,6 +845,35 @@ int mimg_matmul_a8_quantized_q8_0_tiled_dev(uint64_t wh, const float* x, int64_t
     return MIMG_OK;
 }
 
+int mimg_matmul_a8_quantized_b32_tiled_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, float* y,
+                                           const void* ws, uint64_t ws_bytes, void* stream) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    Held w;
+    if ((rc = w.acquire(wh))) return rc;
+    const uint32_t dt = w->dw.dt;
+    if (dt != DT_Q8_0 && dt != DT_Q4_K && dt != DT_Q6_K)
+        return fail(MIMG_ERR_ARG, "%s: the tiled products with blocks of 32 are for Q8_0, Q4_K and Q6_K weights",
+                    dt_name(dt));
+    if (rows < 0) return fail(MIMG_ERR_ARG, "rows = %lld", (long long)rows);
+    if (rows == 0) return MIMG_OK;
+    if (!x || !y || !ws || !aligned(ws, 256)) return fail(MIMG_ERR_ARG, "null or misaligned pointer");
+    ActLayout l = act_layout(rows, w->dw.k);
+    if (ws_bytes < l.total) return fail(MIMG_ERR_WORKSPACE, "workspace %llu < %llu bytes", (unsigned long long)ws_bytes, (unsigned long long)l.total);
+    if ((rc = check_outputs(x, rows, w->dw.k, &w->dw.n, &y, 1))) return rc;
+    if (dt == DT_Q8_0) {
+        if (!gemm_q8_0_ok(w->dw)) return fail(MIMG_NOT_HANDLED, "no tiled Q8_0 product for this shape");
+        HIP_TRY(launch_gemm_q8_0(w->dw, act_ptrs((void*)ws, l), rows, rows, x, bias, y, (hipStream_t)stream));
+        return MIMG_OK;
+    }
+    // the tile copies take Q4_K blocks as whole 16-byte chunks and Q6_K
+    // blocks from the 16-byte boundary below them (even addresses)
+    if (!gemm_kq_b32_ok(w->dw) || !aligned(w->dw.data, dt == DT_Q4_K ? 16 : 2))
+        return fail(MIMG_NOT_HANDLED, "no tiled %s product with blocks of 32 for this shape or alignment", dt_name(dt));
+    HIP_TRY(launch_gemm_kq_b32(w->dw, act_ptrs((void*)ws, l), rows, rows, x, bias, y, (hipStream_t)stream));
+    return MIMG_OK;
+}
+
 // When a single activation row is quantized inside the GEMV kernel: every
 // workgroup then quantizes the whole row, which pays while the group is
 // small (q/k/v, o); for long rows or many weight rows a separate quantize

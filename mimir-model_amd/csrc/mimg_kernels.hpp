@@ -127,6 +127,11 @@ hipError_t launch_gemv_a8k_fused_norm_rope(const DevWeight* const* ws, const flo
 // with K a multiple of 256, on the int8 matrix cores (gemm_q8_0.hip): exact
 // block sums, one float chain in block order (within the spec's tolerance).
 bool gemm_q8_0_ok(const DevWeight& w);
+// Q4_K / Q6_K x activations in blocks of 32 on the int8 matrix cores (one
+// float chain of exact block sums: a tolerance claim, gemm_kq_b32.hip).
+bool gemm_kq_b32_ok(const DevWeight& w);
+hipError_t launch_gemm_kq_b32(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows, const float* x,
+                              const float* bias, float* y, hipStream_t stream);
 hipError_t launch_gemm_q8_0(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows, const float* x,
                             const float* bias, float* y, hipStream_t stream);
 

@@ -60,6 +60,7 @@ SIGNATURES = {
                                            _P, _P, _P, _P, _I, _I, _I, _I, _I, _I64, _P, _P, _I, _P]),
     "mimg_matmul_a8_quantized_dev": (_I, [_U64, _P, _I64, _P, _I, _P, _P, _U64, _P]),
     "mimg_matmul_a8_quantized_q8_0_tiled_dev": (_I, [_U64, _P, _I64, _P, _P, _P, _U64, _P]),
+    "mimg_matmul_a8_quantized_b32_tiled_dev": (_I, [_U64, _P, _I64, _P, _P, _P, _U64, _P]),
     "mimg_linear_f32_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
     "mimg_linear_f32_mfma_dev": (_I, [_U64, _P, _I64, _P, _P, _P]),
     "mimg_dequantize_dev": (_I, [_U32, _P, _U64, _P, _I64, _P]),
@@ -364,6 +365,16 @@ def matmul_a8_quantized_q8_0_tiled_dev(w, x_ptr, rows, bias_ptr, y_ptr, ws_ptr, 
     _check(load().mimg_matmul_a8_quantized_q8_0_tiled_dev(w.handle, _P(x_ptr), rows,
                                                           _P(bias_ptr) if bias_ptr else None, _P(y_ptr),
                                                           _P(ws_ptr), ws_bytes, _P(stream)))
+
+
+def matmul_a8_quantized_b32_tiled_dev(w, x_ptr, rows, bias_ptr, y_ptr, ws_ptr, ws_bytes, stream):
+    """Q8_0, Q4_K or Q6_K x activations quantized in blocks of 32 on the
+    int8 matrix cores (each weight byte read once per tile of rows): one
+    float chain per weight block, a tolerance claim (not the reference's
+    lane order; the default entry points keep that)."""
+    _check(load().mimg_matmul_a8_quantized_b32_tiled_dev(w.handle, _P(x_ptr), rows,
+                                                         _P(bias_ptr) if bias_ptr else None, _P(y_ptr),
+                                                         _P(ws_ptr), ws_bytes, _P(stream)))
 
 
 def matmul_a8_quantized_group_dev(weights, x_ptr, rows, bias_ptrs, block, y_ptrs, ws_ptr, ws_bytes, stream):
