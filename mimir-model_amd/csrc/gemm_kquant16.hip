@@ -161,6 +161,58 @@ __device__ __forceinline__ void gemm_issue_block(const GemmArgs& A, int n0, int 
     }
 }
 
+// The A operands of k step ks (64 k) for this lane's weight row wr (the
+// block in LDS) and k group G. Q4_K: sc = 8*sh + sl with sh, sl <= 7: sh*q
+// and sl*q (q <= 15) are at most 105, so each plane is the packed nibbles
+// times a small constant (16-bit lanes, no carry between the bytes); aM
+// holds the sub-block's min m_s in every byte.
+__device__ __forceinline__ void q4k_operands(const uint8_t* wr, const Q4KScales& s, int ks, int G, v4i& aH, v4i& aL,
+                                             v4i& aM) {
+    const int sub = 2 * ks + (G >> 1);
+    const uint32_t sc = byte_of(s.sc, sub), mm = byte_of(s.m, sub);
+    const u32x4 qraw = *(const u32x4*)(wr + 16 + 32 * ks + 16 * (G & 1));
+    const uint32_t qd[4] = {qraw.x, qraw.y, qraw.z, qraw.w};
+    const short sh = (short)(sc >> 3), sl = (short)(sc & 7);
+    const s16x2 shp = {sh, sh}, slp = {sl, sl};
+    const int shift = 4 * (G >> 1);  // low nibbles for G < 2, high for G >= 2
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const s16x2 nib = as_s16x2((qd[k] >> shift) & 0x0F0F0F0Fu);
+        aH[k] = (int)as_u32(nib * shp);
+        aL[k] = (int)as_u32(nib * slp);
+        aM[k] = (int)(mm * 0x01010101u);
+    }
+}
+
+// Q6_K: the two planes of sc*(q - 32) (hi and lo, S = 128 hi + lo) of k step
+// ks for the block at wr (rsh = wr & 3, wra the dword below it).
+__device__ __forceinline__ void q6k_operands(const uint32_t* wra, uint32_t rsh, const uint8_t* wr, int ks, int G,
+                                             v4i& aH, v4i& aL) {
+    auto rd16 = [&](int off) -> u32x4 {  // 16 bytes at wr + off (off % 4 == 0)
+        const uint32_t* p = wra + off / 4;
+        return u32x4{__builtin_amdgcn_alignbyte(p[1], p[0], rsh), __builtin_amdgcn_alignbyte(p[2], p[1], rsh),
+                     __builtin_amdgcn_alignbyte(p[3], p[2], rsh), __builtin_amdgcn_alignbyte(p[4], p[3], rsh)};
+    };
+    const int h = ks >> 1, p = 2 * (ks & 1) + (G >> 1);
+    const u32x4 ql = rd16(64 * h + 32 * (p & 1) + 16 * (G & 1));
+    const u32x4 qh = rd16(128 + 32 * h + 16 * (G & 1));
+    const int sc = (int)(int8_t)wr[192 + 8 * h + (G & 1) + 2 * p];
+    const s16x2 sc2 = {(short)sc, (short)sc};
+    const uint32_t qld[4] = {ql.x, ql.y, ql.z, ql.w}, qhd[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t q6 = (((p >> 1) ? (qld[k] >> 4) : qld[k]) & 0x0F0F0F0Fu) |
+                            (((qhd[k] >> (2 * p)) & 0x03030303u) << 4);
+        // 16-bit lanes of sc*(q - 32): packed integer ops, exact (|w| <= 4096)
+        const s16x2 we = (as_s16x2(q6 & 0x00FF00FFu) - (s16x2){32, 32}) * sc2;
+        const s16x2 wo = (as_s16x2((q6 >> 8) & 0x00FF00FFu) - (s16x2){32, 32}) * sc2;
+        uint32_t lo, hi;
+        split4(as_u32(we), as_u32(wo), as_u32(we >> (s16x2){7, 7}), as_u32(wo >> (s16x2){7, 7}), lo, hi);
+        aL[k] = (int)lo;
+        aH[k] = (int)hi;
+    }
+}
+
 template <uint32_t DT, class C>
 __global__ __launch_bounds__(C::T) void gemm_a8k_kernel(GemmArgs A) {
     using L = GemmLayout<DT, C>;
@@ -233,24 +285,8 @@ __global__ __launch_bounds__(C::T) void gemm_a8k_kernel(GemmArgs A) {
                     const int row = 16 * (wm * GM_TM + mt) + ar;
                     bvs[mt] = *(const v4i*)(al + row * 256 + 16 * ((4 * ks + G) ^ (row & 15)));
                 }
-                const int sub = 2 * ks + (G >> 1);
-                const uint32_t sc = byte_of(s.sc, sub), mm = byte_of(s.m, sub);
-                const u32x4 qraw = *(const u32x4*)(wr + 16 + 32 * ks + 16 * (G & 1));
-                const uint32_t qd[4] = {qraw.x, qraw.y, qraw.z, qraw.w};
-                // sc = 8*sh + sl with sh, sl <= 7: sh*q and sl*q (q <= 15) are at
-                // most 105, so each plane is the packed nibbles times a small
-                // constant (16-bit lanes, no carry between the bytes).
-                const short sh = (short)(sc >> 3), sl = (short)(sc & 7);
-                const s16x2 shp = {sh, sh}, slp = {sl, sl};
-                const int shift = 4 * (G >> 1);  // low nibbles for G < 2, high for G >= 2
                 v4i aH, aL, aM;
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const s16x2 nib = as_s16x2((qd[k] >> shift) & 0x0F0F0F0Fu);
-                    aH[k] = (int)as_u32(nib * shp);
-                    aL[k] = (int)as_u32(nib * slp);
-                    aM[k] = (int)(mm * 0x01010101u);
-                }
+                q4k_operands(wr, s, ks, G, aH, aL, aM);
 #pragma unroll
                 for (int mt = 0; mt < GM_TM; mt++) {
                     accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bvs[mt], accH[mt], 0, 0, 0);
@@ -268,11 +304,6 @@ __global__ __launch_bounds__(C::T) void gemm_a8k_kernel(GemmArgs A) {
             const uint8_t* wr = wbyte_addr(16 * wn + ar);
             const uint32_t rsh = (uint32_t)((uintptr_t)wr & 3);
             const uint32_t* wra = (const uint32_t*)(wr - rsh);
-            auto rd16 = [&](int off) -> u32x4 {  // 16 bytes at wr + off (off % 4 == 0)
-                const uint32_t* p = wra + off / 4;
-                return u32x4{__builtin_amdgcn_alignbyte(p[1], p[0], rsh), __builtin_amdgcn_alignbyte(p[2], p[1], rsh),
-                             __builtin_amdgcn_alignbyte(p[3], p[2], rsh), __builtin_amdgcn_alignbyte(p[4], p[3], rsh)};
-            };
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const uint8_t* wc = wbyte_addr(16 * wn + 4 * G + r);
@@ -289,25 +320,8 @@ __global__ __launch_bounds__(C::T) void gemm_a8k_kernel(GemmArgs A) {
                     const int row = 16 * (wm * GM_TM + mt) + ar;
                     bvs[mt] = *(const v4i*)(al + row * 256 + 16 * ((4 * ks + G) ^ (row & 15)));
                 }
-                const int h = ks >> 1, p = 2 * (ks & 1) + (G >> 1);
-                const u32x4 ql = rd16(64 * h + 32 * (p & 1) + 16 * (G & 1));
-                const u32x4 qh = rd16(128 + 32 * h + 16 * (G & 1));
-                const int sc = (int)(int8_t)wr[192 + 8 * h + (G & 1) + 2 * p];
-                const s16x2 sc2 = {(short)sc, (short)sc};
-                const uint32_t qld[4] = {ql.x, ql.y, ql.z, ql.w}, qhd[4] = {qh.x, qh.y, qh.z, qh.w};
                 v4i aH, aL;
-#pragma unroll
-                for (int k = 0; k < 4; k++) {
-                    const uint32_t q6 = (((p >> 1) ? (qld[k] >> 4) : qld[k]) & 0x0F0F0F0Fu) |
-                                        (((qhd[k] >> (2 * p)) & 0x03030303u) << 4);
-                    // 16-bit lanes of sc*(q - 32): packed integer ops, exact (|w| <= 4096)
-                    const s16x2 we = (as_s16x2(q6 & 0x00FF00FFu) - (s16x2){32, 32}) * sc2;
-                    const s16x2 wo = (as_s16x2((q6 >> 8) & 0x00FF00FFu) - (s16x2){32, 32}) * sc2;
-                    uint32_t lo, hi;
-                    split4(as_u32(we), as_u32(wo), as_u32(we >> (s16x2){7, 7}), as_u32(wo >> (s16x2){7, 7}), lo, hi);
-                    aL[k] = (int)lo;
-                    aH[k] = (int)hi;
-                }
+                q6k_operands(wra, rsh, wr, ks, G, aH, aL);
 #pragma unroll
                 for (int mt = 0; mt < GM_TM; mt++) {
                     accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bvs[mt], accH[mt], 0, 0, 0);
@@ -367,6 +381,171 @@ __global__ __launch_bounds__(C::T) void gemm_a8k_kernel(GemmArgs A) {
     }
 }
 
+// Up to 64 activation rows with few weight rows (down at 64 prompt rows:
+// 4096 rows, 256 workgroups of 16): the four waves of a workgroup split each
+// block's four k steps of 64 instead of the activation rows, so each weight
+// plane is built once and feeds all four 16-row activation tiles. Each wave
+// writes its exact partial sums (S; Q4_K also the M term) per (activation
+// row, weight row) to an LDS table; after a barrier every thread adds the
+// four partials of its four (weight row, activation row) pairs (exact
+// integers, any order) and runs the block's float step, the same as the
+// other kernels: the result is bit for bit theirs.
+using CfgKs = GCfg<256, 1, 64, 3>;
+constexpr int KS_RS = 20;  // table row stride in ints: 16 weight rows + 4 of padding (banks)
+
+template <uint32_t DT>
+__global__ __launch_bounds__(256) void gemm_a8k_ks_kernel(GemmArgs A) {
+    using C = CfgKs;
+    using L = GemmLayout<DT, C>;
+    constexpr int NS = C::NS, TAB = 4 * 64 * KS_RS;  // ints per table: [k step][activation row][weight row]
+    __shared__ __align__(16) uint8_t smem[NS * L::BUF];
+    __shared__ __align__(16) int tabS[TAB];
+    __shared__ __align__(16) int tabM[DT == DT_Q4_K ? TAB : 4];
+    __shared__ int flags[2];
+    const int t = threadIdx.x, l = t & 63, ks = t >> 6;  // this wave's k step of each block
+    const int ar = l & 15, G = l >> 4;
+    const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 64;
+    const int nb = A.nb;
+    // The float step's pairs of this thread: activation row mc, weight rows 4ng..4ng+3.
+    const int mc = t & 63, ng = t >> 6;
+
+    if (t == 0) flags[0] = 0;
+    __syncthreads();
+    {
+        int f = 0;
+        if (t < 16 && n0 + t < A.N) f |= A.wref[n0 + t] != 0;
+        if (t < 64 && m0 + t < A.M) f |= A.ok[m0 + t] == 0;
+        if (f) flags[0] = 1;
+    }
+    float tot[4] = {0.f, 0.f, 0.f, 0.f}, off[4] = {0.f, 0.f, 0.f, 0.f};
+    // Q6_K: the byte offset mod 4 of block 0 of this lane's row and of the
+    // float step's four rows (a block is 210 bytes, 2 mod 4: block b's
+    // offset is that + 2b mod 4).
+    uint32_t wsh0 = 0, fsh0[4] = {0, 0, 0, 0};
+    if constexpr (DT == DT_Q6_K) {
+        wsh0 = (uint32_t)(uintptr_t)(A.W + (int64_t)min(n0 + ar, A.N - 1) * A.rb) & 3u;
+#pragma unroll
+        for (int r = 0; r < 4; r++) fsh0[r] = (uint32_t)(uintptr_t)(A.W + (int64_t)min(n0 + 4 * ng + r, A.N - 1) * A.rb) & 3u;
+    }
+
+    // The ring as in gemm_a8k_kernel, except that block b + NS - 1 is
+    // issued after the barrier that starts block b (the float step of block
+    // b - 1, which reads its stage, runs after the other barrier): NS - 2
+    // blocks stay in flight while a block is computed.
+#pragma unroll
+    for (int i = 0; i < NS - 1; i++) gemm_issue_block<DT, C>(A, n0, m0, min(i, nb - 1), smem + i * L::BUF);
+    for (int b = 0; b < nb; b++) {
+        uint8_t* buf = smem + (b % NS) * L::BUF;
+        GM_WAIT_VMCNT((NS - 2) * L::NDMA);  // block b's copies have landed
+        gm_barrier();
+        gemm_issue_block<DT, C>(A, n0, m0, min(b + NS - 1, nb - 1), smem + ((b + NS - 1) % NS) * L::BUF);
+        const uint8_t* wl = buf;
+        const uint8_t* al = buf + L::WBYTES;
+        const float* dl = (const float*)(al + L::ABYTES);
+
+        // This wave's k step against the four activation tiles.
+        v4i accH[4], accL[4], accM[4];
+        v4i bvs[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) {
+            const int row = 16 * mt + ar;
+            bvs[mt] = *(const v4i*)(al + row * 256 + 16 * ((4 * ks + G) ^ (row & 15)));
+        }
+        const v4i z = {0, 0, 0, 0};
+        if constexpr (DT == DT_Q4_K) {
+            const uint8_t* wr = wl + ar * L::WSLOT;
+            const uint32_t* sw = (const uint32_t*)(wr + 4);
+            const Q4KScales sq = q4k_scales(sw[0], sw[1], sw[2]);
+            v4i aH, aL, aM;
+            q4k_operands(wr, sq, ks, G, aH, aL, aM);
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++) {
+                accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bvs[mt], z, 0, 0, 0);
+                accL[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, bvs[mt], z, 0, 0, 0);
+                accM[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aM, bvs[mt], z, 0, 0, 0);
+            }
+        } else {
+            const uint32_t bsh = (wsh0 + 2u * (uint32_t)b) & 3u;
+            const uint8_t* wr = wl + ar * L::WSLOT + bsh;
+            const uint32_t rsh = (uint32_t)((uintptr_t)wr & 3);
+            const uint32_t* wra = (const uint32_t*)(wr - rsh);
+            v4i aH, aL;
+            q6k_operands(wra, rsh, wr, ks, G, aH, aL);
+#pragma unroll
+            for (int mt = 0; mt < 4; mt++) {
+                accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bvs[mt], z, 0, 0, 0);
+                accL[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, bvs[mt], z, 0, 0, 0);
+            }
+        }
+        // Partial sums to the table: lane holds weight rows 4G..4G+3 of
+        // activation row 16 mt + ar.
+#pragma unroll
+        for (int mt = 0; mt < 4; mt++) {
+            v4i S;
+#pragma unroll
+            for (int r = 0; r < 4; r++) S[r] = (accH[mt][r] << (DT == DT_Q4_K ? 3 : 7)) + accL[mt][r];
+            const int at = (ks * 64 + 16 * mt + ar) * KS_RS + 4 * G;
+            *(v4i*)(tabS + at) = S;
+            if constexpr (DT == DT_Q4_K) *(v4i*)(tabM + at) = accM[mt];
+        }
+        GM_WAIT_LGKM0();
+        gm_barrier();
+        // The float step of this thread's pairs, in block order.
+        v4i S = *(const v4i*)(tabS + mc * KS_RS + 4 * ng);
+#pragma unroll
+        for (int k2 = 1; k2 < 4; k2++) S += *(const v4i*)(tabS + (k2 * 64 + mc) * KS_RS + 4 * ng);
+        v4i M = {0, 0, 0, 0};
+        if constexpr (DT == DT_Q4_K) {
+            M = *(const v4i*)(tabM + mc * KS_RS + 4 * ng);
+#pragma unroll
+            for (int k2 = 1; k2 < 4; k2++) M += *(const v4i*)(tabM + (k2 * 64 + mc) * KS_RS + 4 * ng);
+        }
+        const float dx = dl[mc];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = 4 * ng + r;
+            float dC, dminC = 0.f;
+            if constexpr (DT == DT_Q4_K) {
+                const uint32_t dd = *(const uint32_t*)(wl + row * L::WSLOT);
+                dC = f16_to_f32(dd & 0xFFFFu);
+                dminC = f16_to_f32(dd >> 16);
+            } else {
+                // d at byte 208 of the block: an even offset in the slot
+                const uint32_t at = (uint32_t)(row * L::WSLOT) + ((fsh0[r] + 2u * (uint32_t)b) & 3u) + 208u;
+                const uint32_t dw = *(const uint32_t*)(wl + (at & ~3u));
+                dC = f16_to_f32(dw >> (8u * (at & 2u)));
+            }
+            tot[r] = __builtin_fmaf((float)S[r], dC * dx, tot[r]);
+            if (DT == DT_Q4_K) off[r] = __builtin_fmaf((float)M[r], dminC * dx, off[r]);
+        }
+    }
+    GM_WAIT_VMCNT(0);  // the ring's extra copies have landed before the workgroup's LDS is given back
+
+    const int m = m0 + mc;
+    const int refused = flags[0];
+    if (m < A.M && !(refused && A.ok[m] == 0)) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int n = n0 + 4 * ng + r;
+            if (n >= A.N) continue;
+            if (refused && A.wref[n] != 0) continue;
+            float res = DT == DT_Q4_K ? tot[r] - off[r] : tot[r];
+            if (A.bias) res += A.bias[n];
+            A.y[(int64_t)m * A.N + n] = res;
+        }
+    }
+    if (!refused) return;
+    const int g = t >> 3;
+    for (int pidx = g; pidx < 16 * 64; pidx += 256 / 8) {
+        const int n = n0 + pidx % 16, mm = m0 + pidx / 16;
+        if (n >= A.N || mm >= A.M) continue;
+        if (A.wref[n] == 0 && A.ok[mm] != 0) continue;
+        float res = f32dot_g8<DT>(A.W + (int64_t)n * A.rb, A.x + (int64_t)mm * A.K, A.K, A.fused != 0);
+        if (A.bias) res += A.bias[n];
+        if ((t & 7) == 0) A.y[(int64_t)mm * A.N + n] = res;
+    }
+}
+
 }  // namespace g16
 
 template <class C>
@@ -404,7 +583,10 @@ hipError_t launch_gemm_a8k_16(const DevWeight& w, const ActPtrs& a, int64_t rows
     A.fused = total_rows <= 8;
     if (rows <= 64) {
         if ((w.n + 31) / 32 >= 256) return launch_g16<CfgM64N32>(A, w.dt, w.n, rows, stream);
-        return launch_g16<CfgM64N16>(A, w.dt, w.n, rows, stream);
+        const dim3 grid((unsigned)((w.n + 15) / 16), (unsigned)((rows + 63) / 64));
+        if (w.dt == DT_Q4_K) hipLaunchKernelGGL(gemm_a8k_ks_kernel<DT_Q4_K>, grid, dim3(256), 0, stream, A);
+        else hipLaunchKernelGGL(gemm_a8k_ks_kernel<DT_Q6_K>, grid, dim3(256), 0, stream, A);
+        return hipGetLastError();
     }
     return launch_g16<CfgWide>(A, w.dt, w.n, rows, stream);
 }

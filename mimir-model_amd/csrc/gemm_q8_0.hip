@@ -34,22 +34,33 @@ namespace q80 {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int T = 512;           // threads: eight waves
-constexpr int NW = 4, WM = 2;    // waves along the weight rows (32 each) and the activation rows (64 each)
-constexpr int BN = 32 * NW;      // 128 weight rows
-constexpr int BM = 64 * WM;      // 128 activation rows
-constexpr int GB = 8;            // Q8_0 blocks per group (256 elements)
-constexpr int WSLOT = GB * Q80_BYTES;           // 272 bytes of a row per group (17 chunks of 16)
-constexpr int WCH = WSLOT / 16;
-constexpr int WDMA = (BN * WCH + T - 1) / T;    // 16-byte copies per thread per group
-constexpr int WBYTES = WDMA * T * 16;
-constexpr int ADMA = BM * 16 / T;
-constexpr int ABYTES = BM * 256;
-constexpr int XDMA = BM * GB / T;               // dword copies of the activation scales
-constexpr int XBYTES = BM * GB * 4;             // [block j][activation row], f32
-constexpr int BUF = WBYTES + ABYTES + XBYTES;
-constexpr int NDMA = WDMA + ADMA + XDMA;
-static_assert(ADMA * T == BM * 16 && XDMA * T == BM * GB, "Q8_0 GEMM tile shape");
+// A workgroup shape: NW waves along the weight rows (32 each), WM along the
+// activation rows (64 each).
+template <int NW_, int WM_>
+struct Cfg {
+    static constexpr int NW = NW_, WM = WM_;
+    static constexpr int T = 64 * NW * WM;
+    static constexpr int BN = 32 * NW;   // weight rows
+    static constexpr int BM = 64 * WM;   // activation rows
+    static constexpr int GB = 8;         // Q8_0 blocks per group (256 elements)
+    static constexpr int WSLOT = GB * Q80_BYTES;           // 272 bytes of a row per group (17 chunks of 16)
+    static constexpr int WCH = WSLOT / 16;
+    static constexpr int WDMA = (BN * WCH + T - 1) / T;    // 16-byte copies per thread per group
+    static constexpr int WBYTES = WDMA * T * 16;
+    static constexpr int ADMA = BM * 16 / T;
+    static constexpr int ABYTES = BM * 256;
+    static constexpr int XDMA = BM * GB / T;               // dword copies of the activation scales
+    static constexpr int XBYTES = BM * GB * 4;             // [block j][activation row], f32
+    static constexpr int BUF = WBYTES + ABYTES + XBYTES;
+    static constexpr int NDMA = WDMA + ADMA + XDMA;
+    static_assert(ADMA * T == BM * 16 && XDMA * T == BM * GB, "Q8_0 GEMM tile shape");
+    static_assert(2 * BUF <= 160 * 1024 && NDMA < 64, "Q8_0 GEMM buffers");
+};
+// 128 x 128 (eight waves) where that gives every CU a workgroup, else
+// 64 x 64 (two waves) or 32 x 64 (one wave).
+using CfgWide = Cfg<4, 2>;
+using CfgMid = Cfg<2, 1>;
+using CfgSmall = Cfg<1, 1>;
 
 struct Args {
     const uint8_t* W;
@@ -90,7 +101,10 @@ __device__ __forceinline__ void q8_barrier() {
 }
 
 // The copies of group gi into `buf` (every thread issues NDMA instructions).
+template <class C>
 __device__ __forceinline__ void issue_group(const Args& A, int n0, int m0, int gi, uint8_t* buf) {
+    constexpr int T = C::T, BN = C::BN, BM = C::BM, GB = C::GB, WSLOT = C::WSLOT, WCH = C::WCH, WDMA = C::WDMA,
+                  WBYTES = C::WBYTES, ADMA = C::ADMA, ABYTES = C::ABYTES, XDMA = C::XDMA;
     const int t = threadIdx.x, wave = t >> 6;
     uint8_t* wl = buf;
     uint8_t* al = buf + WBYTES;
@@ -127,7 +141,10 @@ __device__ __forceinline__ v4i lds_read16_a2(const uint8_t* p) {
                (int)__builtin_amdgcn_alignbyte(w3, w2, sh), (int)__builtin_amdgcn_alignbyte(w4, w3, sh)};
 }
 
-__global__ __launch_bounds__(T) void gemm_q8_0_kernel(Args A) {
+template <class C>
+__global__ __launch_bounds__(C::T) void gemm_q8_0_kernel(Args A) {
+    constexpr int T = C::T, NW = C::NW, BN = C::BN, BM = C::BM, GB = C::GB, WSLOT = C::WSLOT, WBYTES = C::WBYTES,
+                  ABYTES = C::ABYTES, BUF = C::BUF, NDMA = C::NDMA;
     __shared__ __align__(16) uint8_t smem[2 * BUF];
     __shared__ int flags[1];
     const int t = threadIdx.x, l = t & 63, wave = t >> 6;
@@ -153,11 +170,11 @@ __global__ __launch_bounds__(T) void gemm_q8_0_kernel(Args A) {
 #pragma unroll
     for (int i = 0; i < 16; i++) tot[0][i] = tot[1][i] = 0.f;
 
-    issue_group(A, n0, m0, 0, smem);
+    issue_group<C>(A, n0, m0, 0, smem);
     for (int gi = 0; gi < A.ng; gi++) {
         uint8_t* buf = smem + (gi & 1) * BUF;
         if (gi + 1 < A.ng) {
-            issue_group(A, n0, m0, gi + 1, smem + ((gi + 1) & 1) * BUF);
+            issue_group<C>(A, n0, m0, gi + 1, smem + ((gi + 1) & 1) * BUF);
             Q8_WAIT_VMCNT(NDMA);
         } else {
             Q8_WAIT_VMCNT(0);
@@ -236,6 +253,20 @@ __global__ __launch_bounds__(T) void gemm_q8_0_kernel(Args A) {
 
 bool gemm_q8_0_ok(const DevWeight& w) { return w.dt == DT_Q8_0 && w.k % 256 == 0 && w.k > 0; }
 
+template <class C>
+static hipError_t launch_q80(q80::Args A, int64_t n, int64_t rows, hipStream_t stream) {
+    A.tiles_m = (int)((rows + C::BM - 1) / C::BM);
+    const int64_t nwg = (n + C::BN - 1) / C::BN * A.tiles_m;
+    if (nwg > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(q80::gemm_q8_0_kernel<C>, dim3((unsigned)nwg), dim3(C::T), 0, stream, A);
+    return hipGetLastError();
+}
+
+template <class C>
+static int64_t q80_wgs(int64_t n, int64_t rows) {
+    return (n + C::BN - 1) / C::BN * ((rows + C::BM - 1) / C::BM);
+}
+
 hipError_t launch_gemm_q8_0(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows, const float* x,
                             const float* bias, float* y, hipStream_t stream) {
     using namespace q80;
@@ -255,11 +286,10 @@ hipError_t launch_gemm_q8_0(const DevWeight& w, const ActPtrs& a, int64_t rows, 
     A.ok = a.ok;
     A.x = x;
     A.fused = total_rows <= 8;
-    A.tiles_m = (int)((rows + BM - 1) / BM);
-    const int64_t nwg = (w.n + BN - 1) / BN * A.tiles_m;
-    if (nwg > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gemm_q8_0_kernel, dim3((unsigned)nwg), dim3(T), 0, stream, A);
-    return hipGetLastError();
+    A.tiles_m = 1;
+    if (q80_wgs<CfgWide>(w.n, rows) >= 256) return launch_q80<CfgWide>(A, w.n, rows, stream);
+    if (q80_wgs<CfgMid>(w.n, rows) >= 256) return launch_q80<CfgMid>(A, w.n, rows, stream);
+    return launch_q80<CfgSmall>(A, w.n, rows, stream);
 }
 
 }  // namespace mimg

@@ -73,3 +73,27 @@ def test_cfg2_prefill_layer_shapes_bitexact(gpu, oracle, layer_weights, name, n,
     got = gpu.dequant_matmul_a8(W, x, block=256)
     want = oracle.linear_a8(x, wb, dt, n, k, block=256, threads=16)
     assert bits_equal(got, want), first_diff(got, want)
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K], ids=["q4_k", "q6_k"])
+@pytest.mark.parametrize("rows,n,k", [(16, 100, 256), (33, 4096, 1024), (64, 1000, 2048), (50, 24, 512)])
+def test_small_grid_prefill_bitexact_with_refusals(gpu, oracle, dt, rows, n, k):
+    """16..64 activation rows on few weight rows (the k-step-split kernel:
+    16 weight rows a workgroup, the four waves on the four k steps of each
+    block): partial tiles of weight and activation rows, a refused
+    activation row (NaN) and a weight row with an infinite block scale; every
+    output equal to the oracle's, bit for bit."""
+    bb, doff = (144, 0) if dt == Q4_K else (210, 208)
+    wb = bytearray(oracle.synthetic_weight(dt, n, k, seed=rows + n).tobytes())
+    rb = len(wb) // n
+    bad = min(7, n - 1)
+    wb[rb * bad + bb * (k // 256 - 1) + doff:rb * bad + bb * (k // 256 - 1) + doff + 2] = b"\x00\x7c"
+    wb = np.frombuffer(bytes(wb), np.uint8)
+    x = oracle.synthetic_acts(rows, k, seed=rows)
+    x[rows // 2, 3] = np.nan
+    bias = np.random.default_rng(rows).standard_normal(n).astype(np.float32)
+    W = gpu.Weight(wb, dt, n, k)
+    got = gpu.dequant_matmul_a8(W, x, bias=bias, block=256)
+    W.release()
+    want = oracle.linear_a8(x, wb, dt, n, k, bias=bias, block=256, threads=16)
+    assert bits_equal(got, want), first_diff(got, want)
