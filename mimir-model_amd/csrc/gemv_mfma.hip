@@ -29,8 +29,11 @@
 // activations (lane l: activation row l%16, rows past M clamped, their
 // columns never read) come from global memory (L2-resident): straight into
 // the B operand for Q4_K, through the wave's LDS region for Q6_K.
-// Q4_K: per block 12 MFMAs on the GEMM's planes (sh*q, sl*q, and m_s for
-// the mins). Q6_K: the raw 6-bit values q (0..63) are the A operand, and
+// Q4_K: per block 8 MFMAs with the activations as the A operand (each row
+// of it one activation row's half of a 64-k step, so the 16 rows are 8
+// activation rows x 2 sub-blocks) against the raw nibbles (the sub-block
+// scales applied to the int32 results) and against the mins. Q6_K: the raw
+// 6-bit values q (0..63) are the A operand, and
 // the B operand puts each lane group's activation slice into its own four
 // result columns, so one MFMA gives the per-16 sums of q*y for four
 // sub-blocks apart; the sub-block scales are applied to those int32 sums
@@ -217,39 +220,48 @@ __device__ __forceinline__ void mf_lds_w(const uint8_t* p, int G, MfRaw<DT>& r) 
     }
 }
 
-// Q4_K, the block's exact sums: lane l holds, for weight rows 4(l/16) + i
-// (i < 4) and activation row l%16, S in s[i] and the mins term in mt[i].
+// Q4_K, the block's exact sums. The activations are the A operand and the
+// weights the B operand: A row a = l % 16 is activation row a/2's k-slice G
+// when G/2 == a % 2 (the half of the 64-k step holding sub-block 2ks + a%2),
+// zeros otherwise; B is the raw nibbles q of this lane's weight row l % 16.
+// So C row a, column n is sum_{k in sub-block 2ks + a%2} q_k y_k of
+// activation row a/2 and weight row n alone, and lane l (column l % 16 = its
+// own weight row) holds rows 4G + i: the scale of its own row's sub-block
+// 2ks + i%2 multiplies each (exact 24-bit products), and rows 2j, 2j+1 (the
+// two halves) add up to activation row 2G + j. The mins term is a second
+// MFMA with B = the sub-block's min m_s in every byte, accumulated over the
+// k steps. Out: s[j], mt[j] for weight row l % 16, activation row 2G + j.
 template <uint32_t DT>
-__device__ __forceinline__ void mf_block(const MfRaw<DT>& r, int G, v4i& s, v4i& mt) {
-    v4i accH = {0, 0, 0, 0}, accL = {0, 0, 0, 0}, accM = {0, 0, 0, 0};
+__device__ __forceinline__ void mf_block(const MfRaw<DT>& r, int G, int ar, int (&s)[2], int (&mt)[2]) {
     if constexpr (DT == DT_Q4_K) {
         const Q4KScales S = q4k_scales(r.hdr.y, r.hdr.z, r.hdr.w);
+        const v4i zero = {0, 0, 0, 0};
+        const bool on = (G >> 1) == (ar & 1);  // this lane's A row carries its activation slice
+        v4i accM = zero;
+        int acc[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
-            // sub-block 2ks (low nibbles, G < 2) or 2ks+1 (high nibbles); its
-            // scale sc = 8*sh + sl with sh, sl <= 7, so sh*q and sl*q (q <= 15)
-            // are bytes: the packed nibbles times a small constant in 16-bit lanes
-            const int sub = 2 * ks + (G >> 1);
-            const uint32_t sc = byte_of(S.sc, sub), mm = byte_of(S.m, sub);
-            const short sh = (short)(sc >> 3), sl = (short)(sc & 7);
-            const s16x2 shp = {sh, sh}, slp = {sl, sl};
-            const int shift = 4 * (G >> 1);
+            const int shift = 4 * (G >> 1);  // low nibbles for G < 2 (sub-block 2ks), high for G >= 2
+            const uint32_t mm = byte_of(S.m, 2 * ks + (G >> 1));
             const uint32_t qd[4] = {r.qs[ks].x, r.qs[ks].y, r.qs[ks].z, r.qs[ks].w};
-            v4i aH, aL, aM;
+            v4i bq, bm;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                const s16x2 nib = as_s16x2((qd[k] >> shift) & 0x0F0F0F0Fu);
-                aH[k] = (int)as_u32(nib * shp);
-                aL[k] = (int)as_u32(nib * slp);
-                aM[k] = (int)(mm * 0x01010101u);
+                bq[k] = (int)((qd[k] >> shift) & 0x0F0F0F0Fu);
+                bm[k] = (int)(mm * 0x01010101u);
             }
-            accH = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, r.act[ks], accH, 0, 0, 0);
-            accL = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, r.act[ks], accL, 0, 0, 0);
-            accM = __builtin_amdgcn_mfma_i32_16x16x64_i8(aM, r.act[ks], accM, 0, 0, 0);
+            const v4i av = on ? r.act[ks] : zero;
+            const v4i c = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bq, zero, 0, 0, 0);
+            accM = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bm, accM, 0, 0, 0);
+            const int sc0 = (int)byte_of(S.sc, 2 * ks), sc1 = (int)byte_of(S.sc, 2 * ks + 1);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[i] += __mul24((i & 1) ? sc1 : sc0, c[i]);
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) s[i] = (accH[i] << 3) + accL[i];
-        mt = accM;
+        for (int j = 0; j < 2; j++) {
+            s[j] = acc[2 * j] + acc[2 * j + 1];
+            mt[j] = accM[2 * j] + accM[2 * j + 1];
+        }
     }
 }
 
@@ -360,7 +372,7 @@ void gemv_a8k_mfma_kernel(MfmaArgs A) {
     // activation row (B operand).
     const uint8_t* rowp = P.W + (int64_t)rowof(ar) * A.rb;
     const int am = min(ar, M - 1);
-    const int8_t* ya = A.q + (int64_t)am * A.K;
+    const int8_t* yh = A.q + (int64_t)min(ar >> 1, M - 1) * A.K;  // Q4_K: the A operand's activation row
     const float* dxr = A.d32 + (int64_t)am * (A.K / 32);
 
     // Lane t < 16*M owns (row t/M, activation row t%M) at the end. Its
@@ -397,22 +409,23 @@ void gemv_a8k_mfma_kernel(MfmaArgs A) {
     if constexpr (DT == DT_Q4_K) {
         // Block b's table entries, scale bits and dx.
         auto step = [&](const MfRaw<DT>& r, int b) {
-            v4i s, mt;
-            mf_block<DT>(r, G, s, mt);
-            if (ar < M) {
+            int s[2], mt[2];
+            mf_block<DT>(r, G, ar, s, mt);
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    int* e = tab + (((size_t)b * MF_ROWS + 4 * G + i) * M + ar) * TW;
-                    e[0] = s[i];
-                    e[1] = mt[i];
+            for (int j = 0; j < 2; j++) {
+                if (2 * G + j < M) {
+                    int* e = tab + (((size_t)b * MF_ROWS + ar) * M + 2 * G + j) * TW;
+                    e[0] = s[j];
+                    e[1] = mt[j];
                 }
             }
             if (G == 0) dd[b * MF_ROWS + ar] = r.hdr.x;
             if (G == 1 && ar < M) dxs[b * M + ar] = r.dx;
         };
-        // The activation operand and scale of block b.
+        // The activation operand (activation row ar/2, clamped) and the
+        // scale of activation row ar (for the dx table) of block b.
         auto load_a = [&](int b, v4i* act, float& dx) {
-            const int8_t* yb = ya + (int64_t)b * 256;
+            const int8_t* yb = yh + (int64_t)b * 256;
 #pragma unroll
             for (int ks = 0; ks < 4; ks++) act[ks] = *(const v4i*)(yb + 64 * ks + 16 * G);
             dx = dxr[8 * b];
