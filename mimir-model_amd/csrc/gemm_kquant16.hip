@@ -390,42 +390,58 @@ __global__ __launch_bounds__(C::T) void gemm_a8k_kernel(GemmArgs A) {
 // four partials of its four (weight row, activation row) pairs (exact
 // integers, any order) and runs the block's float step, the same as the
 // other kernels: the result is bit for bit theirs.
-using CfgKs = GCfg<256, 1, 64, 3>;
+// The copy layout of these workgroups (gemm_issue_block): 16 weight rows,
+// BM activation rows, 256 threads, a three-stage ring.
+template <int BM_>
+struct KsCfg {
+    static constexpr int T = 256, NW = 1, BN = 16, BM = BM_, NS = 3;
+    static constexpr int ACH = BM * 16 / T;
+    static_assert(ACH * T == BM * 16, "k-step-split tile shape");
+};
 constexpr int KS_RS = 20;  // table row stride in ints: 16 weight rows + 4 of padding (banks)
 
-template <uint32_t DT>
+// BMK activation rows (64, or 32: twice the workgroups, two or three a CU,
+// for grids of few weight rows).
+template <uint32_t DT, int BMK>
 __global__ __launch_bounds__(256) void gemm_a8k_ks_kernel(GemmArgs A) {
-    using C = CfgKs;
+    using C = KsCfg<BMK>;
     using L = GemmLayout<DT, C>;
-    constexpr int NS = C::NS, TAB = 4 * 64 * KS_RS;  // ints per table: [k step][activation row][weight row]
+    constexpr int NS = C::NS, TMK = BMK / 16, PPT = BMK / 16;  // activation tiles; pairs a thread
+    constexpr int TAB = 4 * BMK * KS_RS;  // ints per table: [k step][activation row][weight row]
+    typedef int vP __attribute__((ext_vector_type(PPT)));
     __shared__ __align__(16) uint8_t smem[NS * L::BUF];
     __shared__ __align__(16) int tabS[TAB];
     __shared__ __align__(16) int tabM[DT == DT_Q4_K ? TAB : 4];
     __shared__ int flags[2];
     const int t = threadIdx.x, l = t & 63, ks = t >> 6;  // this wave's k step of each block
     const int ar = l & 15, G = l >> 4;
-    const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 64;
+    const int n0 = blockIdx.x * 16, m0 = blockIdx.y * BMK;
     const int nb = A.nb;
-    // The float step's pairs of this thread: activation row mc, weight rows 4ng..4ng+3.
-    const int mc = t & 63, ng = t >> 6;
+    // The float step's pairs of this thread: activation row mc, weight rows PPT ng .. PPT ng + PPT - 1.
+    const int mc = t % BMK, ng = t / BMK;
 
     if (t == 0) flags[0] = 0;
     __syncthreads();
     {
         int f = 0;
         if (t < 16 && n0 + t < A.N) f |= A.wref[n0 + t] != 0;
-        if (t < 64 && m0 + t < A.M) f |= A.ok[m0 + t] == 0;
+        if (t < BMK && m0 + t < A.M) f |= A.ok[m0 + t] == 0;
         if (f) flags[0] = 1;
     }
-    float tot[4] = {0.f, 0.f, 0.f, 0.f}, off[4] = {0.f, 0.f, 0.f, 0.f};
+    float tot[PPT], off[PPT];
+#pragma unroll
+    for (int r = 0; r < PPT; r++) tot[r] = off[r] = 0.f;
     // Q6_K: the byte offset mod 4 of block 0 of this lane's row and of the
-    // float step's four rows (a block is 210 bytes, 2 mod 4: block b's
-    // offset is that + 2b mod 4).
-    uint32_t wsh0 = 0, fsh0[4] = {0, 0, 0, 0};
+    // float step's rows (a block is 210 bytes, 2 mod 4: block b's offset is
+    // that + 2b mod 4).
+    uint32_t wsh0 = 0, fsh0[PPT];
+#pragma unroll
+    for (int r = 0; r < PPT; r++) fsh0[r] = 0;
     if constexpr (DT == DT_Q6_K) {
         wsh0 = (uint32_t)(uintptr_t)(A.W + (int64_t)min(n0 + ar, A.N - 1) * A.rb) & 3u;
 #pragma unroll
-        for (int r = 0; r < 4; r++) fsh0[r] = (uint32_t)(uintptr_t)(A.W + (int64_t)min(n0 + 4 * ng + r, A.N - 1) * A.rb) & 3u;
+        for (int r = 0; r < PPT; r++)
+            fsh0[r] = (uint32_t)(uintptr_t)(A.W + (int64_t)min(n0 + PPT * ng + r, A.N - 1) * A.rb) & 3u;
     }
 
     // The ring as in gemm_a8k_kernel, except that block b + NS - 1 is
@@ -443,11 +459,11 @@ __global__ __launch_bounds__(256) void gemm_a8k_ks_kernel(GemmArgs A) {
         const uint8_t* al = buf + L::WBYTES;
         const float* dl = (const float*)(al + L::ABYTES);
 
-        // This wave's k step against the four activation tiles.
-        v4i accH[4], accL[4], accM[4];
-        v4i bvs[4];
+        // This wave's k step against the activation tiles.
+        v4i accH[TMK], accL[TMK], accM[TMK];
+        v4i bvs[TMK];
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++) {
+        for (int mt = 0; mt < TMK; mt++) {
             const int row = 16 * mt + ar;
             bvs[mt] = *(const v4i*)(al + row * 256 + 16 * ((4 * ks + G) ^ (row & 15)));
         }
@@ -459,7 +475,7 @@ __global__ __launch_bounds__(256) void gemm_a8k_ks_kernel(GemmArgs A) {
             v4i aH, aL, aM;
             q4k_operands(wr, sq, ks, G, aH, aL, aM);
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++) {
+            for (int mt = 0; mt < TMK; mt++) {
                 accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bvs[mt], z, 0, 0, 0);
                 accL[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, bvs[mt], z, 0, 0, 0);
                 accM[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aM, bvs[mt], z, 0, 0, 0);
@@ -472,7 +488,7 @@ __global__ __launch_bounds__(256) void gemm_a8k_ks_kernel(GemmArgs A) {
             v4i aH, aL;
             q6k_operands(wra, rsh, wr, ks, G, aH, aL);
 #pragma unroll
-            for (int mt = 0; mt < 4; mt++) {
+            for (int mt = 0; mt < TMK; mt++) {
                 accH[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aH, bvs[mt], z, 0, 0, 0);
                 accL[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, bvs[mt], z, 0, 0, 0);
             }
@@ -480,30 +496,30 @@ __global__ __launch_bounds__(256) void gemm_a8k_ks_kernel(GemmArgs A) {
         // Partial sums to the table: lane holds weight rows 4G..4G+3 of
         // activation row 16 mt + ar.
 #pragma unroll
-        for (int mt = 0; mt < 4; mt++) {
+        for (int mt = 0; mt < TMK; mt++) {
             v4i S;
 #pragma unroll
             for (int r = 0; r < 4; r++) S[r] = (accH[mt][r] << (DT == DT_Q4_K ? 3 : 7)) + accL[mt][r];
-            const int at = (ks * 64 + 16 * mt + ar) * KS_RS + 4 * G;
+            const int at = (ks * BMK + 16 * mt + ar) * KS_RS + 4 * G;
             *(v4i*)(tabS + at) = S;
             if constexpr (DT == DT_Q4_K) *(v4i*)(tabM + at) = accM[mt];
         }
         GM_WAIT_LGKM0();
         gm_barrier();
         // The float step of this thread's pairs, in block order.
-        v4i S = *(const v4i*)(tabS + mc * KS_RS + 4 * ng);
+        vP S = *(const vP*)(tabS + mc * KS_RS + PPT * ng);
 #pragma unroll
-        for (int k2 = 1; k2 < 4; k2++) S += *(const v4i*)(tabS + (k2 * 64 + mc) * KS_RS + 4 * ng);
-        v4i M = {0, 0, 0, 0};
+        for (int k2 = 1; k2 < 4; k2++) S += *(const vP*)(tabS + (k2 * BMK + mc) * KS_RS + PPT * ng);
+        vP M = {};
         if constexpr (DT == DT_Q4_K) {
-            M = *(const v4i*)(tabM + mc * KS_RS + 4 * ng);
+            M = *(const vP*)(tabM + mc * KS_RS + PPT * ng);
 #pragma unroll
-            for (int k2 = 1; k2 < 4; k2++) M += *(const v4i*)(tabM + (k2 * 64 + mc) * KS_RS + 4 * ng);
+            for (int k2 = 1; k2 < 4; k2++) M += *(const vP*)(tabM + (k2 * BMK + mc) * KS_RS + PPT * ng);
         }
         const float dx = dl[mc];
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int row = 4 * ng + r;
+        for (int r = 0; r < PPT; r++) {
+            const int row = PPT * ng + r;
             float dC, dminC = 0.f;
             if constexpr (DT == DT_Q4_K) {
                 const uint32_t dd = *(const uint32_t*)(wl + row * L::WSLOT);
@@ -525,8 +541,8 @@ __global__ __launch_bounds__(256) void gemm_a8k_ks_kernel(GemmArgs A) {
     const int refused = flags[0];
     if (m < A.M && !(refused && A.ok[m] == 0)) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int n = n0 + 4 * ng + r;
+        for (int r = 0; r < PPT; r++) {
+            const int n = n0 + PPT * ng + r;
             if (n >= A.N) continue;
             if (refused && A.wref[n] != 0) continue;
             float res = DT == DT_Q4_K ? tot[r] - off[r] : tot[r];
@@ -536,7 +552,7 @@ __global__ __launch_bounds__(256) void gemm_a8k_ks_kernel(GemmArgs A) {
     }
     if (!refused) return;
     const int g = t >> 3;
-    for (int pidx = g; pidx < 16 * 64; pidx += 256 / 8) {
+    for (int pidx = g; pidx < 16 * BMK; pidx += 256 / 8) {
         const int n = n0 + pidx % 16, mm = m0 + pidx / 16;
         if (n >= A.N || mm >= A.M) continue;
         if (A.wref[n] == 0 && A.ok[mm] != 0) continue;
@@ -583,9 +599,17 @@ hipError_t launch_gemm_a8k_16(const DevWeight& w, const ActPtrs& a, int64_t rows
     A.fused = total_rows <= 8;
     if (rows <= 64) {
         if ((w.n + 31) / 32 >= 256) return launch_g16<CfgM64N32>(A, w.dt, w.n, rows, stream);
-        const dim3 grid((unsigned)((w.n + 15) / 16), (unsigned)((rows + 63) / 64));
-        if (w.dt == DT_Q4_K) hipLaunchKernelGGL(gemm_a8k_ks_kernel<DT_Q4_K>, grid, dim3(256), 0, stream, A);
-        else hipLaunchKernelGGL(gemm_a8k_ks_kernel<DT_Q6_K>, grid, dim3(256), 0, stream, A);
+        // 32-row tiles up to 32 rows (down at 32 rows: 51.5 against 61.4 us
+        // with 64-row tiles), 64-row tiles above (62.4 against 65.7 us at 64
+        // rows: the 32-row tiles read each weight twice)
+        const dim3 grid((unsigned)((w.n + 15) / 16), 1);
+        if (rows <= 32) {
+            if (w.dt == DT_Q4_K) hipLaunchKernelGGL((gemm_a8k_ks_kernel<DT_Q4_K, 32>), grid, dim3(256), 0, stream, A);
+            else hipLaunchKernelGGL((gemm_a8k_ks_kernel<DT_Q6_K, 32>), grid, dim3(256), 0, stream, A);
+        } else {
+            if (w.dt == DT_Q4_K) hipLaunchKernelGGL((gemm_a8k_ks_kernel<DT_Q4_K, 64>), grid, dim3(256), 0, stream, A);
+            else hipLaunchKernelGGL((gemm_a8k_ks_kernel<DT_Q6_K, 64>), grid, dim3(256), 0, stream, A);
+        }
         return hipGetLastError();
     }
     return launch_g16<CfgWide>(A, w.dt, w.n, rows, stream);
