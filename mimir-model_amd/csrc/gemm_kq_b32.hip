@@ -50,7 +50,6 @@ struct Cfg {
 };
 using CfgWide = Cfg<4, 2>;  // 128 x 128, eight waves
 using CfgMid = Cfg<2, 1>;   // 64 x 64, two waves
-using CfgSmall = Cfg<1, 1>; // 32 x 64, one wave
 
 template <uint32_t DT, class C>
 struct Lay {
@@ -359,8 +358,8 @@ bool gemm_kq_b32_ok(const DevWeight& w) {
     return (w.dt == DT_Q4_K || w.dt == DT_Q6_K) && w.k % 256 == 0 && w.k > 0;
 }
 
-// The largest tile that still gives every CU a workgroup (256 on MI355X),
-// else the smallest.
+// The largest tile that still gives every CU a workgroup (256 on MI355X);
+// up to 64 rows (or where neither does) the 16 x 64 tiles of gemm_b32s.hip.
 hipError_t launch_gemm_kq_b32(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows, const float* x,
                               const float* bias, float* y, hipStream_t stream) {
     using namespace kq32;
@@ -383,8 +382,8 @@ hipError_t launch_gemm_kq_b32(const DevWeight& w, const ActPtrs& a, int64_t rows
     A.fused = total_rows <= 8;
     A.tiles_m = 1;
     if (wgs<CfgWide>(w.n, rows) >= 256) return launch_cfg<CfgWide>(A, w.dt, w.n, rows, stream);
-    if (wgs<CfgMid>(w.n, rows) >= 256) return launch_cfg<CfgMid>(A, w.dt, w.n, rows, stream);
-    return launch_cfg<CfgSmall>(A, w.dt, w.n, rows, stream);
+    if (rows > 64 && wgs<CfgMid>(w.n, rows) >= 256) return launch_cfg<CfgMid>(A, w.dt, w.n, rows, stream);
+    return launch_gemm_b32_small(w, a, rows, total_rows, x, bias, y, stream);
 }
 
 }  // namespace mimg

@@ -57,10 +57,10 @@ struct Cfg {
     static_assert(2 * BUF <= 160 * 1024 && NDMA < 64, "Q8_0 GEMM buffers");
 };
 // 128 x 128 (eight waves) where that gives every CU a workgroup, else
-// 64 x 64 (two waves) or 32 x 64 (one wave).
+// 64 x 64 (two waves) above 64 rows; otherwise the 16 x 64 tiles of
+// gemm_b32s.hip (four waves).
 using CfgWide = Cfg<4, 2>;
 using CfgMid = Cfg<2, 1>;
-using CfgSmall = Cfg<1, 1>;
 
 struct Args {
     const uint8_t* W;
@@ -288,8 +288,8 @@ hipError_t launch_gemm_q8_0(const DevWeight& w, const ActPtrs& a, int64_t rows, 
     A.fused = total_rows <= 8;
     A.tiles_m = 1;
     if (q80_wgs<CfgWide>(w.n, rows) >= 256) return launch_q80<CfgWide>(A, w.n, rows, stream);
-    if (q80_wgs<CfgMid>(w.n, rows) >= 256) return launch_q80<CfgMid>(A, w.n, rows, stream);
-    return launch_q80<CfgSmall>(A, w.n, rows, stream);
+    if (rows > 64 && q80_wgs<CfgMid>(w.n, rows) >= 256) return launch_q80<CfgMid>(A, w.n, rows, stream);
+    return launch_gemm_b32_small(w, a, rows, total_rows, x, bias, y, stream);
 }
 
 }  // namespace mimg

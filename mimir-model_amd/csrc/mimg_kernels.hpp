@@ -130,6 +130,11 @@ bool gemm_q8_0_ok(const DevWeight& w);
 // Q4_K / Q6_K x activations in blocks of 32 on the int8 matrix cores (one
 // float chain of exact block sums: a tolerance claim, gemm_kq_b32.hip).
 bool gemm_kq_b32_ok(const DevWeight& w);
+// The small-grid tiling of both (16 weight rows x 64 activation rows, four
+// waves; gemm_b32s.hip): the same per-output arithmetic.
+int64_t gemm_b32_small_wgs(int64_t n, int64_t rows);
+hipError_t launch_gemm_b32_small(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows,
+                                 const float* x, const float* bias, float* y, hipStream_t stream);
 hipError_t launch_gemm_kq_b32(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows, const float* x,
                               const float* bias, float* y, hipStream_t stream);
 hipError_t launch_gemm_q8_0(const DevWeight& w, const ActPtrs& a, int64_t rows, int64_t total_rows, const float* x,
