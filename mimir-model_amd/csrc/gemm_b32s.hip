@@ -35,15 +35,19 @@ typedef long v1l;
 
 constexpr int T = 256, BN = 16, BM = 64;
 
-template <uint32_t DT>
+// AL: every weight group starts at a 16-byte boundary (Q4_K always; Q8_0
+// when the data pointer is 16-byte aligned: a row of K elements is
+// 272 K / 256 bytes), so the blocks' offsets within a slot are constants.
+template <uint32_t DT, bool AL>
 struct Lay {
+    static constexpr int GB = DT == DT_Q8_0 ? 8 * Q80_BYTES : DT == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES;
     // 16-byte chunks of a weight row's slot per group of 256 elements: Q8_0
-    // 8 blocks of 34 bytes (2-byte aligned: 18 chunks from the 16-byte
-    // boundary below cover them), Q4_K one block (9 chunks), Q6_K one block
-    // (14 chunks from the boundary below); Q8_0 and Q6_K slots take one
-    // chunk more (copied too), an odd count, so that the 16 rows' dword
-    // reads spread over the banks.
-    static constexpr int WCH = DT == DT_Q8_0 ? 19 : DT == DT_Q4_K ? 9 : 15;
+    // 8 blocks of 34 bytes (aligned: 17 chunks; 2-byte aligned: 18 chunks
+    // from the 16-byte boundary below cover them), Q4_K one block (9
+    // chunks), Q6_K one block (14 chunks from the boundary below); the
+    // unaligned Q8_0 and Q6_K slots take one chunk more (copied too), an odd
+    // count, so that the 16 rows' dword reads spread over the banks.
+    static constexpr int WCH = DT == DT_Q8_0 ? (AL ? 17 : 19) : DT == DT_Q4_K ? 9 : 15;
     static constexpr int WSLOT = 16 * WCH;
     static constexpr int WDMA = (BN * WCH + T - 1) / T;
     static constexpr int WBYTES = WDMA * T * 16;
@@ -99,42 +103,63 @@ __device__ __forceinline__ void bs_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// The first byte of group gi of weight row n (global memory).
-template <uint32_t DT>
-__device__ __forceinline__ const uint8_t* wgroup(const Args& A, int n, int gi) {
-    return A.W + (int64_t)n * A.rb + (int64_t)gi * (DT == DT_Q8_0 ? 8 * Q80_BYTES : DT == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES);
-}
+// A thread's copy sources for group 0, fixed over the groups (group gi adds
+// gi times a row's group stride).
+template <uint32_t DT, bool AL>
+struct CopySrc {
+    const uint8_t* w[Lay<DT, AL>::WDMA];  // its weight chunk (AL), else its row's group 0
+    int wch[Lay<DT, AL>::WDMA];           // the chunk within the slot (not AL)
+    const int8_t* a[Lay<DT, AL>::ADMA];   // its activation chunk
+    const float* x[Lay<DT, AL>::XDMA];    // its dx (and dbs at the same index)
+};
 
-template <uint32_t DT>
-__device__ __forceinline__ void issue_group(const Args& A, int n0, int m0, int gi, uint8_t* buf) {
-    using L = Lay<DT>;
-    const int t = threadIdx.x, wave = t >> 6;
-    uint8_t* wl = buf;
-    uint8_t* al = buf + L::WBYTES;
-    uint8_t* xl = al + L::ABYTES;
+template <uint32_t DT, bool AL>
+__device__ __forceinline__ CopySrc<DT, AL> copy_sources(const Args& A, int n0, int m0) {
+    using L = Lay<DT, AL>;
+    const int t = threadIdx.x;
+    CopySrc<DT, AL> cs;
 #pragma unroll
     for (int i = 0; i < L::WDMA; i++) {
         const int c = min(T * i + t, BN * L::WCH - 1);
         const int r = c / L::WCH, j = c - L::WCH * r;
-        const int n = min(n0 + r, A.N - 1);
-        const uint8_t* src = (const uint8_t*)__builtin_align_down(wgroup<DT>(A, n, gi), 16) + 16 * j;
-        lds_copy16(src, wl + 16 * (T * i + 64 * wave));
+        cs.w[i] = A.W + (int64_t)min(n0 + r, A.N - 1) * A.rb + (AL ? 16 * j : 0);
+        cs.wch[i] = j;
     }
 #pragma unroll
     for (int i = 0; i < L::ADMA; i++) {
         const int c = T * i + t;  // row c/16, chunk c%16 stored at slot (c%16) ^ (row & 15)
         const int r = c >> 4, s = c & 15;
-        const int m = min(m0 + r, A.M - 1);
-        lds_copy16(A.q + (int64_t)m * A.K + 256 * gi + 16 * (s ^ (r & 15)), al + 16 * (T * i + 64 * wave));
+        cs.a[i] = A.q + (int64_t)min(m0 + r, A.M - 1) * A.K + 16 * (s ^ (r & 15));
     }
 #pragma unroll
     for (int i = 0; i < L::XDMA; i++) {
         const int c = T * i + t;  // block j = c / BM, activation row c % BM
         const int j = c / BM, r = c - BM * j;
-        const int m = min(m0 + r, A.M - 1);
-        lds_copy4(A.d32 + (int64_t)m * (A.K / 32) + 8 * gi + j, xl + 4 * (T * i + 64 * wave));
+        cs.x[i] = A.d32 + (int64_t)min(m0 + r, A.M - 1) * (A.K / 32) + j;
+    }
+    return cs;
+}
+
+template <uint32_t DT, bool AL>
+__device__ __forceinline__ void issue_group(const Args& A, const CopySrc<DT, AL>& cs, int gi, uint8_t* buf) {
+    using L = Lay<DT, AL>;
+    const int wave = threadIdx.x >> 6;
+    uint8_t* wl = buf;
+    uint8_t* al = buf + L::WBYTES;
+    uint8_t* xl = al + L::ABYTES;
+#pragma unroll
+    for (int i = 0; i < L::WDMA; i++) {
+        const uint8_t* g = cs.w[i] + (int64_t)L::GB * gi;
+        const uint8_t* src = AL ? g : (const uint8_t*)__builtin_align_down(g, 16) + 16 * cs.wch[i];
+        lds_copy16(src, wl + 16 * (T * i + 64 * wave));
+    }
+#pragma unroll
+    for (int i = 0; i < L::ADMA; i++) lds_copy16(cs.a[i] + 256 * (int64_t)gi, al + 16 * (T * i + 64 * wave));
+#pragma unroll
+    for (int i = 0; i < L::XDMA; i++) {
+        lds_copy4(cs.x[i] + 8 * gi, xl + 4 * (T * i + 64 * wave));
         if constexpr (DT == DT_Q4_K)
-            lds_copy4(A.dbs + (int64_t)m * (A.K / 32) + 8 * gi + j, xl + L::XBYTES + 4 * (T * i + 64 * wave));
+            lds_copy4(A.dbs + (cs.x[i] - A.d32) + 8 * gi, xl + L::XBYTES + 4 * (T * i + 64 * wave));
     }
 }
 
@@ -151,9 +176,26 @@ __device__ __forceinline__ uint32_t lds_u16_a2(const uint8_t* p) {
     return (w[0] >> (8 * ((uint32_t)(uintptr_t)p & 2))) & 0xFFFFu;
 }
 
-template <uint32_t DT>
+// Q8_0 block j of a group that starts 16-byte aligned: its bytes 8G..8G+7
+// (B operand) and its scale, with the offsets mod 4 known (block j at 34 j;
+// j is a constant once the block loop is unrolled).
+__device__ __forceinline__ void q80_block_al(const uint8_t* wr, int j, int G, v1l& bw, float& dj) {
+    const uint8_t* blk = wr + Q80_BYTES * j;
+    if (j & 1) {
+        const uint32_t* p = (const uint32_t*)(blk + 2 + 8 * G);  // 34 j + 2: a multiple of 4
+        bw = (v1l)(((uint64_t)p[1] << 32) | p[0]);
+        dj = f16_to_f32(((const uint32_t*)(blk - 2))[0] >> 16);
+    } else {
+        const uint32_t* p = (const uint32_t*)(blk + 8 * G);  // 34 j: a multiple of 4
+        const uint32_t w0 = p[0], w1 = p[1], w2 = p[2];
+        bw = (v1l)(((uint64_t)__builtin_amdgcn_alignbyte(w2, w1, 2) << 32) | __builtin_amdgcn_alignbyte(w1, w0, 2));
+        dj = f16_to_f32(((const uint32_t*)blk)[0]);
+    }
+}
+
+template <uint32_t DT, bool AL>
 __global__ __launch_bounds__(T) void b32s_kernel(Args A) {
-    using L = Lay<DT>;
+    using L = Lay<DT, AL>;
     constexpr int NS = L::NS;
     __shared__ __align__(16) uint8_t smem[NS * L::BUF];
     __shared__ int flags[1];
@@ -176,10 +218,10 @@ __global__ __launch_bounds__(T) void b32s_kernel(Args A) {
     }
     // This lane's weight row (its B column) and the offset of its groups in
     // their slots (the copies start at the 16-byte boundary below a group).
-    const int nrow = min(n0 + ar, A.N - 1);
-    const uint32_t goff0 = (uint32_t)(uintptr_t)wgroup<DT>(A, nrow, 0) & 15u;
-    constexpr uint32_t GB = DT == DT_Q8_0 ? 8 * Q80_BYTES : DT == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES;
+    const uint32_t goff0 = (uint32_t)(uintptr_t)(A.W + (int64_t)min(n0 + ar, A.N - 1) * A.rb) & 15u;
+    constexpr uint32_t GB = L::GB;
     const int arow = 16 * wave + ar;  // this lane's activation row of the tile (A operand)
+    const CopySrc<DT, AL> cs = copy_sources<DT, AL>(A, n0, m0);
     float tot[4] = {0.f, 0.f, 0.f, 0.f}, off[4] = {0.f, 0.f, 0.f, 0.f};
 
     // The ring: groups 0 .. NS-2 first; at group gi, group gi + NS - 1 goes
@@ -187,16 +229,16 @@ __global__ __launch_bounds__(T) void b32s_kernel(Args A) {
     // that ends group gi - 1). Past the last group the last one is copied
     // again, so every thread always has the same number of copies in flight.
 #pragma unroll
-    for (int i = 0; i < NS - 1; i++) issue_group<DT>(A, n0, m0, min(i, A.ng - 1), smem + i * L::BUF);
+    for (int i = 0; i < NS - 1; i++) issue_group<DT, AL>(A, cs, min(i, A.ng - 1), smem + i * L::BUF);
     for (int gi = 0; gi < A.ng; gi++) {
         uint8_t* buf = smem + (gi % NS) * L::BUF;
-        issue_group<DT>(A, n0, m0, min(gi + NS - 1, A.ng - 1), smem + ((gi + NS - 1) % NS) * L::BUF);
+        issue_group<DT, AL>(A, cs, min(gi + NS - 1, A.ng - 1), smem + ((gi + NS - 1) % NS) * L::BUF);
         BS_WAIT_VMCNT((NS - 1) * L::NDMA);  // group gi's copies (issued NS - 1 groups earlier) have landed
         bs_barrier();
         const uint8_t* al = buf + L::WBYTES;
         const float* xl = (const float*)(al + L::ABYTES);
         const float* yl = xl + BM * 8;
-        const uint8_t* wg0 = buf + ar * L::WSLOT + ((goff0 + (uint32_t)gi * GB) & 15u);  // the lane's group
+        const uint8_t* wg0 = buf + ar * L::WSLOT + (AL ? 0u : ((goff0 + (uint32_t)gi * GB) & 15u));  // the lane's group
         float tb[4] = {0.f, 0.f, 0.f, 0.f};
         float d = 0.f, dmin = 0.f;
         Q4KScales sq = {0, 0};
@@ -216,9 +258,15 @@ __global__ __launch_bounds__(T) void b32s_kernel(Args A) {
             const float dxr[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
             const v4i z = {0, 0, 0, 0};
             if constexpr (DT == DT_Q8_0) {
-                const uint8_t* blk = wg0 + Q80_BYTES * j;
-                const v1l bw = lds_read8_a2(blk + 2 + 8 * G);
-                const float dj = f16_to_f32(lds_u16_a2(blk));
+                v1l bw;
+                float dj;
+                if constexpr (AL) {
+                    q80_block_al(wg0, j, G, bw, dj);
+                } else {
+                    const uint8_t* blk = wg0 + Q80_BYTES * j;
+                    bw = lds_read8_a2(blk + 2 + 8 * G);
+                    dj = f16_to_f32(lds_u16_a2(blk));
+                }
                 const v4i c = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bw, z, 0, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 4; i++) tot[i] = __builtin_fmaf((float)c[i], dj * dxr[i], tot[i]);
@@ -306,6 +354,8 @@ hipError_t launch_gemm_b32_small(const DevWeight& w, const ActPtrs& a, int64_t r
     if ((w.dt != DT_Q8_0 && w.dt != DT_Q4_K && w.dt != DT_Q6_K) || w.k % 256 || w.k <= 0 || rows <= 0 ||
         rows > (1 << 30) || w.n > (1 << 30))
         return hipErrorInvalidValue;
+    const bool al16 = ((uintptr_t)w.data & 15) == 0 && w.row_bytes % 16 == 0;
+    if (w.dt == DT_Q4_K && !al16) return hipErrorInvalidValue;
     Args A;
     A.W = w.data;
     A.wref = w.wref;
@@ -325,9 +375,11 @@ hipError_t launch_gemm_b32_small(const DevWeight& w, const ActPtrs& a, int64_t r
     A.tiles_m = (int)((rows + BM - 1) / BM);
     const int64_t nwg = gemm_b32_small_wgs(w.n, rows);
     if (nwg > 0x7fffffff) return hipErrorInvalidValue;
-    if (w.dt == DT_Q8_0) hipLaunchKernelGGL(b32s_kernel<DT_Q8_0>, dim3((unsigned)nwg), dim3(T), 0, stream, A);
-    else if (w.dt == DT_Q4_K) hipLaunchKernelGGL(b32s_kernel<DT_Q4_K>, dim3((unsigned)nwg), dim3(T), 0, stream, A);
-    else hipLaunchKernelGGL(b32s_kernel<DT_Q6_K>, dim3((unsigned)nwg), dim3(T), 0, stream, A);
+    const dim3 grid((unsigned)nwg);
+    if (w.dt == DT_Q8_0 && al16) hipLaunchKernelGGL((b32s_kernel<DT_Q8_0, true>), grid, dim3(T), 0, stream, A);
+    else if (w.dt == DT_Q8_0) hipLaunchKernelGGL((b32s_kernel<DT_Q8_0, false>), grid, dim3(T), 0, stream, A);
+    else if (w.dt == DT_Q4_K) hipLaunchKernelGGL((b32s_kernel<DT_Q4_K, true>), grid, dim3(T), 0, stream, A);
+    else hipLaunchKernelGGL((b32s_kernel<DT_Q6_K, false>), grid, dim3(T), 0, stream, A);
     return hipGetLastError();
 }
 
