@@ -410,8 +410,8 @@ __global__ __launch_bounds__(256) void gemm_a8k_ks_kernel(GemmArgs A) {
     constexpr int TAB = 4 * BMK * KS_RS;  // ints per table: [k step][activation row][weight row]
     typedef int vP __attribute__((ext_vector_type(PPT)));
     __shared__ __align__(16) uint8_t smem[NS * L::BUF];
-    __shared__ __align__(16) int tabS[TAB];
-    __shared__ __align__(16) int tabM[DT == DT_Q4_K ? TAB : 4];
+    __shared__ __align__(16) int tabS[2 * TAB];  // two tables: block b's partials while block b - 1's are read
+    __shared__ __align__(16) int tabM[DT == DT_Q4_K ? 2 * TAB : 4];
     __shared__ int flags[2];
     const int t = threadIdx.x, l = t & 63, ks = t >> 6;  // this wave's k step of each block
     const int ar = l & 15, G = l >> 4;
@@ -443,21 +443,50 @@ __global__ __launch_bounds__(256) void gemm_a8k_ks_kernel(GemmArgs A) {
         for (int r = 0; r < PPT; r++)
             fsh0[r] = (uint32_t)(uintptr_t)(A.W + (int64_t)min(n0 + PPT * ng + r, A.N - 1) * A.rb) & 3u;
     }
+    // The block scales of the float step's rows, read from a block's stage
+    // while it is current and used one block later.
+    float dP[PPT], dminP[PPT], dxP = 0.f;
+#pragma unroll
+    for (int r = 0; r < PPT; r++) dP[r] = dminP[r] = 0.f;
 
-    // The ring as in gemm_a8k_kernel, except that block b + NS - 1 is
-    // issued after the barrier that starts block b (the float step of block
-    // b - 1, which reads its stage, runs after the other barrier): NS - 2
-    // blocks stay in flight while a block is computed.
+    // The float step of block bb from table bb % 2 (this thread's PPT pairs,
+    // in block order) with the scales read while bb's stage was current.
+    auto float_step = [&](int bb) {
+        const int* tS = tabS + (bb & 1) * TAB;
+        vP S = *(const vP*)(tS + mc * KS_RS + PPT * ng);
+#pragma unroll
+        for (int k2 = 1; k2 < 4; k2++) S += *(const vP*)(tS + (k2 * BMK + mc) * KS_RS + PPT * ng);
+        vP M = {};
+        if constexpr (DT == DT_Q4_K) {
+            const int* tM = tabM + (bb & 1) * TAB;
+            M = *(const vP*)(tM + mc * KS_RS + PPT * ng);
+#pragma unroll
+            for (int k2 = 1; k2 < 4; k2++) M += *(const vP*)(tM + (k2 * BMK + mc) * KS_RS + PPT * ng);
+        }
+#pragma unroll
+        for (int r = 0; r < PPT; r++) {
+            tot[r] = __builtin_fmaf((float)S[r], dP[r] * dxP, tot[r]);
+            if (DT == DT_Q4_K) off[r] = __builtin_fmaf((float)M[r], dminP[r] * dxP, off[r]);
+        }
+    };
+
+    // The ring as in gemm_a8k_kernel, with one barrier a block: at block b
+    // the waves write b's partials to table b % 2 and then run the float
+    // step of block b - 1 from the other table. After the barrier that
+    // starts block b every wave has finished block b - 1 (its reads of stage
+    // b - 1 and of table b % 2), so block b + NS - 1 goes into stage b - 1
+    // and the partials of b into table b % 2; the scales the float step of b
+    // needs are read into registers while stage b is current.
 #pragma unroll
     for (int i = 0; i < NS - 1; i++) gemm_issue_block<DT, C>(A, n0, m0, min(i, nb - 1), smem + i * L::BUF);
     for (int b = 0; b < nb; b++) {
         uint8_t* buf = smem + (b % NS) * L::BUF;
         GM_WAIT_VMCNT((NS - 2) * L::NDMA);  // block b's copies have landed
+        GM_WAIT_LGKM0();                     // this wave's table writes of block b - 1 are done
         gm_barrier();
         gemm_issue_block<DT, C>(A, n0, m0, min(b + NS - 1, nb - 1), smem + ((b + NS - 1) % NS) * L::BUF);
         const uint8_t* wl = buf;
         const uint8_t* al = buf + L::WBYTES;
-        const float* dl = (const float*)(al + L::ABYTES);
 
         // This wave's k step against the activation tiles.
         v4i accH[TMK], accL[TMK], accM[TMK];
@@ -493,48 +522,42 @@ __global__ __launch_bounds__(256) void gemm_a8k_ks_kernel(GemmArgs A) {
                 accL[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aL, bvs[mt], z, 0, 0, 0);
             }
         }
-        // Partial sums to the table: lane holds weight rows 4G..4G+3 of
+        // The float step of block b - 1 (its table is complete since the
+        // barrier) while the MFMAs of block b run.
+        if (b > 0) float_step(b - 1);
+        // Block b's scales for the float step of the next iteration.
+        dxP = ((const float*)(al + L::ABYTES))[mc];
+#pragma unroll
+        for (int r = 0; r < PPT; r++) {
+            const int row = PPT * ng + r;
+            if constexpr (DT == DT_Q4_K) {
+                const uint32_t dd = *(const uint32_t*)(wl + row * L::WSLOT);
+                dP[r] = f16_to_f32(dd & 0xFFFFu);
+                dminP[r] = f16_to_f32(dd >> 16);
+            } else {
+                // d at byte 208 of the block: an even offset in the slot
+                const uint32_t at = (uint32_t)(row * L::WSLOT) + ((fsh0[r] + 2u * (uint32_t)b) & 3u) + 208u;
+                const uint32_t dw = *(const uint32_t*)(wl + (at & ~3u));
+                dP[r] = f16_to_f32(dw >> (8u * (at & 2u)));
+            }
+        }
+        // Partial sums to table b % 2: lane holds weight rows 4G..4G+3 of
         // activation row 16 mt + ar.
+        int* tS = tabS + (b & 1) * TAB;
+        int* tM = tabM + (DT == DT_Q4_K ? (b & 1) * TAB : 0);
 #pragma unroll
         for (int mt = 0; mt < TMK; mt++) {
             v4i S;
 #pragma unroll
             for (int r = 0; r < 4; r++) S[r] = (accH[mt][r] << (DT == DT_Q4_K ? 3 : 7)) + accL[mt][r];
             const int at = (ks * BMK + 16 * mt + ar) * KS_RS + 4 * G;
-            *(v4i*)(tabS + at) = S;
-            if constexpr (DT == DT_Q4_K) *(v4i*)(tabM + at) = accM[mt];
-        }
-        GM_WAIT_LGKM0();
-        gm_barrier();
-        // The float step of this thread's pairs, in block order.
-        vP S = *(const vP*)(tabS + mc * KS_RS + PPT * ng);
-#pragma unroll
-        for (int k2 = 1; k2 < 4; k2++) S += *(const vP*)(tabS + (k2 * BMK + mc) * KS_RS + PPT * ng);
-        vP M = {};
-        if constexpr (DT == DT_Q4_K) {
-            M = *(const vP*)(tabM + mc * KS_RS + PPT * ng);
-#pragma unroll
-            for (int k2 = 1; k2 < 4; k2++) M += *(const vP*)(tabM + (k2 * BMK + mc) * KS_RS + PPT * ng);
-        }
-        const float dx = dl[mc];
-#pragma unroll
-        for (int r = 0; r < PPT; r++) {
-            const int row = PPT * ng + r;
-            float dC, dminC = 0.f;
-            if constexpr (DT == DT_Q4_K) {
-                const uint32_t dd = *(const uint32_t*)(wl + row * L::WSLOT);
-                dC = f16_to_f32(dd & 0xFFFFu);
-                dminC = f16_to_f32(dd >> 16);
-            } else {
-                // d at byte 208 of the block: an even offset in the slot
-                const uint32_t at = (uint32_t)(row * L::WSLOT) + ((fsh0[r] + 2u * (uint32_t)b) & 3u) + 208u;
-                const uint32_t dw = *(const uint32_t*)(wl + (at & ~3u));
-                dC = f16_to_f32(dw >> (8u * (at & 2u)));
-            }
-            tot[r] = __builtin_fmaf((float)S[r], dC * dx, tot[r]);
-            if (DT == DT_Q4_K) off[r] = __builtin_fmaf((float)M[r], dminC * dx, off[r]);
+            *(v4i*)(tS + at) = S;
+            if constexpr (DT == DT_Q4_K) *(v4i*)(tM + at) = accM[mt];
         }
     }
+    GM_WAIT_LGKM0();
+    gm_barrier();
+    float_step(nb - 1);
     GM_WAIT_VMCNT(0);  // the ring's extra copies have landed before the workgroup's LDS is given back
 
     const int m = m0 + mc;
