@@ -391,10 +391,12 @@ __global__ __launch_bounds__(C::T) void gemm_a8k_kernel(GemmArgs A) {
 // integers, any order) and runs the block's float step, the same as the
 // other kernels: the result is bit for bit theirs.
 // The copy layout of these workgroups (gemm_issue_block): 16 weight rows,
-// BM activation rows, 256 threads, a three-stage ring.
-template <int BM_>
+// BM activation rows, 256 threads, a ring of NS stages (Q6_K four: its
+// tables are half Q4_K's, and 64-row down grids leave a CU to one workgroup;
+// Q4_K three, so its 64-row tables fit beside the ring).
+template <int BM_, int NS_>
 struct KsCfg {
-    static constexpr int T = 256, NW = 1, BN = 16, BM = BM_, NS = 3;
+    static constexpr int T = 256, NW = 1, BN = 16, BM = BM_, NS = NS_;
     static constexpr int ACH = BM * 16 / T;
     static_assert(ACH * T == BM * 16, "k-step-split tile shape");
 };
@@ -404,7 +406,7 @@ constexpr int KS_RS = 20;  // table row stride in ints: 16 weight rows + 4 of pa
 // for grids of few weight rows).
 template <uint32_t DT, int BMK>
 __global__ __launch_bounds__(256) void gemm_a8k_ks_kernel(GemmArgs A) {
-    using C = KsCfg<BMK>;
+    using C = KsCfg<BMK, DT == DT_Q6_K ? 4 : 3>;
     using L = GemmLayout<DT, C>;
     constexpr int NS = C::NS, TMK = BMK / 16, PPT = BMK / 16;  // activation tiles; pairs a thread
     constexpr int TAB = 4 * BMK * KS_RS;  // ints per table: [k step][activation row][weight row]
