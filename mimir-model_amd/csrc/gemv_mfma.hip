@@ -533,6 +533,9 @@ void gemv_a8k_mfma_kernel(MfmaArgs A) {
         const int r = t / M, m = t - r * M, row = rowof(r);
         if (row0 + r < N && !flag) {
             float tot = 0.f, off = 0.f;
+            // (unrolled: the table reads of eight blocks are issued together,
+            // so only the fma chain itself is serial)
+#pragma unroll 8
             for (int b = 0; b < nb; b++) {
                 const int* e = tab + (((size_t)b * MF_ROWS + r) * M + m) * TW;
                 const uint32_t bits = dd[b * MF_ROWS + r];
