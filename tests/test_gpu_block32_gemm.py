@@ -240,7 +240,7 @@ def test_q4k_terms_match_the_oracle_test_decode(oracle):
 
 
 @pytest.mark.parametrize("dt", [Q4_K, Q6_K], ids=["q4_k", "q6_k"])
-@pytest.mark.parametrize("rows,n,k,with_bias", [(16, 300, 256, False),     # 32 x 64 tiles
+@pytest.mark.parametrize("rows,n,k,with_bias", [(16, 300, 256, False),     # small-grid 16 x 64 tiles
                                                 (130, 8000, 512, True),    # 64 x 64 tiles
                                                 (300, 16384, 256, False),  # 128 x 128 tiles
                                                 (70, 129, 2048, True), (1030, 200, 1024, False)])
@@ -256,8 +256,8 @@ def test_kq_b32_gemm_within_a8_bound(gpu, oracle, dt, rows, n, k, with_bias):
 
 @pytest.mark.parametrize("dt", [Q4_K, Q6_K], ids=["q4_k", "q6_k"])
 def test_kq_b32_gemm_rows_are_independent(gpu, oracle, dt):
-    """The first 40 rows give the same bits alone (32 x 64 tiles) as inside
-    1100 rows (128 x 128 tiles)."""
+    """The first 40 rows give the same bits alone (the small-grid 16 x 64
+    tiles) as inside 1100 rows (64 x 64 tiles)."""
     n, k = 2100, 1024
     wb = oracle.synthetic_weight(dt, n, k, seed=5)
     x = oracle.synthetic_acts(1100, k, seed=6)
@@ -317,3 +317,47 @@ def test_cfg2_kquant_blocks_of_32_within_a8_bound(gpu, oracle, name, dt, n, k, s
     W.release()
     pick = np.unique(np.linspace(0, rows - 1, 64).astype(int))
     _bound_check_kq(oracle, dt, wb, x[pick], n, k, got[pick])
+
+
+@pytest.mark.parametrize("dt,rows,n,k", [(Q8_0, 64, 300, 1024),     # small-grid tiles
+                                         (Q8_0, 130, 8000, 512),    # 64 x 64 tiles
+                                         (Q6_K, 64, 300, 1024),     # small-grid tiles
+                                         (Q6_K, 130, 8000, 512)],   # 64 x 64 tiles
+                         ids=["q8_0-small", "q8_0-mid", "q6_k-small", "q6_k-mid"])
+def test_block32_gemm_unaligned_weight_view(gpu, oracle, dt, rows, n, k):
+    """The same weight bytes as a view 2 bytes past a 16-byte boundary of an
+    uploaded weights section (the kernels realign the blocks in LDS) and as
+    a 16-byte aligned view (Q8_0: the blocks' offsets as constants): equal
+    bits."""
+    wb = np.ascontiguousarray(oracle.synthetic_weight(dt, n, k, seed=rows + n + 7)).view(np.uint8).ravel()
+    assert wb.size % 16 == 0
+    section = gpu.WeightsSection(np.concatenate([wb, np.zeros(18, np.uint8), wb, np.zeros(256, np.uint8)]))
+    assert section.ptr % 16 == 0
+    x = oracle.synthetic_acts(rows, k, seed=k + 9)
+    run = tiled if dt == Q8_0 else tiled_b32
+    Wa = section.view(0, wb.size, dt, n, k)
+    Wu = section.view(wb.size + 18, wb.size, dt, n, k)
+    try:
+        ya = run(gpu, Wa, x)
+        yu = run(gpu, Wu, x)
+    finally:
+        Wa.release()
+        Wu.release()
+        section.free()
+    assert bits_equal(ya, yu), first_diff(ya, yu)
+
+
+def test_kq_b32_gemm_q4k_unaligned_view_not_handled(gpu, oracle):
+    """Q4_K blocks are copied as whole 16-byte chunks: a view 2 bytes past a
+    boundary is refused (NOT_HANDLED), not computed from shifted bytes."""
+    n, k = 64, 512
+    wb = np.ascontiguousarray(oracle.synthetic_weight(Q4_K, n, k, seed=11)).view(np.uint8).ravel()
+    section = gpu.WeightsSection(np.concatenate([np.zeros(2, np.uint8), wb, np.zeros(256, np.uint8)]))
+    W = section.view(2, wb.size, Q4_K, n, k)
+    x = oracle.synthetic_acts(16, k, seed=3)
+    try:
+        with pytest.raises(gpu.NotHandled):
+            tiled_b32(gpu, W, x)
+    finally:
+        W.release()
+        section.free()
