@@ -50,9 +50,12 @@ struct GCfg {
 };
 // 64 weight rows x 128 activation rows, eight waves (large grids), and the
 // shapes of few activation rows (up to 64): 32 or 16 weight rows, so that
-// the grid holds as many workgroups as the GPU has CUs.
+// the grid holds as many workgroups as the GPU has CUs. The 32-row tiles
+// take two waves, each its 16 weight rows against all 64 activation rows,
+// so each weight plane is built once (gate at 64 rows 29.4 -> 27.7 us
+// against four waves of 16 x 32).
 using CfgWide = GCfg<512, 4, 128, 2>;
-using CfgM64N32 = GCfg<256, 2, 64, 3>;
+using CfgM64N32 = GCfg<128, 2, 64, 3>;
 using CfgM64N16 = GCfg<256, 1, 64, 3>;
 
 template <uint32_t DT, class C>
