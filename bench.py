@@ -12,22 +12,32 @@ runs the seven products. Weights W ~ N(0, 0.02^2) (numpy PCG64, seeds 0..6 in
 the order above), encoded on the GPU by libmimg's encoder; activations
 x ~ N(0, 1) (seeds 100..103). Synthetic data; no checkpoint.
 
+The four inputs are independent, so at one row the step (--step set, the
+default) quantizes them in one launch and runs the seven products in one
+launch (mimg_linear_a8_set_dev, bit for bit the separate calls). The same
+layer set as a decoder layer calls it, one launch per grouped call (q/k/v,
+o, gate/up, down: --step group), is timed beside it and reported under
+config.other_forms_us_per_step; a decoder layer's calls depend on each
+other, and the decode section below runs them that way.
+
 To measure HBM rather than the 256 MB MALL, the weights are copied into
 --rotate (default 32) distinct layers (4.4 GB, a whole 8B model's linears)
-and step s uses layer s mod rotate. Each layer's step is captured in a HIP
-graph. Timed region: exactly --steps steps between two synchronisations.
+and step s uses layer s mod rotate. The steps over the 32 layers (one
+token's linear sets) are captured in one HIP graph (--graph-steps). Timed
+region: exactly --steps steps between two synchronisations.
 
 value = bytes per step / time per step, bytes = the sum of
 N*(K/QK)*block_bytes + K*4 + N*4 over the seven matrices (the benchmark's
 published formula for this metric).
 
-roofline: the step's longest launch, the Q4_K GEMV computing gate and up
-together, timed alone (graphs of --rotate launches over the rotation copies,
-HIP events on the launch stream), its algorithmic bytes over that time
-against 8 TB/s; traffic from the committed rocprofv3 FETCH/WRITE summary.
-The same kernel on gate alone and the Q6_K down launch are reported beside
-it, and the read ceiling: a plain streaming read of the same gate and up
-weight bytes in one launch, timed the same way.
+roofline: the step's longest launch, at one row the set's product launch
+(the seven matrices, 139 MB), timed alone (graphs of --rotate launches over
+the rotation copies, HIP events on the launch stream), its algorithmic bytes
+over that time against 8 TB/s; traffic from the committed rocprofv3
+FETCH/WRITE summary; the read ceiling: a plain streaming read of the same
+weight bytes in one launch, timed the same way. The grouped gate+up launch
+(the roofline kernel of the grouped form), gate alone and the Q6_K down
+launch are reported beside it.
 
 cfg0: the single 4096 x 4096 Q4_K product of one
 activation row, quantized inside the launch, per call.
@@ -334,9 +344,14 @@ def main():
                     help="new tokens per decode run (default: the configs' 128 and 256; fewer for profiler runs)")
     ap.add_argument("--decode", default="llama1b,llama8b",
                     help="whole-model decode runs (comma list of llama1b, llama8b; empty to skip)")
-    ap.add_argument("--step", default="group", choices=["chain", "group"],
-                    help="group: one launch per grouped call (default); chain: the four grouped products as one chain "
-                         "launch (mimg_linear_a8_chain_dev, one row only)")
+    ap.add_argument("--step", default="", choices=["", "chain", "group", "set"],
+                    help="set (default at one row): the four groups' independent inputs quantized in one launch and "
+                         "the seven products in one launch (mimg_linear_a8_set_dev); group (default at more rows): "
+                         "one launch per grouped call, as a decoder layer makes them; chain: the four grouped "
+                         "products as one chain launch (mimg_linear_a8_chain_dev, one row only)")
+    ap.add_argument("--graph-steps", type=int, default=0,
+                    help="steps captured in one HIP graph (consecutive rotation layers; divides --rotate; "
+                         "default: --rotate)")
     ap.add_argument("--roofline-replays", type=int, default=8,
                     help="replays of the graph of --rotate single-kernel launches timed for the roofline")
     args = ap.parse_args()
@@ -455,57 +470,93 @@ def main():
     # their own.
     groups = [[c for c in CFG1 if c[5] == i] for i in range(len(INPUT_K))]
 
-    use_chain = args.step == "chain"
-    if use_chain and M != 1:
-        raise SystemExit("--step chain runs one activation row (--rows 1)")
+    step_kind = args.step or ("set" if M == 1 else "group")
+    if step_kind in ("chain", "set") and M != 1:
+        raise SystemExit("--step chain and --step set run one activation row (--rows 1)")
+
+    def set_groups(l):
+        return [([layers[l][c[0]] for c in grp], xd[i].ptr, None, [yd[c[0]].ptr for c in grp])
+                for i, grp in enumerate(groups)]
+
+    set_ws_bytes = mimg.linear_a8_set_workspace_bytes(set_groups(0)) if M == 1 else 0
+    set_ws = hiprt.DeviceBuffer(set_ws_bytes) if M == 1 else None
     sync_bytes = mimg.chain_sync_bytes()
     sync = hiprt.DeviceBuffer(sync_bytes)
     mimg.chain_sync_init(sync.ptr, sync_bytes, stream.handle)
 
-    def enqueue_step(l):
-        if use_chain:
+    def enqueue_step(kind, l):
+        if kind == "set":
+            # the seven products' independent inputs quantized in one launch,
+            # the products in one launch
+            mimg.linear_a8_set_dev(set_groups(l), set_ws.ptr, set_ws_bytes, stream.handle)
+        elif kind == "chain":
             # the layer set as one launch: four phases, each phase's weights
             # streamed without a break after the one before
             mimg.linear_a8_chain_dev([([layers[l][c[0]] for c in grp], xd[i].ptr, None, [yd[c[0]].ptr for c in grp])
                                       for i, grp in enumerate(groups)], sync.ptr, sync_bytes, stream.handle)
-            return
-        for i, grp in enumerate(groups):
-            mimg.linear_a8_group_dev([layers[l][c[0]] for c in grp], xd[i].ptr, M, None, 256,
-                                     [yd[c[0]].ptr for c in grp], ws[i].ptr, ws_bytes[i], stream.handle)
+        else:
+            for i, grp in enumerate(groups):
+                mimg.linear_a8_group_dev([layers[l][c[0]] for c in grp], xd[i].ptr, M, None, 256,
+                                         [yd[c[0]].ptr for c in grp], ws[i].ptr, ws_bytes[i], stream.handle)
 
-    graphs = []
+    # A graph holds gs consecutive steps (layers l .. l+gs-1 of the rotation:
+    # by default all 32, one token's linear sets, as a decode step's graph
+    # holds all of a token's layers); with gs = 1 the host launches one graph
+    # per step.
+    gs = args.graph_steps or args.rotate
+    if args.rotate % gs or args.steps % gs or args.warmup % gs:
+        raise SystemExit("--graph-steps must divide --rotate, --steps and --warmup")
     if args.eager:
-        run_step = enqueue_step
-    else:
-        graphs = [hiprt.Graph(stream, lambda l=l: enqueue_step(l)) for l in range(args.rotate)]
+        gs = 1
 
-        def run_step(l):
-            graphs[l].launch(stream)
+    def time_steps(kind):
+        """Warm-up, then exactly --steps steps of `kind` between two events
+        on the launch stream (and device synchronisations); us per step and
+        the wall time per step."""
+        graphs = []
+        if args.eager:
+            def run(l):
+                enqueue_step(kind, l)
+        else:
+            def enqueue_steps(l0):
+                for l in range(l0, l0 + gs):
+                    enqueue_step(kind, l)
 
-    for s in range(args.warmup):
-        run_step(s % args.rotate)
-    stream.sync()
-    log("  warmup done")
+            graphs = [hiprt.Graph(stream, lambda l0=l0: enqueue_steps(l0)) for l0 in range(0, args.rotate, gs)]
 
-    e0, e1 = hiprt.Event(), hiprt.Event()
-    hiprt.device_sync()
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for s in range(args.steps):
-        run_step(s % args.rotate)
-    e1.record(stream)
-    e1.sync()
-    hiprt.device_sync()
-    wall = time.perf_counter() - t0
-    ms_gpu = e0.elapsed_ms(e1)
-    ms_per_step = ms_gpu / args.steps
+            def run(l):
+                graphs[l // gs].launch(stream)
+
+        for s in range(0, args.warmup, gs):
+            run(s % args.rotate)
+        stream.sync()
+        e0, e1 = hiprt.Event(), hiprt.Event()
+        hiprt.device_sync()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for s in range(0, args.steps, gs):
+            run(s % args.rotate)
+        e1.record(stream)
+        e1.sync()
+        hiprt.device_sync()
+        wall = time.perf_counter() - t0
+        us = e0.elapsed_ms(e1) * 1e3 / args.steps
+        for g in graphs:
+            g.destroy()
+        if kind == "chain":
+            st = mimg.chain_status(sync.ptr)
+            if st:
+                raise SystemExit(f"chain status {st}: a device barrier wait timed out")
+        log(f"  timed ({kind}, {gs} steps a graph): {args.steps} steps, {us:.2f} us/step (events), "
+            f"wall {wall * 1e6 / args.steps:.2f} us/step, {step_bytes(M) / (us * 1e-6) / 1e9:.1f} GB/s")
+        return us
+
+    step_us = time_steps(step_kind)
+    ms_per_step = step_us * 1e-3
     value = step_bytes(M) / (ms_per_step * 1e-3) / 1e9
-    log(f"  timed ({'chain' if use_chain else 'group calls'}): {args.steps} steps, {ms_per_step * 1e3:.2f} us/step "
-        f"(events), wall {wall * 1e6 / args.steps:.2f} us/step, {value:.1f} GB/s")
-    if use_chain:
-        st = mimg.chain_status(sync.ptr)
-        if st:
-            raise SystemExit(f"chain status {st}: a device barrier wait timed out")
+    # the same layer set as a decoder layer calls it (one launch per grouped
+    # call), timed the same way beside the headline form
+    other_us = {k: round(time_steps(k), 3) for k in ("group", "set") if k != step_kind and (k == "group" or M == 1)}
 
     # Roofline of the dominant kernel of the step: the Q4_K GEMV launch that
     # computes gate and up together (2 x 14336 x 4096, 66 MB; the step's
@@ -548,6 +599,50 @@ def main():
     g_us, g_bytes, g_gbs = per_launch(["gate"])
     d_us, d_bytes, d_gbs = per_launch(["down"])
 
+    def set_launch_bytes():
+        """Algorithmic bytes of the set's product launch: every matrix's
+        weight blocks and outputs, and each group's quantized row once (int8
+        quants, one f32 scale per 256, the per-32 sums if a Q4_K matrix reads
+        it, the per-16 sums if a Q6_K one does)."""
+        total = 0
+        for grp in groups:
+            k = grp[0][2]
+            total += k + (k // 256) * 4
+            total += (k // 32) * 2 if any(c[3] == Q4_K for c in grp) else 0
+            total += (k // 16) * 2 if any(c[3] == Q6_K for c in grp) else 0
+            total += sum(weight_bytes(c[1], c[2], c[3]) + c[1] * 4 for c in grp)
+        return total
+
+    def set_per_launch():
+        """The set's product launch alone (mimg_matmul_a8_quantized_set_dev):
+        the four rows quantized once by a set call, then a HIP graph of
+        `rotate` product launches over the rotation copies, replayed
+        --roofline-replays times between two events on the launch stream."""
+        mimg.linear_a8_set_dev(set_groups(0), set_ws.ptr, set_ws_bytes, stream.handle)
+
+        def launches():
+            for l in range(args.rotate):
+                mimg.matmul_a8_quantized_set_dev(set_groups(l), set_ws.ptr, set_ws_bytes, stream.handle)
+
+        g = hiprt.Graph(stream, launches)
+        for _ in range(2):
+            g.launch(stream)
+        a, b = hiprt.Event(), hiprt.Event()
+        a.record(stream)
+        for _ in range(args.roofline_replays):
+            g.launch(stream)
+        b.record(stream)
+        b.sync()
+        g.destroy()
+        us = a.elapsed_ms(b) * 1e3 / (args.roofline_replays * args.rotate)
+        nbytes = set_launch_bytes()
+        return us, nbytes, nbytes / (us * 1e-6) / 1e9
+
+    use_set_roof = step_kind == "set"
+    if use_set_roof:
+        s_us, s_bytes, s_gbs = set_per_launch()
+        log(f"  set product launch (the seven matrices, {s_bytes} B): {s_us:.2f} us/launch, {s_gbs:.0f} GB/s")
+
     # The read ceiling of the roofline launch, measured here: a plain
     # streaming read (mimg_stream_read_dev: 16-byte nontemporal loads, every
     # load of a thread in flight at once, nothing computed) of the same
@@ -581,6 +676,13 @@ def main():
     c_gbs = gu_weight_bytes / (c_us * 1e-6) / 1e9
     log(f"  read ceiling (gate+up weight bytes, one launch): {c_us:.2f} us, {c_gbs:.0f} GB/s "
         f"({', '.join(f'{p}x16B: {u:.2f} us' for p, u in ceil.items())})")
+    set_weight_bytes = sum(weight_bytes(c[1], c[2], c[3]) for c in CFG1)
+    if use_set_roof:
+        sceil = {per: read_ceiling([c[0] for c in CFG1], per) for per in (4, 8, 16)}
+        sc_per = min(sceil, key=sceil.get)
+        sc_us = sceil[sc_per]
+        sc_gbs = set_weight_bytes / (sc_us * 1e-6) / 1e9
+        log(f"  read ceiling (the seven matrices' weight bytes, one launch): {sc_us:.2f} us, {sc_gbs:.0f} GB/s")
 
     # An HBM ceiling independent of this library's read kernel, in the same
     # run: a 1 GiB device-to-device hipMemcpyAsync (the runtime's own copy;
@@ -664,13 +766,53 @@ def main():
     # rocprofv3 FETCH_SIZE / WRITE_SIZE passes summarised in profiles/ (the
     # counters cannot be read from inside this process).
     def traffic_of(which):
-        tpath = os.path.join(ROOT, "profiles", f"gemv_pairs_q4k_{which}_m{M}_traffic.md")
+        tpath = os.path.join(ROOT, "profiles", f"{which}_m{M}_traffic.md")
         if os.path.exists(tpath):
             for line in open(tpath):
                 if line.startswith("bytes_per_launch:"):
                     return int(line.split(":", 1)[1].strip())
         return None
 
+    gate_up = {"kernel": f"{'gemv_a8k_mfma_kernel<Q4_K>' if M >= 5 else f'gemv_a8k_pairs_kernel<Q4_K,M={M}>'}: "
+                         "gate and up (2 x 14336x4096) in one launch as the grouped call makes them, pre-quantized "
+                         "activations",
+               "launch_bytes": r_bytes, "avg_launch_us": round(r_us, 3), "achieved": round(r_gbs, 1),
+               "frac": round(r_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_of("gemv_pairs_q4k_gateup"),
+               "kernel_over_ceiling": round(r_gbs / c_gbs, 4)}
+    gate_alone = {"avg_launch_us": round(g_us, 3), "launch_bytes": g_bytes, "achieved": round(g_gbs, 1),
+                  "traffic": traffic_of("gemv_pairs_q4k_gate")}
+    q6k_down = {"avg_launch_us": round(d_us, 3), "launch_bytes": d_bytes, "achieved": round(d_gbs, 1)}
+    gu_ceiling = {"kernel": "stream_read_kernel (mimg_stream_read_dev): the gate and up weight bytes read in one "
+                            "launch, 16-byte nontemporal loads, nothing computed",
+                  "bytes": gu_weight_bytes, "avg_launch_us": round(c_us, 3), "achieved": round(c_gbs, 1),
+                  "frac": round(c_gbs / HBM_PEAK_GBS, 4), "loads_per_thread": c_per}
+    if use_set_roof:
+        roofline = {
+            "bound": "hbm", "achieved": round(s_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(s_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_of("gemv_set_cfg1"),
+            "kernel": "gemv_a8k_set_kernel: the seven cfg1 products (Q4_K and Q6_K) in one launch as the set "
+                      "step runs them, rows quantized beforehand",
+            "launch_bytes": s_bytes, "avg_launch_us": round(s_us, 3),
+            "read_ceiling": {"kernel": "stream_read_kernel (mimg_stream_read_dev): the seven matrices' weight bytes "
+                                       "read in one launch, 16-byte nontemporal loads, nothing computed",
+                             "bytes": set_weight_bytes, "avg_launch_us": round(sc_us, 3),
+                             "achieved": round(sc_gbs, 1), "frac": round(sc_gbs / HBM_PEAK_GBS, 4),
+                             "loads_per_thread": sc_per, "kernel_over_ceiling": round(s_gbs / sc_gbs, 4)},
+            "gate_up": gate_up, "gate_alone": gate_alone, "q6k_down": q6k_down, "gate_up_read_ceiling": gu_ceiling,
+            "hbm_ceiling": hbm_ceiling,
+        }
+    else:
+        roofline = {
+            "bound": "hbm", "achieved": round(r_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(r_gbs / HBM_PEAK_GBS, 4), "traffic": gate_up["traffic"], "kernel": gate_up["kernel"],
+            "launch_bytes": r_bytes, "avg_launch_us": round(r_us, 3), "gate_alone": gate_alone,
+            "q6k_down": q6k_down, "read_ceiling": dict(gu_ceiling, kernel_over_ceiling=gate_up["kernel_over_ceiling"]),
+            "hbm_ceiling": hbm_ceiling,
+        }
+    step_forms = {"set": "the four groups' rows quantized in one launch, the seven products in one launch "
+                         "(mimg_linear_a8_set_dev; the inputs are independent)",
+                  "group": "one launch per grouped call (q/k/v, o, gate/up, down), as a decoder layer calls them",
+                  "chain": "the four grouped calls as one chain launch"}
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -688,32 +830,16 @@ def main():
             "workload": f"cfg1: Llama-3-8B decoder-layer linear set, M={M}, Q4_K_M (q,k,o,gate,up Q4_K; v,down Q6_K), "
                         "dequant_matmul_a8.v2 block=256",
             "rows": M,
+            "step": step_kind,
+            "step_form": step_forms[step_kind],
             "bytes_per_step": step_bytes(M),
             "rotation_layers": args.rotate,
             "graphs": not args.eager,
+            "steps_per_graph": gs,
+            "other_forms_us_per_step": other_us,
             "hbm_fraction": round(value / HBM_PEAK_GBS, 4),
         },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(r_gbs, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(r_gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic_of("gateup"),
-            "kernel": f"{'gemv_a8k_mfma_kernel<Q4_K>' if M >= 5 else f'gemv_a8k_pairs_kernel<Q4_K,M={M}>'}: gate and up "
-                      "(2 x 14336x4096) in one launch as the step groups them, pre-quantized activations",
-            "launch_bytes": r_bytes,
-            "avg_launch_us": round(r_us, 3),
-            "gate_alone": {"avg_launch_us": round(g_us, 3), "launch_bytes": g_bytes, "achieved": round(g_gbs, 1),
-                           "traffic": traffic_of("gate")},
-            "q6k_down": {"avg_launch_us": round(d_us, 3), "launch_bytes": d_bytes, "achieved": round(d_gbs, 1)},
-            "read_ceiling": {"kernel": "stream_read_kernel (mimg_stream_read_dev): the gate and up weight bytes "
-                                       "read in one launch, 16-byte nontemporal loads, nothing computed",
-                             "bytes": gu_weight_bytes, "avg_launch_us": round(c_us, 3), "achieved": round(c_gbs, 1),
-                             "frac": round(c_gbs / HBM_PEAK_GBS, 4), "loads_per_thread": c_per,
-                             "kernel_over_ceiling": round(r_gbs / c_gbs, 4)},
-            "hbm_ceiling": hbm_ceiling,
-        },
+        "roofline": roofline,
         "cfg0": {
             "workload": "cfg0: one 4096x4096 Q4_K product (weight seed 0) of one activation row (seed 1), "
                         "dequant_matmul_a8.v2 block 256, quantized inside the launch",
@@ -752,7 +878,6 @@ def main():
             "GB_per_s": round(launch_bytes(CFG1[4][1], CFG1[4][2], Q4_K, M) / (host_us * 1e-6) / 1e9, 1),
         },
     }
-    del graphs
     layers.clear()
     decode_res = {}
     for name in [d for d in args.decode.split(",") if d]:

@@ -228,6 +228,32 @@ int mimg_chain_sync_init(void *sync, uint64_t sync_bytes, void *stream);
  * wait completed) and clears it; synchronises with the device. */
 int mimg_chain_status(void *sync, uint32_t *status);
 
+/* Independent one-row products in two launches: `ngroups` (1..8) groups,
+ * each the grouped product of `count` (1..3) weights sharing K on its own
+ * input row x (the mimg_chain_phase fields; at most 16 weights in all), as
+ * mimg_linear_a8_group_dev with one activation row and blocks of 256 on each
+ * group (interp/fast.go:246-379, dequant_matmul_a8.v2 at block 256), bit for
+ * bit. One launch quantizes every group's row into `ws` (at least
+ * mimg_linear_a8_set_workspace_bytes, 256-byte aligned), one launch runs all
+ * the products, Q4_K and Q6_K mixed, so no product waits for another's
+ * launch to drain. For a layer's linears whose inputs do not depend on each
+ * other's outputs (BASELINE cfg1's linear set; a decoder layer's own calls
+ * are dependent and keep mimg_linear_a8_group_dev). No output may overlap
+ * any group's x or another output (MIMG_ERR_ARG). Returns MIMG_NOT_HANDLED
+ * (nothing launched) unless every weight is Q4_K or Q6_K with K a multiple
+ * of 256 up to 65536. No counterpart in the reference, which runs each
+ * product as a call of its own. */
+int mimg_linear_a8_set_dev(const mimg_chain_phase *groups, int ngroups, void *ws, uint64_t ws_bytes, void *stream);
+int mimg_linear_a8_set_workspace_bytes(const mimg_chain_phase *groups, int ngroups, uint64_t *bytes);
+/* The product launch of mimg_linear_a8_set_dev alone, on rows a set call
+ * with the same groups already quantized into ws (group g's row at the sum
+ * of mimg_a8_workspace_bytes(1, K_h) over the groups h before it; x is
+ * still read for the float32 path of refused rows). No counterpart in the
+ * reference (its products quantize their own rows). */
+int mimg_matmul_a8_quantized_set_dev(const mimg_chain_phase *groups, int ngroups, void *ws, uint64_t ws_bytes,
+                                     void *stream);
+#define MIMG_SET_MAX_GROUPS 8
+
 /* mimg_linear_a8_dev without a workspace argument, for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc): the quantized activations go to a scratch array
@@ -415,7 +441,7 @@ int mimg_dequantize_dev(uint32_t dtype, const void *src, uint64_t len, float *ds
 int mimg_quantize_dev(uint32_t dtype, const float *src, int64_t n, void *dst, uint64_t dst_len,
                       void *stream);
 
-/* A plain streaming read of `count` (1..3) device byte ranges (16-byte
+/* A plain streaming read of `count` (1..8) device byte ranges (16-byte
  * aligned, lengths non-zero multiples of 16) in one launch: one workgroup of
  * 256 threads per per_thread*4 KB (per_thread 16-byte nontemporal loads
  * each, 2, 4, 8 or 16). sink: 1024 uint32 of device memory, written only

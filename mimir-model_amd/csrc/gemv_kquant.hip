@@ -32,6 +32,10 @@
 // Rows of x the quantizer refused and rows of w with a non-finite block scale
 // take the float32 path (reference linearA8, interp/fast.go:323-377), in the
 // reference's AVX2 order (f32path.hpp).
+#include <algorithm>
+#include <climits>
+#include <cstring>
+
 #include "decoder_math.hpp"
 #include "f32path.hpp"
 #include "kquant_lane.hpp"
@@ -117,26 +121,15 @@ __device__ __forceinline__ void quad_of(int pb, int nb, int& b, int& r0) {
 // tile*U.., rows U..2U-1 the same rows of up; a quad of U rows is one
 // matrix's, so each quad loads from its matrix's tile base. The rows'
 // results meet in LDS and out[n] = swiglu(gate[n], up[n]) is written.
-template <uint32_t DT, int M, int R, bool SW = false>
-__global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    constexpr int U = MIMG_PAIRS_U;
+// One workgroup's tile `tile` of the matrix A.W (A.wref, A.bias, A.y, A.N
+// and A.y_stride are that matrix's; SW reads gate and up from A.mat[0..1]).
+template <uint32_t DT, int M, int R, bool SW, int U = MIMG_PAIRS_U>
+__device__ __forceinline__ void pairs_tile(GemvArgs A, int tile, uint8_t* smem) {
     constexpr bool SHARED = R % U == 0;  // a group's U pairs share one block
     constexpr bool PRE = M == 1;         // activation loaded before the weights
     static_assert(!SW || (M == 1 && R == 2 * U && SHARED), "swiglu epilogue: one row, a gate and an up quad");
-    // This workgroup's matrix of the launch.
-    int mi = 0;
-    if (!SW && A.nmat > 1 && (int)blockIdx.x >= A.mat[1].tile0) mi = 1;
-    if (!SW && A.nmat > 2 && (int)blockIdx.x >= A.mat[2].tile0) mi = 2;
-    const PairMat P = mi == 0 ? A.mat[0] : mi == 1 ? A.mat[1] : A.mat[2];
-    A.W = P.W;
-    A.wref = P.wref;
-    A.bias = P.bias;
-    A.y = P.y;
-    A.N = P.N;
-    A.y_stride = P.N;
     const int g = threadIdx.x >> 3, l = threadIdx.x & 7, t = threadIdx.x;
-    const int nb = A.nb, row0 = ((int)blockIdx.x - P.tile0) * (SW ? U : R), npairs = R * nb;
+    const int nb = A.nb, row0 = tile * (SW ? U : R), npairs = R * nb;
     // The tile's R rows: a 4-byte-aligned base (Q6_K rows are 2-byte
     // aligned) and 32-bit offsets from it (SW: the U rows of each matrix).
     const int64_t tbyte = (int64_t)row0 * A.rb;
@@ -292,6 +285,23 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
     }
 }
 
+template <uint32_t DT, int M, int R, bool SW = false>
+__global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    // This workgroup's matrix of the launch.
+    int mi = 0;
+    if (!SW && A.nmat > 1 && (int)blockIdx.x >= A.mat[1].tile0) mi = 1;
+    if (!SW && A.nmat > 2 && (int)blockIdx.x >= A.mat[2].tile0) mi = 2;
+    const PairMat P = mi == 0 ? A.mat[0] : mi == 1 ? A.mat[1] : A.mat[2];
+    A.W = P.W;
+    A.wref = P.wref;
+    A.bias = P.bias;
+    A.y = P.y;
+    A.N = P.N;
+    A.y_stride = P.N;
+    pairs_tile<DT, M, R, SW>(A, (int)blockIdx.x - P.tile0, smem);
+}
+
 // gate and up at one row with swiglu in the epilogue (Q4_K, N % U == 0).
 static hipError_t launch_pairs_swiglu(GemvArgs A, hipStream_t stream) {
     constexpr int U = MIMG_PAIRS_U, R = 2 * U;
@@ -433,6 +443,118 @@ hipError_t launch_gemv_a8k(const DevWeight* const* ws, int nmat, const ActPtrs& 
     if (w.dt == DT_Q4_K) return launch_dt<DT_Q4_K>(A, (int)rows, stream);
     if (w.dt == DT_Q6_K) return launch_dt<DT_Q6_K>(A, (int)rows, stream);
     return hipErrorInvalidValue;
+}
+
+// Independent one-row products in one launch (mimg_linear_a8_set_dev): the
+// segments are matrices with activation rows of their own (a decoder
+// layer's linear set with an input per matrix), Q4_K and Q6_K mixed, K per
+// segment. A workgroup finds its segment in the argument table through the
+// argument segment pointer (indexing the by-value table with the
+// workgroup's segment would make the compiler copy it to private memory)
+// and runs that matrix's tile exactly as the pairs kernel does, so every
+// output is bit for bit the separate call's.
+template <int R4, int R6, int U6, uint32_t ONLY>
+__global__ __launch_bounds__(256) void gemv_a8k_set_kernel(SetArgs args) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const SetArgs* S = (const SetArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    const int bid = (int)blockIdx.x;
+    // the first workgroups of the segments in one 64-byte scalar load
+    // (unused entries hold INT_MAX)
+    int si = 0;
+#pragma unroll
+    for (int i = 1; i < SET_MAXSEG; i++) si += bid >= S->tile0[i] ? 1 : 0;
+    const SetSeg* s = &S->seg[si];
+    GemvArgs A;
+    A.W = s->W;
+    A.rb = s->rb;
+    A.N = s->N;
+    A.nb = s->nb;
+    A.K = s->K;
+    A.q = s->q;
+    A.d32 = s->d32;
+    A.s16 = s->s16;
+    A.ok = s->ok;
+    A.wref = s->wref;
+    A.x = s->x;
+    A.bias = s->bias;
+    A.y = s->y;
+    A.y_stride = s->N;
+    A.fused = 1;
+    A.nmat = 1;
+    A.sw = nullptr;
+    A.sw_total = A.sw_chunk = 0;
+    const int tile = bid - S->tile0[si];
+    if constexpr (ONLY == DT_Q4_K) {
+        pairs_tile<DT_Q4_K, 1, R4, false>(A, tile, smem);
+    } else if constexpr (ONLY == DT_Q6_K) {
+        pairs_tile<DT_Q6_K, 1, R6, false, U6>(A, tile, smem);
+    } else {
+        if (s->dt == DT_Q4_K) pairs_tile<DT_Q4_K, 1, R4, false>(A, tile, smem);
+        else pairs_tile<DT_Q6_K, 1, R6, false, U6>(A, tile, smem);
+    }
+}
+
+// Rows per workgroup in a set launch (the launch has thousands of tiles, so
+// the standalone launch's rule of at least 1024 workgroups does not apply).
+// One launch for both dtypes measured faster than a launch per dtype
+// (cfg1 set 39.0 against 41.0 us a step).
+#ifndef MIMG_SET_R4
+#define MIMG_SET_R4 8
+#endif
+#ifndef MIMG_SET_R6
+#define MIMG_SET_R6 8
+#endif
+// Q6_K pairs in flight per group of eight lanes: two keep the launch at 64
+// VGPRs (eight waves a SIMD for the Q4_K tiles too; measured on MI355X, the
+// cfg1 set 34.3 -> 32.0 us with eight Q6_K rows a workgroup instead of four).
+#ifndef MIMG_SET_U6
+#define MIMG_SET_U6 2
+#endif
+// One launch for both dtypes (0), or a launch per dtype (1).
+#ifndef MIMG_SET_SPLIT
+#define MIMG_SET_SPLIT 0
+#endif
+
+static int set_rows(uint32_t dt) { return dt == DT_Q4_K ? MIMG_SET_R4 : MIMG_SET_R6; }
+
+// Segments in launch order, the longest workgroups first (weight bytes a
+// workgroup reads), so that the grid's tail is made of short ones; tile0 of
+// each set here.
+template <uint32_t ONLY>
+static hipError_t launch_set_part(const SetArgs& in, hipStream_t stream) {
+    SetArgs a;
+    memset(&a, 0, sizeof a);
+    for (int i = 0; i < in.nseg; i++)
+        if (ONLY == 0 || (uint32_t)in.seg[i].dt == ONLY) a.seg[a.nseg++] = in.seg[i];
+    if (a.nseg == 0) return hipSuccess;
+    auto wg_bytes = [](const SetSeg& s) {
+        return (int64_t)set_rows((uint32_t)s.dt) * s.nb * (s.dt == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES);
+    };
+    std::stable_sort(a.seg, a.seg + a.nseg,
+                     [&](const SetSeg& x, const SetSeg& y) { return wg_bytes(x) > wg_bytes(y); });
+    int tiles = 0, nbmax = 1;
+    for (int i = 0; i < SET_MAXSEG; i++) a.tile0[i] = INT_MAX;
+    for (int i = 0; i < a.nseg; i++) {
+        const int R = set_rows((uint32_t)a.seg[i].dt);
+        a.tile0[i] = tiles;
+        tiles += (a.seg[i].N + R - 1) / R;
+        nbmax = a.seg[i].nb * R > nbmax ? a.seg[i].nb * R : nbmax;
+    }
+    const int rmax = MIMG_SET_R4 > MIMG_SET_R6 ? MIMG_SET_R4 : MIMG_SET_R6;
+    const size_t lds = (size_t)nbmax * 16 + (size_t)rmax * 4;
+    if (lds > 64 * 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemv_a8k_set_kernel<MIMG_SET_R4, MIMG_SET_R6, MIMG_SET_U6, ONLY>), dim3((unsigned)tiles), dim3(256), lds,
+                       stream, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_a8k_set(const SetArgs& a, hipStream_t stream) {
+    for (int i = 0; i < a.nseg; i++)
+        if (a.seg[i].dt != (int32_t)DT_Q4_K && a.seg[i].dt != (int32_t)DT_Q6_K) return hipErrorInvalidValue;
+    if (!MIMG_SET_SPLIT) return launch_set_part<0>(a, stream);
+    hipError_t e = launch_set_part<DT_Q6_K>(a, stream);
+    if (e != hipSuccess) return e;
+    return launch_set_part<DT_Q4_K>(a, stream);
 }
 
 }  // namespace mimg

@@ -3,6 +3,7 @@
 // gfx950 kernels. No CPU compute path: every product runs on the GPU.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -1074,6 +1075,133 @@ int mimg_linear_a8_chain_dev(const mimg_chain_phase* phases, int nphase, void* s
     return MIMG_OK;
 }
 
+// Independent one-row groups (each a mimg_linear_a8_group_dev call with one
+// activation row and blocks of 256): one launch quantizes every group's row,
+// one launch runs every product. Checks shared by the entry point and the
+// workspace query; fills held[] and the per-group K.
+static int set_checks(const mimg_chain_phase* groups, int ngroups, Held* held, int64_t* K) {
+    if (!groups || ngroups < 1 || ngroups > MIMG_SET_MAX_GROUPS)
+        return fail(MIMG_ERR_ARG, "a set holds 1 to %d groups, got %d", MIMG_SET_MAX_GROUPS, ngroups);
+    int nmat = 0;
+    for (int g = 0; g < ngroups; g++) {
+        const mimg_chain_phase& gr = groups[g];
+        if (gr.count < 1 || gr.count > 3) return fail(MIMG_ERR_ARG, "group %d: a group holds 1 to 3 weights, got %d", g, gr.count);
+        if (nmat + gr.count > SET_MAXSEG) return fail(MIMG_ERR_ARG, "a set holds at most %d weights", SET_MAXSEG);
+        for (int i = 0; i < gr.count; i++) {
+            int rc;
+            Held& h = held[nmat++];
+            if ((rc = h.acquire(gr.w[i]))) return rc;
+            const DevWeight& dw = h->dw;
+            if (i == 0) K[g] = dw.k;
+            else if (dw.k != K[g]) return fail(MIMG_ERR_ARG, "group %d: the weights of a group must share K", g);
+            if (dw.dt != DT_Q4_K && dw.dt != DT_Q6_K)
+                return fail(MIMG_NOT_HANDLED, "group %d: %s has no set kernel", g, dt_name(dw.dt));
+            if (dw.k % 256 || dw.k > 65536 || dw.n > (1 << 30) || dw.n * dw.row_bytes > ((int64_t)1 << 32))
+                return fail(MIMG_NOT_HANDLED, "group %d: %s [%lld, %lld] does not fit the set kernel", g,
+                            dt_name(dw.dt), (long long)dw.n, (long long)dw.k);
+        }
+    }
+    return MIMG_OK;
+}
+
+int mimg_linear_a8_set_workspace_bytes(const mimg_chain_phase* groups, int ngroups, uint64_t* bytes) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    if (!bytes) return fail(MIMG_ERR_ARG, "bytes is null");
+    Held held[MIMG_SET_MAX_GROUPS * 3];
+    int64_t K[MIMG_SET_MAX_GROUPS];
+    if ((rc = set_checks(groups, ngroups, held, K))) return rc;
+    uint64_t total = 0;
+    for (int g = 0; g < ngroups; g++) total += act_layout(1, K[g]).total;
+    *bytes = total;
+    return MIMG_OK;
+}
+
+// quantize: the set call (x -> ws, then the products); otherwise the
+// products of rows already quantized into ws in the same layout.
+static int set_impl(const mimg_chain_phase* groups, int ngroups, void* ws, uint64_t ws_bytes, void* stream,
+                    bool quantize) {
+    int rc = ensure_device();
+    if (rc) return rc;
+    Held held[MIMG_SET_MAX_GROUPS * 3];
+    int64_t K[MIMG_SET_MAX_GROUPS];
+    if ((rc = set_checks(groups, ngroups, held, K))) return rc;
+    uint64_t need = 0;
+    for (int g = 0; g < ngroups; g++) need += act_layout(1, K[g]).total;
+    if (!ws || !aligned(ws, 256) || ws_bytes < need)
+        return fail(MIMG_ERR_WORKSPACE, "the set needs a 256-byte aligned workspace of %llu bytes (got %llu)",
+                    (unsigned long long)need, (unsigned long long)ws_bytes);
+    // Every output against every input and every other output: the
+    // quantizer reads each x, and refused rows read x inside the product
+    // launch while the other workgroups write their outputs.
+    struct Span {
+        uintptr_t a, e;
+    };
+    Span xs[MIMG_SET_MAX_GROUPS], ys[MIMG_SET_MAX_GROUPS * 3];
+    int ny = 0, m = 0;
+    QaSetArgs Q;
+    memset(&Q, 0, sizeof Q);
+    SetArgs S;
+    memset(&S, 0, sizeof S);
+    int qwgs = 0;
+    uint64_t off = 0;
+    for (int g = 0; g < ngroups; g++) {
+        const mimg_chain_phase& gr = groups[g];
+        if (!gr.x || !aligned(gr.x, 16)) return fail(MIMG_ERR_ARG, "group %d: x must be 16-byte aligned", g);
+        xs[g] = {(uintptr_t)gr.x, (uintptr_t)gr.x + (uint64_t)K[g] * 4};
+        const ActLayout l = act_layout(1, K[g]);
+        const ActPtrs a = act_ptrs((uint8_t*)ws + off, l);
+        off += l.total;
+        QaSetRow& qr = Q.row[g];
+        qr.x = gr.x;
+        qr.K = K[g];
+        qr.a = a;
+        qr.wg0 = qwgs;
+        qwgs += 1 + (int)((K[g] / 256 + 7) / 8);
+        for (int i = 0; i < gr.count; i++, m++) {
+            const DevWeight& dw = held[m]->dw;
+            if (!gr.y[i]) return fail(MIMG_ERR_ARG, "group %d: output %d is null", g, i);
+            ys[ny++] = {(uintptr_t)gr.y[i], (uintptr_t)gr.y[i] + (uint64_t)dw.n * 4};
+            SetSeg& s = S.seg[m];
+            s.W = dw.data;
+            s.wref = dw.wref;
+            s.bias = gr.bias[i];
+            s.y = gr.y[i];
+            s.q = a.q;
+            s.d32 = a.d32;
+            s.s16 = dw.dt == DT_Q4_K ? a.xs : a.ys16;
+            s.ok = a.ok;
+            s.x = gr.x;
+            s.rb = dw.row_bytes;
+            s.K = dw.k;
+            s.N = (int32_t)dw.n;
+            s.nb = (int32_t)(dw.k / 256);
+            s.dt = (int32_t)dw.dt;
+        }
+    }
+    for (int i = 0; i < ny; i++) {
+        for (int g = 0; g < ngroups; g++)
+            if (ys[i].a < xs[g].e && xs[g].a < ys[i].e) return fail(MIMG_ERR_ARG, "output %d overlaps the input of group %d", i, g);
+        for (int j = i + 1; j < ny; j++)
+            if (ys[i].a < ys[j].e && ys[j].a < ys[i].e) return fail(MIMG_ERR_ARG, "outputs %d and %d overlap", i, j);
+    }
+    Q.nrows = ngroups;
+    S.nseg = m;
+    hipStream_t s = (hipStream_t)stream;
+    if (quantize) HIP_TRY(launch_quantize_act_set(Q, qwgs, s));
+    HIP_TRY(launch_gemv_a8k_set(S, s));
+    return MIMG_OK;
+}
+
+int mimg_linear_a8_set_dev(const mimg_chain_phase* groups, int ngroups, void* ws, uint64_t ws_bytes, void* stream) {
+    return set_impl(groups, ngroups, ws, ws_bytes, stream, true);
+}
+
+int mimg_matmul_a8_quantized_set_dev(const mimg_chain_phase* groups, int ngroups, void* ws, uint64_t ws_bytes,
+                                     void* stream) {
+    return set_impl(groups, ngroups, ws, ws_bytes, stream, false);
+}
+
 int mimg_linear_a8_noalloc_dev(uint64_t wh, const float* x, int64_t rows, const float* bias, int block, float* y,
                                void* stream) {
     int rc = ensure_device();
@@ -1443,8 +1571,8 @@ int mimg_stream_read_dev(const void* const* src, const uint64_t* len, int count,
                          void* stream) {
     int rc = ensure_device();
     if (rc) return rc;
-    if (!src || !len || !sink || count < 1 || count > 3)
-        return fail(MIMG_ERR_ARG, "stream read: 1 to 3 ranges and a sink");
+    if (!src || !len || !sink || count < 1 || count > READ_MAX_RANGES)
+        return fail(MIMG_ERR_ARG, "stream read: 1 to %d ranges and a sink", READ_MAX_RANGES);
     if (per_thread != 2 && per_thread != 4 && per_thread != 8 && per_thread != 16)
         return fail(MIMG_ERR_ARG, "stream read: %d loads per thread (2, 4, 8 or 16)", per_thread);
     ReadRanges r{};

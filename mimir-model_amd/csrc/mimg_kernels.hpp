@@ -78,6 +78,44 @@ hipError_t launch_gemv_a8k(const DevWeight* const* ws, int nmat, const ActPtrs& 
                            int64_t total_rows, const float* x, const float* const* bias, float* const* y,
                            hipStream_t stream);
 
+// Independent one-row products in one launch (gemv_kquant.hip): segment i
+// is matrix W (Q4_K or Q6_K, K a multiple of 256) against its own quantized
+// row; the launcher orders the segments and sets tile0.
+struct SetSeg {
+    const uint8_t* W;
+    const uint8_t* wref;
+    const float* bias;    // [N] or null
+    float* y;             // [N]
+    const int8_t* q;      // the segment's quantized row
+    const float* d32;
+    const int16_t* s16;   // Q4_K: xs; Q6_K: ys16
+    const int32_t* ok;
+    const float* x;       // the f32 row (float32 path of refused rows)
+    int64_t rb, K;
+    int32_t N, nb, dt, pad;
+};
+constexpr int SET_MAXSEG = 16;
+struct SetArgs {
+    int32_t tile0[SET_MAXSEG];  // first workgroup of each segment (INT_MAX past nseg)
+    int32_t nseg, pad[3];
+    SetSeg seg[SET_MAXSEG];
+};
+hipError_t launch_gemv_a8k_set(const SetArgs& a, hipStream_t stream);
+// One launch quantizing rows of different K (blocks of 256; each row's own
+// ActPtrs), as launch_quantize_act on each (quantize_act.hip).
+struct QaSetRow {
+    const float* x;
+    int64_t K;
+    ActPtrs a;
+    int32_t wg0, pad;  // first workgroup: the row's scanner, then its chunk workgroups
+};
+constexpr int QA_SET_MAXROWS = 16;
+struct QaSetArgs {
+    QaSetRow row[QA_SET_MAXROWS];
+    int32_t nrows, pad[3];
+};
+hipError_t launch_quantize_act_set(const QaSetArgs& a, int wgs, hipStream_t stream);
+
 // Many activation rows (already quantized) against one Q4_K/Q6_K matrix,
 // on the int8 matrix cores (gemm_kquant.hip); bit-identical to the GEMV.
 bool gemm_a8k_ok(const DevWeight& w);
@@ -179,13 +217,14 @@ hipError_t launch_dequantize(uint32_t dt, const uint8_t* src, int64_t n_elems, f
 
 hipError_t launch_encode(uint32_t dt, const float* x, int64_t n, uint8_t* dst, hipStream_t stream);
 
-// A plain streaming read of up to three byte ranges (misc_kernels.hip), the
+// A plain streaming read of up to eight byte ranges (misc_kernels.hip), the
 // measured ceiling of the HBM-bound kernels; per = 16-byte loads per thread
 // (2, 4, 8 or 16), one workgroup of 256 threads per per*4 KB.
+constexpr int READ_MAX_RANGES = 8;
 struct ReadRanges {
-    const uint8_t* src[3];
-    int64_t len[3];  // multiples of 16
-    int64_t wgs[3];  // workgroups per range (set by the launcher)
+    const uint8_t* src[READ_MAX_RANGES];
+    int64_t len[READ_MAX_RANGES];  // multiples of 16
+    int64_t wgs[READ_MAX_RANGES];  // workgroups per range (set by the launcher)
     int count;
 };
 hipError_t launch_stream_read(const ReadRanges& r, int per, uint32_t* sink, hipStream_t s);

@@ -235,6 +235,52 @@ static hipError_t launch_qa(const float* x, int64_t rows, int64_t K, int block, 
     return hipGetLastError();
 }
 
+// Rows of different K, each with its own ActPtrs, in one launch (the inputs
+// of a set of independent products, mimg_linear_a8_set_dev), blocks of 256.
+// Row i owns workgroups wg0 .. wg0 + ceil(chunks/8): the first scans the row
+// for the refusal flag, the others quantize eight chunks each, exactly as
+// quantize_act_mw_kernel<256, QA_PLAIN> does for a row on its own.
+__global__ __launch_bounds__(64 * QA_MW_WAVES) void quantize_act_set_kernel(QaSetArgs args) {
+    const QaSetArgs* S = (const QaSetArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    const int bid = (int)blockIdx.x;
+    int ri = 0;
+    for (int i = 1; i < S->nrows; i++) ri = bid >= S->row[i].wg0 ? i : ri;
+    const QaSetRow* r = &S->row[ri];
+    const int64_t K = r->K, nch = (K + 255) / 256;
+    const float* xr = r->x;
+    const ActPtrs a = r->a;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, gi = bid - r->wg0;
+    if (gi > 0) {
+        const int64_t c = (int64_t)(gi - 1) * QA_MW_WAVES + wave;
+        if (c >= nch) return;  // uniform within the wave
+        const int64_t e0 = c * 256 + 4 * lane, el = min(e0, K - 4);
+        const float4 v = *(const float4*)(xr + el);
+        qa_chunk<256>(v, 0, e0, K, a, lane);
+        return;
+    }
+    constexpr int SCAN = 8, STEP = 4 * 64 * QA_MW_WAVES;
+    bool bad = false;
+    for (int64_t e0 = 4 * (int64_t)threadIdx.x; e0 < K; e0 += (int64_t)STEP * SCAN) {
+        float4 v[SCAN];
+#pragma unroll
+        for (int j = 0; j < SCAN; j++) v[j] = *(const float4*)(xr + min(e0 + (int64_t)STEP * j, K - 4));
+#pragma unroll
+        for (int j = 0; j < SCAN; j++) {
+            if (e0 + (int64_t)STEP * j >= K) continue;
+            const float xv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) bad |= !(fabsf(xv[k]) <= 0x1p60f);
+        }
+    }
+    const int any_bad = __syncthreads_or(bad ? 1 : 0);
+    if (threadIdx.x == 0) a.ok[0] = any_bad ? 0 : 1;
+}
+
+hipError_t launch_quantize_act_set(const QaSetArgs& a, int wgs, hipStream_t stream) {
+    hipLaunchKernelGGL(quantize_act_set_kernel, dim3((unsigned)wgs), dim3(64 * QA_MW_WAVES), 0, stream, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_quantize_act(const float* x, int64_t rows, int64_t K, int block, const ActPtrs& a,
                                hipStream_t stream) {
     return launch_qa<QA_PLAIN>(x, rows, K, block, a, QaSource{}, stream);

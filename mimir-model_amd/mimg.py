@@ -46,6 +46,9 @@ SIGNATURES = {
     "mimg_linear_a8_group_dev": (_I, [ctypes.POINTER(_U64), _I, _P, _I64, ctypes.POINTER(_P), _I,
                                       ctypes.POINTER(_P), _P, _U64, _P]),
     "mimg_linear_a8_chain_dev": (_I, [_P, _I, _P, _U64, _P]),
+    "mimg_linear_a8_set_dev": (_I, [_P, _I, _P, _U64, _P]),
+    "mimg_linear_a8_set_workspace_bytes": (_I, [_P, _I, ctypes.POINTER(_U64)]),
+    "mimg_matmul_a8_quantized_set_dev": (_I, [_P, _I, _P, _U64, _P]),
     "mimg_chain_sync_bytes": (_U64, []),
     "mimg_vcache_elems": (_U64, [_I64, _I64, _I64]),
     "mimg_chain_sync_init": (_I, [_P, _U64, _P]),
@@ -303,6 +306,44 @@ def linear_a8_chain_dev(phases, sync_ptr, sync_bytes, stream):
     _check(load().mimg_linear_a8_chain_dev(ctypes.cast(arr, _P), len(phases), _P(sync_ptr), sync_bytes, _P(stream)))
 
 
+def _groups(groups):
+    arr = (_ChainPhase * len(groups))()
+    for i, (weights, x_ptr, bias_ptrs, y_ptrs) in enumerate(groups):
+        ph = arr[i]
+        ph.x = x_ptr
+        ph.count = len(weights)
+        for j, w in enumerate(weights):
+            ph.w[j] = w.handle
+            ph.y[j] = y_ptrs[j]
+            ph.bias[j] = bias_ptrs[j] if bias_ptrs and bias_ptrs[j] else None
+    return arr
+
+
+def linear_a8_set_workspace_bytes(groups):
+    """Workspace bytes of linear_a8_set_dev for these groups."""
+    v = _U64(0)
+    arr = _groups(groups)
+    _check(load().mimg_linear_a8_set_workspace_bytes(ctypes.cast(arr, _P), len(groups), ctypes.byref(v)))
+    return int(v.value)
+
+
+def linear_a8_set_dev(groups, ws_ptr, ws_bytes, stream):
+    """Independent one-row grouped products (rows 1, block 256) in one
+    quantize launch and one product launch, bit for bit the
+    linear_a8_group_dev calls. groups: a list of (weights, x_ptr, bias_ptrs
+    or None, y_ptrs); raises NotHandled where the set kernel does not apply."""
+    arr = _groups(groups)
+    _check(load().mimg_linear_a8_set_dev(ctypes.cast(arr, _P), len(groups), _P(ws_ptr), ws_bytes, _P(stream)))
+
+
+def matmul_a8_quantized_set_dev(groups, ws_ptr, ws_bytes, stream):
+    """The product launch of linear_a8_set_dev alone, on rows an earlier set
+    call with the same groups quantized into ws."""
+    arr = _groups(groups)
+    _check(load().mimg_matmul_a8_quantized_set_dev(ctypes.cast(arr, _P), len(groups), _P(ws_ptr), ws_bytes,
+                                                   _P(stream)))
+
+
 def rms_norm_linear_a8_group_dev(weights, x_ptr, resid_ptr, scale_ptr, eps, x_out_ptr, bias_ptrs, y_ptrs, stream):
     """One row: x_out = x + resid, h = rms_norm(x_out) * scale, y_ptrs[i] =
     h . W_i^T (+ bias) in one launch; raises NotHandled where the fused
@@ -512,7 +553,7 @@ def row_bytes(dt, k):
 
 
 def stream_read_dev(ranges, per_thread, sink_ptr, stream):
-    """A plain streaming read of up to three (device pointer, bytes) ranges
+    """A plain streaming read of up to eight (device pointer, bytes) ranges
     in one launch (mimg_stream_read_dev): the HBM read ceiling."""
     n = len(ranges)
     ps = (_P * n)(*[_P(p) for p, _ in ranges])
