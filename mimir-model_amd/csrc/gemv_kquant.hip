@@ -285,7 +285,7 @@ __device__ __forceinline__ void pairs_tile(GemvArgs A, int tile, uint8_t* smem) 
     }
 }
 
-template <uint32_t DT, int M, int R, bool SW = false>
+template <uint32_t DT, int M, int R, bool SW = false, int U = MIMG_PAIRS_U>
 __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
     // This workgroup's matrix of the launch.
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
     A.y = P.y;
     A.N = P.N;
     A.y_stride = P.N;
-    pairs_tile<DT, M, R, SW>(A, (int)blockIdx.x - P.tile0, smem);
+    pairs_tile<DT, M, R, SW, U>(A, (int)blockIdx.x - P.tile0, smem);
 }
 
 // gate and up at one row with swiglu in the epilogue (Q4_K, N % U == 0).
@@ -312,7 +312,7 @@ static hipError_t launch_pairs_swiglu(GemvArgs A, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <uint32_t DT, int M, int R>
+template <uint32_t DT, int M, int R, int U = MIMG_PAIRS_U>
 static hipError_t launch_pairs_r(GemvArgs A, hipStream_t stream) {
     int tiles = 0;
     for (int i = 0; i < A.nmat; i++) {
@@ -320,7 +320,7 @@ static hipError_t launch_pairs_r(GemvArgs A, hipStream_t stream) {
         tiles += (A.mat[i].N + R - 1) / R;
     }
     const size_t lds = (size_t)R * A.nb * M * 16 + (size_t)R * M * 4;
-    hipLaunchKernelGGL((gemv_a8k_pairs_kernel<DT, M, R>), dim3((unsigned)tiles), dim3(256), lds, stream, A);
+    hipLaunchKernelGGL((gemv_a8k_pairs_kernel<DT, M, R, false, U>), dim3((unsigned)tiles), dim3(256), lds, stream, A);
     return hipGetLastError();
 }
 
@@ -339,6 +339,7 @@ template <uint32_t DT, int M>
 static hipError_t launch_pairs(GemvArgs A, hipStream_t stream) {
     int total_n = 0;
     for (int i = 0; i < A.nmat; i++) total_n += A.mat[i].N;
+
     switch (pairs_rows(total_n, A.nb, M)) {
     case 8: return launch_pairs_r<DT, M, 8>(A, stream);
     case 4: return launch_pairs_r<DT, M, 4>(A, stream);
