@@ -97,3 +97,22 @@ def test_small_grid_prefill_bitexact_with_refusals(gpu, oracle, dt, rows, n, k):
     W.release()
     want = oracle.linear_a8(x, wb, dt, n, k, bias=bias, block=256, threads=16)
     assert bits_equal(got, want), first_diff(got, want)
+
+
+@pytest.mark.parametrize("dt", [Q4_K, Q6_K], ids=["q4_k", "q6_k"])
+@pytest.mark.parametrize("rows,n,k", [(512, 1024, 4096), (130, 1024, 4096), (300, 520, 2048), (1000, 2000, 1024)])
+def test_few_weight_rows_many_activation_rows_bitexact(gpu, oracle, dt, rows, n, k):
+    """More than 64 activation rows on few weight rows (a prompt's k and v
+    products: 1024 x 4096 at 512 rows), where the 128 x 128 tiles leave CUs
+    idle and a small-grid tiling runs: partial tiles, a refused activation
+    row (NaN) and bias; every output equal to the oracle's, bit for bit."""
+    wb = oracle.synthetic_weight(dt, n, k, seed=rows + n + k)
+    x = oracle.synthetic_acts(rows, k, seed=rows + 1)
+    x[rows // 3, 5] = np.nan
+    bias = np.random.default_rng(rows + 2).standard_normal(n).astype(np.float32)
+    print(f"few weight rows: dt {dt} rows {rows} n {n} k {k}", flush=True)
+    W = gpu.Weight(wb, dt, n, k)
+    got = gpu.dequant_matmul_a8(W, x, bias=bias, block=256)
+    W.release()
+    want = oracle.linear_a8(x, wb, dt, n, k, bias=bias, block=256, threads=16)
+    assert bits_equal(got, want), first_diff(got, want)
