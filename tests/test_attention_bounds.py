@@ -1,7 +1,8 @@
 """Host-side range check of the attention kernels' address arithmetic.
 
 Every global and LDS address that att_scores_kernel, att_decode_kernel,
-att_wsum_kernel and att_wsum_q4_kernel (mimir-model_amd/csrc/decoder_ops.hip)
+att_wsum_kernel, att_wsum_q4_kernel, att_scores_kpl_kernel and
+att_wsum_qpl_kernel (mimir-model_amd/csrc/decoder_ops.hip)
 compute is restated here per workgroup of the launch grid that
 launch_attention picks, and its extremes are checked against the sizes of
 the buffers: the key cache [kv_heads][C][D], the value cache blocked by eight
@@ -163,12 +164,87 @@ def check_wsum_q4(b, ranges):
                     assert 8 * nblk <= VS and offc + rows <= VS
 
 
+def check_scores_kpl(b, ranges):
+    """att_scores_kpl_kernel: workgroup (x, h, z) walks tiles of 256 cache
+    entries from the smallest first entry of its 32 queries, gridDim.x
+    apart; thread i reads key kb + i (clamped to the cache), stores the
+    score of key j = kb + i - k0 for 0 <= j < n."""
+    D, C, QG = b.D, b.C, 32
+    assert QG * D * 4 <= 64 * 1024  # the query rows in LDS
+    gx = (b.maxk + 255) // 256
+    for z in range((b.T + QG - 1) // QG):
+        r = [ranges[QG * z + i] if QG * z + i < b.T else (0, 0) for i in range(QG)]
+        live = [(k0, n) for k0, n in r if n > 0]
+        if not live:
+            continue
+        kmin = min(k0 for k0, _ in live)
+        kfin = max(k0 + n for k0, n in live)
+        for h in range(b.H):
+            hk = h // (b.H // b.Hkv)
+            for x in range(gx):
+                kb = kmin + 256 * x
+                while kb < kfin:
+                    a_lo, a_hi = min(kb, C - 1), min(kb + 255, C - 1)
+                    b.check((hk * C + a_lo) * D, (hk * C + a_hi) * D + D - 1, b.kc_len, "scores_kpl: key element")
+                    for i, (k0, n) in enumerate(r):
+                        if n <= 0:
+                            continue
+                        j_lo, j_hi = max(kb - k0, 0), min(kb + 255 - k0, n - 1)
+                        if j_lo > j_hi:
+                            continue
+                        t = QG * z + i
+                        assert t < b.T and j_hi < b.maxk
+                        b.check((t * b.H + h) * b.maxk + j_lo, (t * b.H + h) * b.maxk + j_hi, b.ws_len,
+                                "scores_kpl: out")
+                    kb += 256 * gx
+
+
+def check_wsum_qpl(b, ranges):
+    """att_wsum_qpl_kernel: workgroup (h, z) of 16 queries; the scores of
+    each query (j < n) into LDS [key][16]; per pass (all queries when they
+    share the first entry, else one query at a time) the value blocks from
+    the block holding k0, four ahead and clamped to the last block, and the
+    LDS rows of keys below the pass's largest count."""
+    D, C, QG = b.D, b.C, 16
+    assert b.maxk * QG * 4 + 1024 <= LDS_BYTES
+    for z in range((b.T + QG - 1) // QG):
+        r = [ranges[QG * z + i] if QG * z + i < b.T else (0, 0) for i in range(QG)]
+        ns = [n for _, n in r]
+        for i, n in enumerate(ns):
+            assert n <= b.maxk
+            if n > 0:
+                assert QG * z + i < b.T
+        live = [i for i in range(QG) if ns[i] > 0]
+        if not live:
+            continue
+        same = all(r[i][0] == r[live[0]][0] for i in live)
+        passes = [live] if same else [[i] for i in live]
+        for h in range(b.H):
+            hk = h // (b.H // b.Hkv)
+            for qs in passes:
+                k0 = r[qs[0]][0]
+                nmax = max(ns[i] for i in qs)
+                off = k0 & 7
+                kbeg = k0 - off
+                nblk = (off + nmax + 7) >> 3
+                last_blk = kbeg + 8 * (nblk - 1)
+                assert kbeg >= 0 and last_blk < ((C + 7) // 8) * 8
+                for d in (0, D - 1):
+                    b.check(b.vcache_at(hk, kbeg, d), b.vcache_at(hk, last_blk, d) + 7, b.vc_len,
+                            "wsum_qpl: value element")
+                assert nmax - 1 < b.maxk  # LDS rows of the keys read
+
+
 def run_launch(T, H, Hkv, D, C, maxk, f16, kend, kstart):
     b = Bounds(T, H, Hkv, D, C, maxk, f16)
     ranges = [att_range(kend, kstart, t, C, maxk) for t in range(T)]
     for k0, n in ranges:
         assert 0 <= k0 < C and 0 <= n <= min(C - k0, maxk)
     many = T >= 16 and D % 64 == 0 and maxk <= 2048
+    if many and T >= 256 and (D == 64 or (D == 128 and f16)) and maxk <= 1024:
+        check_scores_kpl(b, ranges)
+        check_wsum_qpl(b, ranges)
+        return "prompt"
     if many:
         check_scores(b, ranges, 4)
         check_wsum_q4(b, ranges)
@@ -207,7 +283,8 @@ def test_attention_addresses_in_bounds(D, f16):
     rng = np.random.default_rng(D + (1000 if f16 else 0))
     seen = set()
     for T, (H, Hkv), C, slots, maxk_kind in itertools.product(
-            (1, 3, 8, 16, 37), ((4, 1), (8, 2), (4, 4)), (1, 7, 42, 301, 2048, 8200), (1, 3), ("C", "small", "max")):
+            (1, 3, 8, 16, 37, 300), ((4, 1), (8, 2), (4, 4)), (1, 7, 42, 301, 2048, 8200), (1, 3),
+            ("C", "small", "max")):
         if slots > C:
             continue
         maxk = {"C": min(C, 8192), "small": max(1, min(C, 8192) // 3), "max": 8192}[maxk_kind]
@@ -215,7 +292,9 @@ def test_attention_addresses_in_bounds(D, f16):
             continue
         kend, kstart = ranges_for(T, C, maxk, slots, rng)
         seen.add(run_launch(T, H, Hkv, D, C, maxk, f16, kend, kstart if slots > 1 or T > 5 else None))
-    if D in (64, 128):
+    if D == 64 or (D == 128 and f16):
+        assert seen == {"many", "decode", "two", "prompt"}
+    elif D == 128:
         assert seen == {"many", "decode", "two"}
     elif D % 64 == 0:
         assert seen == {"many", "two"}

@@ -1038,13 +1038,16 @@ def test_matmul_quantized_group_equals_single(gpu, oracle, rt):
 
 @pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
 @pytest.mark.parametrize("T,slots,D,C", [(20, 1, 64, 64), (37, 1, 128, 64), (24, 3, 64, 64), (18, 2, 128, 64),
-                                         (24, 3, 64, 44), (18, 2, 128, 42)])
+                                         (24, 3, 64, 44), (18, 2, 128, 42), (300, 1, 64, 320), (260, 2, 64, 140),
+                                         (256, 4, 128, 70), (270, 3, 64, 100), (257, 1, 128, 300)])
 def test_attention_many_queries_bitexact(gpu, oracle, rt, f16, T, slots, D, C):
-    """Prompt-like batches (T >= 16 rows: four queries per workgroup): rows of
-    one sequence at consecutive positions (the causal prefill), and rows of
-    several slots interleaved (slot starts inside an 8-key block of the value
-    cache when C is not a multiple of 8), against the C restatement bit for
-    bit."""
+    """Prompt-like batches (T >= 16 rows: four queries per workgroup; from
+    256 rows a key per lane for the scores and eight queries' chains a lane
+    for the weighted sum): rows of one sequence at consecutive positions (the
+    causal prefill), and rows of several slots interleaved (slot starts
+    inside an 8-key block of the value cache when C is not a multiple of 8;
+    a workgroup's queries then see different first entries), against the C
+    restatement bit for bit."""
     H, Hkv = 4, 2
     rng = np.random.default_rng(T + slots + D)
     L = slots * C
