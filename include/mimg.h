@@ -301,8 +301,8 @@ int mimg_matmul_a8_quantized_swiglu_dev(const uint64_t *w, const float *x, int64
 /* The q, k, v products (w = {q, k, v}) of 4 to 8 activation rows already
  * quantized into ws (blocks of 256), then rope.v1 on q and k and the cache
  * scatter of k and v at cache_index[t] of each row t (reference
- * interp/fast.go:507-557, importer/llama.go:489-503), in two launches (q
- * with k, then v) instead of four: bit for bit
+ * interp/fast.go:507-557, importer/llama.go:489-503), in one launch
+ * instead of four: bit for bit
  * mimg_matmul_a8_quantized_group_dev then mimg_rope_kv_dev, with q written
  * to q [rows, heads, d] and k and v to the caches only. Returns
  * MIMG_NOT_HANDLED (nothing launched) outside 4..8 rows, block 256, d 64 or

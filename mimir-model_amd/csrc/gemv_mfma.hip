@@ -343,21 +343,19 @@ __device__ __forceinline__ void mf_store_v(const MfmaArgs& A, int row, int64_t p
     }
 }
 
-// Q4_K fits 5 waves per SIMD (at most 102 registers) with one block ahead.
-template <uint32_t DT, int NW, int RD = 0>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K ? 5 : 1)))
-void gemv_a8k_mfma_kernel(MfmaArgs A) {
+// Workgroup `bid` of the launch's tiles of A (its 16 rows of one matrix).
+template <uint32_t DT, int NW, int RD>
+__device__ __forceinline__ void mfma_tile(const MfmaArgs& A, int bid, uint8_t* smem) {
     using S = MfWave<DT>;
     constexpr int MF_T = 64 * NW;
-    extern __shared__ __align__(16) uint8_t smem[];
     int mi = 0;
-    if (A.nmat > 1 && (int)blockIdx.x >= A.mat[1].tile0) mi = 1;
-    if (A.nmat > 2 && (int)blockIdx.x >= A.mat[2].tile0) mi = 2;
+    if (A.nmat > 1 && bid >= A.mat[1].tile0) mi = 1;
+    if (A.nmat > 2 && bid >= A.mat[2].tile0) mi = 2;
     const MfmaMat P = mi == 0 ? A.mat[0] : mi == 1 ? A.mat[1] : A.mat[2];
     const int t = threadIdx.x, l = t & 63, ar = l & 15, G = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: the block loop is scalar
     const int nb = A.nb, M = A.M, N = P.N;
-    const int tile = (int)blockIdx.x - P.tile0, row0 = tile * MF_ROWS;
+    const int tile = bid - P.tile0, row0 = tile * MF_ROWS;
     const bool epi = RD != 0 && P.kind != MF_PLAIN;  // a decoder epilogue (uniform)
     auto rowof = [&](int r) { return min(mf_row<RD>(A, P, tile, r), N - 1); };
     constexpr int TW = DT == DT_Q4_K ? 2 : 1;  // table words per entry
@@ -593,6 +591,25 @@ void gemv_a8k_mfma_kernel(MfmaArgs A) {
     }
 }
 
+// Q4_K fits 5 waves per SIMD (at most 102 registers) with one block ahead.
+template <uint32_t DT, int NW, int RD = 0>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K ? 5 : 1)))
+void gemv_a8k_mfma_kernel(MfmaArgs A) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    mfma_tile<DT, NW, RD>(A, (int)blockIdx.x, smem);
+}
+
+// q and k (rope; k to the key cache) and v (to the value cache) in one
+// launch: workgroups below `split` take QK's tiles, the others V's, four
+// waves each. Both parts are latency-bound on their own (8B at 8 rows: q+k
+// 320 workgroups, v 64), so one launch saves the second one's ramp and drain.
+template <uint32_t DT0, uint32_t DT1, int RD>
+__global__ __launch_bounds__(256) void gemv_a8k_mfma_qkv_kernel(MfmaArgs QK, MfmaArgs V, int split) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    if ((int)blockIdx.x < split) mfma_tile<DT0, 4, RD>(QK, (int)blockIdx.x, smem);
+    else mfma_tile<DT1, 4, RD>(V, (int)blockIdx.x - split, smem);
+}
+
 // Waves per workgroup: 4, or for Q6_K 12 while the grid holds fewer than
 // 4096 waves (16 per CU) and K has 16 blocks or more, else 8. Measured at
 // the llama-8B shapes and 8 rows: Q4_K is fastest at 4 whatever the grid
@@ -666,8 +683,7 @@ hipError_t launch_gemv_a8k_mfma(const DevWeight* const* ws, int nmat, const ActP
     return hipGetLastError();
 }
 
-// q, k (rope) and v (cache scatter) at 2..8 activation rows: two launches,
-// q and k together, then v.
+// q, k (rope) and v (cache scatter) at 2..8 activation rows: one launch.
 bool gemv_mfma_qkv_ok(const DevWeight* const* ws, int64_t rows, int heads, int kv_heads, int d, int rotary) {
     if ((d != 64 && d != 128) || rotary <= 0 || rotary % 2 || rotary > d) return false;
     if (ws[0]->n != (int64_t)heads * d || ws[1]->n != (int64_t)kv_heads * d || ws[2]->n != (int64_t)kv_heads * d)
@@ -675,23 +691,29 @@ bool gemv_mfma_qkv_ok(const DevWeight* const* ws, int64_t rows, int heads, int k
     return gemv_mfma_ok(ws, 2, rows) && gemv_mfma_ok(ws + 2, 1, rows);
 }
 
-template <int RD>
-static hipError_t launch_mfma_epi(MfmaArgs A, uint32_t dt, hipStream_t stream) {
+// Sets the parts' first tiles; returns the launch's tile count.
+static int mf_tiles(MfmaArgs& A) {
     int tiles = 0;
     for (int i = 0; i < A.nmat; i++) {
         A.mat[i].tile0 = tiles;
         tiles += (A.mat[i].N + MF_ROWS - 1) / MF_ROWS;
     }
-    const int nw = mf_waves(dt, tiles, A.nb);
-    const size_t lds = mf_lds(dt, A.nb, A.M, nw);
-    const dim3 grid((unsigned)tiles), block((unsigned)(64 * nw));
-    if (dt == DT_Q4_K) {
-        hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q4_K, 4, RD>), grid, block, lds, stream, A);
-    } else {
-        if (nw == 4) hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 4, RD>), grid, block, lds, stream, A);
-        else if (nw == 8) hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 8, RD>), grid, block, lds, stream, A);
-        else hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 12, RD>), grid, block, lds, stream, A);
-    }
+    return tiles;
+}
+
+template <int RD>
+static hipError_t launch_mfma_qkv(MfmaArgs QK, MfmaArgs V, uint32_t dt0, uint32_t dt1, hipStream_t stream) {
+    const int split = mf_tiles(QK), tiles = split + mf_tiles(V);
+    const size_t lds = std::max(mf_lds(dt0, QK.nb, QK.M, 4), mf_lds(dt1, V.nb, V.M, 4));
+    const dim3 grid((unsigned)tiles), block(256);
+    if (dt0 == DT_Q4_K && dt1 == DT_Q4_K)
+        hipLaunchKernelGGL((gemv_a8k_mfma_qkv_kernel<DT_Q4_K, DT_Q4_K, RD>), grid, block, lds, stream, QK, V, split);
+    else if (dt0 == DT_Q4_K)
+        hipLaunchKernelGGL((gemv_a8k_mfma_qkv_kernel<DT_Q4_K, DT_Q6_K, RD>), grid, block, lds, stream, QK, V, split);
+    else if (dt1 == DT_Q4_K)
+        hipLaunchKernelGGL((gemv_a8k_mfma_qkv_kernel<DT_Q6_K, DT_Q4_K, RD>), grid, block, lds, stream, QK, V, split);
+    else
+        hipLaunchKernelGGL((gemv_a8k_mfma_qkv_kernel<DT_Q6_K, DT_Q6_K, RD>), grid, block, lds, stream, QK, V, split);
     return hipGetLastError();
 }
 
@@ -701,10 +723,11 @@ hipError_t launch_gemv_a8k_mfma_qkv(const DevWeight* const* ws, const ActPtrs& a
                                     int interleaved, int64_t context, void* kc, void* vc, int f16,
                                     hipStream_t stream) {
     if (!gemv_mfma_qkv_ok(ws, rows, heads, kv_heads, d, rotary)) return hipErrorInvalidValue;
+    MfmaArgs AP[2];
     for (int part = 0; part < 2; part++) {
         const int nmat = part == 0 ? 2 : 1;
         const DevWeight* const* wp = ws + (part == 0 ? 0 : 2);
-        MfmaArgs A;
+        MfmaArgs& A = AP[part];
         A.nmat = nmat;
         A.rb = wp[0]->row_bytes;
         A.nb = (int)(wp[0]->k / 256);
@@ -734,10 +757,9 @@ hipError_t launch_gemv_a8k_mfma_qkv(const DevWeight* const* ws, const ActPtrs& a
         A.C = context;
         A.kc = kc;
         A.vc = vc;
-        const hipError_t e = d == 64 ? launch_mfma_epi<64>(A, wp[0]->dt, stream) : launch_mfma_epi<128>(A, wp[0]->dt, stream);
-        if (e != hipSuccess) return e;
     }
-    return hipSuccess;
+    return d == 64 ? launch_mfma_qkv<64>(AP[0], AP[1], ws[0]->dt, ws[2]->dt, stream)
+                   : launch_mfma_qkv<128>(AP[0], AP[1], ws[0]->dt, ws[2]->dt, stream);
 }
 
 }  // namespace mimg

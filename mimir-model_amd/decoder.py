@@ -240,7 +240,7 @@ class Decoder:
     def _qkv_rope_rows(self, l, resid, qkv, qkv_b, T, pos, cidx):
         """4..8 rows with 8-bit activations of blocks of 256: x += resid and
         the quantized rms_norm (one launch), then the q, k, v products with
-        rope and the cache scatter in their epilogues (two launches). False
+        rope and the cache scatter in their epilogues (one launch). False
         (nothing launched) where the library has no such launch."""
         c, s = self.c, self.stream.handle
         p = f"blk.{l}."

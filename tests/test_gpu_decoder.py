@@ -817,6 +817,7 @@ _ROPE_QKV_ROWS = {
     "partial_b6": (6, 1024, 16, 4, 64, 32, False, False, 16, None),
     "refused_b8": (8, 1024, 8, 8, 128, 128, True, True, 16, "huge"),
     "q6k_qk_b7": (7, 1024, 8, 2, 64, 64, True, True, 16, "q6k"),
+    "q4k_v_b8": (8, 1024, 8, 2, 128, 128, True, True, 16, "q4kv"),
 }
 
 
@@ -827,14 +828,15 @@ def test_qkv_rope_kv_rows_equal_separate_calls(gpu, oracle, rt, name):
     bit for bit matmul_a8_quantized_group_dev then rope_kv_dev, rows in
     different slots (one cache index past the cache), adjacent-pair and
     half rotation, a partial rotary span, biases, f16/f32 caches, a refused
-    activation row and Q6_K q/k."""
+    activation row, Q6_K q/k and Q4_K v (one launch, q/k and v of either
+    dtype)."""
     T, K, H, Hkv, D, rot, inter, f16, C, case = _ROPE_QKV_ROWS[name]
     rng = np.random.default_rng(T * K + H + D)
     x = rng.standard_normal((T, K)).astype(np.float32)
     if case == "huge":
         x[3, 17] = np.float32(5e18)
     qk_dt = Q6_K if case == "q6k" else Q4_K
-    specs = [(qk_dt, H * D), (qk_dt, Hkv * D), (Q6_K, Hkv * D)]
+    specs = [(qk_dt, H * D), (qk_dt, Hkv * D), (Q4_K if case == "q4kv" else Q6_K, Hkv * D)]
     W = [gpu.Weight(oracle.synthetic_weight(dt, n, K, seed=70 + i), dt, n, K) for i, (dt, n) in enumerate(specs)]
     bias = [rng.standard_normal(n).astype(np.float32) if case == "bias" else None for _, n in specs]
     dbs = [dev(rt, b) if b is not None else None for b in bias]
