@@ -285,15 +285,17 @@ int mimg_rms_norm_linear_a8_group_dev(const uint64_t *w, int count, const float 
                                       const float *scale, float eps, float *x_out, const float *const *bias,
                                       float *const *y, void *stream);
 
-/* The gate and up products of the FFN (w = {gate, up}) on one row of
+/* The gate and up products of the FFN (w = {gate, up}) on 1 to 8 rows of
  * activations already quantized into ws, and swiglu.v1 (reference
  * interp/fast.go:487-498, SiluMulF32 over the pieces of parallel() with
- * GOMAXPROCS = procs) of the two, in one launch: out[n] = swiglu(gate[n],
- * up[n]), bit for bit mimg_matmul_a8_quantized_group_dev then
- * mimg_swiglu_dev; the products themselves are not written. bias may be
- * NULL or hold NULLs. Returns MIMG_NOT_HANDLED (nothing launched) unless
- * rows is 1, block is 256 and both weights are Q4_K of one shape with N a
- * multiple of 4. No reference counterpart beyond the ops it equals. */
+ * GOMAXPROCS = procs, over the flattened [rows, N] products) of the two, in
+ * one launch: out[t][n] = swiglu(gate[t][n], up[t][n]), bit for bit
+ * mimg_matmul_a8_quantized_group_dev then mimg_swiglu_dev of rows*N
+ * elements; the products themselves are not written. bias may be NULL or
+ * hold NULLs. Returns MIMG_NOT_HANDLED (nothing launched) unless block is
+ * 256, both weights are Q4_K of one shape and N is a multiple of 4 (one
+ * row) or 8 (2..8 rows). No reference counterpart beyond the ops it
+ * equals. */
 int mimg_matmul_a8_quantized_swiglu_dev(const uint64_t *w, const float *x, int64_t rows, const float *const *bias,
                                         int block, float *out, int procs, const void *ws, uint64_t ws_bytes,
                                         void *stream);

@@ -90,6 +90,10 @@ struct MfmaArgs {
     int64_t C;
     void* kc;
     void* vc;
+    // swiglu in the epilogue (mat[0] gate, mat[1] up): sw [M][N] = swiglu.v1
+    // of the flattened [M][N] products with the reference's pieces
+    float* sw;
+    int64_t sw_total, sw_chunk;
 };
 
 // Row of local row r of tile `tile`: q and k rows in rotation pairs (local
@@ -150,22 +154,22 @@ struct MfWave {
 };
 
 // A lane's part of every block's loads: chunk q = 64i + lane (clamped to
-// the last) of row r = q / CPR (rows past N read the last), stored at LDS
+// the last) of local row r = q / CPR (first byte rowptr(r)), stored at LDS
 // byte 16 (RST r + j), j = q % CPR. Computed once per workgroup.
 template <uint32_t DT>
 struct MfLanes {
     const uint8_t* row[MfWave<DT>::NLD];  // the row's first byte (+16j for Q4_K)
     uint32_t j16[MfWave<DT>::NLD];        // 16j (Q6_K)
     uint32_t lds[MfWave<DT>::NLD];
-    template <class RowOf>
-    __device__ MfLanes(const uint8_t* W, int64_t rb, RowOf rowof) {
+    template <class RowPtr>
+    __device__ MfLanes(RowPtr rowptr) {
         using S = MfWave<DT>;
         const int l = threadIdx.x & 63;
 #pragma unroll
         for (int i = 0; i < S::NLD; i++) {
             const int q = min(64 * i + l, S::CH - 1);
             const int r = q / S::CPR, j = q - S::CPR * r;
-            row[i] = W + (int64_t)rowof(r) * rb + (DT == DT_Q4_K ? 16 * j : 0);
+            row[i] = rowptr(r) + (DT == DT_Q4_K ? 16 * j : 0);
             j16[i] = 16 * j;
             lds[i] = 16 * (S::RST * r + j);
         }
@@ -343,21 +347,27 @@ __device__ __forceinline__ void mf_store_v(const MfmaArgs& A, int row, int64_t p
     }
 }
 
-// Workgroup `bid` of the launch's tiles of A (its 16 rows of one matrix).
-template <uint32_t DT, int NW, int RD>
+// Workgroup `bid` of the launch's tiles of A (its 16 rows of one matrix;
+// SW: rows 8 bid .. 8 bid + 7 of gate as local rows 0..7 and the same rows
+// of up as local rows 8..15, swiglu of each pair in the epilogue).
+template <uint32_t DT, int NW, int RD, bool SW = false>
 __device__ __forceinline__ void mfma_tile(const MfmaArgs& A, int bid, uint8_t* smem) {
+    static_assert(!SW || (DT == DT_Q4_K && RD == 0), "swiglu epilogue: Q4_K gate and up, no rope");
     using S = MfWave<DT>;
     constexpr int MF_T = 64 * NW;
-    int mi = 0;
-    if (A.nmat > 1 && bid >= A.mat[1].tile0) mi = 1;
-    if (A.nmat > 2 && bid >= A.mat[2].tile0) mi = 2;
+    int mi = 0;  // (SW: mat[0], gate; up is matof's)
+    if (!SW && A.nmat > 1 && bid >= A.mat[1].tile0) mi = 1;
+    if (!SW && A.nmat > 2 && bid >= A.mat[2].tile0) mi = 2;
     const MfmaMat P = mi == 0 ? A.mat[0] : mi == 1 ? A.mat[1] : A.mat[2];
     const int t = threadIdx.x, l = t & 63, ar = l & 15, G = l >> 4;
     const int w = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: the block loop is scalar
     const int nb = A.nb, M = A.M, N = P.N;
     const int tile = bid - P.tile0, row0 = tile * MF_ROWS;
     const bool epi = RD != 0 && P.kind != MF_PLAIN;  // a decoder epilogue (uniform)
-    auto rowof = [&](int r) { return min(mf_row<RD>(A, P, tile, r), N - 1); };
+    // local row r: its row of its matrix (clamped), the matrix, in range
+    auto rowof = [&](int r) { return SW ? min(tile * 8 + (r & 7), N - 1) : min(mf_row<RD>(A, P, tile, r), N - 1); };
+    auto matof = [&](int r) -> const MfmaMat& { return SW && r >= 8 ? A.mat[1] : P; };
+    auto inrange = [&](int r) { return SW ? tile * 8 + (r & 7) < N : row0 + r < N; };
     constexpr int TW = DT == DT_Q4_K ? 2 : 1;  // table words per entry
     uint8_t* wl = smem + w * S::LBYTES;                               // this wave's staging
     int* tab = (int*)(smem + NW * S::LBYTES);                         // [nb][16][M][TW]
@@ -379,8 +389,9 @@ __device__ __forceinline__ void mfma_tile(const MfmaArgs& A, int bid, uint8_t* s
     int fm = ft - fr * M;
     asm volatile("v_mov_b32 %0, %1" : "=v"(fm) : "v"(fm));  // a vector index: ok[] through the vector cache
     const int frow = rowof(fr);
-    const int wr = P.wref[frow], okm = A.ok[fm];
-    const float bias = P.bias ? P.bias[frow] : 0.f;
+    const MfmaMat& FM = matof(fr);
+    const int wr = FM.wref[frow], okm = A.ok[fm];
+    const float bias = FM.bias ? FM.bias[frow] : 0.f;
     const int64_t pidx = RD != 0 && P.kind != MF_PLAIN ? A.cidx[fm] : 0;  // (epilogues: cache index of row fm)
     // (rope: this lane's position and frequency, loaded before the weights)
     const bool rot_lane = RD != 0 && (P.kind == MF_ROPE_Q || P.kind == MF_ROPE_K) && t < MF_ROWS * M;
@@ -393,7 +404,7 @@ __device__ __forceinline__ void mfma_tile(const MfmaArgs& A, int bid, uint8_t* s
     const int64_t rot_pos = rot_on ? A.pos[fm] : 0;
     const double rot_f = rot_on ? A.inv_freq[rot_i] : 0.0;
 
-    const MfLanes<DT> L(P.W, A.rb, rowof);
+    const MfLanes<DT> L([&](int r) { return matof(r).W + (int64_t)rowof(r) * A.rb; });
     // rope: the rotation of chain lane t's (row t/M, activation row t%M),
     // computed once the first weights are requested
     float rc = 1.f, rs = 0.f;
@@ -529,7 +540,7 @@ __device__ __forceinline__ void mfma_tile(const MfmaArgs& A, int bid, uint8_t* s
     // The serial float chain, one lane per (weight row, activation row).
     if (t < MF_ROWS * M) {
         const int r = t / M, m = t - r * M, row = rowof(r);
-        if (row0 + r < N && !flag) {
+        if (inrange(r) && !flag) {
             float tot = 0.f, off = 0.f;
             // (unrolled: the table reads of eight blocks are issued together,
             // so only the fma chain itself is serial)
@@ -542,9 +553,9 @@ __device__ __forceinline__ void mfma_tile(const MfmaArgs& A, int bid, uint8_t* s
                 if constexpr (DT == DT_Q4_K) off = __builtin_fmaf((float)e[1], f16_to_f32(bits >> 16) * dx, off);
             }
             float res = DT == DT_Q4_K ? tot - off : tot;
-            if (P.bias) res += bias;
+            if (FM.bias) res += bias;  // (FM: this lane's row's matrix, fr == r)
             if (epi && P.kind == MF_STORE_V) mf_store_v<RD>(A, row, pidx, res);
-            else if (epi) yres[r * M + m] = res;
+            else if (epi || SW) yres[r * M + m] = res;
             else P.y[(int64_t)m * N + row] = res;
         }
     }
@@ -552,14 +563,24 @@ __device__ __forceinline__ void mfma_tile(const MfmaArgs& A, int bid, uint8_t* s
     const int g = t >> 3;
     for (int qq = g; qq < MF_ROWS * M; qq += MF_T / 8) {
         const int r = qq / M, m = qq - r * M, row = rowof(r);
-        if (row0 + r < N && refl[qq]) {
-            float res = f32dot_g8<DT>(P.W + (int64_t)row * A.rb, A.x + (int64_t)m * A.K, A.K, A.fused != 0);
-            if (P.bias) res += P.bias[row];
+        if (inrange(r) && refl[qq]) {
+            const MfmaMat& RM = matof(r);
+            float res = f32dot_g8<DT>(RM.W + (int64_t)row * A.rb, A.x + (int64_t)m * A.K, A.K, A.fused != 0);
+            if (RM.bias) res += RM.bias[row];
             if ((t & 7) == 0) {
                 if (epi && P.kind == MF_STORE_V) mf_store_v<RD>(A, row, A.cidx[m], res);
-                else if (epi) yres[qq] = res;
+                else if (epi || SW) yres[qq] = res;
                 else P.y[(int64_t)m * N + row] = res;
             }
+        }
+    }
+    if constexpr (SW) {
+        // every (row, activation row) result of gate and up is in yres: one lane a pair
+        __syncthreads();
+        if (t < 8 * M) {
+            const int r = t / M, m = t - r * M, n = tile * 8 + r;
+            const int64_t i = (int64_t)m * N + n;
+            if (n < N) A.sw[i] = swiglu_at(yres[r * M + m], yres[(r + 8) * M + m], i, A.sw_total, A.sw_chunk);
         }
     }
     if constexpr (RD != 0) {
@@ -592,11 +613,11 @@ __device__ __forceinline__ void mfma_tile(const MfmaArgs& A, int bid, uint8_t* s
 }
 
 // Q4_K fits 5 waves per SIMD (at most 102 registers) with one block ahead.
-template <uint32_t DT, int NW, int RD = 0>
+template <uint32_t DT, int NW, int RD = 0, bool SW = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(DT == DT_Q4_K ? 5 : 1)))
 void gemv_a8k_mfma_kernel(MfmaArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
-    mfma_tile<DT, NW, RD>(A, (int)blockIdx.x, smem);
+    mfma_tile<DT, NW, RD, SW>(A, (int)blockIdx.x, smem);
 }
 
 // q and k (rope; k to the key cache) and v (to the value cache) in one
@@ -670,6 +691,8 @@ hipError_t launch_gemv_a8k_mfma(const DevWeight* const* ws, int nmat, const ActP
     A.rotary = A.interleaved = A.f16 = 0;
     A.C = 0;
     A.kc = A.vc = nullptr;
+    A.sw = nullptr;
+    A.sw_total = A.sw_chunk = 0;
     const int nw = mf_waves(w.dt, tiles, A.nb);
     const size_t lds = mf_lds(w.dt, A.nb, A.M, nw);
     const dim3 grid((unsigned)tiles), block((unsigned)(64 * nw));
@@ -680,6 +703,55 @@ hipError_t launch_gemv_a8k_mfma(const DevWeight* const* ws, int nmat, const ActP
         else if (nw == 8) hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 8>), grid, block, lds, stream, A);
         else hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q6_K, 12>), grid, block, lds, stream, A);
     }
+    return hipGetLastError();
+}
+
+// gate and up at 2..8 activation rows with swiglu in the epilogue (Q4_K,
+// N % 8 == 0): a workgroup per 8 rows of each, four waves.
+bool gemv_mfma_swiglu_ok(const DevWeight& gate, const DevWeight& up, int64_t rows) {
+    if (rows < 2 || rows > 8) return false;
+    if (gate.dt != DT_Q4_K || up.dt != DT_Q4_K || gate.n != up.n || gate.k != up.k || gate.k % 256 ||
+        gate.k <= 0 || gate.n % 8 || gate.n > (1 << 30))
+        return false;
+    return mf_lds(DT_Q4_K, (int)(gate.k / 256), (int)rows, 4) <= 160 * 1024;
+}
+
+hipError_t launch_gemv_a8k_mfma_swiglu(const DevWeight& gate, const DevWeight& up, const ActPtrs& a, int64_t rows,
+                                       const float* x, const float* const* bias, float* out, int64_t total,
+                                       int64_t chunk, hipStream_t stream) {
+    if (!gemv_mfma_swiglu_ok(gate, up, rows)) return hipErrorInvalidValue;
+    MfmaArgs A;
+    A.nmat = 2;
+    A.rb = gate.row_bytes;
+    A.nb = (int)(gate.k / 256);
+    A.M = (int)rows;
+    A.K = gate.k;
+    A.q = a.q;
+    A.d32 = a.d32;
+    A.ok = a.ok;
+    A.x = x;
+    A.fused = 1;  // (the call's rows are all of it: at most 8)
+    const DevWeight* gu[3] = {&gate, &up, &up};
+    for (int i = 0; i < 3; i++) {
+        A.mat[i].W = gu[i]->data;
+        A.mat[i].wref = gu[i]->wref;
+        A.mat[i].bias = i < 2 && bias ? bias[i] : nullptr;
+        A.mat[i].y = nullptr;
+        A.mat[i].N = (int)gu[i]->n;
+        A.mat[i].tile0 = 0;
+        A.mat[i].kind = MF_PLAIN;
+    }
+    A.pos = A.cidx = nullptr;
+    A.inv_freq = nullptr;
+    A.rotary = A.interleaved = A.f16 = 0;
+    A.C = 0;
+    A.kc = A.vc = nullptr;
+    A.sw = out;
+    A.sw_total = total;
+    A.sw_chunk = chunk;
+    const size_t lds = mf_lds(DT_Q4_K, A.nb, A.M, 4);
+    hipLaunchKernelGGL((gemv_a8k_mfma_kernel<DT_Q4_K, 4, 0, true>), dim3((unsigned)(gate.n / 8)), dim3(256), lds,
+                       stream, A);
     return hipGetLastError();
 }
 
@@ -757,6 +829,8 @@ hipError_t launch_gemv_a8k_mfma_qkv(const DevWeight* const* ws, const ActPtrs& a
         A.C = context;
         A.kc = kc;
         A.vc = vc;
+        A.sw = nullptr;
+        A.sw_total = A.sw_chunk = 0;
     }
     return d == 64 ? launch_mfma_qkv<64>(AP[0], AP[1], ws[0]->dt, ws[2]->dt, stream)
                    : launch_mfma_qkv<128>(AP[0], AP[1], ws[0]->dt, ws[2]->dt, stream);

@@ -1298,7 +1298,10 @@ int mimg_matmul_a8_quantized_swiglu_dev(const uint64_t* whs, const float* x, int
         w[i] = wi;
     }
     if (rows == 0) return MIMG_OK;
-    if (rows != 1 || block != 256 || !gemv_swiglu_ok(w[0]->dw, w[1]->dw))
+    // one row: the pair kernel's epilogue; 2..8 rows: the matrix-core GEMV's
+    const bool one = rows == 1 && gemv_swiglu_ok(w[0]->dw, w[1]->dw);
+    const bool few = rows >= 2 && rows <= 8 && gemv_mfma_swiglu_ok(w[0]->dw, w[1]->dw, rows);
+    if (block != 256 || !(one || few))
         return fail(MIMG_NOT_HANDLED, "no swiglu epilogue for %lld rows, block %d, %s/%s", (long long)rows, block,
                     dt_name(w[0]->dw.dt), dt_name(w[1]->dw.dt));
     if (!x || !ws || !aligned(ws, 256)) return fail(MIMG_ERR_ARG, "null or misaligned pointer");
@@ -1309,15 +1312,20 @@ int mimg_matmul_a8_quantized_swiglu_dev(const uint64_t* whs, const float* x, int
     int64_t ns[1] = {N};
     float* ys[1] = {out};
     if ((rc = check_outputs(x, rows, K, ns, ys, 1))) return rc;
-    if ((uintptr_t)out < (uintptr_t)ws + ws_bytes && (uintptr_t)ws < (uintptr_t)out + (uint64_t)N * 4)
+    if ((uintptr_t)out < (uintptr_t)ws + ws_bytes && (uintptr_t)ws < (uintptr_t)out + (uint64_t)(rows * N) * 4)
         return fail(MIMG_ERR_ARG, "out overlaps the workspace");
-    // swiglu.v1's pieces (the reference's parallel(): GOMAXPROCS procs)
-    const int64_t total = N, wk = procs < total ? procs : total;
+    // swiglu.v1's pieces over the flattened [rows, N] products (the
+    // reference's parallel(): GOMAXPROCS procs)
+    const int64_t total = rows * N, wk = procs < total ? procs : total;
     int64_t chunk = total;
     if (wk > 1) chunk = total / (wk * 8) > 1 ? total / (wk * 8) : 1;
     const float* bs[2] = {bias ? bias[0] : nullptr, bias ? bias[1] : nullptr};
-    HIP_TRY(launch_gemv_a8k_swiglu(w[0]->dw, w[1]->dw, act_ptrs((void*)ws, l), x, bs, out, total, chunk,
-                                   (hipStream_t)stream));
+    if (one)
+        HIP_TRY(launch_gemv_a8k_swiglu(w[0]->dw, w[1]->dw, act_ptrs((void*)ws, l), x, bs, out, total, chunk,
+                                       (hipStream_t)stream));
+    else
+        HIP_TRY(launch_gemv_a8k_mfma_swiglu(w[0]->dw, w[1]->dw, act_ptrs((void*)ws, l), rows, x, bs, out, total,
+                                            chunk, (hipStream_t)stream));
     return MIMG_OK;
 }
 

@@ -71,6 +71,10 @@ hipError_t launch_gemv_a8k_mfma(const DevWeight* const* ws, int nmat, const ActP
 // in the epilogue: out[n] = swiglu(gate[n], up[n]) with the reference's
 // pieces of `chunk` elements of `total` (gemv_kquant.hip).
 bool gemv_swiglu_ok(const DevWeight& gate, const DevWeight& up);
+bool gemv_mfma_swiglu_ok(const DevWeight& gate, const DevWeight& up, int64_t rows);
+hipError_t launch_gemv_a8k_mfma_swiglu(const DevWeight& gate, const DevWeight& up, const ActPtrs& a, int64_t rows,
+                                       const float* x, const float* const* bias, float* out, int64_t total,
+                                       int64_t chunk, hipStream_t stream);
 hipError_t launch_gemv_a8k_swiglu(const DevWeight& gate, const DevWeight& up, const ActPtrs& a, const float* x,
                                   const float* const* bias, float* out, int64_t total, int64_t chunk,
                                   hipStream_t stream);

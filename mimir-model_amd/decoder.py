@@ -159,8 +159,9 @@ class Decoder:
         # one row: norm, q/k/v, rope and the cache scatter in one launch
         # (until the library answers NotHandled for the shape)
         self.rope_fused = bool(fuse_rope)
-        # one row: gate/up products with swiglu in their epilogue
+        # one row, and 2..8 rows: gate/up products with swiglu in their epilogue
         self.swiglu_fused = bool(fuse_swiglu)
+        self.swiglu_rows_fused = bool(fuse_swiglu)
         # 4..8 rows: q/k/v products with rope and the cache scatter
         self.qkv_rows_fused = bool(fuse_rope)
         self.q, self.o = B(R * H * D * 4), B(R * H * D * 4)
@@ -265,33 +266,37 @@ class Decoder:
                              self.f16, s)
         return True
 
-    def _ffn_one_row(self, l):
-        """The FFN at one row with 8-bit activations of blocks of 256: x +=
-        the attention output; h = rms_norm(x) * scale quantized (one launch);
-        gate and up products with swiglu in their epilogue (one launch); the
-        quantizer on the swiglu output; down. False (nothing launched) where
-        the swiglu epilogue does not take the shape."""
+    def _ffn_rows(self, l, T):
+        """The FFN at 1..8 rows with 8-bit activations of blocks of 256: x
+        += the attention output; h = rms_norm(x) * scale quantized (one
+        launch); gate and up products with swiglu in their epilogue (one
+        launch); the quantizer on the swiglu output; down. False (nothing
+        launched) where the swiglu epilogue does not take the shape."""
         c, s = self.c, self.stream.handle
         p = f"blk.{l}."
         gate, up, down = (self.w[p + n] for n in ("ffn_gate.weight", "ffn_up.weight", "ffn_down.weight"))
         F, E = c.ffn, c.embed
-        if not (self.a8 and self.swiglu_fused and gate.dt == mimg.Q4_K and up.dt == mimg.Q4_K and
-                self._block(gate) == 256 and self._block(down) in (32, 256) and gate.n == up.n == F and F % 4 == 0
-                and E % 256 == 0 and E <= 16384 and F <= 32768 and p + "ffn_gate.bias" not in self.vec
-                and p + "ffn_up.bias" not in self.vec):
+        fused = self.swiglu_fused if T == 1 else self.swiglu_rows_fused
+        if not (self.a8 and fused and 1 <= T <= 8 and gate.dt == mimg.Q4_K and up.dt == mimg.Q4_K and
+                self._block(gate) == 256 and self._block(down) in (32, 256) and gate.n == up.n == F
+                and F % (4 if T == 1 else 8) == 0 and E % 256 == 0 and E <= 16384 and F <= 32768
+                and p + "ffn_gate.bias" not in self.vec and p + "ffn_up.bias" not in self.vec):
             return False
-        mimg.rms_norm_quant_dev(self.x.ptr, self.ao.ptr, self.vec[p + "ffn_norm.weight"].ptr, c.norm_eps, 1, E,
+        mimg.rms_norm_quant_dev(self.x.ptr, self.ao.ptr, self.vec[p + "ffn_norm.weight"].ptr, c.norm_eps, T, E,
                                 self.h.ptr, 256, self.ws.ptr, self.ws_bytes, s)
         try:
-            mimg.matmul_a8_quantized_swiglu_dev([gate, up], self.h.ptr, 1, None, 256, self.sw.ptr, self.procs,
+            mimg.matmul_a8_quantized_swiglu_dev([gate, up], self.h.ptr, T, None, 256, self.sw.ptr, self.procs,
                                                 self.ws.ptr, self.ws_bytes, s)
         except mimg.NotHandled:  # (the norm is done: the products and swiglu separately)
-            self.swiglu_fused = False
-            mimg.matmul_a8_quantized_group_dev([gate, up], self.h.ptr, 1, None, 256, [self.g.ptr, self.u.ptr],
+            if T == 1:
+                self.swiglu_fused = False
+            else:
+                self.swiglu_rows_fused = False
+            mimg.matmul_a8_quantized_group_dev([gate, up], self.h.ptr, T, None, 256, [self.g.ptr, self.u.ptr],
                                                self.ws.ptr, self.ws_bytes, s)
-            mimg.swiglu_dev(self.g.ptr, self.u.ptr, self.sw.ptr, F, self.procs, s)
-        mimg.quantize_act_dev(self.sw.ptr, 1, F, self._block(down), self.ws.ptr, self.ws_bytes, s)
-        mimg.matmul_a8_quantized_group_dev([down], self.sw.ptr, 1, None, self._block(down), [self.ao.ptr],
+            mimg.swiglu_dev(self.g.ptr, self.u.ptr, self.sw.ptr, T * F, self.procs, s)
+        mimg.quantize_act_dev(self.sw.ptr, T, F, self._block(down), self.ws.ptr, self.ws_bytes, s)
+        mimg.matmul_a8_quantized_group_dev([down], self.sw.ptr, T, None, self._block(down), [self.ao.ptr],
                                            self.ws.ptr, self.ws_bytes, s)
         return True
 
@@ -347,7 +352,7 @@ class Decoder:
                                self.cache_len, c.context, self.f16, self.o.ptr, self.att_ws.ptr, self.att_ws_bytes, s)
             self._linears([p + "attn_output.weight"], self.o.ptr, T, [self.ao.ptr])
             down = self.w[p + "ffn_down.weight"]
-            if T == 1 and self._ffn_one_row(l):
+            if T <= 8 and self._ffn_rows(l, T):
                 pass
             elif self.a8 and self._block(down) in (32, 256) and F <= 32768:
                 self._norm_linears(self.ao.ptr, p + "ffn_norm.weight", T, [p + "ffn_gate.weight", p + "ffn_up.weight"],

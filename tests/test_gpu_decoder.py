@@ -735,12 +735,19 @@ def test_rms_norm_qkv_rope_kv_equals_separate_calls(gpu, oracle, rt, name):
 
 
 _SWIGLU_FUSED = {
-    # K, N, procs, case
-    "llama8b_ffn": (4096, 14336, 16, None),
-    "procs3_tails": (1024, 1000, 3, None),  # pieces of 41 elements: f64 tails in every piece
-    "procs1": (2048, 512, 1, "bias"),
-    "refused_row": (1024, 256, 16, "huge"),
-    "refused_weight": (1024, 512, 7, "inf_scale"),
+    # K, N, procs, case, rows
+    "llama8b_ffn": (4096, 14336, 16, None, 1),
+    "procs3_tails": (1024, 1000, 3, None, 1),  # pieces of 41 elements: f64 tails in every piece
+    "procs1": (2048, 512, 1, "bias", 1),
+    "refused_row": (1024, 256, 16, "huge", 1),
+    "refused_weight": (1024, 512, 7, "inf_scale", 1),
+    # 2..8 rows (the matrix-core GEMV's epilogue; pieces over rows * N)
+    "llama8b_ffn_b8": (4096, 14336, 16, None, 8),
+    "b2_procs3_tails": (1024, 1000, 3, None, 2),  # pieces of 83: tails inside rows
+    "b5_procs1_bias": (2048, 512, 1, "bias", 5),
+    "b8_refused_row": (1024, 256, 16, "huge", 8),
+    "b4_refused_weight": (1024, 512, 7, "inf_scale", 4),
+    "b3_procs7": (1024, 136, 7, None, 3),  # 17 workgroups of 8 rows
 }
 
 
@@ -748,14 +755,14 @@ _SWIGLU_FUSED = {
 def test_matmul_swiglu_equals_group_then_swiglu(gpu, oracle, rt, name):
     """gate/up products with swiglu in the epilogue: out bit for bit
     matmul_a8_quantized_group_dev then swiglu_dev (the reference's pieces for
-    several GOMAXPROCS, f64 tails included), with biases, a refused
-    activation row and a weight row with a non-finite block scale (both on
-    the float32 path)."""
-    K, N, procs, case = _SWIGLU_FUSED[name]
-    rng = np.random.default_rng(K + N + procs)
-    x = rng.standard_normal((1, K)).astype(np.float32)
+    several GOMAXPROCS, f64 tails included), one row and 2..8 rows, with
+    biases, a refused activation row and a weight row with a non-finite
+    block scale (both on the float32 path)."""
+    K, N, procs, case, T = _SWIGLU_FUSED[name]
+    rng = np.random.default_rng(K + N + procs + T)
+    x = rng.standard_normal((T, K)).astype(np.float32)
     if case == "huge":
-        x[0, 5] = np.float32(3e18)  # above 2^60: the row is refused
+        x[T // 2, 5] = np.float32(3e18)  # above 2^60: the row is refused
     wbs = []
     for i in range(2):
         wb = oracle.synthetic_weight(Q4_K, N, K, seed=80 + i)
@@ -770,16 +777,16 @@ def test_matmul_swiglu_equals_group_then_swiglu(gpu, oracle, rt, name):
     dbs = [dev(rt, b) for b in bias] if bias else None
     s = rt.Stream()
     dx = dev(rt, x)
-    wsb = gpu.a8_workspace_bytes(1, K)
+    wsb = gpu.a8_workspace_bytes(T, K)
     ws = rt.DeviceBuffer(wsb)
-    gpu.quantize_act_dev(dx.ptr, 1, K, 256, ws.ptr, wsb, s.handle)
-    out = rt.DeviceBuffer(N * 4)
-    gpu.matmul_a8_quantized_swiglu_dev(W, dx.ptr, 1, [b.ptr for b in dbs] if dbs else None, 256, out.ptr, procs,
+    gpu.quantize_act_dev(dx.ptr, T, K, 256, ws.ptr, wsb, s.handle)
+    out = rt.DeviceBuffer(T * N * 4)
+    gpu.matmul_a8_quantized_swiglu_dev(W, dx.ptr, T, [b.ptr for b in dbs] if dbs else None, 256, out.ptr, procs,
                                        ws.ptr, wsb, s.handle)
-    g, u, want = rt.DeviceBuffer(N * 4), rt.DeviceBuffer(N * 4), rt.DeviceBuffer(N * 4)
-    gpu.matmul_a8_quantized_group_dev(W, dx.ptr, 1, [b.ptr for b in dbs] if dbs else None, 256, [g.ptr, u.ptr],
+    g, u, want = rt.DeviceBuffer(T * N * 4), rt.DeviceBuffer(T * N * 4), rt.DeviceBuffer(T * N * 4)
+    gpu.matmul_a8_quantized_group_dev(W, dx.ptr, T, [b.ptr for b in dbs] if dbs else None, 256, [g.ptr, u.ptr],
                                       ws.ptr, wsb, s.handle)
-    gpu.swiglu_dev(g.ptr, u.ptr, want.ptr, N, procs, s.handle)
+    gpu.swiglu_dev(g.ptr, u.ptr, want.ptr, T * N, procs, s.handle)
     s.sync()
     a, b = out.download(np.float32), want.download(np.float32)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), np.flatnonzero(a.view(np.uint32) != b.view(np.uint32))[:8]
@@ -791,21 +798,23 @@ def test_matmul_swiglu_equals_group_then_swiglu(gpu, oracle, rt, name):
 
 def test_matmul_swiglu_not_handled(gpu, oracle, rt):
     """Shapes without the swiglu epilogue are refused before any launch:
-    two rows, blocks of 32, a Q6_K weight, mismatched shapes."""
+    nine rows, blocks of 32, a Q6_K weight, mismatched shapes, N a multiple
+    of 4 but not of 8 at two rows."""
     s = rt.Stream()
     K = 512
     q4 = [gpu.Weight(oracle.synthetic_weight(Q4_K, 64, K, seed=9 + i), Q4_K, 64, K) for i in range(2)]
     q6 = gpu.Weight(oracle.synthetic_weight(Q6_K, 64, K, seed=11), Q6_K, 64, K)
     q4b = gpu.Weight(oracle.synthetic_weight(Q4_K, 32, K, seed=12), Q4_K, 32, K)
-    x = rt.DeviceBuffer(2 * K * 4)
-    wsb = gpu.a8_workspace_bytes(2, K)
-    ws, out = rt.DeviceBuffer(wsb), rt.DeviceBuffer(64 * 4 * 2)
-    for ws_pair, rows, block in (((q4[0], q4[1]), 2, 256), ((q4[0], q4[1]), 1, 32), ((q4[0], q6), 1, 256),
-                                 ((q4[0], q4b), 1, 256)):
+    q4c = [gpu.Weight(oracle.synthetic_weight(Q4_K, 36, K, seed=13 + i), Q4_K, 36, K) for i in range(2)]
+    x = rt.DeviceBuffer(9 * K * 4)
+    wsb = gpu.a8_workspace_bytes(9, K)
+    ws, out = rt.DeviceBuffer(wsb), rt.DeviceBuffer(64 * 4 * 9)
+    for ws_pair, rows, block in (((q4[0], q4[1]), 9, 256), ((q4[0], q4[1]), 1, 32), ((q4[0], q6), 1, 256),
+                                 ((q4[0], q4b), 1, 256), ((q4[0], q6), 4, 256), (tuple(q4c), 2, 256)):
         with pytest.raises(gpu.NotHandled):
             gpu.matmul_a8_quantized_swiglu_dev(list(ws_pair), x.ptr, rows, None, block, out.ptr, 16, ws.ptr, wsb,
                                                s.handle)
-    for w in q4 + [q6, q4b]:
+    for w in q4 + [q6, q4b] + q4c:
         w.release()
 
 
