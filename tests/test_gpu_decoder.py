@@ -157,13 +157,51 @@ def test_attention_long_context_bitexact(gpu, oracle, rt, f16, C, D):
 @pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
 @pytest.mark.parametrize("T,H,Hkv,D,slots,C", [(2, 32, 8, 128, 2, 1100), (3, 16, 2, 64, 1, 3000), (8, 32, 8, 128, 8, 300),
                                                (4, 8, 4, 64, 2, 1100), (1, 32, 8, 128, 1, 2100),
-                                               (2, 32, 8, 128, 2, 400)])
+                                               (2, 32, 8, 128, 2, 400), (4, 16, 2, 64, 2, 600),
+                                               (2, 4, 4, 128, 1, 300), (3, 8, 4, 64, 1, 700), (1, 32, 8, 128, 1, 768)])
 def test_attention_grouped_heads_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, slots, C):
     """Past 256 keys at few queries, when tiles x kv heads x queries reaches
     256 workgroups, the scores of the query heads that share a kv head come
-    from one workgroup (groups of 2, 4 and 8 heads, slots; the last case stays
-    per head): bit for bit the restatement."""
+    from one workgroup (groups of 2, 4 and 8 heads, slots, the 8B decode
+    shape at 768 keys; one head per kv head and short grids stay per head):
+    bit for bit the restatement."""
     test_kv_store_and_attention_bitexact(gpu, oracle, rt, f16, T, H, Hkv, D, slots, C=C)
+
+
+@pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
+@pytest.mark.parametrize("T,H,Hkv,D,C,sign", [(2, 32, 8, 128, 300, 1), (3, 8, 2, 64, 520, -1), (1, 8, 2, 128, 700, 1)])
+def test_attention_nonfinite_key(gpu, oracle, rt, f16, T, H, Hkv, D, C, sign):
+    """A key with an infinite element in one kv head: that key's scores are
+    +inf (its query heads give NaN) or -inf (its exponential is 0 and the
+    heads stay finite), as the reference computes them; every other head
+    keeps the restatement's bits."""
+    rng = np.random.default_rng(T * 7 + H + D + C)
+    cdt = np.float16 if f16 else np.float32
+    wk = (rng.standard_normal((Hkv, C, D)) * 2).astype(cdt)
+    wv = rng.standard_normal((Hkv, C, D)).astype(cdt)
+    wk[1, 5, 3] = sign * np.inf
+    q = rng.standard_normal((T, H, D)).astype(np.float32)
+    q[:, :, 3] = np.abs(q[:, :, 3]) + 0.25  # the key's scores are sign * inf in every head of kv head 1
+    cidx = np.array([C - 1 - 3 * t for t in range(T)], np.int64)
+    kc, vc = dev(rt, wk), dev(rt, gpu.pack_vcache(wv))
+    dq, dc = dev(rt, q), dev(rt, cidx)
+    out = rt.DeviceBuffer(q.nbytes)
+    wsb = gpu.attention_workspace_bytes(T, H, C)
+    ws = rt.DeviceBuffer(wsb)
+    s = rt.Stream()
+    gpu.attention_dev(dq.ptr, kc.ptr, vc.ptr, dc.ptr, None, T, H, Hkv, D, C, C, f16, out.ptr, ws.ptr, wsb, s.handle)
+    s.sync()
+    want = oracle.attention(q, wk, wv, cidx, None)
+    got = out.download(np.float32).reshape(T, H, D)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
+    G = H // Hkv
+    if sign > 0:  # the largest score is +inf: NaN
+        assert np.isnan(got[:, G:2 * G]).all()
+    else:  # -inf: the key's exponential is 0
+        assert not np.isnan(got).any()
+    assert not np.isnan(got[:, :G]).any()
 
 
 @pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
