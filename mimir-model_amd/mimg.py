@@ -357,9 +357,10 @@ def rms_norm_linear_a8_group_dev(weights, x_ptr, resid_ptr, scale_ptr, eps, x_ou
 
 
 def matmul_a8_quantized_swiglu_dev(weights, x_ptr, rows, bias_ptrs, block, out_ptr, procs, ws_ptr, ws_bytes, stream):
-    """gate/up products of activations already quantized into ws, and
-    swiglu of the two into out, in one launch; raises NotHandled where the
-    fused launch does not apply (then make the group and swiglu calls)."""
+    """gate/up products of 1..8 rows of activations already quantized into
+    ws, and swiglu of the two into out [rows, N], in one launch; raises
+    NotHandled where the fused launch does not apply (then make the group
+    and swiglu calls)."""
     hs = (_U64 * 2)(*[w.handle for w in weights])
     bs = None if bias_ptrs is None else (_P * 2)(*[_P(p) if p else None for p in bias_ptrs])
     _check(load().mimg_matmul_a8_quantized_swiglu_dev(hs, _P(x_ptr), rows, bs, block, _P(out_ptr), procs, _P(ws_ptr),
