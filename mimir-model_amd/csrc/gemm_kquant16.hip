@@ -164,6 +164,63 @@ __device__ __forceinline__ void gemm_issue_block(const GemmArgs& A, int n0, int 
     }
 }
 
+// A thread's copy sources for block 0, fixed over the blocks (block b adds
+// b times the block size), and the wave index as a scalar, so that each
+// block's copies cost one 64-bit add each (and the Q6_K realignment) and
+// their LDS bases are scalar: gemm_issue_block's copies, in the same order
+// to the same LDS bytes.
+template <uint32_t DT, class C>
+struct KsCopy {
+    using L = GemmLayout<DT, C>;
+    const uint8_t* w[L::WDMA];  // Q4_K: the chunk's bytes in block 0; Q6_K: the row's block 0
+    uint32_t j4[L::WDMA];       // Q6_K: the dword within the aligned block
+    const int8_t* a[C::ACH];
+    const float* dx;
+    int wave;
+    __device__ KsCopy(const GemmArgs& A, int n0, int m0) {
+        const int t = threadIdx.x;
+        wave = __builtin_amdgcn_readfirstlane(t >> 6);
+#pragma unroll
+        for (int i = 0; i < L::WDMA; i++) {
+            if constexpr (DT == DT_Q4_K) {
+                const int c = min(C::T * i + t, C::BN * 9 - 1);
+                const int r = c / 9, j = c - 9 * r;
+                w[i] = A.W + (int64_t)min(n0 + r, A.N - 1) * A.rb + 16 * j;
+                j4[i] = 0;
+            } else {
+                const int c = min(C::T * i + t, C::BN * 54 - 1);
+                const int r = c / 54, j = c - 54 * r;
+                w[i] = A.W + (int64_t)min(n0 + r, A.N - 1) * A.rb;
+                j4[i] = 4 * j;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::ACH; i++) {
+            const int c = C::T * i + t;
+            const int r = c >> 4, s = c & 15;
+            a[i] = A.q + (int64_t)min(m0 + r, A.M - 1) * A.K + 16 * (s ^ (r & 15));
+        }
+        dx = A.d32 + (int64_t)min(m0 + min(t, C::BM - 1), A.M - 1) * (A.K / 32);
+    }
+    __device__ __forceinline__ void issue(int b, uint8_t* buf) const {
+        uint8_t* wl = buf;
+        uint8_t* al = buf + L::WBYTES;
+        uint8_t* dl = al + L::ABYTES;
+#pragma unroll
+        for (int i = 0; i < L::WDMA; i++) {
+            if constexpr (DT == DT_Q4_K) {
+                lds_copy16(w[i] + (uint32_t)(b * Q4K_BYTES), wl + 16 * (C::T * i + 64 * wave));
+            } else {
+                const uint8_t* blk = w[i] + (uint32_t)(b * Q6K_BYTES);
+                lds_copy4((const uint8_t*)__builtin_align_down(blk, 4) + j4[i], wl + 4 * (C::T * i + 64 * wave));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::ACH; i++) lds_copy16(a[i] + (uint32_t)(256 * b), al + 16 * (C::T * i + 64 * wave));
+        lds_copy4(dx + 8 * b, dl + 4 * (64 * wave));  // slots t >= BM are slack
+    }
+};
+
 // The A operands of k step ks (64 k) for this lane's weight row wr (the
 // block in LDS) and k group G. Q4_K: sc = 8*sh + sl with sh, sl <= 7: sh*q
 // and sl*q (q <= 15) are at most 105, so each plane is the packed nibbles
@@ -255,11 +312,12 @@ __global__ __launch_bounds__(C::T) void gemm_a8k_kernel(GemmArgs A) {
     // that ends block b - 1). Past the last block the last one is copied
     // again into the free stage, so every thread always has the same
     // number of copies in flight and one wait count serves every block.
+    const KsCopy<DT, C> cp(A, n0, m0);
 #pragma unroll
-    for (int i = 0; i < NS - 1; i++) gemm_issue_block<DT, C>(A, n0, m0, min(i, nb - 1), smem + i * L::BUF);
+    for (int i = 0; i < NS - 1; i++) cp.issue(min(i, nb - 1), smem + i * L::BUF);
     for (int b = 0; b < nb; b++) {
         uint8_t* buf = smem + (b % NS) * L::BUF;
-        gemm_issue_block<DT, C>(A, n0, m0, min(b + NS - 1, nb - 1), smem + ((b + NS - 1) % NS) * L::BUF);
+        cp.issue(min(b + NS - 1, nb - 1), smem + ((b + NS - 1) % NS) * L::BUF);
         GM_WAIT_VMCNT((NS - 1) * L::NDMA);  // block b's copies (issued NS - 1 blocks earlier) have landed
         gm_barrier();
         const uint8_t* wl = buf;
@@ -397,63 +455,6 @@ __global__ __launch_bounds__(C::T) void gemm_a8k_kernel(GemmArgs A) {
 // BM activation rows, 256 threads, a ring of NS stages (Q6_K four: its
 // tables are half Q4_K's, and 64-row down grids leave a CU to one workgroup;
 // Q4_K three, so its 64-row tables fit beside the ring).
-// A thread's copy sources for block 0, fixed over the blocks (block b adds
-// b times the block size), and the wave index as a scalar, so that each
-// block's copies cost one 64-bit add each (and the Q6_K realignment) and
-// their LDS bases are scalar: gemm_issue_block's copies, in the same order
-// to the same LDS bytes.
-template <uint32_t DT, class C>
-struct KsCopy {
-    using L = GemmLayout<DT, C>;
-    const uint8_t* w[L::WDMA];  // Q4_K: the chunk's bytes in block 0; Q6_K: the row's block 0
-    uint32_t j4[L::WDMA];       // Q6_K: the dword within the aligned block
-    const int8_t* a[C::ACH];
-    const float* dx;
-    int wave;
-    __device__ KsCopy(const GemmArgs& A, int n0, int m0) {
-        const int t = threadIdx.x;
-        wave = __builtin_amdgcn_readfirstlane(t >> 6);
-#pragma unroll
-        for (int i = 0; i < L::WDMA; i++) {
-            if constexpr (DT == DT_Q4_K) {
-                const int c = min(C::T * i + t, C::BN * 9 - 1);
-                const int r = c / 9, j = c - 9 * r;
-                w[i] = A.W + (int64_t)min(n0 + r, A.N - 1) * A.rb + 16 * j;
-                j4[i] = 0;
-            } else {
-                const int c = min(C::T * i + t, C::BN * 54 - 1);
-                const int r = c / 54, j = c - 54 * r;
-                w[i] = A.W + (int64_t)min(n0 + r, A.N - 1) * A.rb;
-                j4[i] = 4 * j;
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < C::ACH; i++) {
-            const int c = C::T * i + t;
-            const int r = c >> 4, s = c & 15;
-            a[i] = A.q + (int64_t)min(m0 + r, A.M - 1) * A.K + 16 * (s ^ (r & 15));
-        }
-        dx = A.d32 + (int64_t)min(m0 + min(t, C::BM - 1), A.M - 1) * (A.K / 32);
-    }
-    __device__ __forceinline__ void issue(int b, uint8_t* buf) const {
-        uint8_t* wl = buf;
-        uint8_t* al = buf + L::WBYTES;
-        uint8_t* dl = al + L::ABYTES;
-#pragma unroll
-        for (int i = 0; i < L::WDMA; i++) {
-            if constexpr (DT == DT_Q4_K) {
-                lds_copy16(w[i] + (uint32_t)(b * Q4K_BYTES), wl + 16 * (C::T * i + 64 * wave));
-            } else {
-                const uint8_t* blk = w[i] + (uint32_t)(b * Q6K_BYTES);
-                lds_copy4((const uint8_t*)__builtin_align_down(blk, 4) + j4[i], wl + 4 * (C::T * i + 64 * wave));
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < C::ACH; i++) lds_copy16(a[i] + (uint32_t)(256 * b), al + 16 * (C::T * i + 64 * wave));
-        lds_copy4(dx + 8 * b, dl + 4 * (64 * wave));  // slots t >= BM are slack
-    }
-};
-
 template <int BM_, int NS_>
 struct KsCfg {
     static constexpr int T = 256, NW = 1, BN = 16, BM = BM_, NS = NS_;
