@@ -12,8 +12,8 @@
 // internal/kernels/q8k_test.go:38-102; tiles as amx.go:194-316).
 //
 // Exact products on int8 MFMA: Q4_K sc = 8*sh + sl (sh, sl <= 7), planes
-// sh*q and sl*q (each <= 105), S = 8*H + L; Q6_K w = 128*hi + lo, lo in
-// [0,127], hi in [-32,31]; Q4_K's M term is a third plane with A = m_s.
+// sh*q and sl*q (each <= 105), S = 8*H + L; Q6_K w = 256*hi + lo, lo in
+// [-128,127], hi in [-16,16]; Q4_K's M term is a third plane with A = m_s.
 //
 // Tiling (a shape C: T threads, NW waves along the weight rows, BM
 // activation rows, NS stages): wave w takes weight rows 16(w % NW).. (A
@@ -244,7 +244,7 @@ __device__ __forceinline__ void q4k_operands(const uint8_t* wr, const Q4KScales&
     }
 }
 
-// Q6_K: the two planes of sc*(q - 32) (hi and lo, S = 128 hi + lo) of k step
+// Q6_K: the two planes of sc*(q - 32) (hi and lo, S = 256 hi + lo) of k step
 // ks for the block at wr (rsh = wr & 3, wra the dword below it).
 __device__ __forceinline__ void q6k_operands(const uint32_t* wra, uint32_t rsh, const uint8_t* wr, int ks, int G,
                                              v4i& aH, v4i& aL) {
@@ -257,19 +257,22 @@ __device__ __forceinline__ void q6k_operands(const uint32_t* wra, uint32_t rsh, 
     const u32x4 ql = rd16(64 * h + 32 * (p & 1) + 16 * (G & 1));
     const u32x4 qh = rd16(128 + 32 * h + 16 * (G & 1));
     const int sc = (int)(int8_t)wr[192 + 8 * h + (G & 1) + 2 * p];
-    const s16x2 sc2 = {(short)sc, (short)sc};
+    // u = sc*q - 32*sc + 128 = w + 128 in 16-bit lanes (packed integer
+    // multiply-add, exact: |u| <= 4224); hi = u's high byte, lo = w's low
+    // byte = u's with the top bit flipped, so w = 256 hi + lo
+    const short cu = (short)(128 - 32 * sc);
+    const s16x2 sc2 = {(short)sc, (short)sc}, c2 = {cu, cu};
     const uint32_t qld[4] = {ql.x, ql.y, ql.z, ql.w}, qhd[4] = {qh.x, qh.y, qh.z, qh.w};
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         const uint32_t q6 = (((p >> 1) ? (qld[k] >> 4) : qld[k]) & 0x0F0F0F0Fu) |
                             (((qhd[k] >> (2 * p)) & 0x03030303u) << 4);
-        // 16-bit lanes of sc*(q - 32): packed integer ops, exact (|w| <= 4096)
-        const s16x2 we = (as_s16x2(q6 & 0x00FF00FFu) - (s16x2){32, 32}) * sc2;
-        const s16x2 wo = (as_s16x2((q6 >> 8) & 0x00FF00FFu) - (s16x2){32, 32}) * sc2;
-        uint32_t lo, hi;
-        split4(as_u32(we), as_u32(wo), as_u32(we >> (s16x2){7, 7}), as_u32(wo >> (s16x2){7, 7}), lo, hi);
-        aL[k] = (int)lo;
-        aH[k] = (int)hi;
+        // bytes 0, 2 (ue) and 1, 3 (uo) of q6 as 16-bit lanes (selector 0x0C: a zero byte)
+        const uint32_t ue = as_u32(as_s16x2(__builtin_amdgcn_perm(0u, q6, 0x0C020C00u)) * sc2 + c2);
+        const uint32_t uo = as_u32(as_s16x2(__builtin_amdgcn_perm(0u, q6, 0x0C030C01u)) * sc2 + c2);
+        // v_perm selector [src1.bX, src0.bX, src1.bY, src0.bY]: w0 w1 w2 w3
+        aH[k] = (int)__builtin_amdgcn_perm(uo, ue, 0x07030501u);
+        aL[k] = (int)(__builtin_amdgcn_perm(uo, ue, 0x06020400u) ^ 0x80808080u);
     }
 }
 
@@ -397,7 +400,7 @@ __global__ __launch_bounds__(C::T) void gemm_a8k_kernel(GemmArgs A) {
             const float dx = dl[16 * (wm * GM_TM + mt) + ar];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int S = (accH[mt][r] << (DT == DT_Q4_K ? 3 : 7)) + accL[mt][r];
+                const int S = (accH[mt][r] << (DT == DT_Q4_K ? 3 : 8)) + accL[mt][r];
                 tot[mt][r] = __builtin_fmaf((float)S, dC[r] * dx, tot[mt][r]);
                 if (DT == DT_Q4_K) off[mt][r] = __builtin_fmaf((float)accM[mt][r], dminC[r] * dx, off[mt][r]);
             }
@@ -613,7 +616,7 @@ __global__ __launch_bounds__(256) void gemm_a8k_ks_kernel(GemmArgs A) {
         for (int mt = 0; mt < TMK; mt++) {
             v4i S;
 #pragma unroll
-            for (int r = 0; r < 4; r++) S[r] = (accH[mt][r] << (DT == DT_Q4_K ? 3 : 7)) + accL[mt][r];
+            for (int r = 0; r < 4; r++) S[r] = (accH[mt][r] << (DT == DT_Q4_K ? 3 : 8)) + accL[mt][r];
             const int at = (ks * BMK + 16 * mt + ar) * KS_RS + 4 * G;
             *(v4i*)(tS + at) = S;
             if constexpr (DT == DT_Q4_K) *(v4i*)(tM + at) = accM[mt];

@@ -125,16 +125,6 @@ __device__ __forceinline__ uint32_t byte_of(uint64_t v, int j) { return (uint32_
 // Packed 16-bit lanes (int8 MFMA operand building).
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 
-// Four scaled weights w_i, as 16-bit lanes (pe: w0, w2; po: w1, w3; he/ho:
-// the same shifted right by 7 within each lane), to the bytes of
-// lo = w & 127 and hi = w >> 7 in the order w0 w1 w2 w3.
-__device__ __forceinline__ void split4(uint32_t pe, uint32_t po, uint32_t he, uint32_t ho, uint32_t& lo,
-                                       uint32_t& hi) {
-    // v_perm selector [src1.b0, src0.b0, src1.b2, src0.b2]
-    lo = __builtin_amdgcn_perm(po, pe, 0x06020400u) & 0x7F7F7F7Fu;
-    hi = __builtin_amdgcn_perm(ho, he, 0x06020400u);
-}
-
 __device__ __forceinline__ uint32_t as_u32(s16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ s16x2 as_s16x2(uint32_t v) { return __builtin_bit_cast(s16x2, v); }
 
