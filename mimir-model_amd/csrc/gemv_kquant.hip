@@ -85,28 +85,19 @@ struct KQ {
 };
 
 // Pairs per group and iteration (all their weight loads in flight at once).
-#ifndef MIMG_PAIRS_U
-#define MIMG_PAIRS_U 4
-#endif
-#ifndef MIMG_PAIRS_QMAJOR
-#define MIMG_PAIRS_QMAJOR 1  // measured: Q6_K down 13.6 -> 12.9 us, gate unchanged
-#endif
+constexpr int PAIRS_U = 4;
 
 // With U dividing R, the U-row quads (block b, rows r0..r0+U-1) of group g:
-// the pair base pb = p0 + U*g (< npairs) names quad pb/U. Block-major (b =
-// pb/R) or, QMAJOR, block-fastest (b = (pb/U) % nb), so that the eight
-// groups of a wave read eight consecutive blocks of the same rows.
+// the pair base pb = p0 + U*g (< npairs) names quad pb/U, block-fastest (b =
+// (pb/U) % nb), so that the eight groups of a wave read eight consecutive
+// blocks of the same rows (measured: Q6_K down 13.6 -> 12.9 us against
+// block-major quads, gate unchanged).
 template <int R, int U>
 __device__ __forceinline__ void quad_of(int pb, int nb, int& b, int& r0) {
-    if constexpr (MIMG_PAIRS_QMAJOR) {
-        const int q = pb / U;
-        const int rq = q / nb;
-        b = q - rq * nb;
-        r0 = rq * U;
-    } else {
-        b = pb / R;
-        r0 = pb - b * R;
-    }
+    const int q = pb / U;
+    const int rq = q / nb;
+    b = q - rq * nb;
+    r0 = rq * U;
 }
 
 // Pairs are numbered block-major (p = b*R + r), and group g of an iteration
@@ -123,7 +114,7 @@ __device__ __forceinline__ void quad_of(int pb, int nb, int& b, int& r0) {
 // results meet in LDS and out[n] = swiglu(gate[n], up[n]) is written.
 // One workgroup's tile `tile` of the matrix A.W (A.wref, A.bias, A.y, A.N
 // and A.y_stride are that matrix's; SW reads gate and up from A.mat[0..1]).
-template <uint32_t DT, int M, int R, bool SW, int U = MIMG_PAIRS_U>
+template <uint32_t DT, int M, int R, bool SW, int U = PAIRS_U>
 __device__ __forceinline__ void pairs_tile(GemvArgs A, int tile, uint8_t* smem) {
     constexpr bool SHARED = R % U == 0;  // a group's U pairs share one block
     constexpr bool PRE = M == 1;         // activation loaded before the weights
@@ -285,7 +276,7 @@ __device__ __forceinline__ void pairs_tile(GemvArgs A, int tile, uint8_t* smem) 
     }
 }
 
-template <uint32_t DT, int M, int R, bool SW = false, int U = MIMG_PAIRS_U>
+template <uint32_t DT, int M, int R, bool SW = false, int U = PAIRS_U>
 __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
     extern __shared__ __align__(16) uint8_t smem[];
     // This workgroup's matrix of the launch.
@@ -304,7 +295,7 @@ __global__ __launch_bounds__(256) void gemv_a8k_pairs_kernel(GemvArgs A) {
 
 // gate and up at one row with swiglu in the epilogue (Q4_K, N % U == 0).
 static hipError_t launch_pairs_swiglu(GemvArgs A, hipStream_t stream) {
-    constexpr int U = MIMG_PAIRS_U, R = 2 * U;
+    constexpr int U = PAIRS_U, R = 2 * U;
     A.mat[0].tile0 = A.mat[1].tile0 = 0;
     const int tiles = A.N / U;
     const size_t lds = (size_t)R * A.nb * 16 + (size_t)R * 4 + (size_t)R * 4;
@@ -312,7 +303,7 @@ static hipError_t launch_pairs_swiglu(GemvArgs A, hipStream_t stream) {
     return hipGetLastError();
 }
 
-template <uint32_t DT, int M, int R, int U = MIMG_PAIRS_U>
+template <uint32_t DT, int M, int R, int U = PAIRS_U>
 static hipError_t launch_pairs_r(GemvArgs A, hipStream_t stream) {
     int tiles = 0;
     for (int i = 0; i < A.nmat; i++) {
@@ -327,9 +318,6 @@ static hipError_t launch_pairs_r(GemvArgs A, hipStream_t stream) {
 // Rows per workgroup: enough (row, block) pairs to keep 32 groups busy, as
 // many workgroups as possible, and the pair table within 48 KB of LDS.
 static int pairs_rows(int N, int nb, int M) {
-#ifdef MIMG_PAIRS_R
-    if ((size_t)MIMG_PAIRS_R * nb * M * 16 <= 48 * 1024) return MIMG_PAIRS_R;  // a tuning build
-#endif
     int R = 8;
     while (R > 1 && ((N + R - 1) / R < 1024 || (size_t)R * nb * M * 16 > 48 * 1024)) R >>= 1;
     return R;
@@ -365,7 +353,7 @@ static hipError_t launch_dt(GemvArgs A, int rows, hipStream_t stream) {
 
 bool gemv_swiglu_ok(const DevWeight& gate, const DevWeight& up) {
     return gate.dt == DT_Q4_K && up.dt == DT_Q4_K && gate.n == up.n && gate.k == up.k && gate.k % 256 == 0 &&
-           gate.n % MIMG_PAIRS_U == 0 && gate.k <= 16384 && gate.n <= (1 << 30);
+           gate.n % PAIRS_U == 0 && gate.k <= 16384 && gate.n <= (1 << 30);
 }
 
 hipError_t launch_gemv_a8k_swiglu(const DevWeight& gate, const DevWeight& up, const ActPtrs& a, const float* x,
@@ -454,7 +442,7 @@ hipError_t launch_gemv_a8k(const DevWeight* const* ws, int nmat, const ActPtrs& 
 // workgroup's segment would make the compiler copy it to private memory)
 // and runs that matrix's tile exactly as the pairs kernel does, so every
 // output is bit for bit the separate call's.
-template <int R4, int R6, int U6, uint32_t ONLY>
+template <int R4, int R6, int U6>
 __global__ __launch_bounds__(256) void gemv_a8k_set_kernel(SetArgs args) {
     extern __shared__ __align__(16) uint8_t smem[];
     const SetArgs* S = (const SetArgs*)__builtin_amdgcn_kernarg_segment_ptr();
@@ -485,48 +473,29 @@ __global__ __launch_bounds__(256) void gemv_a8k_set_kernel(SetArgs args) {
     A.sw = nullptr;
     A.sw_total = A.sw_chunk = 0;
     const int tile = bid - S->tile0[si];
-    if constexpr (ONLY == DT_Q4_K) {
-        pairs_tile<DT_Q4_K, 1, R4, false>(A, tile, smem);
-    } else if constexpr (ONLY == DT_Q6_K) {
-        pairs_tile<DT_Q6_K, 1, R6, false, U6>(A, tile, smem);
-    } else {
-        if (s->dt == DT_Q4_K) pairs_tile<DT_Q4_K, 1, R4, false>(A, tile, smem);
-        else pairs_tile<DT_Q6_K, 1, R6, false, U6>(A, tile, smem);
-    }
+    if (s->dt == DT_Q4_K) pairs_tile<DT_Q4_K, 1, R4, false>(A, tile, smem);
+    else pairs_tile<DT_Q6_K, 1, R6, false, U6>(A, tile, smem);
 }
 
 // Rows per workgroup in a set launch (the launch has thousands of tiles, so
 // the standalone launch's rule of at least 1024 workgroups does not apply).
 // One launch for both dtypes measured faster than a launch per dtype
 // (cfg1 set 39.0 against 41.0 us a step).
-#ifndef MIMG_SET_R4
-#define MIMG_SET_R4 8
-#endif
-#ifndef MIMG_SET_R6
-#define MIMG_SET_R6 8
-#endif
+constexpr int SET_R4 = 8, SET_R6 = 8;
 // Q6_K pairs in flight per group of eight lanes: two keep the launch at 64
 // VGPRs (eight waves a SIMD for the Q4_K tiles too; measured on MI355X, the
 // cfg1 set 34.3 -> 32.0 us with eight Q6_K rows a workgroup instead of four).
-#ifndef MIMG_SET_U6
-#define MIMG_SET_U6 2
-#endif
-// One launch for both dtypes (0), or a launch per dtype (1).
-#ifndef MIMG_SET_SPLIT
-#define MIMG_SET_SPLIT 0
-#endif
+constexpr int SET_U6 = 2;
 
-static int set_rows(uint32_t dt) { return dt == DT_Q4_K ? MIMG_SET_R4 : MIMG_SET_R6; }
+static int set_rows(uint32_t dt) { return dt == DT_Q4_K ? SET_R4 : SET_R6; }
 
 // Segments in launch order, the longest workgroups first (weight bytes a
 // workgroup reads), so that the grid's tail is made of short ones; tile0 of
 // each set here.
-template <uint32_t ONLY>
-static hipError_t launch_set_part(const SetArgs& in, hipStream_t stream) {
+static hipError_t launch_set(const SetArgs& in, hipStream_t stream) {
     SetArgs a;
     memset(&a, 0, sizeof a);
-    for (int i = 0; i < in.nseg; i++)
-        if (ONLY == 0 || (uint32_t)in.seg[i].dt == ONLY) a.seg[a.nseg++] = in.seg[i];
+    for (int i = 0; i < in.nseg; i++) a.seg[a.nseg++] = in.seg[i];
     if (a.nseg == 0) return hipSuccess;
     auto wg_bytes = [](const SetSeg& s) {
         return (int64_t)set_rows((uint32_t)s.dt) * s.nb * (s.dt == DT_Q4_K ? Q4K_BYTES : Q6K_BYTES);
@@ -541,21 +510,17 @@ static hipError_t launch_set_part(const SetArgs& in, hipStream_t stream) {
         tiles += (a.seg[i].N + R - 1) / R;
         nbmax = a.seg[i].nb * R > nbmax ? a.seg[i].nb * R : nbmax;
     }
-    const int rmax = MIMG_SET_R4 > MIMG_SET_R6 ? MIMG_SET_R4 : MIMG_SET_R6;
+    const int rmax = SET_R4 > SET_R6 ? SET_R4 : SET_R6;
     const size_t lds = (size_t)nbmax * 16 + (size_t)rmax * 4;
     if (lds > 64 * 1024) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((gemv_a8k_set_kernel<MIMG_SET_R4, MIMG_SET_R6, MIMG_SET_U6, ONLY>), dim3((unsigned)tiles), dim3(256), lds,
-                       stream, a);
+    hipLaunchKernelGGL((gemv_a8k_set_kernel<SET_R4, SET_R6, SET_U6>), dim3((unsigned)tiles), dim3(256), lds, stream, a);
     return hipGetLastError();
 }
 
 hipError_t launch_gemv_a8k_set(const SetArgs& a, hipStream_t stream) {
     for (int i = 0; i < a.nseg; i++)
         if (a.seg[i].dt != (int32_t)DT_Q4_K && a.seg[i].dt != (int32_t)DT_Q6_K) return hipErrorInvalidValue;
-    if (!MIMG_SET_SPLIT) return launch_set_part<0>(a, stream);
-    hipError_t e = launch_set_part<DT_Q6_K>(a, stream);
-    if (e != hipSuccess) return e;
-    return launch_set_part<DT_Q4_K>(a, stream);
+    return launch_set(a, stream);
 }
 
 }  // namespace mimg
